@@ -1,0 +1,240 @@
+#!/usr/bin/env python3
+"""Benchmark of the GPTQ-2D layer-quantization path on one MI355X.
+
+One step quantizes one layer end to end on the GPU: the two feedback factors
+L = ldl_of_inverse(A) and U = ldl_of_inverse(B)^T (blocked HIP Cholesky + triangular inverse) and
+the GPTQ-2D sweep of W with the INT4 quantizer fused into the HIP tile sweep.  The workload is the
+headline layer of the benchmark definition, "H": W 8192 x 8192 fp32 ~ N(0, 0.02^2) with 0.5%
+Student-t(3) x 0.1 outliers, Wishart-like Kronecker factors A, B (G 8192 x 32768 Gaussian, s_i =
+i^-0.5, + 1e-2 I), INT4 symmetric per-row static scale (bf16-rounded abs-max of the row / 7.5,
+zero point 0).  Inputs are synthetic (seeded numpy PCG64, instances.py) and resident in HBM before
+the timed region, which covers --steps full steps after --warmup untimed ones.
+
+Printed: one JSON line with the layer time (``value``, seconds per layer, lower is better), the
+per-part breakdown, the roofline of the dominant kernel (the cross-tile feedback panels, fp32,
+measured with HIP events around every launch inside the library during the timed steps) and the
+CPU baseline: the restated reference PyTorch path (oracle: torch.linalg LDL + ``gptq_2d_torch``)
+on the host cores, on a bounded sample (both LDLs in full, an evenly spaced sample of sweep stages
+on the full-size tensors, extrapolated to all stages by each stage's exact work).
+"""
+
+from __future__ import annotations
+
+import argparse
+import functools
+import json
+import os
+import pathlib
+import platform
+import statistics
+import sys
+import time
+
+ROOT = pathlib.Path(__file__).resolve().parent
+for _p in (str(ROOT / "gptq-2d_amd"), str(ROOT)):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "layer quantize time (s) @8192² INT4; panel MFMA util %; Viterbi weights/s"
+FP32_MFMA_PEAK_TFLOPS = 157.3
+HBM_PEAK_GBS = 8000.0
+
+
+def _parse():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=3)
+    ap.add_argument("--warmup", type=int, default=1)
+    ap.add_argument("--config", default="H", help="workload from instances.CONFIGS (default: the headline layer)")
+    ap.add_argument("--cpu-stages", type=int, default=4096, help="sweep stages in the CPU baseline sample")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    return ap.parse_args()
+
+
+def _cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def _cpu_baseline(cfg, x, a, b, scale, zp, l_dev, u_dev, stages_in_sample):
+    """The reference's PyTorch CPU path (restated in oracle/): LDL of both factors in full, and a sample of
+    sweep stages on the full-size tensors extrapolated by exact per-stage work."""
+    import torch
+
+    from oracle import algorithms as OA
+    from oracle import quantize as OQ
+    from oracle import sweep as OS
+
+    threads = torch.get_num_threads()
+    ac, bc = a.cpu(), b.cpu()
+    t0 = time.perf_counter()
+    OA.ldl_of_inverse(ac)
+    t_ldl_a = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    OA.ldl_of_inverse(bc).t()
+    t_ldl_b = time.perf_counter() - t0
+    m, n = x.shape
+    q = functools.partial(OQ.affine_quantizer, qmin=cfg.qmin, qmax=cfg.qmax)
+    state = OS.TorchSweepState(x.cpu(), l_dev.cpu(), u_dev.cpu(), quantizer=q,
+                               quantizer_inputs=(scale.cpu(), zp.cpu()))
+    stages = m + n - 1
+    sample = sorted({int(round(i * (stages - 1) / max(1, stages_in_sample - 1))) for i in range(stages_in_sample)})
+    t_sample = 0.
+    w_sample = 0
+    for s in sample:
+        t0 = time.perf_counter()
+        state.run_stage(s)
+        t_sample += time.perf_counter() - t0
+        w_sample += OS.stage_work(m, n, s)
+    w_total = sum(OS.stage_work(m, n, s) for s in range(stages))
+    t_sweep = t_sample * w_total / w_sample
+    value = t_ldl_a + t_ldl_b + t_sweep
+    return {
+        "value": value,
+        "unit": "s/layer",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"restated reference PyTorch path on {threads} threads of {_cpu_model()}: ldl_of_inverse(A) "
+                   f"{t_ldl_a:.2f} s and ldl_of_inverse(B) {t_ldl_b:.2f} s in full; gptq_2d_torch {len(sample)} of "
+                   f"{stages} stages on the full {m}x{n} tensors ({t_sample:.1f} s), extrapolated by exact "
+                   f"per-stage work to {t_sweep:.1f} s"),
+        "extrapolated": True,
+    }
+
+
+def main() -> int:
+    args = _parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: the layer quantization runs on a single MI355X (--gpus {args.gpus} "
+              "is not supported; independent layers shard across GPUs without any exchange)", file=sys.stderr)
+        return 2
+
+    import torch
+
+    import _hip
+    import gptq_2d as G
+    import gptq_2d_ldl as LDL
+    import instances
+    import quantizer_int as QI
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    cfg = instances.CONFIGS[args.config]
+    m, n = cfg.m, cfg.n
+
+    # ---------------------------------------------------------------- inputs, resident in HBM
+    w64 = instances.weights(m, n, cfg.seeds[0], cfg.outliers, cfg.bf16)
+    x = w64.float().to(dev)
+    del w64
+    a = instances.wishart_factor(m, cfg.alpha, cfg.seeds[1], device=dev).float()
+    b = instances.wishart_factor(n, cfg.alpha, cfg.seeds[2], device=dev).float()
+    scale, zp = instances.quantizer_inputs(cfg, x)
+    quant = functools.partial(QI.affine_quantizer_hip, qmin=cfg.qmin, qmax=cfg.qmax)
+    torch.cuda.synchronize()
+
+    def step(events=None):
+        if events:
+            events[0].record()
+        lo = LDL.ldl_of_inverse(a, check=False)
+        if events:
+            events[1].record()
+        up = LDL.ldl_of_inverse(b, check=False).t()
+        if events:
+            events[2].record()
+        z = G.gptq_2d(x, lo, up, quantizer=quant, quantizer_inputs=(scale, zp))
+        if events:
+            events[3].record()
+        return z, lo, up
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    # ---------------------------------------------------------------- timed region
+    events = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(args.steps)]
+    _hip.profile_start(8192)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for k in range(args.steps):
+        z, lo, up = step(events[k])
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    flush_ms, flush_flops, flush_n = _hip.profile_read(_hip.PROF_FLUSH)
+    tile_ms, tile_entries, tile_n = _hip.profile_read(_hip.PROF_TILE_SWEEP)
+    _hip.profile_stop()
+    ms_per_step = 1e3 * elapsed / args.steps
+    parts = {name: statistics.median(ev[i].elapsed_time(ev[i + 1]) for ev in events)
+             for i, name in enumerate(("ldl_a_ms", "ldl_b_ms", "sweep_ms"))}
+
+    # ---------------------------------------------------------------- sanity: INT4 codes, objective vs RTN
+    codes = z / scale
+    assert torch.equal(codes, codes.round()) and codes.min() >= cfg.qmin and codes.max() <= cfg.qmax, "bad codes"
+    a64, b64 = a.double(), b.double()
+
+    def objective(zz):
+        r = (zz - x).double()
+        return float(((a64 @ r) * (r @ b64)).sum())
+
+    rtn = torch.clamp(torch.round(x / scale), cfg.qmin, cfg.qmax) * scale
+    obj_ratio = objective(z) / objective(rtn)
+
+    avg_us = 1e3 * flush_ms / max(1, flush_n)
+    achieved = flush_flops / max(1, flush_n) / (avg_us * 1e-6) / 1e12 if flush_n else None
+    roofline = {
+        "bound": "mfma",
+        "achieved": achieved,
+        "peak": FP32_MFMA_PEAK_TFLOPS,
+        "unit": "TFLOP/s",
+        "frac": achieved / FP32_MFMA_PEAK_TFLOPS if achieved else None,
+        "traffic": None,
+        "kernel": "cross-tile feedback panels (flush), fp32",
+        "launches": flush_n // max(1, args.steps),
+        "avg_launch_us": avg_us,
+        "flops_per_launch": flush_flops / max(1, flush_n),
+    }
+    stages = m + n - 1
+    result = {
+        "metric": METRIC,
+        "value": ms_per_step / 1e3,
+        "unit": "s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded PCG64 weights and Wishart-like Kronecker factors; no checkpoint)",
+        "config": {
+            "workload": f"{cfg.name}: {m}x{n} INT4 symmetric per-row static bf16 scale, Wishart-like A, B "
+                        f"(s_i = i^-{cfg.alpha:g}, 1e-2 damping); LDL(A) + LDL(B) + fused GPTQ-2D sweep",
+            "m": m, "n": n, "stages": stages, "quantizer": "affine INT4 [-8, 7], zero point 0",
+        },
+        "breakdown": {
+            **{k: round(v, 3) for k, v in parts.items()},
+            "sweep_us_per_stage": round(1e3 * parts["sweep_ms"] / stages, 3),
+            "flush_ms_per_step": round(flush_ms / args.steps, 3),
+            "tile_sweep_ms_per_step": round(tile_ms / args.steps, 3),
+            "tile_sweep_launches_per_step": tile_n // max(1, args.steps),
+            "objective_vs_rtn": round(obj_ratio, 5),
+        },
+        "roofline": roofline,
+        "viterbi_weights_per_s": None,
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu:
+        result["cpu_baseline"] = _cpu_baseline(cfg, x, a, b, scale, zp, lo, up, args.cpu_stages)
+        result["gpu_vs_cpu_speedup"] = result["cpu_baseline"]["value"] / result["value"]
+    print(json.dumps(result))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

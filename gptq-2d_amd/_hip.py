@@ -39,8 +39,11 @@ _SIGNATURES = {
     "round_quantize_se": [_P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I32, _AP, _P],
     "absmax_scale": [_P, _P, _I64, _I64, _I64, _I64, _F64, _F64, _I32, _P],
     "absmax_quantize_se": [_P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _F64, _F64, _I32, _P],
+    "ldl_of_inverse": [_P, _P, _P, _P, _I64, _I64, _I64, _P],
+    "ldl": [_P, _P, _P, _P, _I64, _I64, _I64, _P],
+    "gemm": [_I64, _I64, _I64, _I64, _P, _I64, _I64, _I64, _P, _I64, _I64, _I64, _P, _I64, _I64, _I64, _F64, _F64,
+             _I32, _I32, _I32, _P],
 }
-_OPTIONAL = {"viterbi", "ldl_of_inverse"}
 
 _lib = None
 
@@ -61,6 +64,13 @@ def lib() -> ctypes.CDLL:
                 fn = getattr(handle, f"gptq2d_{name}_{suffix}")
                 fn.argtypes = argtypes
                 fn.restype = ctypes.c_int
+        handle.gptq2d_profile_start.argtypes = [_I64]
+        handle.gptq2d_profile_start.restype = ctypes.c_int
+        handle.gptq2d_profile_read.argtypes = [_I32, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double),
+                                               ctypes.POINTER(ctypes.c_int64)]
+        handle.gptq2d_profile_read.restype = ctypes.c_int
+        handle.gptq2d_profile_stop.argtypes = []
+        handle.gptq2d_profile_stop.restype = ctypes.c_int
         _lib = handle
     return _lib
 
@@ -74,6 +84,30 @@ def call(name: str, dtype: torch.dtype, *args) -> None:
     rc = fn(*args)
     if rc != 0:
         raise GPTQ2DError(f"gptq2d_{name}_{suffix} failed with code {rc}")
+
+
+# Kernel classes of the launch profiler (csrc/profile.h).
+PROF_FLUSH, PROF_TILE_SWEEP, PROF_LDL_GEMM = 0, 1, 2
+
+
+def profile_start(capacity: int = 4096) -> None:
+    """Time every launch of the profiled kernel classes with HIP events until ``profile_stop``."""
+    rc = lib().gptq2d_profile_start(capacity)
+    if rc:
+        raise GPTQ2DError(f"gptq2d_profile_start failed with code {rc}")
+
+
+def profile_read(kind: int):
+    """(summed launch ms, summed algorithmic work, launches) of one kernel class; waits for its events."""
+    ms, work, n = ctypes.c_double(), ctypes.c_double(), ctypes.c_int64()
+    rc = lib().gptq2d_profile_read(kind, ctypes.byref(ms), ctypes.byref(work), ctypes.byref(n))
+    if rc:
+        raise GPTQ2DError(f"gptq2d_profile_read failed with code {rc}")
+    return ms.value, work.value, n.value
+
+
+def profile_stop() -> None:
+    lib().gptq2d_profile_stop()
 
 
 def ptr(t: torch.Tensor | None):

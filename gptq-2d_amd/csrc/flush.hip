@@ -18,6 +18,7 @@
 // _flush_down_kernel :766-902 and _flush_right_kernel :936-1057, applied in that order by
 // _flush_block :1090-1119.  The band of E is read in matrix layout with a mask, so no repack.
 #include "common.h"
+#include "profile.h"
 
 namespace {
 
@@ -205,6 +206,25 @@ static int64_t flush_grid_x(const FlushGeom& g, int64_t& nrow_tiles) {
   return nx;
 }
 
+// Useful flops of one flush: 2 per (target, source) pair that the two band products sum, i.e.
+// for a coarse target cell (a, b) of h(a) x w(b) entries, 2 h(a) w(b) (sum of h(a') over the down
+// sources a' + sum of w(b') over the right sources b').  Host-side, for the launch profiler.
+double gptq2d_flush_flops(int64_t m, int64_t n, int64_t P, int64_t Q, int64_t s0, int64_t s1, int64_t s_end) {
+  const int64_t mc = cdiv(m, P), nc = cdiv(n, Q);
+  auto h = [&](int64_t a) { return (double)((a + 1) * P < m ? P : m - a * P); };
+  auto w = [&](int64_t b) { return (double)((b + 1) * Q < n ? Q : n - b * Q); };
+  double total = 0.;
+  for (int64_t a = 0; a < mc; ++a) {
+    for (int64_t b = s1 - a > 0 ? s1 - a : 0; b < nc && a + b < s_end; ++b) {
+      double rows = 0., cols = 0.;
+      for (int64_t a2 = s0 - b > 0 ? s0 - b : 0; a2 < s1 - b && a2 < a; ++a2) rows += h(a2);
+      for (int64_t b2 = s0 - a > 0 ? s0 - a : 0; b2 < s1 - a && b2 < b; ++b2) cols += w(b2);
+      total += 2. * h(a) * w(b) * (rows + cols);
+    }
+  }
+  return total;
+}
+
 template <typename T>
 int gptq2d_flush(T* y, T* c, const T* e, const T* l, const T* u, int64_t m, int64_t n, int64_t P, int64_t Q,
                  int64_t s0, int64_t s1, int64_t s_end, const BatchMap& lmap, const BatchMap& umap, int64_t B,
@@ -216,7 +236,10 @@ int gptq2d_flush(T* y, T* c, const T* e, const T* l, const T* u, int64_t m, int6
   const int64_t nx = flush_grid_x(g, nrow_tiles);
   if (nx == 0 || nrow_tiles == 0) return 0;
   Grid3 gr = make_grid(nx, nrow_tiles, B);
+  const bool prof = gptq2d_prof_on(PROF_FLUSH);
+  if (prof) gptq2d_prof_begin(PROF_FLUSH, stream);
   hipLaunchKernelGGL(flush_valu_kernel<T>, gr.grid, dim3(256), 0, stream, y, c, e, l, u, g, lmap, umap, gr.nx, gr.ny);
+  if (prof) gptq2d_prof_end(PROF_FLUSH, (double)B * gptq2d_flush_flops(m, n, P, Q, s0, s1, s_end), stream);
   return (int)hipGetLastError();
 }
 

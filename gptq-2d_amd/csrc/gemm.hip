@@ -1,0 +1,232 @@
+// Strided batched GEMM with triangular operand structure, for the LDL preprocessing.
+//
+// D = beta D + alpha A B over arbitrary element strides, so the callers express transposes,
+// reversals (negative strides) and sub-blocks without copies.  Structurally zero parts of
+// triangular operands are skipped in the K loop and masked at load time, so they are never
+// read.  fp32 runs on the MFMA path (v_mfma_f32_32x32x2_f32: 128 x 128 output tile per
+// workgroup, four waves of 64 x 64, K staged through LDS 16 deep); fp64 and tiles that
+// are mostly empty use the VALU path (64 x 64 tile, 4 x 4 outputs per thread).
+#include "linalg.h"
+
+namespace {
+
+// ------------------------------------------------------------------------------------------------ shared
+
+struct TileRange {
+  int64_t k_lo, k_hi;
+  bool empty;
+};
+
+template <typename T>
+__device__ __forceinline__ TileRange tile_k_range(const GemmProblem<T>& p, int64_t i0, int64_t i1, int64_t j0,
+                                                  int64_t j1) {
+  TileRange r{0, p.K, false};
+  if (p.a_tri == TRI_LOWER && i1 < r.k_hi) r.k_hi = i1;  // A(i,k) = 0 for k > i
+  if (p.a_tri == TRI_UPPER && i0 > r.k_lo) r.k_lo = i0;  // A(i,k) = 0 for k < i
+  if (p.b_tri == TRI_LOWER && j0 > r.k_lo) r.k_lo = j0;  // B(k,j) = 0 for k < j
+  if (p.b_tri == TRI_UPPER && j1 < r.k_hi) r.k_hi = j1;  // B(k,j) = 0 for k > j
+  if (p.d_tri == TRI_LOWER && j0 > i1 - 1) r.empty = true;
+  if (p.d_tri == TRI_UPPER && i0 > j1 - 1) r.empty = true;
+  return r;
+}
+
+template <typename T>
+__device__ __forceinline__ T load_a(const GemmProblem<T>& p, const T* a, int64_t i, int64_t k, int64_t k_hi) {
+  if (i >= p.M || k >= k_hi || k < 0) return T(0);
+  if (p.a_tri == TRI_LOWER && k > i) return T(0);
+  if (p.a_tri == TRI_UPPER && k < i) return T(0);
+  return a[i * p.a_rs + k * p.a_cs];
+}
+
+template <typename T>
+__device__ __forceinline__ T load_b(const GemmProblem<T>& p, const T* b, int64_t k, int64_t j, int64_t k_hi) {
+  if (j >= p.N || k >= k_hi || k < 0) return T(0);
+  if (p.b_tri == TRI_LOWER && k < j) return T(0);
+  if (p.b_tri == TRI_UPPER && k > j) return T(0);
+  return b[k * p.b_rs + j * p.b_cs];
+}
+
+template <typename T>
+__device__ __forceinline__ void store_d(const GemmProblem<T>& p, T* d, int64_t i, int64_t j, T acc) {
+  if (i >= p.M || j >= p.N) return;
+  if (p.d_tri == TRI_LOWER && j > i) return;
+  if (p.d_tri == TRI_UPPER && j < i) return;
+  T* dst = d + i * p.d_rs + j * p.d_cs;
+  const T v = p.alpha * acc;
+  *dst = p.beta == T(0) ? v : p.beta * *dst + v;
+}
+
+// ------------------------------------------------------------------------------------------------ VALU path
+
+constexpr int VT = 64, VK = 16;
+
+template <typename T>
+__global__ __launch_bounds__(256) void gemm_valu_kernel(GemmProblem<T> p) {
+  __shared__ T As[VK][VT + 1];
+  __shared__ T Bs[VK][VT + 1];
+  const int64_t bi = blockIdx.z;
+  const int64_t i0 = (int64_t)blockIdx.y * VT, j0 = (int64_t)blockIdx.x * VT;
+  const int64_t i1 = i0 + VT < p.M ? i0 + VT : p.M, j1 = j0 + VT < p.N ? j0 + VT : p.N;
+  const TileRange kr = tile_k_range(p, i0, i1, j0, j1);
+  if (kr.empty) return;
+  const T* a = p.A + bi * p.a_bs;
+  const T* b = p.B + bi * p.b_bs;
+  T* d = p.D + bi * p.d_bs;
+  const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
+  T acc[4][4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) acc[r][c] = T(0);
+  for (int64_t kb = kr.k_lo; kb < kr.k_hi; kb += VK) {
+#pragma unroll
+    for (int ld = 0; ld < 4; ++ld) {
+      const int kl = tid & 15, il = (tid >> 4) + 16 * ld;
+      As[kl][il] = load_a(p, a, i0 + il, kb + kl, kr.k_hi);
+      const int jl = tid & 63, kl2 = (tid >> 6) + 4 * ld;
+      Bs[kl2][jl] = load_b(p, b, kb + kl2, j0 + jl, kr.k_hi);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int kk = 0; kk < VK; ++kk) {
+      T av[4], bv[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) av[r] = As[kk][ty + 16 * r];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) bv[c] = Bs[kk][tx + 16 * c];
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) acc[r][c] += av[r] * bv[c];
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) store_d(p, d, i0 + ty + 16 * r, j0 + tx + 16 * c, acc[r][c]);
+}
+
+// ------------------------------------------------------------------------------------------------ MFMA path (fp32)
+
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+constexpr int MT = 128, MK = 16;
+
+// 256 threads = 4 waves; wave w owns rows 64*(w/2).. and cols 64*(w%2).. of the 128 x 128 tile as
+// 2 x 2 blocks of 32 x 32 (v_mfma_f32_32x32x2_f32).  Operand layout of that instruction: lane l
+// supplies A(l%32, kslot) and B(kslot, l%32) with kslot = l/32; the 16 accumulators of lane l hold
+// D(8*(r/4) + 4*(l/32) + r%4, l%32).  Which k a slot carries is free as long as A and B agree: the
+// lane half h takes k = 8*h + s (s = 0..7) over the 8 instructions of one 16-deep K step, so each
+// lane reads its 8 values as two 16-byte LDS loads.
+__global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmProblem<float> p) {
+  __shared__ __align__(16) float As[MT][MK + 4];  // A(i, k), k fastest
+  __shared__ __align__(16) float Bs[MT][MK + 4];  // B(k, j) stored transposed: [j][k]
+  const int64_t bi = blockIdx.z;
+  const int64_t i0 = (int64_t)blockIdx.y * MT, j0 = (int64_t)blockIdx.x * MT;
+  const int64_t i1 = i0 + MT < p.M ? i0 + MT : p.M, j1 = j0 + MT < p.N ? j0 + MT : p.N;
+  const TileRange kr = tile_k_range(p, i0, i1, j0, j1);
+  if (kr.empty) return;
+  const float* a = p.A + bi * p.a_bs;
+  const float* b = p.B + bi * p.b_bs;
+  float* d = p.D + bi * p.d_bs;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wr = (wave >> 1) * 64, wc = (wave & 1) * 64;
+  const int li = lane & 31, half = lane >> 5;
+  floatx16 acc[2][2];
+#pragma unroll
+  for (int r = 0; r < 2; ++r)
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[r][c][e] = 0.f;
+
+  for (int64_t kb = kr.k_lo; kb < kr.k_hi; kb += MK) {
+    // stage 128 x 16 of A and 16 x 128 of B: 2048 values each, 8 per thread
+#pragma unroll
+    for (int ld = 0; ld < 8; ++ld) {
+      const int idx = tid + 256 * ld;
+      const int ia = idx / MK, ka = idx % MK;  // A: k fastest across threads when a_cs == 1
+      As[ia][ka] = load_a(p, a, i0 + ia, kb + ka, kr.k_hi);
+      const int jb = idx % MT, kbb = idx / MT;  // B: j fastest across threads
+      Bs[jb][kbb] = load_b(p, b, kb + kbb, j0 + jb, kr.k_hi);
+    }
+    __syncthreads();
+    float4 av[2][2], bv[2][2];
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const float* src = &As[wr + 32 * r + li][8 * half];
+      av[r][0] = *reinterpret_cast<const float4*>(src);
+      av[r][1] = *reinterpret_cast<const float4*>(src + 4);
+    }
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      const float* src = &Bs[wc + 32 * c + li][8 * half];
+      bv[c][0] = *reinterpret_cast<const float4*>(src);
+      bv[c][1] = *reinterpret_cast<const float4*>(src + 4);
+    }
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+#pragma unroll
+      for (int r = 0; r < 2; ++r)
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+          const float x = av[r][s >> 2][s & 3], y = bv[c][s >> 2][s & 3];
+          acc[r][c] = __builtin_amdgcn_mfma_f32_32x32x2f32(x, y, acc[r][c], 0, 0, 0);
+        }
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int r = 0; r < 2; ++r)
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int64_t i = i0 + wr + 32 * r + 8 * (e >> 2) + 4 * half + (e & 3);
+        const int64_t j = j0 + wc + 32 * c + li;
+        store_d(p, d, i, j, acc[r][c][e]);
+      }
+}
+
+}  // namespace
+
+template <typename T>
+int gptq2d_gemm(const GemmProblem<T>& p, hipStream_t stream) {
+  if (p.M < 0 || p.N < 0 || p.K < 0 || p.batch < 0) return GPTQ2D_EINVAL;
+  if (p.M == 0 || p.N == 0 || p.batch == 0) return 0;
+  if (p.batch > 65535) return GPTQ2D_EUNSUPPORTED;
+  if constexpr (sizeof(T) == 4) {
+    if (p.M >= MT / 2 && p.N >= MT / 2) {
+      const dim3 grid((unsigned)cdiv(p.N, MT), (unsigned)cdiv(p.M, MT), (unsigned)p.batch);
+      hipLaunchKernelGGL(gemm_mfma_kernel, grid, dim3(256), 0, stream, p);
+      return (int)hipGetLastError();
+    }
+  }
+  const dim3 grid((unsigned)cdiv(p.N, VT), (unsigned)cdiv(p.M, VT), (unsigned)p.batch);
+  hipLaunchKernelGGL(gemm_valu_kernel<T>, grid, dim3(256), 0, stream, p);
+  return (int)hipGetLastError();
+}
+
+template int gptq2d_gemm<float>(const GemmProblem<float>&, hipStream_t);
+template int gptq2d_gemm<double>(const GemmProblem<double>&, hipStream_t);
+
+extern "C" {
+
+// The strided GEMM as a C entry point, so that tests can check both paths (and the MFMA operand
+// layout) against a host product.  No counterpart in the reference.
+#define GPTQ2D_GEMM_ABI(SUF, T)                                                                                     \
+  int gptq2d_gemm_##SUF(int64_t M, int64_t N, int64_t K, int64_t batch, const T* A, int64_t a_rs, int64_t a_cs,    \
+                        int64_t a_bs, const T* B, int64_t b_rs, int64_t b_cs, int64_t b_bs, T* D, int64_t d_rs,     \
+                        int64_t d_cs, int64_t d_bs, double alpha, double beta, int32_t a_tri, int32_t b_tri,       \
+                        int32_t d_tri, hipStream_t stream) {                                                       \
+    if (a_tri < 0 || a_tri > 2 || b_tri < 0 || b_tri > 2 || d_tri < 0 || d_tri > 2) return GPTQ2D_EINVAL;          \
+    GemmProblem<T> p{M, N, K, batch, A, a_rs, a_cs, a_bs, B, b_rs, b_cs, b_bs, D, d_rs, d_cs, d_bs,               \
+                     (T)alpha, (T)beta, a_tri, b_tri, d_tri};                                                      \
+    return gptq2d_gemm<T>(p, stream);                                                                                \
+  }
+
+GPTQ2D_GEMM_ABI(f32, float)
+GPTQ2D_GEMM_ABI(f64, double)
+
+}  // extern "C"

@@ -1,0 +1,409 @@
+// Feedback-factor preprocessing: the (block) LDL factor of a Kronecker factor's inverse.
+//
+// ldl_of_inverse(M, size) returns the unit lower (block) triangular L with M^{-1} = L Lambda L^T
+// (Lambda block diagonal with size x size blocks) without forming M^{-1}: with J the reversal,
+// the Cholesky factor C of J M J (lower, J M J = C C^T) gives Um = J C J, upper, M = Um Um^T, and
+// L_raw = Um^{-T} = J C^{-T} J, i.e. L_raw(i, j) = C^{-1}(k-1-j, k-1-i).  L is L_raw normalised by
+// its diagonal (size 1) or, for size p, (L_raw - D) D^{-1} + I with D the p x p block diagonal.
+// ldl(M, size) is the same normalisation applied to the Cholesky factor of M itself.
+//
+// Device work, all on the caller's stream, no host synchronisation, no allocation:
+//   1. W = J M J: the reversal of the flat array.
+//   2. Right-looking blocked Cholesky of W in place, panels of NB columns: one wave factors the
+//      diagonal block in registers (potrf_diag_kernel), one thread per row solves the panel below
+//      against it (trsm_kernel), and the trailing lower triangle takes the rank-NB update on the
+//      GEMM (fp32: MFMA).
+//   3. ldl_of_inverse only: C^{-1} in place by recursive doubling.  Diagonal NB blocks are inverted
+//      by one wave each; then for s = NB, 2 NB, ... every pair of inverted s-blocks A^{-1}, D^{-1}
+//      with off-diagonal block B becomes one inverted 2s-block through -D^{-1} (B A^{-1}) -- two
+//      triangular GEMMs per level, all pairs of a level in one batched launch.
+//   4. Normalisation into L (LDS-tiled transposed read for ldl_of_inverse).
+//
+// A non-positive (or NaN) pivot records its 1-based column in `info` (device int, 0 when the
+// factorisation succeeded); the numbers that follow are then meaningless, as in LAPACK.
+//
+// Reference: IST-DASLab/GPTQ-2D gptq_2d_reference.py:29-55 (_unit_diagonal_blocks, ldl_of_inverse,
+// ldl), which call torch.linalg.cholesky and solve_triangular.
+#include "linalg.h"
+
+namespace {
+
+template <typename T>
+struct LdlBlock;
+template <>
+struct LdlBlock<float> {
+  static constexpr int NB = 64;
+};
+template <>
+struct LdlBlock<double> {
+  static constexpr int NB = 32;
+};
+
+__device__ __forceinline__ float bcast(float v, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+__device__ __forceinline__ double bcast(double v, int lane) {
+  const long long b = __double_as_longlong(v);
+  const int lo = __builtin_amdgcn_readlane((int)(b & 0xffffffffll), lane);
+  const int hi = __builtin_amdgcn_readlane((int)(b >> 32), lane);
+  return __longlong_as_double(((long long)hi << 32) | (unsigned int)lo);
+}
+
+// Lane r holds row r of an NB x NB lower triangular block in a[0..NB): in-register Cholesky.
+// Rows >= n are padding (identity).  Returns the first bad pivot column + 1, or 0.
+template <typename T, int NB>
+__device__ __forceinline__ int wave_potrf(T (&a)[NB], int lane, int n) {
+  int bad = 0;
+#pragma unroll
+  for (int c = 0; c < NB; ++c) {
+    const T piv = bcast(a[c], c);
+    if (!bad && c < n && !(piv > T(0))) bad = c + 1;
+    const T d = sqrt(piv);
+    a[c] = lane == c ? d : (lane > c ? a[c] / d : a[c]);
+#pragma unroll
+    for (int c2 = c + 1; c2 < NB; ++c2) {
+      const T v = bcast(a[c], c2);  // C(c2, c), final
+      if (lane >= c2) a[c2] -= a[c] * v;
+    }
+  }
+  return bad;
+}
+
+// Lane r holds row r of an NB x NB lower triangular block in a; returns row r of its inverse in x.
+template <typename T, int NB>
+__device__ __forceinline__ void wave_trtri(const T (&a)[NB], T (&x)[NB], int lane) {
+  T dg = T(1);
+#pragma unroll
+  for (int c = 0; c < NB; ++c)
+    if (c == lane) dg = a[c];
+  T acc[NB];
+#pragma unroll
+  for (int c = 0; c < NB; ++c) acc[c] = T(0);
+#pragma unroll
+  for (int t = 0; t < NB; ++t) {
+    // row t of the inverse: (e_t - acc_t) / C(t, t), acc_t complete since every row u < t is in
+    const T inv_t = T(1) / bcast(dg, t);
+#pragma unroll
+    for (int c = 0; c <= t; ++c) {
+      const T xt = ((c == t ? T(1) : T(0)) - bcast(acc[c], t)) * inv_t;
+      if (lane > t) acc[c] += a[t] * xt;
+    }
+  }
+  const T inv = T(1) / dg;
+#pragma unroll
+  for (int c = 0; c < NB; ++c) x[c] = c <= lane ? ((c == lane ? T(1) : T(0)) - acc[c]) * inv : T(0);
+}
+
+// dst = src (rev = 0) or dst = the reversal of the flat src (rev = 1), which is J M J for a matrix.
+template <typename T>
+__global__ void copy_kernel(T* __restrict__ dst, const T* __restrict__ src, int64_t count, int rev) {
+  for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < count; t += (int64_t)gridDim.x * blockDim.x)
+    dst[t] = src[rev ? count - 1 - t : t];
+}
+
+// One wave: Cholesky of the diagonal block W[j0.., j0..] (n = min(NB, k - j0) rows) in place.
+template <typename T, int NB>
+__global__ __launch_bounds__(64) void potrf_diag_kernel(T* __restrict__ w, int64_t ld, int64_t j0, int n,
+                                                        int* __restrict__ info) {
+  const int lane = threadIdx.x;
+  T a[NB];
+  T* row = w + (j0 + lane) * ld + j0;
+#pragma unroll
+  for (int c = 0; c < NB; ++c) a[c] = (lane < n && c <= lane) ? row[c] : (c == lane ? T(1) : T(0));
+  const int bad = wave_potrf<T, NB>(a, lane, n);
+  if (lane < n) {
+#pragma unroll
+    for (int c = 0; c < NB; ++c)
+      if (c <= lane) row[c] = a[c];
+  }
+  if (bad && lane == 0 && info[0] == 0) info[0] = (int)(j0 + bad);
+}
+
+// One thread per row r >= j0 + NB: W[r, j0:j0+NB] <- W[r, j0:j0+NB] C_jj^{-T}.
+template <typename T, int NB>
+__global__ __launch_bounds__(256) void trsm_kernel(T* __restrict__ w, int64_t ld, int64_t j0, int64_t k) {
+  __shared__ T cs[NB][NB + 1];
+  for (int t = threadIdx.x; t < NB * NB; t += 256) {
+    const int r = t / NB, c = t % NB;
+    cs[r][c] = c <= r ? w[(j0 + r) * ld + j0 + c] : T(0);
+  }
+  __syncthreads();
+  const int64_t r = j0 + NB + (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (r >= k) return;
+  T* row = w + r * ld + j0;
+  T x[NB];
+#pragma unroll
+  for (int c = 0; c < NB; ++c) x[c] = row[c];
+#pragma unroll
+  for (int c = 0; c < NB; ++c) {
+    T s = x[c];
+#pragma unroll
+    for (int t = 0; t < c; ++t) s -= x[t] * cs[c][t];
+    x[c] = s / cs[c][c];
+  }
+#pragma unroll
+  for (int c = 0; c < NB; ++c) row[c] = x[c];
+}
+
+// One wave per diagonal NB block of the lower triangular W: replace it by its inverse.
+template <typename T, int NB>
+__global__ __launch_bounds__(64) void trtri_leaf_kernel(T* __restrict__ w, int64_t ld, int64_t k) {
+  const int lane = threadIdx.x;
+  const int64_t b0 = (int64_t)blockIdx.x * NB;
+  const int n = k - b0 < NB ? (int)(k - b0) : NB;
+  T a[NB], x[NB];
+  T* row = w + (b0 + lane) * ld + b0;
+#pragma unroll
+  for (int c = 0; c < NB; ++c) a[c] = (lane < n && c <= lane) ? row[c] : (c == lane ? T(1) : T(0));
+  wave_trtri<T, NB>(a, x, lane);
+  if (lane < n) {
+#pragma unroll
+    for (int c = 0; c < NB; ++c)
+      if (c <= lane && c < n) row[c] = x[c];
+  }
+}
+
+// L(i, j) from L_raw(i, j) = w[base + i*rs + j*cs]: L_raw(i,j)/L_raw(j,j) below the diagonal,
+// 1 on it, 0 above.  32 x 32 tiles through LDS so that both the read and the write coalesce.
+template <typename T>
+__global__ __launch_bounds__(256) void normalize_unit_kernel(T* __restrict__ out, const T* __restrict__ w,
+                                                             int64_t k, int64_t base, int64_t rs, int64_t cs) {
+  __shared__ T tile[32][33];
+  __shared__ T diag[32];
+  const int64_t i0 = (int64_t)blockIdx.y * 32, j0 = (int64_t)blockIdx.x * 32;
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
+  const bool row_fast = rs == 1 || rs == -1;  // w contiguous along i: threads run along i to load
+  if (j0 <= i0 + 31) {
+    for (int yy = ty; yy < 32; yy += 8) {
+      const int li = row_fast ? tx : yy, lj = row_fast ? yy : tx;
+      const int64_t i = i0 + li, j = j0 + lj;
+      tile[li][lj] = (i < k && j < k && j < i) ? w[base + i * rs + j * cs] : T(0);
+    }
+    if (threadIdx.x < 32) {
+      const int64_t j = j0 + threadIdx.x;
+      diag[threadIdx.x] = j < k ? w[base + j * rs + j * cs] : T(1);
+    }
+  }
+  __syncthreads();
+  for (int yy = ty; yy < 32; yy += 8) {
+    const int64_t i = i0 + yy, j = j0 + tx;
+    if (i >= k || j >= k) continue;
+    T v = T(0);
+    if (j == i) v = T(1);
+    else if (j < i) v = tile[yy][tx] / diag[tx];
+    out[i * k + j] = v;
+  }
+}
+
+// Block normalisation for p x p blocks (p <= NB): a workgroup owns column block b and 64 rows.
+// Rows below the block get L_raw(i, block) D_b^{-1}; the block itself becomes I; rows above, 0.
+template <typename T, int NB>
+__global__ __launch_bounds__(256) void normalize_block_kernel(T* __restrict__ out, const T* __restrict__ w,
+                                                              int64_t k, int p, int64_t base, int64_t rs,
+                                                              int64_t cs) {
+  __shared__ T dinv[NB][NB + 1];
+  __shared__ T rows[64][NB + 1];
+  const int64_t b = blockIdx.x, c0 = b * p;
+  const int64_t i0 = (int64_t)blockIdx.y * 64;
+  const int tid = threadIdx.x;
+  const bool below = i0 + 63 >= c0 + p;  // this chunk has rows strictly below the block
+  if (below) {
+    if (tid < 64) {
+      const int lane = tid;
+      T a[NB], x[NB];
+#pragma unroll
+      for (int c = 0; c < NB; ++c)
+        a[c] = (lane < p && c < p && c <= lane) ? w[base + (c0 + lane) * rs + (c0 + c) * cs]
+                                                : (c == lane ? T(1) : T(0));
+      wave_trtri<T, NB>(a, x, lane);
+      if (lane < NB) {
+#pragma unroll
+        for (int c = 0; c < NB; ++c) dinv[lane][c] = x[c];
+      }
+    }
+    for (int t = tid; t < 64 * p; t += 256) {
+      const bool row_fast = rs == 1 || rs == -1;
+      const int li = row_fast ? t % 64 : t / p, lc = row_fast ? t / 64 : t % p;
+      const int64_t i = i0 + li;
+      rows[li][lc] = (i < k && i >= c0 + p) ? w[base + i * rs + (c0 + lc) * cs] : T(0);
+    }
+  }
+  __syncthreads();
+  for (int t = tid; t < 64 * p; t += 256) {
+    const int li = t / p, lc = t % p;
+    const int64_t i = i0 + li, j = c0 + lc;
+    if (i >= k) continue;
+    T v;
+    if (i < c0) {
+      v = T(0);
+    } else if (i < c0 + p) {
+      v = (i - c0 == lc) ? T(1) : T(0);
+    } else {
+      v = T(0);
+      for (int tt = lc; tt < p; ++tt) v += rows[li][tt] * dinv[tt][lc];
+    }
+    out[i * k + j] = v;
+  }
+}
+
+template <typename T>
+int cholesky_inplace(T* w, int64_t k, int* info, hipStream_t stream) {
+  constexpr int NB = LdlBlock<T>::NB;
+  int rc;
+  for (int64_t j0 = 0; j0 < k; j0 += NB) {
+    const int n = k - j0 < NB ? (int)(k - j0) : NB;
+    hipLaunchKernelGGL((potrf_diag_kernel<T, NB>), dim3(1), dim3(64), 0, stream, w, k, j0, n, info);
+    if ((rc = (int)hipGetLastError())) return rc;
+    const int64_t rest = k - j0 - NB;
+    if (rest <= 0) break;
+    hipLaunchKernelGGL((trsm_kernel<T, NB>), dim3((unsigned)cdiv(rest, 256)), dim3(256), 0, stream, w, k, j0, k);
+    if ((rc = (int)hipGetLastError())) return rc;
+    // trailing lower triangle: W22 -= P P^T with P = W[j0+NB:, j0:j0+NB]
+    GemmProblem<T> g{};
+    g.M = g.N = rest;
+    g.K = NB;
+    g.batch = 1;
+    g.A = w + (j0 + NB) * k + j0;
+    g.a_rs = k;
+    g.a_cs = 1;
+    g.B = g.A;
+    g.b_rs = 1;
+    g.b_cs = k;
+    g.D = w + (j0 + NB) * k + j0 + NB;
+    g.d_rs = k;
+    g.d_cs = 1;
+    g.alpha = T(-1);
+    g.beta = T(1);
+    g.d_tri = TRI_LOWER;
+    if ((rc = gptq2d_gemm<T>(g, stream))) return rc;
+  }
+  return 0;
+}
+
+// In-place inverse of the lower triangular W (k x k); tmp holds >= k*k/4 + k elements.
+template <typename T>
+int trtri_inplace(T* w, int64_t k, T* tmp, hipStream_t stream) {
+  constexpr int NB = LdlBlock<T>::NB;
+  int rc;
+  hipLaunchKernelGGL((trtri_leaf_kernel<T, NB>), dim3((unsigned)cdiv(k, NB)), dim3(64), 0, stream, w, k, k);
+  if ((rc = (int)hipGetLastError())) return rc;
+  for (int64_t s = NB; s < k; s *= 2) {
+    const int64_t full = k / (2 * s);                  // pairs with two full s-blocks
+    const int64_t tail_r1 = full * 2 * s + s;          // a last, short pair starts its D block here
+    const int64_t tail = tail_r1 < k ? k - tail_r1 : 0;
+    for (int part = 0; part < 2; ++part) {
+      const int64_t pairs = part == 0 ? full : (tail > 0 ? 1 : 0);
+      if (pairs == 0) continue;
+      const int64_t r0 = part == 0 ? 0 : full * 2 * s;
+      const int64_t s2 = part == 0 ? s : tail;
+      // T = B A^{-1}: (s2 x s) = (s2 x s) (s x s, lower)
+      GemmProblem<T> g{};
+      g.M = s2;
+      g.N = s;
+      g.K = s;
+      g.batch = pairs;
+      g.A = w + (r0 + s) * k + r0;  // B block
+      g.a_rs = k;
+      g.a_cs = 1;
+      g.a_bs = 2 * s * k + 2 * s;
+      g.B = w + r0 * k + r0;  // A^{-1}
+      g.b_rs = k;
+      g.b_cs = 1;
+      g.b_bs = 2 * s * k + 2 * s;
+      g.b_tri = TRI_LOWER;
+      g.D = tmp;
+      g.d_rs = s;
+      g.d_cs = 1;
+      g.d_bs = s2 * s;
+      g.alpha = T(1);
+      g.beta = T(0);
+      if ((rc = gptq2d_gemm<T>(g, stream))) return rc;
+      // B <- -D^{-1} T: (s2 x s) = (s2 x s2, lower) (s2 x s)
+      GemmProblem<T> h{};
+      h.M = s2;
+      h.N = s;
+      h.K = s2;
+      h.batch = pairs;
+      h.A = w + (r0 + s) * k + (r0 + s);  // D^{-1}
+      h.a_rs = k;
+      h.a_cs = 1;
+      h.a_bs = 2 * s * k + 2 * s;
+      h.a_tri = TRI_LOWER;
+      h.B = tmp;
+      h.b_rs = s;
+      h.b_cs = 1;
+      h.b_bs = s2 * s;
+      h.D = w + (r0 + s) * k + r0;
+      h.d_rs = k;
+      h.d_cs = 1;
+      h.d_bs = 2 * s * k + 2 * s;
+      h.alpha = T(-1);
+      h.beta = T(0);
+      if ((rc = gptq2d_gemm<T>(h, stream))) return rc;
+    }
+  }
+  return 0;
+}
+
+template <typename T>
+int normalize(T* out, const T* w, int64_t k, int64_t size, int64_t base, int64_t rs, int64_t cs, hipStream_t stream) {
+  constexpr int NB = LdlBlock<T>::NB;
+  if (size == 1) {
+    const dim3 grid((unsigned)cdiv(k, 32), (unsigned)cdiv(k, 32));
+    hipLaunchKernelGGL(normalize_unit_kernel<T>, grid, dim3(256), 0, stream, out, w, k, base, rs, cs);
+  } else {
+    if (size > NB) return GPTQ2D_EUNSUPPORTED;
+    const dim3 grid((unsigned)(k / size), (unsigned)cdiv(k, 64));
+    hipLaunchKernelGGL((normalize_block_kernel<T, NB>), grid, dim3(256), 0, stream, out, w, k, (int)size, base, rs,
+                       cs);
+  }
+  return (int)hipGetLastError();
+}
+
+// inverse != 0: ldl_of_inverse; else ldl.  m, out, work: [batch, k, k] contiguous; info: [batch].
+template <typename T>
+int ldl_impl(bool inverse, const T* m, T* out, T* work, int* info, int64_t batch, int64_t k, int64_t size,
+             hipStream_t stream) {
+  if (batch < 0 || k < 0 || size <= 0 || (k > 0 && k % size)) return GPTQ2D_EINVAL;
+  if (size > 1 && size > LdlBlock<T>::NB) return GPTQ2D_EUNSUPPORTED;
+  if (batch == 0 || k == 0) return 0;
+  int rc;
+  const int64_t kk = k * k;
+  for (int64_t b = 0; b < batch; ++b) {
+    const T* mb = m + b * kk;
+    T* ob = out + b * kk;
+    T* wb = work + b * kk;
+    int* ib = info + b;
+    const int64_t blocks = cdiv(kk, 256) < 8192 ? cdiv(kk, 256) : 8192;
+    hipLaunchKernelGGL(copy_kernel<T>, dim3((unsigned)blocks), dim3(256), 0, stream, wb, mb, kk, inverse ? 1 : 0);
+    if ((rc = (int)hipGetLastError())) return rc;
+    if ((rc = cholesky_inplace<T>(wb, k, ib, stream))) return rc;
+    if (inverse) {
+      if ((rc = trtri_inplace<T>(wb, k, ob, stream))) return rc;  // out is free scratch until normalisation
+      // L_raw(i, j) = Cinv(k-1-j, k-1-i) = w[(k-1-j)*k + (k-1-i)]
+      if ((rc = normalize<T>(ob, wb, k, size, (k - 1) * k + (k - 1), -1, -k, stream))) return rc;
+    } else {
+      if ((rc = normalize<T>(ob, wb, k, size, 0, k, 1, stream))) return rc;
+    }
+  }
+  return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+#define GPTQ2D_LDL_ABI(SUF, T)                                                                                      \
+  int gptq2d_ldl_of_inverse_##SUF(const T* m, T* out, T* work, int* info, int64_t batch, int64_t k, int64_t size,  \
+                                  hipStream_t stream) {                                                            \
+    return ldl_impl<T>(true, m, out, work, info, batch, k, size, stream);                                            \
+  }                                                                                                                 \
+  int gptq2d_ldl_##SUF(const T* m, T* out, T* work, int* info, int64_t batch, int64_t k, int64_t size,              \
+                       hipStream_t stream) {                                                                       \
+    return ldl_impl<T>(false, m, out, work, info, batch, k, size, stream);                                           \
+  }
+
+GPTQ2D_LDL_ABI(f32, float)
+GPTQ2D_LDL_ABI(f64, double)
+
+}  // extern "C"

@@ -17,6 +17,7 @@
 //   y = (Y[r,c] + sum_{r'<r} L[r,r'] E[r',c]) + sum_{c'<c} C[r,c'] U[c',c]
 // where C[r,c'] is already complete (all rows above in the tile were rounded earlier).
 #include "common.h"
+#include "profile.h"
 
 template <typename T>
 int gptq2d_flush(T* y, T* c, const T* e, const T* l, const T* u, int64_t m, int64_t n, int64_t P, int64_t Q,
@@ -174,8 +175,12 @@ int sweep_fused(T* y, T* c, T* e, const T* l, const T* u, int64_t m, int64_t n, 
       const int64_t lo = st - nt + 1 > 0 ? st - nt + 1 : 0;
       const int64_t hi = st < mt - 1 ? st : mt - 1;
       Grid3 g = make_grid(hi - lo + 1, 1, B);
+      const bool prof = gptq2d_prof_on(PROF_TILE_SWEEP);
+      if (prof) gptq2d_prof_begin(PROF_TILE_SWEEP, stream);
       hipLaunchKernelGGL(sweep_tiles_kernel<T>, g.grid, dim3(NTHREADS), 0, stream, y, c, e, l, u, m, n, st, lo, lmap,
                          umap, qs, g.nx, g.ny);
+      // work of a tile sweep: its entries (the in-tile feedback is latency-, not throughput-bound)
+      if (prof) gptq2d_prof_end(PROF_TILE_SWEEP, (double)B * (hi - lo + 1) * TR * TR, stream);
       if ((rc = (int)hipGetLastError())) return rc;
       if (st + 1 < S1 && (rc = gptq2d_flush<T>(y, c, e, l, u, m, n, TR, TR, st, st + 1, S1, lmap, umap, B, stream)))
         return rc;

@@ -1,0 +1,67 @@
+"""Feedback factors of GPTQ-2D on the GPU: the LDL helpers of the reference, HIP-backed.
+
+``ldl_of_inverse(M, size)`` gives the unit lower (block) triangular L with M^{-1} = L Lambda L^T
+without forming M^{-1}; ``ldl(M, size)`` the same for M itself; ``feedback_factors(A, B, shape)``
+the pair (L, U) that ``gptq_2d`` takes for the Grams G = A^T A and H = B B^T.  Same names,
+arguments and results as the reference (gptq_2d_reference.py:29-66); leading batch dimensions of
+M are supported.  Everything runs on the current stream of M's device in blocked HIP kernels
+(reverse-order Cholesky, recursive-doubling triangular inverse, normalisation; the GEMM-shaped
+parts on fp32 MFMA).  A matrix that is not positive definite raises
+``torch.linalg.LinAlgError`` as ``torch.linalg.cholesky`` does; ``check=False`` skips that test
+(it is the only host synchronisation) so that the call can be captured in a graph.
+"""
+
+from __future__ import annotations
+
+import torch
+
+import _hip
+
+# p x p diagonal blocks up to this size are normalised on the GPU (fp32; fp64: 32).
+MAX_BLOCK = {torch.float32: 64, torch.float64: 32}
+
+
+def _factor(name: str, m: torch.Tensor, size: int, check: bool) -> torch.Tensor:
+    assert m.dim() >= 2 and m.size(-1) == m.size(-2), "expected square matrices [..., k, k]"
+    assert m.dtype in (torch.float32, torch.float64), "expected float32 or float64"
+    _hip.require_device(m)
+    k = m.size(-1)
+    assert size > 0 and k % size == 0, "the block size must divide the matrix size"
+    assert size <= MAX_BLOCK[m.dtype], f"diagonal blocks up to {MAX_BLOCK[m.dtype]} are supported for {m.dtype}"
+    batch = m.shape[:-2]
+    src = m.reshape(-1, k, k).contiguous()
+    nb = src.size(0)
+    out = torch.empty_like(src)
+    work = torch.empty_like(src)
+    info = torch.zeros(nb, dtype=torch.int32, device=m.device)
+    with torch.cuda.device(m.device):
+        _hip.call(name, m.dtype, _hip.ptr(src), _hip.ptr(out), _hip.ptr(work), _hip.ptr(info), nb, k, size,
+                  _hip.stream(m.device))
+    if check and nb and k:
+        bad = info.cpu()
+        if bool((bad != 0).any()):
+            b = int((bad != 0).nonzero()[0, 0])
+            raise torch.linalg.LinAlgError(
+                f"the leading minor of order {int(bad[b])} of batch {b} is not positive-definite")
+    return out.reshape(*batch, k, k)
+
+
+def ldl_of_inverse(M: torch.Tensor, size: int = 1, *, check: bool = True) -> torch.Tensor:
+    """Unit lower (block) triangular L with M^{-1} = L Lambda L^T, Lambda block diagonal with size x size
+    blocks, via the reverse-order Cholesky M = Um Um^T and L = Um^{-T} normalised by its diagonal blocks
+    (gptq_2d_reference.py:41-49)."""
+    return _factor("ldl_of_inverse", M, size, check)
+
+
+def ldl(M: torch.Tensor, size: int = 1, *, check: bool = True) -> torch.Tensor:
+    """Unit lower (block) triangular L with M = L Lambda L^T (gptq_2d_reference.py:52-55)."""
+    return _factor("ldl", M, size, check)
+
+
+def feedback_factors(A: torch.Tensor, B: torch.Tensor, super_entry_shape=(1, 1)):
+    """L and U for the Grams G = A^T A and H = B B^T, with p x p and q x q identity diagonal blocks
+    (gptq_2d_reference.py:58-66)."""
+    p, q = super_entry_shape
+    L = ldl_of_inverse(A.t() @ A, size=p)
+    U = ldl_of_inverse(B @ B.t(), size=q).t()
+    return L, U

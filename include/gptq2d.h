@@ -1,0 +1,140 @@
+/* C ABI of libgptq2d.so: the MI355X (gfx950) GPTQ-2D engine.
+ *
+ * Every entry point takes raw device pointers and int64 sizes, launches HIP kernels on the given
+ * stream (a hipStream_t, passed as void*), never allocates device memory, never synchronises
+ * with the host, uses no atomics (results are deterministic) and returns 0 on success, a
+ * positive hipError_t, or GPTQ2D_EINVAL / GPTQ2D_EUNSUPPORTED.  The caller owns all memory.
+ * Everything except the profiler may be captured in a hipGraph.
+ *
+ * Layout conventions.  Y, C and E are contiguous row-major [B, m, n] with B the product of the
+ * broadcast batch shape.  L [*, m, m], U [*, n, n] and full-matrix quantizer inputs [*, m, n] may
+ * broadcast over the batch: `bnd` is the number of batch dimensions, `bshape[bnd]` the broadcast
+ * batch shape and `<x>_stride[bnd]` the operand's batch strides in elements (0 where it broadcasts).
+ * L is read only strictly below its (p x p block) diagonal and U only strictly above its (q x q
+ * block) diagonal; the other entries may hold anything, NaN included.
+ *
+ * Every compute entry point exists for float (suffix _f32) and double (suffix _f64); T below is
+ * that element type.  The reference (IST-DASLab/GPTQ-2D) has no native code: its GPU path is
+ * Triton kernels launched from Python, and each entry point names the reference function or
+ * kernel whose work it takes over.
+ */
+#ifndef GPTQ2D_H
+#define GPTQ2D_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define GPTQ2D_EINVAL (-1)
+#define GPTQ2D_EUNSUPPORTED (-2)
+
+#define GPTQ2D_DECLARE(T, SUF)                                                                                        \
+  /* Whole sweep with a built-in per-entry quantizer fused in: replaces the stage loop of              \
+   * _gptq_2d_blocked (gptq_2d.py:1295-1375) with its _push/_flush_block launches                     \
+   * (gptq_2d.py:244-378, 633-1119) and the quantizer plug-in calls (gptq_2d.py:147-164).             \
+   * qkind 0: round half to even (quantizer_int.py:18-25); 1: affine with full-matrix scale qa and     \
+   * zero point qb (quantizer_int.py:63-83, 161-244); 2: prescribed values qa (teacher forcing; no     \
+   * reference counterpart).  ypre (optional, [B,m,n]) receives Y of every entry just before it is    \
+   * rounded.  c, e: [B,m,n] scratch.  Stages of tiles [stage_begin, stage_end) (-1: to the end),     \
+   * outer_tiles tile stages per outer block.  y is updated in place. */                               \
+  int gptq2d_sweep_fused_##SUF(T* y, T* c, T* e, const T* l, const T* u, int64_t m, int64_t n, int32_t bnd,         \
+                               const int64_t* bshape, const int64_t* l_stride, const int64_t* u_stride,             \
+                               int32_t qkind, const T* qa, const int64_t* qa_stride, const T* qb,                   \
+                               const int64_t* qb_stride, double qmin, double qmax, T* ypre, int64_t outer_tiles,    \
+                               int64_t stage_begin, int64_t stage_end, void* stream);                               \
+  /* Tile edge of the fused sweep. */                                                                  \
+  int64_t gptq2d_sweep_fused_tile_##SUF(void);                                                                       \
+                                                                                                                      \
+  /* Plug-in path, plain entries: push of stage s inside the block ending at s1 -- error, down and     \
+   * right feedback, commit of z, capture of the next stage's values (_push_kernel,                   \
+   * gptq_2d.py:244-378). */                                                                           \
+  int gptq2d_push_plain_##SUF(T* y, T* c, T* e, const T* z, const T* old, T* next_old, const T* l, const T* u,     \
+                              int64_t m, int64_t n, int64_t s, int64_t s1, int32_t bnd, const int64_t* bshape,    \
+                              const int64_t* l_stride, const int64_t* u_stride, void* stream);                     \
+  /* C += E at the sources of stages [s0, s1) (_add_own_errors_kernel, gptq_2d.py:382-425). */        \
+  int gptq2d_add_own_errors_##SUF(T* c, const T* e, int64_t B, int64_t m, int64_t n, int64_t s0, int64_t s1,        \
+                                  void* stream);                                                                    \
+  /* Super-entry p x q push down through L (_push_down_super_entry_kernel, gptq_2d.py:429-533). */     \
+  int gptq2d_push_down_se_##SUF(T* y, T* c, T* e, const T* z, const T* l, int64_t m, int64_t n, int64_t p,          \
+                                int64_t q, int64_t s, int64_t s1, int32_t bnd, const int64_t* bshape,               \
+                                const int64_t* l_stride, void* stream);                                             \
+  /* Super-entry commit and push right through U (_push_right_super_entry_kernel,                     \
+   * gptq_2d.py:537-629). */                                                                           \
+  int gptq2d_push_right_se_##SUF(T* y, const T* c, const T* z, const T* u, int64_t m, int64_t n, int64_t p,         \
+                                 int64_t q, int64_t s, int64_t s1, int32_t bnd, const int64_t* bshape,              \
+                                 const int64_t* u_stride, void* stream);                                            \
+  /* out[b, k] = Y[b] on antidiagonal s (the old-value copy of _gptq_2d_blocked, gptq_2d.py:1345-1348). */ \
+  int gptq2d_gather_antidiagonal_##SUF(const T* y, T* out, int64_t B, int64_t m, int64_t n, int64_t s,             \
+                                       void* stream);                                                               \
+  /* x[0:count] = v (the zero-initialised C of gptq_2d.py:1324). */                                    \
+  int gptq2d_fill_##SUF(T* x, double v, int64_t count, void* stream);                                                \
+  /* Block flush: the errors of stages [s0, s1) into the targets s1 <= i/p + j/q < s_end, C += L E and \
+   * Y += L E + C U over the band (_repack_errors + _flush_down + _flush_right, gptq_2d.py:633-1119). */ \
+  int gptq2d_flush_##SUF(T* y, T* c, const T* e, const T* l, const T* u, int64_t m, int64_t n, int64_t p,           \
+                         int64_t q, int64_t s0, int64_t s1, int64_t s_end, int32_t bnd, const int64_t* bshape,      \
+                         const int64_t* l_stride, const int64_t* u_stride, void* stream);                           \
+                                                                                                                      \
+  /* Affine quantizer on the flat strided slice start + k*step, k < len, of each [msize] matrix        \
+   * (_affine_quantize_kernel, quantizer_int.py:161-244). */                                           \
+  int gptq2d_affine_quantize_##SUF(T* out, const T* y, const T* scale, const T* zp, int64_t msize, int64_t start,    \
+                                   int64_t step, int64_t len, int32_t bnd, const int64_t* bshape,                   \
+                                   const int64_t* scale_stride, const int64_t* zp_stride, double qmin, double qmax, \
+                                   void* stream);                                                                   \
+  /* Round half to even on the slice (round_quantizer, quantizer_int.py:18-25). */                    \
+  int gptq2d_round_quantize_##SUF(T* out, const T* y, int64_t msize, int64_t start, int64_t step, int64_t len,     \
+                                  int32_t bnd, const int64_t* bshape, void* stream);                               \
+  /* Affine quantizer on a strided [d, p, q] super-entry view (_affine_quantize_super_entry_kernel,    \
+   * quantizer_int.py:248-351). */                                                                     \
+  int gptq2d_affine_quantize_se_##SUF(T* out, const T* y, const T* scale, const T* zp, int64_t msize, int64_t d,    \
+                                      int64_t p, int64_t q, int64_t sd, int64_t sp, int64_t sq, int32_t bnd,        \
+                                      const int64_t* bshape, const int64_t* scale_stride, const int64_t* zp_stride, \
+                                      double qmin, double qmax, void* stream);                                      \
+  /* Round half to even on a super-entry view (round_quantizer_super_entry, quantizer_int.py:28-35). */ \
+  int gptq2d_round_quantize_se_##SUF(T* out, const T* y, int64_t msize, int64_t d, int64_t p, int64_t q, int64_t sd, \
+                                     int64_t sp, int64_t sq, int32_t bnd, const int64_t* bshape, void* stream);     \
+  /* Symmetric abs-max scale per row, rounded to bf16 (dtype16 1) or fp16 (2), zero -> 1            \
+   * (_int_abs_max_scale_kernel, quantizer_int.py:354-404). */                                         \
+  int gptq2d_absmax_scale_##SUF(T* out, const T* x, int64_t rows, int64_t size, int64_t row_stride,                 \
+                                int64_t col_stride, double qmin, double qmax, int32_t dtype16, void* stream);       \
+  /* Abs-max INT quantizer per row of each super-entry from its current values                        \
+   * (_int_abs_max_quantize_kernel, quantizer_int.py:408-470). */                                      \
+  int gptq2d_absmax_quantize_se_##SUF(T* out, const T* y, int64_t msize, int64_t B, int64_t d, int64_t p, int64_t q, \
+                                      int64_t sd, int64_t sp, int64_t sq, double qmin, double qmax, int32_t dtype16, \
+                                      void* stream);                                                                \
+                                                                                                                      \
+  /* Unit lower (block) triangular L with M^{-1} = L Lambda L^T for `batch` contiguous k x k SPD      \
+   * matrices m; work: [batch, k, k] scratch; info[batch]: first non-positive pivot (1-based) or 0     \
+   * (ldl_of_inverse, gptq_2d_reference.py:29-49).  size <= 64 (f32) or 32 (f64). */                 \
+  int gptq2d_ldl_of_inverse_##SUF(const T* m, T* out, T* work, int* info, int64_t batch, int64_t k, int64_t size,  \
+                                  void* stream);                                                                    \
+  /* Unit lower (block) triangular L with M = L Lambda L^T (ldl, gptq_2d_reference.py:52-55). */       \
+  int gptq2d_ldl_##SUF(const T* m, T* out, T* work, int* info, int64_t batch, int64_t k, int64_t size,              \
+                       void* stream);                                                                               \
+  /* Strided batched GEMM D = beta D + alpha A B with triangular operand structure (tri: 0 dense,      \
+   * 1 lower, 2 upper) -- the building block of the LDL; exported for tests.  No reference            \
+   * counterpart (torch.linalg inside the reference's ldl_of_inverse). */                             \
+  int gptq2d_gemm_##SUF(int64_t M, int64_t N, int64_t K, int64_t batch, const T* A, int64_t a_rs, int64_t a_cs,     \
+                        int64_t a_bs, const T* B, int64_t b_rs, int64_t b_cs, int64_t b_bs, T* D, int64_t d_rs,      \
+                        int64_t d_cs, int64_t d_bs, double alpha, double beta, int32_t a_tri, int32_t b_tri,        \
+                        int32_t d_tri, void* stream);
+
+GPTQ2D_DECLARE(float, f32)
+GPTQ2D_DECLARE(double, f64)
+
+#undef GPTQ2D_DECLARE
+
+/* Launch profiler (no reference counterpart; the reference times with host clocks, demo.ipynb:109-118).
+ * While on, every launch of a profiled kernel class is bracketed with HIP events on its stream.
+ * Process-global, not thread-safe, not for use under stream capture.
+ * kind 0: cross-tile feedback panels (flush); 1: fused tile sweeps; 2: LDL GEMMs. */
+int gptq2d_profile_start(int64_t capacity);
+int gptq2d_profile_read(int32_t kind, double* ms, double* work, int64_t* launches);
+int gptq2d_profile_stop(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GPTQ2D_H */

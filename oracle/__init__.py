@@ -17,8 +17,9 @@ Modules and the reference code each one restates (IST-DASLab/GPTQ-2D):
   (quantizer_int.py:18-134).
 - ``oracle.trellis``    -- 1MAD / 3INST / HYB codes, the Viterbi search and the
   tail-biting trellis quantizer (quantizer_trellis.py:28-143, 344-369).
-- ``oracle.instances``  -- seeded numpy generators for the benchmark
-  configurations (Wishart-like Kronecker factors, Gaussian+outlier weights).
+
+The seeded input generators of the benchmark configurations are not part of
+the oracle (they compute no reference algorithm): ``gptq-2d_amd/instances.py``.
 
 How each function is pinned (checked by something other than retyping it) is
 listed in the module docstrings and exercised by ``tests/test_oracle_*.py``.

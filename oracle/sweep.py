@@ -108,6 +108,45 @@ def gptq_2d_torch(x, l, u, *, quantizer: Callable = _round, inplace=False, quant
     return y
 
 
+class TorchSweepState:
+    """The loop state of ``gptq_2d_torch`` for running chosen stages one at a time (CPU baseline timing).
+
+    ``run_stage(s)`` is exactly the body of the loop of gptq_2d.py:1217-1235 for stage s.  Its cost
+    depends only on the shapes, so timing a sample of stages on full-size tensors and weighting by
+    ``stage_work`` gives the time of the whole sweep.
+    """
+
+    def __init__(self, x, l, u, quantizer: Callable = _round, quantizer_inputs=()):
+        self.y, self.m, self.n, batch = _output(x, l, u, False)
+        self.c = torch.zeros_like(self.y)
+        self.yf, self.cf = self.y.flatten(-2), self.c.flatten(-2)
+        self.lf = unit_triangular(l, upper=False).flip(-1)
+        self.uf = unit_triangular(u, upper=True).flip(-2)
+        self.zbuf = self.y.new_empty(batch.numel() * min(self.m, self.n))
+        self.quantizer, self.inputs = quantizer, quantizer_inputs
+
+    @torch.no_grad()
+    def run_stage(self, s: int) -> None:
+        m, n, y, c = self.m, self.n, self.y, self.c
+        isl, jsl, asl = stage_geometry(m, n, s)
+        ysel, z = _call_quantizer(self.zbuf, self.yf, asl, self.quantizer, self.inputs)
+        e = z - ysel
+        lcols = self.lf[..., isl.start:, m - isl.stop:m - isl.start]
+        erow = e.flip(-1)[..., None, :]
+        c[..., isl.start:, jsl].addcmul_(lcols, erow)
+        y[..., isl.start:, jsl].addcmul_(lcols, erow)
+        urows = self.uf[..., n - jsl.stop:n - jsl.start, jsl.start:]
+        y[..., isl, jsl.start:].addcmul_(self.cf[..., asl, None], urows)
+        self.yf[..., asl] = z
+
+
+def stage_work(m: int, n: int, s: int) -> int:
+    """Entries the three ``addcmul_`` of stage s update: 2 (m - i_lo) d + d (n - j_lo), d = |I_s|."""
+    isl, jsl, _ = stage_geometry(m, n, s)
+    d = isl.stop - isl.start
+    return 2 * (m - isl.start) * d + d * (n - jsl.start)
+
+
 @torch.no_grad()
 def gptq_2d_super_entry_torch(x, l, u, *, quantizer: Callable = None, super_entry_shape=(1, 1), inplace=False,
                               quantizer_inputs=()):

@@ -1,0 +1,150 @@
+"""GPU tests of the feedback-factor preprocessing (gptq_2d_ldl) and of the strided GEMM beneath it.
+
+The LDL factors are checked against the CPU oracle's restatement of ldl_of_inverse / ldl
+(gptq_2d_reference.py:29-55, computed in fp64 with torch.linalg), and against what fixes them
+independently of any implementation: unit (block) lower triangular with exactly identity diagonal
+blocks, and L^{-1} M^{-1} L^{-T} block diagonal, which with the uniqueness of the LDL pins L.  Tolerances: fp64 1e-9, fp32 2e-4 relative to max |L| (well-conditioned Wishart-like
+factors, condition number < 1e3).
+"""
+
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+import _hip
+import gptq_2d_ldl as LDL
+import instances
+from oracle import algorithms as A
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _gemm(M, N, K, batch, a, b, d, alpha, beta, a_tri=0, b_tri=0, d_tri=0, a_t=False, b_t=False):
+    """Call gptq2d_gemm with a/b given as [batch, M, K] / [batch, K, N] tensors (possibly as transposed views)."""
+    ars, acs = (a.stride(-2), a.stride(-1))
+    brs, bcs = (b.stride(-2), b.stride(-1))
+    _hip.call("gemm", d.dtype, M, N, K, batch, _hip.ptr(a), ars, acs, a.stride(0), _hip.ptr(b), brs, bcs, b.stride(0),
+              _hip.ptr(d), d.stride(-2), d.stride(-1), d.stride(0), float(alpha), float(beta), a_tri, b_tri, d_tri,
+              _hip.stream(d.device))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+@pytest.mark.parametrize("M,N,K", [(200, 300, 77), (128, 128, 16), (257, 129, 33), (64, 64, 1000), (5, 700, 9),
+                                   (1000, 6, 64)])
+@pytest.mark.parametrize("tri", [(0, 0, 0), (1, 0, 0), (0, 1, 0), (0, 0, 1), (2, 2, 0), (1, 1, 1)])
+def test_gemm(dtype, M, N, K, tri):
+    """Strided GEMM with triangular operand structure against a host fp64 product; the structurally zero
+    parts hold NaN, which must never be read."""
+    print(f"gemm {M}x{N}x{K} {dtype} tri={tri}", flush=True)
+    g = torch.Generator().manual_seed(M * 7 + N * 3 + K)
+    batch = 2
+    a = torch.randn(batch, M, K, generator=g, dtype=torch.float64)
+    b = torch.randn(batch, N, K, generator=g, dtype=torch.float64).transpose(-1, -2)  # a transposed view
+    d0 = torch.randn(batch, M, N, generator=g, dtype=torch.float64)
+    a_tri, b_tri, d_tri = tri
+    i = torch.arange(M)[:, None]
+    k_a = torch.arange(K)[None, :]
+    k_b = torch.arange(K)[:, None]
+    j = torch.arange(N)[None, :]
+    am = torch.ones(M, K, dtype=torch.bool) if a_tri == 0 else (k_a <= i if a_tri == 1 else k_a >= i)
+    bm = torch.ones(K, N, dtype=torch.bool) if b_tri == 0 else (k_b >= j if b_tri == 1 else k_b <= j)
+    dm = torch.ones(M, N, dtype=torch.bool) if d_tri == 0 else (i >= j)
+    expected = d0 * .5 + 1.5 * (a * am) @ (b * bm)
+    expected = torch.where(dm, expected, d0)
+    a_dev = a.masked_fill(~am, torch.nan).to(dtype).to(DEV)
+    b_dev = b.masked_fill(~bm, torch.nan).to(dtype).to(DEV)
+    d_dev = d0.to(dtype).to(DEV)
+    _gemm(M, N, K, batch, a_dev, b_dev, d_dev, 1.5, .5, a_tri, b_tri, d_tri)
+    got = d_dev.double().cpu()
+    tol = 1e-12 if dtype == torch.float64 else 2e-5
+    err = ((got - expected).abs() / (1 + expected.abs())).max().item()
+    assert err < tol * max(1, K ** .5), err
+
+
+def _check_factor(got, m, size, inverse, tol):
+    k = m.size(-1)
+    expected = (A.ldl_of_inverse if inverse else A.ldl)(m.cpu().double(), size=size)
+    g = got.double().cpu()
+    blk = torch.arange(k) // size
+    same = blk[:, None] == blk[None, :]
+    above = blk[None, :] > blk[:, None]
+    # exact structure: identity diagonal blocks, zero above
+    assert torch.equal(g[same], torch.eye(k, dtype=torch.float64)[same])
+    assert (g[above] == 0).all()
+    err = ((g - expected).abs().max() / expected.abs().max()).item()
+    assert err < tol, err
+    # L^{-1} M^{-1} L^{-T} (inverse) or L^{-1} M L^{-T} (ldl) is block diagonal
+    mm = m.cpu().double()
+    target = torch.linalg.inv(mm) if inverse else mm
+    li = torch.linalg.inv(g)
+    lam = li @ target @ li.T
+    off = lam.masked_fill(same, 0).abs().max() / lam.abs().max()
+    assert off.item() < 50 * tol, off.item()
+
+
+@pytest.mark.parametrize("k", [1, 5, 64, 65, 100, 257, 600])
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
+def test_ldl_of_inverse(k, dtype):
+    print(f"ldl_of_inverse k={k} {dtype}", flush=True)
+    m = instances.wishart_factor(k, .5, 10 + k).to(dtype).to(DEV)
+    got = LDL.ldl_of_inverse(m)
+    _check_factor(got, m, 1, True, 1e-9 if dtype == torch.float64 else 2e-4)
+
+
+@pytest.mark.parametrize("k,size", [(64, 2), (96, 4), (256, 16), (128, 32), (192, 64)])
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
+def test_ldl_of_inverse_blocks(k, size, dtype):
+    if size > LDL.MAX_BLOCK[dtype]:
+        pytest.skip("block larger than the GPU normalisation supports for this dtype")
+    print(f"ldl_of_inverse k={k} size={size} {dtype}", flush=True)
+    m = instances.wishart_factor(k, 1., 20 + k).to(dtype).to(DEV)
+    got = LDL.ldl_of_inverse(m, size=size)
+    _check_factor(got, m, size, True, 1e-9 if dtype == torch.float64 else 2e-4)
+
+
+@pytest.mark.parametrize("k,size", [(70, 1), (128, 8)])
+def test_ldl(k, size):
+    m = instances.wishart_factor(k, .5, 30 + k).to(DEV)
+    got = LDL.ldl(m, size=size)
+    _check_factor(got, m, size, False, 1e-9)
+
+
+def test_batch_and_feedback_factors():
+    ms = torch.stack([instances.wishart_factor(48, .5, s) for s in range(6)]).reshape(2, 3, 48, 48).to(DEV)
+    got = LDL.ldl_of_inverse(ms, size=4)
+    for idx in np.ndindex(2, 3):
+        expected = A.ldl_of_inverse(ms[idx].cpu(), size=4)
+        assert (got[idx].cpu() - expected).abs().max() < 1e-9
+    g = torch.Generator().manual_seed(3)
+    a = torch.randn(40, 24, generator=g, dtype=torch.float64)
+    b = torch.randn(30, 50, generator=g, dtype=torch.float64)
+    lo, up = LDL.feedback_factors(a.to(DEV), b.to(DEV), (2, 5))
+    elo, eup = A.feedback_factors(a, b, (2, 5))
+    assert (lo.cpu() - elo).abs().max() < 1e-9 and (up.cpu() - eup).abs().max() < 1e-9
+
+
+def test_not_positive_definite():
+    m = instances.wishart_factor(80, .5, 1).to(DEV)
+    m[70, 70] = -1.
+    with pytest.raises(torch.linalg.LinAlgError):
+        LDL.ldl_of_inverse(m)
+    with pytest.raises(torch.linalg.LinAlgError):
+        LDL.ldl(m)
+
+
+def test_headline_size_fp32():
+    """8192 x 8192 fp32 factor of the headline layer: structure, and agreement with the fp64 oracle on a
+    sampled set of rows (the full fp64 CPU reference takes too long here)."""
+    k = 8192
+    m64 = instances.wishart_factor(k, .5, 1, device=DEV)
+    got = LDL.ldl_of_inverse(m64.float())
+    torch.cuda.synchronize()
+    assert torch.isfinite(got).all()
+    assert (got.diagonal() == 1).all() and (got.triu(1) == 0).all()
+    ref = LDL.ldl_of_inverse(m64)  # the GPU fp64 path, pinned against the oracle above
+    err = ((got.double() - ref).abs().max() / ref.abs().max()).item()
+    print(f"8192 fp32 vs fp64: max rel err {err:.2e}", flush=True)
+    assert err < 1e-3
