@@ -225,12 +225,26 @@ double gptq2d_flush_flops(int64_t m, int64_t n, int64_t P, int64_t Q, int64_t s0
   return total;
 }
 
+int gptq2d_flush_tiles_mfma(float* y, float* c, const float* e, const float* l, const float* u, int64_t m, int64_t n,
+                            int64_t S0, int64_t S1, int64_t S_end, const BatchMap& lmap, const BatchMap& umap,
+                            int64_t B, hipStream_t stream);
+
 template <typename T>
 int gptq2d_flush(T* y, T* c, const T* e, const T* l, const T* u, int64_t m, int64_t n, int64_t P, int64_t Q,
                  int64_t s0, int64_t s1, int64_t s_end, const BatchMap& lmap, const BatchMap& umap, int64_t B,
                  hipStream_t stream) {
   if (m <= 0 || n <= 0 || P <= 0 || Q <= 0 || s0 < 0 || s1 <= s0 || s_end < s1) return GPTQ2D_EINVAL;
   if (B == 0 || s_end == s1) return 0;
+  if constexpr (sizeof(T) == 4) {
+    // 32 x 32 coarse cells (the fused engine's tiles, or 32 x 32 super-entries): fp32 MFMA
+    if (P == 32 && Q == 32) {
+      const bool prof = gptq2d_prof_on(PROF_FLUSH);
+      if (prof) gptq2d_prof_begin(PROF_FLUSH, stream);
+      const int rc = gptq2d_flush_tiles_mfma(y, c, e, l, u, m, n, s0, s1, s_end, lmap, umap, B, stream);
+      if (prof) gptq2d_prof_end(PROF_FLUSH, (double)B * gptq2d_flush_flops(m, n, P, Q, s0, s1, s_end), stream);
+      return rc;
+    }
+  }
   FlushGeom g{m, n, P, Q, s0, s1, s_end};
   int64_t nrow_tiles;
   const int64_t nx = flush_grid_x(g, nrow_tiles);

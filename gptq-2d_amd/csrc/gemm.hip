@@ -189,6 +189,190 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmProblem<float> p) {
       }
 }
 
+// ------------------------------------------------------------------------------------------------ MFMA, vectorised
+
+// Fast path for the LDL's problems: A contiguous along k (a_cs == 1), B contiguous along k
+// (b_rs == 1, BK) or along j (b_cs == 1), every base pointer 16-byte aligned, every stride and K a
+// multiple of 4, so panels move as float4.  Tile 128 x 128, K step 32, register prefetch one step
+// ahead, four waves of 64 x 64 (2 x 2 blocks of 32 x 32).  LDS: A as [i][k] (pitch 36), B as
+// [j][k] (BK, pitch 36) or [k][j] (pitch 132); the MFMA k-slot of lane half h in MFMA s is
+// 16 h + s for both operands.  Structurally zero entries are replaced by 0 element-wise.
+constexpr int VKT = 32;
+
+// Workgroups are dispatched round-robin over the 8 XCDs, each with its own L2.  Re-number them so
+// that every XCD receives one contiguous share of the tiles, and walk that share in groups of
+// GROUP tile rows, so that concurrently running tiles of one XCD share their A and B panels.
+__device__ __forceinline__ void xcd_tile(int64_t gx, int64_t gy, int64_t& tx, int64_t& ty) {
+  constexpr int XCDS = 8, GROUP = 8;
+  const int64_t n = gx * gy;
+  const int64_t lin = (int64_t)blockIdx.y * gx + blockIdx.x;
+  const int64_t base = n / XCDS, extra = n % XCDS;
+  const int64_t x = lin % XCDS, q = lin / XCDS;
+  const int64_t id = x * base + (x < extra ? x : extra) + q;
+  const int64_t per_group = GROUP * gx;
+  const int64_t g = id / per_group, first = g * GROUP;
+  const int64_t rows = gy - first < GROUP ? gy - first : GROUP;
+  const int64_t in = id % per_group;
+  ty = first + in % rows;
+  tx = in / rows;
+}
+
+template <bool BK>
+__global__ __launch_bounds__(256, 2) void gemm_mfma_vec_kernel(GemmProblem<float> p) {
+  constexpr int APITCH = VKT + 4;
+  constexpr int BPITCH = BK ? VKT + 4 : MT + 4;
+  __shared__ __align__(16) float As[MT * APITCH];
+  __shared__ __align__(16) float Bs[BK ? MT * BPITCH : VKT * BPITCH];
+  const int64_t bi = blockIdx.z;
+  int64_t tx, ty;
+  xcd_tile(gridDim.x, gridDim.y, tx, ty);
+  const int64_t i0 = ty * MT, j0 = tx * MT;
+  const int64_t i1 = i0 + MT < p.M ? i0 + MT : p.M, j1 = j0 + MT < p.N ? j0 + MT : p.N;
+  TileRange kr = tile_k_range(p, i0, i1, j0, j1);
+  if (kr.empty) return;
+  kr.k_lo &= ~int64_t(3);  // float4 granules; the masks zero what lies outside
+  const float* a = p.A + bi * p.a_bs;
+  const float* b = p.B + bi * p.b_bs;
+  float* d = p.D + bi * p.d_bs;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wr = (wave >> 1) * 64, wc = (wave & 1) * 64;
+  const int li = lane & 31, hh = lane >> 5;
+  floatx16 acc[2][2];
+#pragma unroll
+  for (int r = 0; r < 2; ++r)
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[r][c][e] = 0.f;
+
+  float4 ra[4], rb[4];
+  auto stage = [&](int64_t kb) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int f = tid + 256 * q;
+      {  // A: row ia, k = kb + 4 kq ..
+        const int ia = f / (VKT / 4), kq = f % (VKT / 4);
+        const int64_t i = i0 + ia, k = kb + 4 * kq;
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (i < p.M && k < kr.k_hi) {
+          v = *reinterpret_cast<const float4*>(a + i * p.a_rs + k);
+          float* e = reinterpret_cast<float*>(&v);
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            const int64_t kk = k + t;
+            const bool z = kk >= kr.k_hi || (p.a_tri == TRI_LOWER && kk > i) || (p.a_tri == TRI_UPPER && kk < i);
+            e[t] = z ? 0.f : e[t];
+          }
+        }
+        ra[q] = v;
+      }
+      if (BK) {  // B(k, j) = b[j * b_cs + k]: row jb of the transposed panel
+        const int jb = f / (VKT / 4), kq = f % (VKT / 4);
+        const int64_t j = j0 + jb, k = kb + 4 * kq;
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (j < p.N && k < kr.k_hi) {
+          v = *reinterpret_cast<const float4*>(b + j * p.b_cs + k);
+          float* e = reinterpret_cast<float*>(&v);
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            const int64_t kk = k + t;
+            const bool z = kk >= kr.k_hi || (p.b_tri == TRI_LOWER && kk < j) || (p.b_tri == TRI_UPPER && kk > j);
+            e[t] = z ? 0.f : e[t];
+          }
+        }
+        rb[q] = v;
+      } else {  // B(k, j) = b[k * b_rs + j]: row kk of the panel
+        const int kk = f / (MT / 4), jq = f % (MT / 4);
+        const int64_t k = kb + kk, j = j0 + 4 * jq;
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (k < kr.k_hi && j < p.N) {
+          v = *reinterpret_cast<const float4*>(b + k * p.b_rs + j);
+          float* e = reinterpret_cast<float*>(&v);
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            const int64_t jj = j + t;
+            const bool z = jj >= p.N || (p.b_tri == TRI_LOWER && k < jj) || (p.b_tri == TRI_UPPER && k > jj);
+            e[t] = z ? 0.f : e[t];
+          }
+        }
+        rb[q] = v;
+      }
+    }
+  };
+
+  if (kr.k_lo < kr.k_hi) stage(kr.k_lo);
+  for (int64_t kb = kr.k_lo; kb < kr.k_hi; kb += VKT) {
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int f = tid + 256 * q;
+      *reinterpret_cast<float4*>(&As[(f / (VKT / 4)) * APITCH + 4 * (f % (VKT / 4))]) = ra[q];
+      if (BK)
+        *reinterpret_cast<float4*>(&Bs[(f / (VKT / 4)) * BPITCH + 4 * (f % (VKT / 4))]) = rb[q];
+      else
+        *reinterpret_cast<float4*>(&Bs[(f / (MT / 4)) * BPITCH + 4 * (f % (MT / 4))]) = rb[q];
+    }
+    __syncthreads();
+    if (kb + VKT < kr.k_hi) stage(kb + VKT);
+    float4 af[2][4];
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+        af[r][v] = *reinterpret_cast<const float4*>(&As[(wr + 32 * r + li) * APITCH + 16 * hh + 4 * v]);
+    if (BK) {
+      float4 bf[2][4];
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+          bf[c][v] = *reinterpret_cast<const float4*>(&Bs[(wc + 32 * c + li) * BPITCH + 16 * hh + 4 * v]);
+#pragma unroll
+      for (int s2 = 0; s2 < 16; ++s2)
+#pragma unroll
+        for (int r = 0; r < 2; ++r)
+#pragma unroll
+          for (int c = 0; c < 2; ++c)
+            acc[r][c] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[r][s2 >> 2][s2 & 3], bf[c][s2 >> 2][s2 & 3], acc[r][c],
+                                                             0, 0, 0);
+    } else {
+#pragma unroll
+      for (int s2 = 0; s2 < 16; ++s2) {
+        float bv[2];
+#pragma unroll
+        for (int c = 0; c < 2; ++c) bv[c] = Bs[(16 * hh + s2) * BPITCH + wc + 32 * c + li];
+#pragma unroll
+        for (int r = 0; r < 2; ++r)
+#pragma unroll
+          for (int c = 0; c < 2; ++c)
+            acc[r][c] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[r][s2 >> 2][s2 & 3], bv[c], acc[r][c], 0, 0, 0);
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < 2; ++r)
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int64_t i = i0 + wr + 32 * r + 8 * (e >> 2) + 4 * hh + (e & 3);
+        const int64_t j = j0 + wc + 32 * c + li;
+        store_d(p, d, i, j, acc[r][c][e]);
+      }
+}
+
+bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15) == 0; }
+
+// The vectorised path applies: strides, offsets and the K extent in float4 granules.
+bool vec_ok(const GemmProblem<float>& p, bool& bk) {
+  if (p.a_cs != 1 || p.a_rs % 4 || p.a_bs % 4 || !aligned16(p.A)) return false;
+  if (!aligned16(p.B) || p.b_bs % 4 || p.K % 4) return false;
+  if (p.b_rs == 1 && p.b_cs % 4 == 0) bk = true;
+  else if (p.b_cs == 1 && p.b_rs % 4 == 0 && p.N % 4 == 0) bk = false;
+  else return false;
+  return p.M >= MT / 2 && p.N >= MT / 2;
+}
+
 }  // namespace
 
 template <typename T>
@@ -197,6 +381,15 @@ int gptq2d_gemm(const GemmProblem<T>& p, hipStream_t stream) {
   if (p.M == 0 || p.N == 0 || p.batch == 0) return 0;
   if (p.batch > 65535) return GPTQ2D_EUNSUPPORTED;
   if constexpr (sizeof(T) == 4) {
+    bool bk = false;
+    if (vec_ok(p, bk)) {
+      const dim3 grid((unsigned)cdiv(p.N, MT), (unsigned)cdiv(p.M, MT), (unsigned)p.batch);
+      if (bk)
+        hipLaunchKernelGGL(gemm_mfma_vec_kernel<true>, grid, dim3(256), 0, stream, p);
+      else
+        hipLaunchKernelGGL(gemm_mfma_vec_kernel<false>, grid, dim3(256), 0, stream, p);
+      return (int)hipGetLastError();
+    }
     if (p.M >= MT / 2 && p.N >= MT / 2) {
       const dim3 grid((unsigned)cdiv(p.N, MT), (unsigned)cdiv(p.M, MT), (unsigned)p.batch);
       hipLaunchKernelGGL(gemm_mfma_kernel, grid, dim3(256), 0, stream, p);

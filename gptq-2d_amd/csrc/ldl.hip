@@ -9,10 +9,10 @@
 //
 // Device work, all on the caller's stream, no host synchronisation, no allocation:
 //   1. W = J M J: the reversal of the flat array.
-//   2. Right-looking blocked Cholesky of W in place, panels of NB columns: one wave factors the
-//      diagonal block in registers (potrf_diag_kernel), one thread per row solves the panel below
-//      against it (trsm_kernel), and the trailing lower triangle takes the rank-NB update on the
-//      GEMM (fp32: MFMA).
+//   2. Right-looking blocked Cholesky of W in place, panels of NB columns: one launch factors the
+//      diagonal block (redundantly in every workgroup, in LDS) and solves the panel below against
+//      it, one thread per row (potrf_panel_kernel); the trailing lower triangle takes the rank-NB
+//      update on the GEMM (fp32: MFMA).
 //   3. ldl_of_inverse only: C^{-1} in place by recursive doubling.  Diagonal NB blocks are inverted
 //      by one wave each; then for s = NB, 2 NB, ... every pair of inverted s-blocks A^{-1}, D^{-1}
 //      with off-diagonal block B becomes one inverted 2s-block through -D^{-1} (B A^{-1}) -- two
@@ -30,13 +30,17 @@ namespace {
 
 template <typename T>
 struct LdlBlock;
+// NB: diagonal blocks inverted by one wave in registers (trtri leaves, block normalisation);
+// PB: Cholesky panel width (the diagonal block is factored in LDS, the trailing update has K = PB).
 template <>
 struct LdlBlock<float> {
   static constexpr int NB = 64;
+  static constexpr int PB = 64;
 };
 template <>
 struct LdlBlock<double> {
   static constexpr int NB = 32;
+  static constexpr int PB = 32;
 };
 
 __device__ __forceinline__ float bcast(float v, int lane) {
@@ -47,26 +51,6 @@ __device__ __forceinline__ double bcast(double v, int lane) {
   const int lo = __builtin_amdgcn_readlane((int)(b & 0xffffffffll), lane);
   const int hi = __builtin_amdgcn_readlane((int)(b >> 32), lane);
   return __longlong_as_double(((long long)hi << 32) | (unsigned int)lo);
-}
-
-// Lane r holds row r of an NB x NB lower triangular block in a[0..NB): in-register Cholesky.
-// Rows >= n are padding (identity).  Returns the first bad pivot column + 1, or 0.
-template <typename T, int NB>
-__device__ __forceinline__ int wave_potrf(T (&a)[NB], int lane, int n) {
-  int bad = 0;
-#pragma unroll
-  for (int c = 0; c < NB; ++c) {
-    const T piv = bcast(a[c], c);
-    if (!bad && c < n && !(piv > T(0))) bad = c + 1;
-    const T d = sqrt(piv);
-    a[c] = lane == c ? d : (lane > c ? a[c] / d : a[c]);
-#pragma unroll
-    for (int c2 = c + 1; c2 < NB; ++c2) {
-      const T v = bcast(a[c], c2);  // C(c2, c), final
-      if (lane >= c2) a[c2] -= a[c] * v;
-    }
-  }
-  return bad;
 }
 
 // Lane r holds row r of an NB x NB lower triangular block in a; returns row r of its inverse in x.
@@ -101,48 +85,116 @@ __global__ void copy_kernel(T* __restrict__ dst, const T* __restrict__ src, int6
     dst[t] = src[rev ? count - 1 - t : t];
 }
 
-// One wave: Cholesky of the diagonal block W[j0.., j0..] (n = min(NB, k - j0) rows) in place.
-template <typename T, int NB>
-__global__ __launch_bounds__(64) void potrf_diag_kernel(T* __restrict__ w, int64_t ld, int64_t j0, int n,
-                                                        int* __restrict__ info) {
-  const int lane = threadIdx.x;
-  T a[NB];
-  T* row = w + (j0 + lane) * ld + j0;
-#pragma unroll
-  for (int c = 0; c < NB; ++c) a[c] = (lane < n && c <= lane) ? row[c] : (c == lane ? T(1) : T(0));
-  const int bad = wave_potrf<T, NB>(a, lane, n);
-  if (lane < n) {
-#pragma unroll
-    for (int c = 0; c < NB; ++c)
-      if (c <= lane) row[c] = a[c];
-  }
-  if (bad && lane == 0 && info[0] == 0) info[0] = (int)(j0 + bad);
+// Value of lane (lane & ~3) | O for every lane of each quad (DPP quad_perm, no LDS).
+template <int O>
+__device__ __forceinline__ float quad_bcast(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), O | (O << 2) | (O << 4) | (O << 6), 0xf, 0xf,
+                                                 false));
+}
+template <int O>
+__device__ __forceinline__ double quad_bcast(double v) {
+  const long long b = __double_as_longlong(v);
+  constexpr int ctl = O | (O << 2) | (O << 4) | (O << 6);
+  const int lo = __builtin_amdgcn_mov_dpp((int)(b & 0xffffffffll), ctl, 0xf, 0xf, false);
+  const int hi = __builtin_amdgcn_mov_dpp((int)(b >> 32), ctl, 0xf, 0xf, false);
+  return __longlong_as_double(((long long)hi << 32) | (unsigned int)lo);
 }
 
-// One thread per row r >= j0 + NB: W[r, j0:j0+NB] <- W[r, j0:j0+NB] C_jj^{-T}.
-template <typename T, int NB>
-__global__ __launch_bounds__(256) void trsm_kernel(T* __restrict__ w, int64_t ld, int64_t j0, int64_t k) {
-  __shared__ T cs[NB][NB + 1];
-  for (int t = threadIdx.x; t < NB * NB; t += 256) {
-    const int r = t / NB, c = t % NB;
-    cs[r][c] = c <= r ? w[(j0 + r) * ld + j0 + c] : T(0);
+template <int T0, int PB, typename T>
+__device__ __forceinline__ void quad_solve_step(T (&x)[PB / 4], int q, const T* __restrict__ a, int cp) {
+  // column T0: its owner (lane q == T0 % 4, slot T0 / 4) finalises x_T0, the quad shares it, and every
+  // lane removes it from its own later columns c = 4 idx + q > T0
+  constexpr int O = T0 & 3, IT = T0 >> 2;
+  T xt = x[IT] / a[T0 * cp + T0];
+  xt = quad_bcast<O>(xt);
+  if (q == O) x[IT] = xt;
+#pragma unroll
+  for (int idx = IT; idx < PB / 4; ++idx) {
+    const int c = 4 * idx + q;
+    if (c > T0) x[idx] -= xt * a[c * cp + T0];
+  }
+}
+
+template <int T0, int PB, typename T>
+__device__ __forceinline__ void quad_solve(T (&x)[PB / 4], int q, const T* __restrict__ a, int cp) {
+  if constexpr (T0 < PB) {
+    quad_solve_step<T0, PB, T>(x, q, a, cp);
+    quad_solve<T0 + 1, PB, T>(x, q, a, cp);
+  }
+}
+
+// One panel of the blocked Cholesky.  Every workgroup factors the diagonal block W[j0.., j0..]
+// (n = min(PB, k - j0) rows) in LDS, right-looking with one barrier per column (the trailing update
+// uses the unscaled column, A(r, c2) -= A(r, c) A(c2, c) / A(c, c); the columns are scaled by
+// 1/sqrt(pivot) at the end); workgroup 0 writes it back.  Then the panel below is solved against it,
+// W[r, j0:j0+PB] <- W[r, j0:j0+PB] C_jj^{-T}, in chunks of 64 rows staged through LDS (coalesced
+// loads and stores): four lanes share a row, lane q owning the columns c = q mod 4, and the
+// forward substitution runs column by column with the finished x_t broadcast inside the quad.
+template <typename T, int PB>
+__global__ __launch_bounds__(256) void potrf_panel_kernel(T* __restrict__ w, int64_t ld, int64_t j0, int n,
+                                                          int64_t k, int* __restrict__ info) {
+  constexpr int CP = PB + 1;  // odd pitch: row and column walks are both conflict-free
+  __shared__ T a[PB * CP];
+  __shared__ T rs[64 * CP];
+  __shared__ T piv[PB];
+  const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
+  for (int t = tid; t < PB * PB; t += 256) {
+    const int r = t / PB, c = t % PB;
+    a[r * CP + c] = (r < n && c <= r) ? w[(j0 + r) * ld + j0 + c] : (r == c ? T(1) : T(0));
   }
   __syncthreads();
-  const int64_t r = j0 + NB + (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (r >= k) return;
-  T* row = w + r * ld + j0;
-  T x[NB];
-#pragma unroll
-  for (int c = 0; c < NB; ++c) x[c] = row[c];
-#pragma unroll
-  for (int c = 0; c < NB; ++c) {
-    T s = x[c];
-#pragma unroll
-    for (int t = 0; t < c; ++t) s -= x[t] * cs[c][t];
-    x[c] = s / cs[c][c];
+  for (int c = 0; c < PB; ++c) {
+    const T p = a[c * CP + c];
+    const T ip = T(1) / p;
+    if (tid == 0) piv[c] = p;
+    for (int r = c + 1 + ty; r < PB; r += 16) {
+      const T lrc = a[r * CP + c] * ip;
+      for (int c2 = c + 1 + tx; c2 <= r; c2 += 16) a[r * CP + c2] -= lrc * a[c2 * CP + c];
+    }
+    __syncthreads();
   }
+  if (blockIdx.x == 0 && tid == 0 && info[0] == 0) {
+    for (int c = 0; c < n; ++c)
+      if (!(piv[c] > T(0))) {
+        info[0] = (int)(j0 + c + 1);
+        break;
+      }
+  }
+  for (int t = tid; t < PB * PB; t += 256) {
+    const int r = t / PB, c = t % PB;
+    if (c < r) a[r * CP + c] = a[r * CP + c] / sqrt(piv[c]);
+  }
+  __syncthreads();
+  if (tid < PB) a[tid * CP + tid] = sqrt(piv[tid]);
+  __syncthreads();
+  if (blockIdx.x == 0) {
+    for (int t = tid; t < PB * PB; t += 256) {
+      const int r = t / PB, c = t % PB;
+      if (r < n && c <= r) w[(j0 + r) * ld + j0 + c] = a[r * CP + c];
+    }
+  }
+  if (n < PB) return;
+  const int64_t first = j0 + PB;
+  const int q = tid & 3, rr = tid >> 2;
+  for (int64_t r0 = first + (int64_t)blockIdx.x * 64; r0 < k; r0 += (int64_t)gridDim.x * 64) {
+    __syncthreads();
+    for (int t = tid; t < 64 * PB; t += 256) {
+      const int i = t / PB, c = t % PB;
+      rs[i * CP + c] = r0 + i < k ? w[(r0 + i) * ld + j0 + c] : T(0);
+    }
+    __syncthreads();
+    T x[PB / 4];
 #pragma unroll
-  for (int c = 0; c < NB; ++c) row[c] = x[c];
+    for (int idx = 0; idx < PB / 4; ++idx) x[idx] = rs[rr * CP + 4 * idx + q];
+    quad_solve<0, PB, T>(x, q, a, CP);
+#pragma unroll
+    for (int idx = 0; idx < PB / 4; ++idx) rs[rr * CP + 4 * idx + q] = x[idx];
+    __syncthreads();
+    for (int t = tid; t < 64 * PB; t += 256) {
+      const int i = t / PB, c = t % PB;
+      if (r0 + i < k) w[(r0 + i) * ld + j0 + c] = rs[i * CP + c];
+    }
+  }
 }
 
 // One wave per diagonal NB block of the lower triangular W: replace it by its inverse.
@@ -246,30 +298,102 @@ __global__ __launch_bounds__(256) void normalize_block_kernel(T* __restrict__ ou
   }
 }
 
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+// Trailing update of one Cholesky panel on fp32 MFMA: D -= P P^T on the lower triangle of the
+// trailing square D = W[r0.., r0..] (R x R), P = W[r0.., r0-K .. r0) the solved panel.  One
+// workgroup per 64 x 64 lower tile, numbered along the triangle and re-numbered so that each XCD
+// (own L2) runs a contiguous share; it issues all its loads at once -- its D block into the
+// accumulators, both 64 x K panels through LDS as float4 -- then 16 MFMAs (32x32x2) per 32 k,
+// A negated so that the accumulation is D - P P^T directly.  Lane layout as in gemm.hip.
+template <int K>
+__global__ __launch_bounds__(256) void syrk_lower_kernel(float* __restrict__ w, int64_t ld, int64_t r0, int64_t R) {
+  constexpr int TP = 64, PP = K + 4;
+  __shared__ __align__(16) float As[TP * PP];
+  __shared__ __align__(16) float Bs[TP * PP];
+  const int64_t n = gridDim.x, lin = blockIdx.x;
+  const int64_t base = n / 8, extra = n % 8, xcd = lin % 8;
+  const int64_t id = xcd * base + (xcd < extra ? xcd : extra) + lin / 8;
+  int64_t ti = (int64_t)((sqrt(8.0 * (double)id + 1.0) - 1.0) * 0.5);
+  while ((ti + 1) * (ti + 2) / 2 <= id) ++ti;
+  while (ti * (ti + 1) / 2 > id) --ti;
+  const int64_t tj = id - ti * (ti + 1) / 2;
+  const int64_t i0 = ti * TP, j0 = tj * TP;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wy = wave >> 1, wx = wave & 1, li = lane & 31, hh = lane >> 5;
+  const bool active = !(ti == tj && wy < wx);  // the upper block of a diagonal tile has nothing to do
+  float* d = w + r0 * ld + r0;
+  const float* P = w + r0 * ld + (r0 - K);
+  floatx16 acc;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) {
+    const int64_t i = i0 + 32 * wy + 8 * (e >> 2) + 4 * hh + (e & 3), j = j0 + 32 * wx + li;
+    acc[e] = (active && i < R && j < R) ? d[i * ld + j] : 0.f;
+  }
+#pragma unroll
+  for (int q = 0; q < TP * K / 4 / 256; ++q) {
+    const int f = tid + 256 * q;
+    const int r = f / (K / 4), kq = f % (K / 4);
+    const int64_t ia = i0 + r, ib = j0 + r;
+    const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+    *reinterpret_cast<float4*>(&As[r * PP + 4 * kq]) =
+        ia < R ? *reinterpret_cast<const float4*>(P + ia * ld + 4 * kq) : z;
+    *reinterpret_cast<float4*>(&Bs[r * PP + 4 * kq]) =
+        ib < R ? *reinterpret_cast<const float4*>(P + ib * ld + 4 * kq) : z;
+  }
+  __syncthreads();
+  if (!active) return;
+#pragma unroll
+  for (int kc = 0; kc < K / 32; ++kc) {
+    float4 af[4], bf[4];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      af[v] = *reinterpret_cast<const float4*>(&As[(32 * wy + li) * PP + 32 * kc + 16 * hh + 4 * v]);
+      bf[v] = *reinterpret_cast<const float4*>(&Bs[(32 * wx + li) * PP + 32 * kc + 16 * hh + 4 * v]);
+    }
+#pragma unroll
+    for (int s2 = 0; s2 < 16; ++s2)
+      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(-af[s2 >> 2][s2 & 3], bf[s2 >> 2][s2 & 3], acc, 0, 0, 0);
+  }
+#pragma unroll
+  for (int e = 0; e < 16; ++e) {
+    const int64_t i = i0 + 32 * wy + 8 * (e >> 2) + 4 * hh + (e & 3), j = j0 + 32 * wx + li;
+    if (i < R && j < R && j <= i) d[i * ld + j] = acc[e];
+  }
+}
+
 template <typename T>
 int cholesky_inplace(T* w, int64_t k, int* info, hipStream_t stream) {
-  constexpr int NB = LdlBlock<T>::NB;
+  constexpr int PB = LdlBlock<T>::PB;
   int rc;
-  for (int64_t j0 = 0; j0 < k; j0 += NB) {
-    const int n = k - j0 < NB ? (int)(k - j0) : NB;
-    hipLaunchKernelGGL((potrf_diag_kernel<T, NB>), dim3(1), dim3(64), 0, stream, w, k, j0, n, info);
+  for (int64_t j0 = 0; j0 < k; j0 += PB) {
+    const int n = k - j0 < PB ? (int)(k - j0) : PB;
+    const int64_t rest = k - j0 - PB;
+    const unsigned blocks = rest > 0 ? (unsigned)(cdiv(rest, 64) < 256 ? cdiv(rest, 64) : 256) : 1u;
+    hipLaunchKernelGGL((potrf_panel_kernel<T, PB>), dim3(blocks), dim3(256), 0, stream, w, k, j0, n, k, info);
     if ((rc = (int)hipGetLastError())) return rc;
-    const int64_t rest = k - j0 - NB;
     if (rest <= 0) break;
-    hipLaunchKernelGGL((trsm_kernel<T, NB>), dim3((unsigned)cdiv(rest, 256)), dim3(256), 0, stream, w, k, j0, k);
-    if ((rc = (int)hipGetLastError())) return rc;
-    // trailing lower triangle: W22 -= P P^T with P = W[j0+NB:, j0:j0+NB]
+    // trailing lower triangle: W22 -= P P^T with P = W[j0+PB:, j0:j0+PB]
+    if constexpr (sizeof(T) == 4) {
+      if (k % 4 == 0) {
+        const int64_t nt = cdiv(rest, 64);
+        hipLaunchKernelGGL((syrk_lower_kernel<PB>), dim3((unsigned)(nt * (nt + 1) / 2)), dim3(256), 0, stream, w, k,
+                           j0 + PB, rest);
+        if ((rc = (int)hipGetLastError())) return rc;
+        continue;
+      }
+    }
     GemmProblem<T> g{};
     g.M = g.N = rest;
-    g.K = NB;
+    g.K = PB;
     g.batch = 1;
-    g.A = w + (j0 + NB) * k + j0;
+    g.A = w + (j0 + PB) * k + j0;
     g.a_rs = k;
     g.a_cs = 1;
     g.B = g.A;
     g.b_rs = 1;
     g.b_cs = k;
-    g.D = w + (j0 + NB) * k + j0 + NB;
+    g.D = w + (j0 + PB) * k + j0 + PB;
     g.d_rs = k;
     g.d_cs = 1;
     g.alpha = T(-1);

@@ -58,6 +58,29 @@ def ldl(M: torch.Tensor, size: int = 1, *, check: bool = True) -> torch.Tensor:
     return _factor("ldl", M, size, check)
 
 
+def feedback_factors_of_grams(G: torch.Tensor, H: torch.Tensor, super_entry_shape=(1, 1), *, check: bool = True):
+    """(L, U) = (ldl_of_inverse(G, p), ldl_of_inverse(H, q)^T) from the Grams themselves, the two
+    factorisations running concurrently on two side streams of the current device (each is a
+    sequence of latency-bound panel steps, so they fill each other's gaps).  No counterpart in the
+    reference, whose callers compute the two factors one after the other (demo.ipynb cell 5)."""
+    p, q = super_entry_shape
+    main = torch.cuda.current_stream(G.device)
+    streams = [torch.cuda.Stream(device=G.device) for _ in range(2)]
+    out = []
+    for s, (m, size) in zip(streams, ((G, p), (H, q))):
+        s.wait_stream(main)
+        with torch.cuda.stream(s):
+            out.append(ldl_of_inverse(m, size=size, check=False))
+    for s, t in zip(streams, out):
+        main.wait_stream(s)
+        t.record_stream(main)
+    if check:
+        for t, m in zip(out, (G, H)):
+            if not bool(torch.isfinite(t).all()):
+                ldl_of_inverse(m, size=1)  # raises the LinAlgError with the failing minor
+    return out[0], out[1].transpose(-1, -2)
+
+
 def feedback_factors(A: torch.Tensor, B: torch.Tensor, super_entry_shape=(1, 1)):
     """L and U for the Grams G = A^T A and H = B B^T, with p x p and q x q identity diagonal blocks
     (gptq_2d_reference.py:58-66)."""

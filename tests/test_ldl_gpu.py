@@ -33,16 +33,21 @@ def _gemm(M, N, K, batch, a, b, d, alpha, beta, a_tri=0, b_tri=0, d_tri=0, a_t=F
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
 @pytest.mark.parametrize("M,N,K", [(200, 300, 77), (128, 128, 16), (257, 129, 33), (64, 64, 1000), (5, 700, 9),
-                                   (1000, 6, 64)])
+                                   (1000, 6, 64), (320, 256, 96), (130, 260, 36)])
 @pytest.mark.parametrize("tri", [(0, 0, 0), (1, 0, 0), (0, 1, 0), (0, 0, 1), (2, 2, 0), (1, 1, 1)])
-def test_gemm(dtype, M, N, K, tri):
+@pytest.mark.parametrize("b_layout", ["nk", "kn"])
+def test_gemm(dtype, M, N, K, tri, b_layout):
     """Strided GEMM with triangular operand structure against a host fp64 product; the structurally zero
-    parts hold NaN, which must never be read."""
-    print(f"gemm {M}x{N}x{K} {dtype} tri={tri}", flush=True)
+    parts hold NaN, which must not reach the result.  B is either a transposed view (contiguous along k)
+    or contiguous along j, which selects the two layouts of the vectorised MFMA path."""
+    print(f"gemm {M}x{N}x{K} {dtype} tri={tri} B {b_layout}", flush=True)
     g = torch.Generator().manual_seed(M * 7 + N * 3 + K)
     batch = 2
     a = torch.randn(batch, M, K, generator=g, dtype=torch.float64)
-    b = torch.randn(batch, N, K, generator=g, dtype=torch.float64).transpose(-1, -2)  # a transposed view
+    if b_layout == "nk":
+        b = torch.randn(batch, N, K, generator=g, dtype=torch.float64).transpose(-1, -2)  # a transposed view
+    else:
+        b = torch.randn(batch, K, N, generator=g, dtype=torch.float64)
     d0 = torch.randn(batch, M, N, generator=g, dtype=torch.float64)
     a_tri, b_tri, d_tri = tri
     i = torch.arange(M)[:, None]
@@ -55,7 +60,9 @@ def test_gemm(dtype, M, N, K, tri):
     expected = d0 * .5 + 1.5 * (a * am) @ (b * bm)
     expected = torch.where(dm, expected, d0)
     a_dev = a.masked_fill(~am, torch.nan).to(dtype).to(DEV)
-    b_dev = b.masked_fill(~bm, torch.nan).to(dtype).to(DEV)
+    b_dev = b.masked_fill(~bm, torch.nan).to(dtype)
+    b_dev = (b_dev.transpose(-1, -2).contiguous().to(DEV).transpose(-1, -2) if b_layout == "nk"
+             else b_dev.contiguous().to(DEV))
     d_dev = d0.to(dtype).to(DEV)
     _gemm(M, N, K, batch, a_dev, b_dev, d_dev, 1.5, .5, a_tri, b_tri, d_tri)
     got = d_dev.double().cpu()
