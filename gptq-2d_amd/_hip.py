@@ -64,7 +64,7 @@ def lib() -> ctypes.CDLL:
                 fn = getattr(handle, f"gptq2d_{name}_{suffix}")
                 fn.argtypes = argtypes
                 fn.restype = ctypes.c_int
-        handle.gptq2d_profile_start.argtypes = [_I64]
+        handle.gptq2d_profile_start.argtypes = [_I64, ctypes.c_uint32]
         handle.gptq2d_profile_start.restype = ctypes.c_int
         handle.gptq2d_profile_read.argtypes = [_I32, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double),
                                                ctypes.POINTER(ctypes.c_int64)]
@@ -90,9 +90,9 @@ def call(name: str, dtype: torch.dtype, *args) -> None:
 PROF_FLUSH, PROF_TILE_SWEEP, PROF_LDL_GEMM = 0, 1, 2
 
 
-def profile_start(capacity: int = 4096) -> None:
-    """Time every launch of the profiled kernel classes with HIP events until ``profile_stop``."""
-    rc = lib().gptq2d_profile_start(capacity)
+def profile_start(capacity: int = 4096, kinds=(PROF_FLUSH, PROF_TILE_SWEEP, PROF_LDL_GEMM)) -> None:
+    """Time every launch of the kernel classes ``kinds`` with HIP events until ``profile_stop``."""
+    rc = lib().gptq2d_profile_start(capacity, sum(1 << k for k in kinds))
     if rc:
         raise GPTQ2DError(f"gptq2d_profile_start failed with code {rc}")
 

@@ -15,6 +15,7 @@ struct KindState {
 
 struct Profiler {
   bool on = false;
+  uint32_t mask = 0;
   KindState kind[PROF_KINDS];
 };
 
@@ -35,7 +36,7 @@ void release() {
 }  // namespace
 
 bool gptq2d_prof_on(int32_t kind) {
-  return g_prof.on && kind >= 0 && kind < PROF_KINDS &&
+  return g_prof.on && kind >= 0 && kind < PROF_KINDS && (g_prof.mask >> kind & 1u) &&
          g_prof.kind[kind].used < (int64_t)g_prof.kind[kind].start.size();
 }
 
@@ -55,12 +56,16 @@ void gptq2d_prof_end(int32_t kind, double work, hipStream_t stream) {
 
 extern "C" {
 
-// Turn profiling on with room for `capacity` launches per kernel class (creates the events).
-// Launches beyond the capacity are not recorded.  Returns 0 or a hipError_t.
-int gptq2d_profile_start(int64_t capacity) {
+// Turn profiling on for the kernel classes in `kinds` (bit k: class k) with room for `capacity`
+// launches per class (creates the events).  Launches beyond the capacity are not recorded.
+// Returns 0 or a hipError_t.
+int gptq2d_profile_start(int64_t capacity, uint32_t kinds) {
   release();
   if (capacity <= 0) return GPTQ2D_EINVAL;
-  for (auto& k : g_prof.kind) {
+  g_prof.mask = kinds;
+  for (int kind = 0; kind < PROF_KINDS; ++kind) {
+    if (!(kinds >> kind & 1u)) continue;
+    KindState& k = g_prof.kind[kind];
     k.start.resize(capacity);
     k.stop.resize(capacity);
     k.work.assign(capacity, 0.);

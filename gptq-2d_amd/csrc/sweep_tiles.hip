@@ -143,6 +143,235 @@ __global__ __launch_bounds__(NTHREADS) void sweep_tiles_kernel(T* __restrict__ y
   }
 }
 
+// ------------------------------------------------------------------------------------------------ fp32: pull + sweep
+
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+// Sum over the 8 lanes of each aligned group of 8 (all lanes receive it): xor 1 and xor 2 inside the
+// quad (quad_perm [1,0,3,2] and [2,3,0,1]), then the other quad of the group (row_half_mirror,
+// which maps lane i of each half-row to lane 7 - i).  VALU data movement only, no LDS.
+__device__ __forceinline__ float group8_sum(float v) {
+  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xf, 0xf, false));
+  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xf, 0xf, false));
+  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xf, 0xf, false));
+  return v;
+}
+
+// Quantizer of the fused sweeps, applied to one value.
+template <int KIND>
+__device__ __forceinline__ float quantize_entry(float yv, float sv, float zv, float qmin, float qmax) {
+  if constexpr (KIND == Q_AFFINE) {
+    const float code = clamp_val(round_even(yv / sv + zv), qmin, qmax);
+    return (code - zv) * sv;
+  } else if constexpr (KIND == Q_FORCED) {
+    return sv;
+  } else {
+    return round_even(yv);
+  }
+}
+
+// Pull one band product into acc: sum over k-tiles t in [lo, hi), t = lo + wave + 4 q, of
+// A[i0.., t] B[t, j0..] with A row-major (lda) and B row-major (ldb), both 32 x 32 tiles read
+// straight into the MFMA operand layout; per chunk of 16 k-tiles every load is issued first.
+template <bool VEC>
+__device__ __forceinline__ void pull_product(floatx16& acc, const float* __restrict__ A, int64_t lda, int64_t a_rows,
+                                             int64_t a_cols, const float* __restrict__ Bm, int64_t ldb,
+                                             int64_t b_rows, int64_t b_cols, int64_t i0, int64_t j0, int64_t lo,
+                                             int64_t hi, int wave, int li, int hh) {
+  const int64_t ia = i0 + li, jb = j0 + li;
+  for (int64_t base = lo; base < hi; base += 4 * 4) {
+    float av[4][16], bv[4][16];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int64_t t = base + wave + 4 * q;
+      const int64_t k0 = t * TR + 16 * hh;
+      const bool ok = t < hi;
+      if (VEC) {
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const float4 f = (ok && ia < a_rows && k0 + 4 * v < a_cols)
+                               ? *reinterpret_cast<const float4*>(A + ia * lda + k0 + 4 * v)
+                               : make_float4(0.f, 0.f, 0.f, 0.f);
+          av[q][4 * v] = f.x, av[q][4 * v + 1] = f.y, av[q][4 * v + 2] = f.z, av[q][4 * v + 3] = f.w;
+        }
+      } else {
+#pragma unroll
+        for (int s2 = 0; s2 < 16; ++s2) av[q][s2] = (ok && ia < a_rows && k0 + s2 < a_cols) ? A[ia * lda + k0 + s2] : 0.f;
+      }
+#pragma unroll
+      for (int s2 = 0; s2 < 16; ++s2) bv[q][s2] = (ok && k0 + s2 < b_rows && jb < b_cols) ? Bm[(k0 + s2) * ldb + jb] : 0.f;
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      if (base + wave + 4 * q >= hi) break;
+#pragma unroll
+      for (int s2 = 0; s2 < 16; ++s2) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[q][s2], bv[q][s2], acc, 0, 0, 0);
+    }
+  }
+}
+
+// LDS row pitch of the tile arrays: 40 = 8 (mod 32) keeps the antidiagonal walks (32 r + t) and the
+// column walks (8 lanes x 8 rows) at most 2-way bank-conflicted; a pitch of 33 puts a whole
+// antidiagonal into one bank.
+constexpr int SP = 40;
+
+// One tile (I, J) of coarse stage T = I + J inside the outer block that starts at tile stage S0.
+//  1. Pull, on MFMA: the feedback of the tiles of this outer block swept before T, which no flush
+//     has delivered yet -- D = sum L[I,t] E[t,J] over t in [max(0, S0-J), I) and
+//     R = sum C[I,t] U[t,J] over t in [max(0, S0-I), J) -- the four waves taking every fourth
+//     k-tile and reducing through LDS.  Operands go straight from global memory into the MFMA
+//     layout (lane l: A(l%32, 16 (l/32) + s), B(16 (l/32) + s, l%32)).  Then C += D, Y += D + R.
+//  2. The tile's 63 antidiagonals in LDS, 8 lanes per row: each lane reads its 4 terms of the
+//     in-tile down and right feedback of its row's entry on the antidiagonal, and that entry's Y,
+//     C and quantizer inputs, all at once; the 8 partial sums meet through DPP; all 8 lanes round
+//     and one writes Y, E and C back; one barrier per antidiagonal.
+template <bool VEC, int KIND>
+__global__ __launch_bounds__(NTHREADS) void tile_pull_sweep_kernel(float* __restrict__ y, float* __restrict__ c,
+                                                                   float* __restrict__ e,
+                                                                   const float* __restrict__ l,
+                                                                   const float* __restrict__ u, int64_t m, int64_t n,
+                                                                   int64_t stage, int64_t S0, int64_t tile_lo,
+                                                                   BatchMap lmap, BatchMap umap, QSpec<float> qs,
+                                                                   int64_t nx, int64_t ny) {
+  __shared__ float red[4][2][TR][TR + 1];
+  __shared__ float Ys[TR][SP];
+  __shared__ float Cs[TR][SP];
+  __shared__ float Es[TR][SP];
+  __shared__ float Ls[TR][SP];
+  __shared__ float Us[TR][SP];
+  __shared__ float Ss[TR][SP];
+  __shared__ float Zs[TR][SP];
+
+  const GridIds id = grid_ids(nx, ny);
+  const int64_t b = id.b;
+  const int64_t I = tile_lo + id.x, J = stage - I;
+  const int64_t i0 = I * TR, j0 = J * TR;
+  const int64_t mat = b * m * n;
+  const float* lb = l + lmap.offset(b);
+  const float* ub = u + umap.offset(b);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int li = lane & 31, hh = lane >> 5;
+
+  // ---- 1. pull
+  const int64_t dlo = S0 - J > 0 ? S0 - J : 0, rlo = S0 - I > 0 ? S0 - I : 0;
+  const bool any = dlo < I || rlo < J;
+  if (any) {
+    floatx16 accd, accr;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) accd[r] = accr[r] = 0.f;
+    pull_product<VEC>(accd, lb, m, m, m, e + mat, n, m, n, i0, j0, dlo, I, wave, li, hh);
+    pull_product<VEC>(accr, c + mat, n, m, n, ub, n, n, n, i0, j0, rlo, J, wave, li, hh);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int row = 8 * (r >> 2) + 4 * hh + (r & 3);
+      red[wave][0][row][li] = accd[r];
+      red[wave][1][row][li] = accr[r];
+    }
+  }
+  __syncthreads();
+
+  // ---- load the tile
+  for (int t = tid; t < TR * TR; t += NTHREADS) {
+    const int r = t / TR, cc = t % TR;
+    const int64_t gi = i0 + r, gj = j0 + cc;
+    const bool in = gi < m && gj < n;
+    const int64_t off = mat + gi * n + gj;
+    float dd = 0.f, rr = 0.f;
+    if (any) {
+      dd = (red[0][0][r][cc] + red[1][0][r][cc]) + (red[2][0][r][cc] + red[3][0][r][cc]);
+      rr = (red[0][1][r][cc] + red[1][1][r][cc]) + (red[2][1][r][cc] + red[3][1][r][cc]);
+    }
+    Ys[r][cc] = in ? y[off] + (dd + rr) : 0.f;
+    Cs[r][cc] = in ? c[off] + dd : 0.f;
+    Es[r][cc] = 0.f;
+    Ls[r][cc] = (cc < r && gi < m) ? lb[gi * m + (i0 + cc)] : 0.f;
+    Us[r][cc] = (r < cc && j0 + cc < n) ? ub[(j0 + r) * n + (j0 + cc)] : 0.f;
+    if constexpr (KIND == Q_AFFINE) {
+      Ss[r][cc] = in ? qs.scale[qs.smap.offset(b) + gi * n + gj] : 1.f;
+      Zs[r][cc] = in ? qs.zp[qs.zmap.offset(b) + gi * n + gj] : 0.f;
+    } else if constexpr (KIND == Q_FORCED) {
+      Ss[r][cc] = in ? qs.scale[qs.smap.offset(b) + gi * n + gj] : 0.f;
+    }
+  }
+  __syncthreads();
+
+  // ---- 2. in-tile sweep
+  const int r = tid / PARTS, part = tid % PARTS;
+  const int64_t gi = i0 + r;
+  const int rows_in = m - i0 < TR ? (int)(m - i0) : TR;  // tile rows / columns inside the matrix
+  const int cols_in = n - j0 < TR ? (int)(n - j0) : TR;
+  const bool row_in = r < rows_in;
+  float lrow[TR / PARTS];
+#pragma unroll
+  for (int k = 0; k < TR / PARTS; ++k) lrow[k] = part + PARTS * k < r ? Ls[r][part + PARTS * k] : 0.f;
+  float* ypre_row = qs.ypre ? qs.ypre + mat + gi * n + j0 : nullptr;
+  for (int t = 0; t < 2 * TR - 1; ++t) {
+    const int cc = t - r;
+    const bool active = row_in && cc >= 0 && cc < cols_in;
+    const int ccs = active ? cc : 0;
+    float ev[TR / PARTS], uv[TR / PARTS], cv[TR / PARTS];
+#pragma unroll
+    for (int k = 0; k < TR / PARTS; ++k) {
+      const int rr = part + PARTS * k;
+      ev[k] = Es[rr][ccs];
+      uv[k] = Us[rr][ccs];
+      cv[k] = Cs[r][rr];
+    }
+    const float y0 = Ys[r][ccs], c0 = Cs[r][ccs];
+    float sv = 0.f, zv = 0.f;
+    if constexpr (KIND == Q_AFFINE) {
+      sv = Ss[r][ccs];
+      zv = Zs[r][ccs];
+    } else if constexpr (KIND == Q_FORCED) {
+      sv = Ss[r][ccs];
+    }
+    float down = 0.f, right = 0.f;
+#pragma unroll
+    for (int k = 0; k < TR / PARTS; ++k) {
+      down += lrow[k] * ev[k];
+      right += (part + PARTS * k < ccs ? cv[k] : 0.f) * uv[k];
+    }
+    down = group8_sum(down);
+    right = group8_sum(right);
+    const float yv = (y0 + down) + right;
+    const float z = quantize_entry<KIND>(yv, sv, zv, qs.qmin, qs.qmax);
+    const float evn = z - yv;
+    if (active && part == 0) {
+      Ys[r][cc] = z;
+      Es[r][cc] = evn;
+      Cs[r][cc] = (c0 + down) + evn;
+      if (ypre_row) ypre_row[cc] = yv;
+    }
+    __syncthreads();
+  }
+
+  for (int t = tid; t < TR * TR; t += NTHREADS) {
+    const int rr = t / TR, cc = t % TR;
+    const int64_t gi2 = i0 + rr, gj = j0 + cc;
+    if (gi2 < m && gj < n) {
+      const int64_t off = mat + gi2 * n + gj;
+      y[off] = Ys[rr][cc];
+      c[off] = Cs[rr][cc];
+      e[off] = Es[rr][cc];
+    }
+  }
+}
+
+template <bool VEC>
+void launch_tile_pull(int32_t kind, dim3 grid, hipStream_t stream, float* y, float* c, float* e, const float* l,
+                      const float* u, int64_t m, int64_t n, int64_t st, int64_t S0, int64_t lo, const BatchMap& lmap,
+                      const BatchMap& umap, const QSpec<float>& qs, int64_t nx, int64_t ny) {
+  if (kind == Q_AFFINE)
+    hipLaunchKernelGGL((tile_pull_sweep_kernel<VEC, Q_AFFINE>), grid, dim3(NTHREADS), 0, stream, y, c, e, l, u, m, n,
+                       st, S0, lo, lmap, umap, qs, nx, ny);
+  else if (kind == Q_FORCED)
+    hipLaunchKernelGGL((tile_pull_sweep_kernel<VEC, Q_FORCED>), grid, dim3(NTHREADS), 0, stream, y, c, e, l, u, m, n,
+                       st, S0, lo, lmap, umap, qs, nx, ny);
+  else
+    hipLaunchKernelGGL((tile_pull_sweep_kernel<VEC, Q_ROUND>), grid, dim3(NTHREADS), 0, stream, y, c, e, l, u, m, n,
+                       st, S0, lo, lmap, umap, qs, nx, ny);
+}
+
 template <typename T>
 int sweep_fused(T* y, T* c, T* e, const T* l, const T* u, int64_t m, int64_t n, int32_t bnd, const int64_t* bshape,
                 const int64_t* lstride, const int64_t* ustride, int32_t qkind, const T* qa, const int64_t* qa_stride,
@@ -177,13 +406,23 @@ int sweep_fused(T* y, T* c, T* e, const T* l, const T* u, int64_t m, int64_t n, 
       Grid3 g = make_grid(hi - lo + 1, 1, B);
       const bool prof = gptq2d_prof_on(PROF_TILE_SWEEP);
       if (prof) gptq2d_prof_begin(PROF_TILE_SWEEP, stream);
-      hipLaunchKernelGGL(sweep_tiles_kernel<T>, g.grid, dim3(NTHREADS), 0, stream, y, c, e, l, u, m, n, st, lo, lmap,
-                         umap, qs, g.nx, g.ny);
+      if constexpr (sizeof(T) == 4) {
+        // fp32: every tile pulls the feedback of this outer block's earlier tile stages itself
+        if (m % 4 == 0 && n % 4 == 0)
+          launch_tile_pull<true>(qkind, g.grid, stream, y, c, e, l, u, m, n, st, S0, lo, lmap, umap, qs, g.nx, g.ny);
+        else
+          launch_tile_pull<false>(qkind, g.grid, stream, y, c, e, l, u, m, n, st, S0, lo, lmap, umap, qs, g.nx, g.ny);
+      } else {
+        hipLaunchKernelGGL(sweep_tiles_kernel<T>, g.grid, dim3(NTHREADS), 0, stream, y, c, e, l, u, m, n, st, lo,
+                           lmap, umap, qs, g.nx, g.ny);
+      }
       // work of a tile sweep: its entries (the in-tile feedback is latency-, not throughput-bound)
       if (prof) gptq2d_prof_end(PROF_TILE_SWEEP, (double)B * (hi - lo + 1) * TR * TR, stream);
       if ((rc = (int)hipGetLastError())) return rc;
-      if (st + 1 < S1 && (rc = gptq2d_flush<T>(y, c, e, l, u, m, n, TR, TR, st, st + 1, S1, lmap, umap, B, stream)))
-        return rc;
+      if constexpr (sizeof(T) == 8) {
+        if (st + 1 < S1 && (rc = gptq2d_flush<T>(y, c, e, l, u, m, n, TR, TR, st, st + 1, S1, lmap, umap, B, stream)))
+          return rc;
+      }
     }
     if (S1 < stages && (rc = gptq2d_flush<T>(y, c, e, l, u, m, n, TR, TR, S0, S1, stages, lmap, umap, B, stream)))
       return rc;

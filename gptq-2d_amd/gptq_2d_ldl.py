@@ -20,6 +20,17 @@ import _hip
 # p x p diagonal blocks up to this size are normalised on the GPU (fp32; fp64: 32).
 MAX_BLOCK = {torch.float32: 64, torch.float64: 32}
 
+# Two side streams per device for feedback_factors_of_grams (created once: a new stream per call
+# would cost a stream creation and defeat the caching allocator's reuse of its blocks).
+_SIDE_STREAMS: dict = {}
+
+
+def _side_streams(device: torch.device):
+    key = torch.device(device).index if torch.device(device).index is not None else torch.cuda.current_device()
+    if key not in _SIDE_STREAMS:
+        _SIDE_STREAMS[key] = tuple(torch.cuda.Stream(device=key) for _ in range(2))
+    return _SIDE_STREAMS[key]
+
 
 def _factor(name: str, m: torch.Tensor, size: int, check: bool) -> torch.Tensor:
     assert m.dim() >= 2 and m.size(-1) == m.size(-2), "expected square matrices [..., k, k]"
@@ -65,7 +76,7 @@ def feedback_factors_of_grams(G: torch.Tensor, H: torch.Tensor, super_entry_shap
     reference, whose callers compute the two factors one after the other (demo.ipynb cell 5)."""
     p, q = super_entry_shape
     main = torch.cuda.current_stream(G.device)
-    streams = [torch.cuda.Stream(device=G.device) for _ in range(2)]
+    streams = _side_streams(G.device)
     out = []
     for s, (m, size) in zip(streams, ((G, p), (H, q))):
         s.wait_stream(main)

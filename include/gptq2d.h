@@ -129,7 +129,7 @@ GPTQ2D_DECLARE(double, f64)
  * While on, every launch of a profiled kernel class is bracketed with HIP events on its stream.
  * Process-global, not thread-safe, not for use under stream capture.
  * kind 0: cross-tile feedback panels (flush); 1: fused tile sweeps; 2: LDL GEMMs. */
-int gptq2d_profile_start(int64_t capacity);
+int gptq2d_profile_start(int64_t capacity, uint32_t kinds); /* kinds: bit k enables class k */
 int gptq2d_profile_read(int32_t kind, double* ms, double* work, int64_t* launches);
 int gptq2d_profile_stop(void);
 

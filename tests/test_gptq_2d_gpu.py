@@ -213,3 +213,33 @@ def test_graph_capture_fused():
         eager = G.gptq_2d(xs, lu, uu, quantizer_inputs=(sc, zp), **opts)
         torch.cuda.synchronize()
         assert replay(xs, lu, uu, sc, zp).equal(eager), k
+
+
+@pytest.mark.parametrize("m,n", [(100, 70), (300, 260), (520, 1030), (1024, 512)])
+@pytest.mark.parametrize("outer", [32, 64, 512])
+def test_fused_fp32_trajectory(m, n, outer):
+    """The fp32 fused engine (MFMA pulls inside an outer block, MFMA flushes between blocks) follows the fp64
+    engine's trajectory: with every stage forced to the fp64 run's codes, each entry's Y just before rounding
+    agrees with the fp64 value to 1e-4 absolute (values are O(10); fp32 summation error is O(1e-5)).
+    The fp64 engine itself equals the oracle's Algorithm 3 exactly (test_reference, test_fused_multi_tile)."""
+    print(f"fp32 trajectory {m}x{n} outer={outer}", flush=True)
+    g = torch.Generator().manual_seed(m * 3 + n)
+    x = 4. * torch.randn(m, n, generator=g, dtype=torch.float64)
+    lo = S.unit_triangular(.3 / m ** .5 * torch.randn(m, m, generator=g, dtype=torch.float64), upper=False)
+    up = S.unit_triangular(.3 / n ** .5 * torch.randn(n, n, generator=g, dtype=torch.float64), upper=True)
+    x, lo, up = x.to(DEV), lo.to(DEV), up.to(DEV)
+    z64 = G.gptq_2d(x, lo, up, outer_block_size=outer)
+    pre64 = torch.full_like(x, float("nan"))
+    assert G.gptq_2d(x, lo, up, quantizer=QI.teacher_forced_quantizer, quantizer_inputs=(z64, pre64),
+                     outer_block_size=outer).equal(z64)
+    pre32 = torch.full_like(x, float("nan"), dtype=torch.float32)
+    z32 = G.gptq_2d(x.float(), lo.float(), up.float(), quantizer=QI.teacher_forced_quantizer,
+                    quantizer_inputs=(z64.float(), pre32), outer_block_size=outer)
+    assert z32.equal(z64.float())
+    err = (pre32.double() - pre64).abs()
+    assert not err.isnan().any()
+    print(f"  max |dY| {err.max().item():.2e}, mean {err.mean().item():.2e}", flush=True)
+    assert err.max().item() < 1e-4
+    # free-running fp32 codes agree except at near-ties of the fp32 trajectory
+    z32f = G.gptq_2d(x.float(), lo.float(), up.float(), outer_block_size=outer)
+    assert (z32f.double() != z64).float().mean().item() < 1e-3
