@@ -43,6 +43,7 @@ _SIGNATURES = {
     "ldl": [_P, _P, _P, _P, _I64, _I64, _I64, _P],
     "gemm": [_I64, _I64, _I64, _I64, _P, _I64, _I64, _I64, _P, _I64, _I64, _I64, _P, _I64, _I64, _I64, _F64, _F64,
              _I32, _I32, _I32, _P],
+    "viterbi": [_P, _P, _P, _P, _P, _P, _I64, _I64, _I32, _I32, _I32, _I32, _P],
 }
 
 _lib = None
@@ -64,6 +65,8 @@ def lib() -> ctypes.CDLL:
                 fn = getattr(handle, f"gptq2d_{name}_{suffix}")
                 fn.argtypes = argtypes
                 fn.restype = ctypes.c_int
+        handle.gptq2d_viterbi_workspace.argtypes = [_I64, _I64, _I32, _I32, _I32]
+        handle.gptq2d_viterbi_workspace.restype = ctypes.c_int64
         handle.gptq2d_profile_start.argtypes = [_I64, ctypes.c_uint32]
         handle.gptq2d_profile_start.restype = ctypes.c_int
         handle.gptq2d_profile_read.argtypes = [_I32, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double),

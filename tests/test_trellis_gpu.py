@@ -1,0 +1,180 @@
+"""GPU tests of the HIP trellis quantizer (one-launch Viterbi search), following the reference's
+quantizer_trellis.py:406-519 and test_gptq_2d.py:91-111.
+
+Bitwise targets: the golden values and states written from the reference's _trellis_quantize_torch
+(tests/golden/trellis.npz, including L=16 HYB and a table with many equal costs); the PyTorch
+formulation in this package and the CPU oracle on fresh random sequences; brute-force optimality on
+tiny trellises; path validity (consecutive states share L - K V bits, circular when tail-biting).
+"""
+
+import functools
+import itertools
+import pathlib
+
+import numpy as np
+import pytest
+import torch
+
+import gptq_2d as G
+import quantizer_trellis as QT
+from oracle import algorithms as A
+from oracle import sweep as S
+from oracle import trellis as OT
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+GOLDEN = pathlib.Path(__file__).resolve().parent / "golden"
+SHAPES = (5, 1, 1, 7), (4, 1, 2, 8), (6, 1, 2, 14), (10, 2, 2, 64), (9, 3, 1, 21), (12, 4, 2, 40), (7, 1, 1, 1)
+
+
+def _valid_path(states, table, K, tail_biting):
+    shift = K * table.size(1)
+    shared = (table.size(0) >> shift) - 1
+    assert ((states[..., 1:] >> shift) == (states[..., :-1] & shared)).all()
+    assert not tail_biting or ((states[..., 0] >> shift) == (states[..., -1] & shared)).all()
+
+
+def test_golden_vectors():
+    data = np.load(GOLDEN / "trellis.npz")
+    for idx, (L, K, V, T) in enumerate(SHAPES):
+        for dname in ("float32", "float64"):
+            for tb in (0, 1):
+                key = f"s{idx}_{dname[-7:]}_{tb}"
+                print(key, flush=True)
+                table = torch.from_numpy(data[key + "_table"]).to(DEV)
+                x = torch.from_numpy(data[key + "_x"]).to(DEV)
+                vals, st = QT.trellis_quantize_hip(x, table, K, bool(tb))
+                assert np.array_equal(st.cpu().numpy(), data[key + "_states"]), key
+                assert np.array_equal(vals.cpu().numpy(), data[key + "_values"]), key
+                _valid_path(st, table, K, bool(tb))
+    vals, st = QT.trellis_quantize_hip(torch.from_numpy(data["ties_x"]).to(DEV),
+                                       torch.from_numpy(data["ties_table"]).to(DEV), 2, True)
+    assert np.array_equal(st.cpu().numpy(), data["ties_states"])
+    hyb = QT.hyb(device=DEV)
+    for tb in (0, 1):
+        vals, st = QT.trellis_quantize_hip(torch.from_numpy(data[f"hyb16_x_{tb}"]).to(DEV), hyb, 2, bool(tb))
+        assert np.array_equal(st.cpu().numpy(), data[f"hyb16_states_{tb}"])
+        assert np.array_equal(vals.cpu().numpy(), data[f"hyb16_values_{tb}"])
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+def test_against_torch_and_oracle(dtype):
+    """HIP search == this package's PyTorch formulation on the GPU == the CPU oracle, values and states, on fresh
+    sequences of every shape (quantizer_trellis.py:450-479), with leading batch dimensions."""
+    g = torch.Generator().manual_seed(11)
+    for (L, K, V, T), tb in itertools.product(SHAPES, (False, True)):
+        table = torch.randn(1 << L, V, generator=g, dtype=dtype)
+        x = torch.randn(3, 5, T, generator=g, dtype=dtype)
+        vals, st = QT.trellis_quantize_hip(x.to(DEV), table.to(DEV), K, tb)
+        tv, ts = QT.trellis_quantize_torch(x.to(DEV), table.to(DEV), K, tb)
+        ov, os_ = OT.trellis_quantize(x, table, K, tb)
+        assert st.equal(ts) and vals.equal(tv), (L, K, V, T, tb)
+        assert st.cpu().equal(os_) and vals.cpu().equal(ov), (L, K, V, T, tb)
+    table = torch.randint(-3, 4, (1 << 8, 2), generator=g).to(dtype)  # many equal costs
+    x = torch.randint(-3, 4, (40, 64), generator=g).to(dtype)
+    vals, st = QT.trellis_quantize_hip(x.to(DEV), table.to(DEV), 2, True)
+    assert st.cpu().equal(OT.trellis_quantize(x, table, 2, True)[1])
+
+
+def test_codes_and_k():
+    """The real codes at L = 16 with several K, against the oracle (quantizer_trellis.py:474-479)."""
+    g = torch.Generator().manual_seed(12)
+    for code, Ks in (QT.hyb(), (2, 3, 4)), (QT.one_mad(), (2, 4)), (QT.three_inst(), (2,)):
+        for K in Ks:
+            x = torch.randn(6, 256, generator=g)
+            vals, st = QT.trellis_quantize_hip(x.to(DEV), code.to(DEV), K, True)
+            _, os_ = OT.trellis_quantize(x, code, K, True)
+            assert st.cpu().equal(os_), (code.size(1), K)
+            assert vals.cpu().equal(code[os_, :].flatten(start_dim=-2))
+
+
+def test_brute_force():
+    """Without tail-biting the search is optimal over all paths (quantizer_trellis.py:407-417)."""
+    g = torch.Generator().manual_seed(0)
+    for L, K, V, T in (5, 1, 1, 7), (4, 1, 2, 8):
+        table = torch.randn(1 << L, V, generator=g, dtype=torch.float64)
+        x = torch.randn(3, T, generator=g, dtype=torch.float64)
+        vals, _ = QT.trellis_quantize_hip(x.to(DEV), table.to(DEV), K, False)
+        for b in range(3):
+            best = OT.brute_force(x[b], table, K)
+            assert abs((vals[b].cpu() - x[b]).square().sum().item() - best) < 1e-12
+
+
+def test_plugins_equal():
+    """The two plug-ins write the same values for a scale per matrix or per batch (quantizer_trellis.py:482-492)."""
+    g = torch.Generator().manual_seed(5)
+    table = QT.hyb(device=DEV)
+    y_flat = torch.randn(2, 6 * 16 * 16, generator=g).to(DEV)
+    select = lambda t: t.unflatten(-1, (6, 16, 16))
+    for scale in torch.tensor(1.3, device=DEV), torch.tensor([1.3, .7], device=DEV)[:, None, None, None]:
+        expected, out = torch.empty(2, 6, 16, 16, device=DEV), torch.empty(2, 6, 16, 16, device=DEV)
+        QT.trellis_quantizer_super_entry_torch(y_flat, select, scale, out=expected, table=table, K=2)
+        QT.trellis_quantizer_super_entry_hip(y_flat, select, scale, out=out, table=table, K=2)
+        assert out.equal(expected)
+
+
+def test_plugin_graph():
+    """The captured HIP plug-in replays on new inputs and scales, each replay checked against an eager call
+    (quantizer_trellis.py:494-519)."""
+    g = torch.Generator().manual_seed(6)
+    table = QT.hyb(device=DEV)
+    select = lambda t: t.unflatten(-1, (6, 16, 16))
+    y_flat, scale = torch.randn(6 * 16 * 16, generator=g).to(DEV), torch.tensor(1.3, device=DEV)
+    out = torch.empty(6, 16, 16, device=DEV)
+    run = lambda: QT.trellis_quantizer_super_entry_hip(y_flat, select, scale, out=out, table=table, K=2)
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        run()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        run()
+    for factor in (1., 2.5, .5):
+        new_y, new_scale = factor * torch.randn(6 * 16 * 16, generator=g).to(DEV), torch.tensor(.9 * factor, device=DEV)
+        y_flat.copy_(new_y)
+        scale.copy_(new_scale)
+        graph.replay()
+        torch.cuda.synchronize()
+        expected = torch.empty_like(out)
+        QT.trellis_quantizer_super_entry_hip(new_y, select, new_scale, out=expected, table=table, K=2)
+        torch.cuda.synchronize()
+        assert out.equal(expected), factor
+
+
+def _instance(m, n, seed, se):
+    gen = torch.Generator().manual_seed(seed)
+    x = 4. * torch.randn(m, n, generator=gen, dtype=torch.float64)
+    l, u = (.05 * torch.randn(k, k, generator=gen, dtype=torch.float64) for k in (m, n))
+    for f, size, unused in ((l, se[0], torch.ge), (u, se[1], torch.le)):
+        blk = torch.arange(f.size(0)) // size
+        f[unused(blk[None, :], blk[:, None])] = torch.nan
+    return x.to(DEV), l.to(DEV), u.to(DEV)
+
+
+def test_joint_quantizer_in_sweep():
+    """A trellis rounds each 16 x 16 super-entry as one sequence inside GPTQ-2D, also in a graph with new inputs
+    (test_gptq_2d.py:91-111): the sweep equals super-entry Algorithm 3 with the oracle's trellis quantizer."""
+    table = torch.randn(1 << 8, 2, generator=torch.Generator().manual_seed(0), dtype=torch.float64)
+    opts = dict(quantizer=functools.partial(QT.trellis_quantizer_super_entry_hip, table=table.to(DEV), K=2),
+                super_entry_shape=(16, 16))
+
+    def reference(x, l, u, scale):
+        def trellis(y, i, j):
+            out = torch.empty_like(y)
+            OT.trellis_quantizer_super_entry(y, lambda t: t, scale, out=out, table=table, K=2)
+            return out
+
+        lu = S.unit_triangular(l.cpu(), False, 16)
+        uu = S.unit_triangular(u.cpu(), True, 16)
+        return A.alg3_super_entry(x.cpu(), lu, uu, Q=trellis, super_entry_shape=(16, 16)).to(DEV)
+
+    x, l, u = _instance(32, 64, 7, (16, 16))
+    scale = torch.tensor(4., dtype=torch.float64, device=DEV)
+    expected = reference(x, l, u, scale.cpu())
+    for inner, outer in ((0, 0), (1, 0), (1, 2)):
+        got = G.gptq_2d_super_entry(x, l, u, quantizer_inputs=(scale,), inner_block_size=inner,
+                                    outer_block_size=outer, **opts)
+        assert got.equal(expected), (inner, outer)
+    replay = G.capture_gptq_2d(x, l, u, quantizer_inputs=(scale,), **opts)
+    assert replay(x, l, u, scale).equal(expected)
+    assert replay(x + .375, 1.5 * l, .5 * u, 2 * scale).equal(reference(x + .375, 1.5 * l, .5 * u, 2 * scale.cpu()))
