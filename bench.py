@@ -38,6 +38,12 @@ for _p in (str(ROOT / "gptq-2d_amd"), str(ROOT)):
 METRIC = "layer quantize time (s) @8192² INT4; panel MFMA util %; Viterbi weights/s"
 FP32_MFMA_PEAK_TFLOPS = 157.3
 HBM_PEAK_GBS = 8000.0
+# fp32 VALU without packed instructions (which this build does not use): half the published 157.3
+# TFLOP/s vector figure, i.e. 78.6 TFLOP/s of FMA = 39.3e12 single fp32 operations per second.
+VALU_FP32_OPS_PEAK = 39.3e12
+# fp32 VALU operations per trellis state evaluation: 2 sub, 2 mul, 1 add (the squared distance),
+# 1 add (the predecessor group's minimum), 1 min.
+OPS_PER_STATE_EVAL = 7
 
 
 def _parse():
@@ -104,6 +110,37 @@ def _cpu_baseline(cfg, x, a, b, scale, zp, l_dev, u_dev, stages_in_sample):
                    f"{stages} stages on the full {m}x{n} tensors ({t_sample:.1f} s), extrapolated by exact "
                    f"per-stage work to {t_sweep:.1f} s"),
         "extrapolated": True,
+    }
+
+
+def _viterbi_bench(torch, dev, steps_timed=3):
+    """Throughput of the trellis search on the longest antidiagonal of configuration C4: 512 super-entries
+    of 16 x 16 (T = 256) with the HYB code, L = 16, K = 2, V = 2, tail-biting (two passes)."""
+    import quantizer_trellis as QT
+
+    rows, T, L, K, V = 512, 256, 16, 2, 2
+    table = QT.hyb(L=L, device=dev)
+    x = torch.randn(rows, T, generator=torch.Generator().manual_seed(0)).to(dev)
+    out = torch.empty_like(x)
+    scale = torch.ones(rows, device=dev)
+    QT.trellis_quantize_hip(x, table, K, True, out=out, scale=scale)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps_timed):
+        QT.trellis_quantize_hip(x, table, K, True, out=out, scale=scale)
+    e1.record()
+    torch.cuda.synchronize()
+    sec = e0.elapsed_time(e1) / steps_timed / 1e3
+    evals = rows * 2 * (T // V) * (1 << L)  # two passes, every state at every step
+    ops = evals * OPS_PER_STATE_EVAL
+    return {
+        "workload": "C4 longest antidiagonal: 512 sequences of 256 (16x16 super-entries), HYB L=16 K=2 V=2, "
+                    "tail-biting",
+        "weights_per_s": rows * T / sec,
+        "ms_per_call": sec * 1e3,
+        "roofline": {"bound": "valu", "achieved": ops / sec / 1e12, "peak": VALU_FP32_OPS_PEAK / 1e12,
+                     "unit": "Tops/s (fp32, 7 per state evaluation)", "frac": ops / sec / VALU_FP32_OPS_PEAK},
     }
 
 
@@ -221,8 +258,12 @@ def main() -> int:
         },
         "roofline": roofline,
         "viterbi_weights_per_s": None,
+        "viterbi": None,
         "cpu_baseline": None,
     }
+    vit = _viterbi_bench(torch, dev)
+    result["viterbi"] = vit
+    result["viterbi_weights_per_s"] = vit["weights_per_s"]
     if not args.no_cpu:
         result["cpu_baseline"] = _cpu_baseline(cfg, x, a, b, scale, zp, lo, up, args.cpu_stages)
         result["gpu_vs_cpu_speedup"] = result["cpu_baseline"]["value"] / result["value"]
