@@ -237,7 +237,9 @@ int gptq2d_flush(T* y, T* c, const T* e, const T* l, const T* u, int64_t m, int6
   if (B == 0 || s_end == s1) return 0;
   if constexpr (sizeof(T) == 4) {
     // 32 x 32 coarse cells (the fused engine's tiles, or 32 x 32 super-entries): fp32 MFMA
-    if (P == 32 && Q == 32) {
+    // (staging uses 32-bit byte offsets: every operand matrix under 2^31 bytes)
+    const int64_t big = m > n ? m : n;
+    if (P == 32 && Q == 32 && big * big < ((int64_t)1 << 29) - 16) {
       const bool prof = gptq2d_prof_on(PROF_FLUSH);
       if (prof) gptq2d_prof_begin(PROF_FLUSH, stream);
       const int rc = gptq2d_flush_tiles_mfma(y, c, e, l, u, m, n, s0, s1, s_end, lmap, umap, B, stream);

@@ -12,7 +12,7 @@
 // A workgroup owns WT x WT target tiles and four waves, each wave (WT/2) x (WT/2) tiles with one
 // 16-register accumulator per tile.  The K loop walks the union of the tiles' k-tile ranges; each
 // k-tile's panels (A: the WG's rows x 32 of L, then of C; B: 32 x the WG's columns of E, then of U)
-// are prefetched into registers with 128-bit loads one k-tile ahead and stored to LDS, and a wave
+// are prefetched into registers one k-tile ahead and stored to LDS, and a wave
 // issues a tile's 16 MFMAs only when the k-tile lies in that tile's own range -- no MFMA is spent
 // on a masked zero, and tiles that receive nothing are not read or written.  Staging loads are
 // masked to exactly the entries a product may read: L strictly below, U strictly above its
@@ -20,12 +20,15 @@
 //
 // Operand layout (lane l, i = l % 32, h = l / 32): A(i, kslot = h), B(kslot = h, j = i); the 16
 // accumulators hold D(8 (r / 4) + 4 h + r % 4, i).  The k carried by slot h in MFMA s is 16 h + s
-// for both operands, so 16 MFMAs cover the 32-deep k-tile; A is read from LDS as four 128-bit loads
-// of 16 consecutive k, B as 16 conflict-free 32-bit loads along j.
+// for both operands, so 16 MFMAs cover the 32-deep k-tile.
 //
 // Reference counterparts (IST-DASLab/GPTQ-2D, gptq_2d.py): _flush_down_kernel :766-932 and
 // _flush_right_kernel :936-1087 (fp32 `tl.dot` with input_precision="ieee"); one kernel here, with
 // one read-modify-write of Y and C per target tile.
+//
+// LDS: A as [row][k] (k fastest), B k-interleaved as [k / 4][j][k % 4], so that a lane's 16 values
+// of either operand for one k-tile are four 128-bit reads; both panels double-buffered, so one
+// barrier per k-tile; a k-tile's fragments are read before its MFMAs are issued.
 #include "common.h"
 
 namespace {
@@ -51,26 +54,205 @@ __device__ __forceinline__ void tile_range(const TileFlush& g, int phase, int64_
   hi = g.S1 - a < b ? g.S1 - a : b;
 }
 
+// Workgroups of a launch are exactly the (row block, column block) pairs that can hold targets:
+// row block `by` (tile rows WT by ..) spans the column blocks [first, last] below.  Launching no
+// empty workgroups matters: the dispatcher hands workgroups to the XCDs and shader engines in
+// turn, and a stride of empty ones leaves whole engines idle while others queue.
+template <int WT>
+__host__ __device__ inline void row_block_span(const TileFlush& g, int64_t by, int64_t& first, int64_t& count) {
+  const int64_t I0 = by * WT;
+  int64_t jt_lo = g.S1 - (I0 + WT - 1);
+  if (jt_lo < 0) jt_lo = 0;
+  int64_t jt_hi = g.S_end - 1 - I0;  // inclusive
+  if (jt_hi > g.nt - 1) jt_hi = g.nt - 1;
+  // a tile with I, J >= S1 receives nothing (its down range needs J < S1, its right range I < S1)
+  if (I0 >= g.S1 && jt_hi > g.S1 - 1) jt_hi = g.S1 - 1;
+  first = jt_lo / WT;
+  count = (I0 < g.mt && jt_hi >= jt_lo) ? jt_hi / WT - first + 1 : 0;
+}
+
+// Raw buffer resource over one matrix: loads at a byte offset at or beyond `bytes` return zeros
+// without touching memory, which is how every masked staging load is made (no branches).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t matrix_rsrc(const float* base, int64_t elems) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), (short)0, (int)(elems * 4), 0x00020000);
+}
+constexpr int OOB = 0x7ffffff0;  // a byte offset past every matrix the MFMA flush accepts
+
+__device__ __forceinline__ float4 buf_ld4(__amdgpu_buffer_rsrc_t r, int off, bool ok) {
+  return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, ok ? off : OOB, 0, 0));
+}
+__device__ __forceinline__ float buf_ld1(__amdgpu_buffer_rsrc_t r, int off, bool ok) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, ok ? off : OOB, 0, 0));
+}
+
+// One product phase (0: D = L E, 1: R = C U) of a workgroup, accumulated into acc.
+template <int WT, bool VEC, int PHASE>
+__device__ __forceinline__ void flush_phase(floatx16 (&acc)[WT / 2][WT / 2], float* As, float* Bs,
+                                            __amdgpu_buffer_rsrc_t ra_src, __amdgpu_buffer_rsrc_t rb_src,
+                                            const TileFlush& g, int64_t I0, int64_t J0, int wi, int wj,
+                                            int64_t t_lo, int64_t t_hi, const int (&tlo)[WT / 2][WT / 2],
+                                            const int (&thi)[WT / 2][WT / 2]) {
+  constexpr int H = WT / 2;
+  constexpr int ROWS = WT * TS;
+  constexpr int NV = ROWS * TS / 4 / 256;
+  constexpr int ABUF = ROWS * AP;
+  constexpr int BBUF = TS * ROWS;
+  const int tid = threadIdx.x, lane = tid & 63, li = lane & 31, hh = lane >> 5;
+  const int64_t kmax = PHASE == 0 ? g.m : g.n;  // k extent of both operands
+  const int64_t alda = PHASE == 0 ? g.m : g.n;  // row stride of A (L or C)
+
+  // staging geometry: A entry (row ar, k 4 akq..+3), B entries (k 4 bkg..+3, column bjc)
+  int aoff[NV], boff[NV];
+  bool arow_ok[NV], bcol_ok[NV];
+  int arow_t[NV], bcol_t[NV];
+#pragma unroll
+  for (int q = 0; q < NV; ++q) {
+    const int f = tid + 256 * q;
+    const int64_t i = I0 * TS + f / (TS / 4), ka = 4 * (f % (TS / 4));
+    arow_ok[q] = i < g.m;
+    arow_t[q] = (int)(i >> 5);
+    aoff[q] = (int)((arow_ok[q] ? i * alda : 0) + ka) * 4;
+    const int64_t j = J0 * TS + f % ROWS, kb = 4 * (f / ROWS);
+    bcol_ok[q] = j < g.n;
+    bcol_t[q] = (int)(j >> 5);
+    boff[q] = (int)(kb * g.n + (bcol_ok[q] ? j : 0)) * 4;
+  }
+  float4 ra[NV], rb[NV];
+  auto load = [&](int64_t t) {
+    const int64_t k0 = t * TS;
+#pragma unroll
+    for (int q = 0; q < NV; ++q) {
+      const int f = tid + 256 * q;
+      const int64_t ka = k0 + 4 * (f % (TS / 4)), kb = k0 + 4 * (f / ROWS);
+      const int ts = (int)t, s0 = (int)g.S0, s1 = (int)g.S1;
+      const bool aband = PHASE == 0 ? ts < arow_t[q] : (arow_t[q] + ts >= s0 && arow_t[q] + ts < s1);
+      const bool bband = PHASE == 0 ? (ts + bcol_t[q] >= s0 && ts + bcol_t[q] < s1) : ts < bcol_t[q];
+      const bool aok = arow_ok[q] && aband, bok = bcol_ok[q] && bband;
+      const int ao = aoff[q] + (int)k0 * 4, bo = boff[q] + (int)(k0 * g.n) * 4, bs = (int)g.n * 4;
+      if (VEC) {
+        ra[q] = buf_ld4(ra_src, ao, aok && ka < kmax);
+        const bool bk = bok && kb < kmax;
+        rb[q].x = buf_ld1(rb_src, bo, bk);
+        rb[q].y = buf_ld1(rb_src, bo + bs, bk);
+        rb[q].z = buf_ld1(rb_src, bo + 2 * bs, bk);
+        rb[q].w = buf_ld1(rb_src, bo + 3 * bs, bk);
+      } else {
+        ra[q].x = buf_ld1(ra_src, ao, aok && ka < kmax);
+        ra[q].y = buf_ld1(ra_src, ao + 4, aok && ka + 1 < kmax);
+        ra[q].z = buf_ld1(ra_src, ao + 8, aok && ka + 2 < kmax);
+        ra[q].w = buf_ld1(ra_src, ao + 12, aok && ka + 3 < kmax);
+        rb[q].x = buf_ld1(rb_src, bo, bok && kb < kmax);
+        rb[q].y = buf_ld1(rb_src, bo + bs, bok && kb + 1 < kmax);
+        rb[q].z = buf_ld1(rb_src, bo + 2 * bs, bok && kb + 2 < kmax);
+        rb[q].w = buf_ld1(rb_src, bo + 3 * bs, bok && kb + 3 < kmax);
+      }
+    }
+  };
+  auto store = [&](int buf) {
+#pragma unroll
+    for (int q = 0; q < NV; ++q) {
+      const int f = tid + 256 * q;
+      *reinterpret_cast<float4*>(&As[buf * ABUF + (f / (TS / 4)) * AP + 4 * (f % (TS / 4))]) = ra[q];
+      *reinterpret_cast<float4*>(&Bs[buf * BBUF + 4 * f]) = rb[q];
+    }
+  };
+
+  if (t_lo >= t_hi) return;
+  __syncthreads();  // the previous phase's last reads of both buffers are done
+  load(t_lo);
+  store(t_lo & 1);
+  if (t_lo + 1 < t_hi) load(t_lo + 1);
+  for (int64_t t = t_lo; t < t_hi; ++t) {
+    __syncthreads();  // buffer t & 1 is complete; buffer (t + 1) & 1 is no longer read
+    if (t + 1 < t_hi) {
+      store((t + 1) & 1);
+      if (t + 2 < t_hi) load(t + 2);
+    }
+    // tile masks as 32-bit scalar compares, so the MFMA branches are uniform; a step on which all
+    // of the wave's tiles are active (most of them) runs one straight MFMA block
+    const int ts = (int)t;
+    int mask = 0;
+#pragma unroll
+    for (int a = 0; a < H; ++a)
+#pragma unroll
+      for (int d = 0; d < H; ++d) mask |= (ts >= tlo[a][d] && ts < thi[a][d]) << (a * H + d);
+    mask = __builtin_amdgcn_readfirstlane(mask);
+    if (mask == 0) continue;
+    const float* as = As + (t & 1) * ABUF + (wi * TS + li) * AP + 16 * hh;
+    const float* bsrc = Bs + (t & 1) * BBUF + (4 * hh * ROWS + wj * TS + li) * 4;
+    float4 fa[2][H], fb[2][H];
+    auto frag = [&](int v, int slot) {
+#pragma unroll
+      for (int a = 0; a < H; ++a) fa[slot][a] = *reinterpret_cast<const float4*>(as + a * TS * AP + 4 * v);
+#pragma unroll
+      for (int d = 0; d < H; ++d) fb[slot][d] = *reinterpret_cast<const float4*>(bsrc + (v * ROWS + d * TS) * 4);
+    };
+    if (mask == (1 << (H * H)) - 1) {
+      frag(0, 0);
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        if (v < 3) frag(v + 1, (v + 1) & 1);
+#pragma unroll
+        for (int s2 = 0; s2 < 4; ++s2)
+#pragma unroll
+          for (int a = 0; a < H; ++a)
+#pragma unroll
+            for (int d = 0; d < H; ++d)
+              acc[a][d] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[v & 1][a][s2], fb[v & 1][d][s2], acc[a][d], 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    } else {
+      // partial step (first and last steps of a tile's range): tile by tile
+#pragma unroll
+      for (int a = 0; a < H; ++a)
+#pragma unroll
+        for (int d = 0; d < H; ++d)
+          if (mask >> (a * H + d) & 1) {
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+              const float4 xa = *reinterpret_cast<const float4*>(as + a * TS * AP + 4 * v);
+              const float4 xb = *reinterpret_cast<const float4*>(bsrc + (v * ROWS + d * TS) * 4);
+#pragma unroll
+              for (int s2 = 0; s2 < 4; ++s2)
+                acc[a][d] = __builtin_amdgcn_mfma_f32_32x32x2f32(xa[s2], xb[s2], acc[a][d], 0, 0, 0);
+            }
+          }
+    }
+  }
+}
+
 template <int WT, bool VEC>
 __global__ __launch_bounds__(256, 2) void flush_tiles_mfma_kernel(float* __restrict__ y, float* __restrict__ c,
                                                                   const float* __restrict__ e,
                                                                   const float* __restrict__ l,
                                                                   const float* __restrict__ u, TileFlush g,
-                                                                  BatchMap lmap, BatchMap umap, int64_t nx,
-                                                                  int64_t ny) {
-  constexpr int H = WT / 2;               // tiles per wave per direction
-  constexpr int ROWS = WT * TS;           // panel rows (A) / columns (B)
-  constexpr int BPITCH = ROWS + 4;        // LDS pitch of the B panel rows (j fastest)
-  constexpr int NV = ROWS * TS / 4 / 256; // float4 per thread per panel
-  __shared__ __align__(16) float As[ROWS * AP];
-  __shared__ __align__(16) float Bs[TS * BPITCH];
+                                                                  BatchMap lmap, BatchMap umap, int64_t b0) {
+  constexpr int H = WT / 2;        // tiles per wave per direction
+  constexpr int ROWS = WT * TS;    // panel rows (A) / columns (B)
+  __shared__ __align__(16) float As[2 * ROWS * AP];  // A panel: [row][k], k fastest, pitch AP
+  __shared__ __align__(16) float Bs[2 * TS * ROWS];  // B panel: [k / 4][j][k % 4]
 
-  const GridIds id = grid_ids(nx, ny);
-  const int64_t b = id.b;
-  const int64_t I0 = id.y * WT;
-  int64_t jt_lo = g.S1 - (I0 + WT - 1);
-  if (jt_lo < 0) jt_lo = 0;
-  const int64_t J0 = (jt_lo / WT + id.x) * WT;
+  // XCD-aware order: the hardware deals workgroup w to XCD w % 8; runs of XG consecutive work items
+  // (neighbouring column blocks of a row block, which share L / C rows) go to one XCD and its L2,
+  // and the XCDs take turns run by run, so that all of them see the same mix of item sizes
+  constexpr int64_t XG = 16;
+  const int64_t nwg = gridDim.x, w = blockIdx.x;
+  const int64_t full = nwg / (8 * XG) * (8 * XG);
+  int64_t item = w;
+  if (w < full) {
+    const int64_t within = w % (8 * XG);
+    item = w - within + (within % 8) * XG + within / 8;
+  }
+  const int64_t b = b0 + blockIdx.y;
+  int64_t by = 0, first = 0, count = 0;
+  for (; by * WT < g.mt; ++by) {
+    row_block_span<WT>(g, by, first, count);
+    if (item < count) break;
+    item -= count;
+  }
+  if (by * WT >= g.mt) return;
+  const int64_t I0 = by * WT;
+  const int64_t J0 = (first + item) * WT;
   if (J0 >= g.nt || I0 + J0 >= g.S_end || I0 + J0 + 2 * WT - 2 < g.S1) return;
 
   // workgroup-wide k ranges; nothing to do -> no memory touched
@@ -93,26 +275,26 @@ __global__ __launch_bounds__(256, 2) void flush_tiles_mfma_kernel(float* __restr
     }
   if (lo0 >= hi0 && lo1 >= hi1) return;
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: keeps the tile masks scalar
   const int li = lane & 31, hh = lane >> 5;
   const int wi = (wave >> 1) * H, wj = (wave & 1) * H;  // wave's first tile, relative to (I0, J0)
   const int64_t mat = b * g.m * g.n;
-  const float* lb = l + lmap.offset(b);
-  const float* ub = u + umap.offset(b);
 
-  // per-tile k ranges of this wave (uniform)
-  int64_t tlo[2][H][H], thi[2][H][H];
-  bool tgt[H][H];
+  // per-tile k ranges of this wave (uniform); an empty range for tiles that are not targets
+  int tlo[2][H][H], thi[2][H][H];
 #pragma unroll
   for (int a = 0; a < H; ++a)
 #pragma unroll
     for (int d = 0; d < H; ++d) {
       const int64_t I = I0 + wi + a, J = J0 + wj + d;
-      tgt[a][d] = is_target(g, I, J);
+      const bool tgt = is_target(g, I, J);
 #pragma unroll
       for (int p = 0; p < 2; ++p) {
-        tile_range(g, p, I, J, tlo[p][a][d], thi[p][a][d]);
-        if (!tgt[a][d]) thi[p][a][d] = tlo[p][a][d];
+        int64_t lo, hi;
+        tile_range(g, p, I, J, lo, hi);
+        tlo[p][a][d] = (int)lo;
+        thi[p][a][d] = tgt ? (int)hi : (int)lo;
       }
     }
 
@@ -124,127 +306,37 @@ __global__ __launch_bounds__(256, 2) void flush_tiles_mfma_kernel(float* __restr
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[a][d][r] = 0.f;
 
-  float4 ra[NV], rb[NV];
-
+  // phase 0: D = L E, then C += D; phase 1: R = C U on top of D, then Y += D + R
+  const __amdgpu_buffer_rsrc_t rl = matrix_rsrc(l + lmap.offset(b), g.m * g.m);
+  const __amdgpu_buffer_rsrc_t re = matrix_rsrc(e + mat, g.m * g.n);
+  const __amdgpu_buffer_rsrc_t rc = matrix_rsrc(c + mat, g.m * g.n);
+  const __amdgpu_buffer_rsrc_t ru = matrix_rsrc(u + umap.offset(b), g.n * g.n);
+  flush_phase<WT, VEC, 0>(acc, As, Bs, rl, re, g, I0, J0, wi, wj, lo0, hi0, tlo[0], thi[0]);
 #pragma unroll
-  for (int phase = 0; phase < 2; ++phase) {
-    const int64_t t_lo = phase == 0 ? lo0 : lo1, t_hi = phase == 0 ? hi0 : hi1;
-    // A source: L (phase 0) or C (phase 1), rows of the WG, row-major with k fastest
-    const float* abase = phase == 0 ? lb : c + mat;
-    const int64_t alda = phase == 0 ? g.m : g.n;   // row stride of A
-    const int64_t akmax = phase == 0 ? g.m : g.n;  // k extent of A
-    // B source: E (phase 0) or U (phase 1), row-major with j fastest
-    const float* bbase = phase == 0 ? e + mat : ub;
-    const int64_t bkmax = phase == 0 ? g.m : g.n;  // k extent of B
-
-    auto stage = [&](int64_t t) {
-      const int64_t k0 = t * TS;
-#pragma unroll
-      for (int q = 0; q < NV; ++q) {
-        const int f = tid + 256 * q;
-        // A: row r, k = 4 kq .. 4 kq + 3
-        {
-          const int r = f / (TS / 4), kq = f % (TS / 4);
-          const int64_t i = I0 * TS + r, k = k0 + 4 * kq;
-          const int64_t ti = i >> 5;
-          const bool ok = i < g.m && (phase == 0 ? t < ti : (ti + t >= g.S0 && ti + t < g.S1));
-          const float* src = abase + i * alda + k;
-          float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-          if (VEC) {
-            if (ok && k < akmax) v = *reinterpret_cast<const float4*>(src);
-          } else if (ok) {
-            v.x = k < akmax ? src[0] : 0.f;
-            v.y = k + 1 < akmax ? src[1] : 0.f;
-            v.z = k + 2 < akmax ? src[2] : 0.f;
-            v.w = k + 3 < akmax ? src[3] : 0.f;
-          }
-          ra[q] = v;
-        }
-        // B: row kk, j = 4 cq .. 4 cq + 3 (one tile column per 8 float4)
-        {
-          const int kk = f / (ROWS / 4), cq = f % (ROWS / 4);
-          const int64_t k = k0 + kk, j = J0 * TS + 4 * cq;
-          const int64_t tj = j >> 5;
-          const bool ok = k < bkmax && (phase == 0 ? (t + tj >= g.S0 && t + tj < g.S1) : t < tj);
-          const float* src = bbase + k * g.n + j;
-          float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-          if (VEC) {
-            if (ok && j < g.n) v = *reinterpret_cast<const float4*>(src);
-          } else if (ok) {
-            v.x = j < g.n ? src[0] : 0.f;
-            v.y = j + 1 < g.n ? src[1] : 0.f;
-            v.z = j + 2 < g.n ? src[2] : 0.f;
-            v.w = j + 3 < g.n ? src[3] : 0.f;
-          }
-          rb[q] = v;
-        }
-      }
-    };
-
-    if (t_lo < t_hi) stage(t_lo);
-    for (int64_t t = t_lo; t < t_hi; ++t) {
-      __syncthreads();
-#pragma unroll
-      for (int q = 0; q < NV; ++q) {
-        const int f = tid + 256 * q;
-        const int r = f / (TS / 4), kq = f % (TS / 4);
-        *reinterpret_cast<float4*>(&As[r * AP + 4 * kq]) = ra[q];
-        const int kk = f / (ROWS / 4), cq = f % (ROWS / 4);
-        *reinterpret_cast<float4*>(&Bs[kk * BPITCH + 4 * cq]) = rb[q];
-      }
-      __syncthreads();
-      if (t + 1 < t_hi) stage(t + 1);
-
-      bool ok[H][H];
-      bool any = false;
-#pragma unroll
-      for (int a = 0; a < H; ++a)
-#pragma unroll
-        for (int d = 0; d < H; ++d) {
-          ok[a][d] = t >= tlo[phase][a][d] && t < thi[phase][a][d];
-          any |= ok[a][d];
-        }
-      if (!any) continue;
-      float4 af[H][4];
-#pragma unroll
-      for (int a = 0; a < H; ++a) {
-        const float* src = &As[((wi + a) * TS + li) * AP + 16 * hh];
-#pragma unroll
-        for (int v = 0; v < 4; ++v) af[a][v] = *reinterpret_cast<const float4*>(src + 4 * v);
-      }
-      const float* bsrc = &Bs[(16 * hh) * BPITCH + wj * TS + li];
-#pragma unroll
-      for (int s = 0; s < 16; ++s) {
-        float bf[H];
-#pragma unroll
-        for (int d = 0; d < H; ++d) bf[d] = bsrc[s * BPITCH + d * TS];
-#pragma unroll
-        for (int a = 0; a < H; ++a)
-#pragma unroll
-          for (int d = 0; d < H; ++d)
-            if (ok[a][d]) acc[a][d] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[a][s >> 2][s & 3], bf[d], acc[a][d], 0,
-                                                                           0, 0);
-      }
-    }
-
+  for (int ph = 0; ph < 2; ++ph) {
+    if (ph == 1) flush_phase<WT, VEC, 1>(acc, As, Bs, rc, ru, g, I0, J0, wi, wj, lo1, hi1, tlo[1], thi[1]);
     // epilogue of the phase: C += D after the down products, Y += D + R after the right ones
 #pragma unroll
     for (int a = 0; a < H; ++a)
 #pragma unroll
       for (int d = 0; d < H; ++d) {
-        const bool has = phase == 0 ? tlo[0][a][d] < thi[0][a][d]
-                                    : (tlo[0][a][d] < thi[0][a][d] || tlo[1][a][d] < thi[1][a][d]);
+        const bool has = ph == 0 ? tlo[0][a][d] < thi[0][a][d]
+                                 : (tlo[0][a][d] < thi[0][a][d] || tlo[1][a][d] < thi[1][a][d]);
         if (!has) continue;
         const int64_t I = I0 + wi + a, J = J0 + wj + d;
-        float* dst = (phase == 0 ? c : y) + mat;
+        const __amdgpu_buffer_rsrc_t rd = ph == 0 ? rc : matrix_rsrc(y + mat, g.m * g.n);
+        // all 16 reads in flight before the first write; masked lanes address past the matrix
+        int off[16];
+        float cur[16];
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int64_t i = I * TS + 8 * (r >> 2) + 4 * hh + (r & 3), j = J * TS + li;
-          if (i < g.m && j < g.n) {
-            const int64_t off = i * g.n + j;
-            dst[off] = dst[off] + acc[a][d][r];
-          }
+          off[r] = (i < g.m && j < g.n) ? (int)(i * g.n + j) * 4 : OOB;
+          cur[r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rd, off[r], 0, 0));
         }
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, cur[r] + acc[a][d][r]), rd, off[r], 0, 0);
       }
   }
 }
@@ -252,29 +344,25 @@ __global__ __launch_bounds__(256, 2) void flush_tiles_mfma_kernel(float* __restr
 template <int WT>
 int launch(float* y, float* c, const float* e, const float* l, const float* u, const TileFlush& g,
            const BatchMap& lmap, const BatchMap& umap, int64_t B, hipStream_t stream) {
-  // block rows with targets, and the widest block-column range over them
   const int64_t rows_hi = g.S_end < g.mt ? g.S_end : g.mt;
-  const int64_t nby = cdiv(rows_hi, WT);
-  int64_t nbx = 0;
-  for (int64_t by = 0; by < nby; ++by) {
-    const int64_t I0 = by * WT;
-    int64_t jt_lo = g.S1 - (I0 + WT - 1);
-    if (jt_lo < 0) jt_lo = 0;
-    int64_t jt_hi = g.S_end - 1 - I0;  // inclusive
-    if (jt_hi > g.nt - 1) jt_hi = g.nt - 1;
-    if (jt_hi < jt_lo) continue;
-    const int64_t cnt = jt_hi / WT - jt_lo / WT + 1;
-    if (cnt > nbx) nbx = cnt;
+  int64_t items = 0;
+  for (int64_t by = 0; by * WT < rows_hi; ++by) {
+    int64_t first, count;
+    row_block_span<WT>(g, by, first, count);
+    items += count;
   }
-  if (nbx == 0) return 0;
-  Grid3 gr = make_grid(nbx, nby, B);
+  if (items == 0 || B == 0) return 0;
+  if (items > 0x7fffffff) return GPTQ2D_EUNSUPPORTED;
   const bool vec = g.m % 4 == 0 && g.n % 4 == 0;
-  if (vec)
-    hipLaunchKernelGGL((flush_tiles_mfma_kernel<WT, true>), gr.grid, dim3(256), 0, stream, y, c, e, l, u, g, lmap,
-                       umap, gr.nx, gr.ny);
-  else
-    hipLaunchKernelGGL((flush_tiles_mfma_kernel<WT, false>), gr.grid, dim3(256), 0, stream, y, c, e, l, u, g, lmap,
-                       umap, gr.nx, gr.ny);
+  for (int64_t b0 = 0; b0 < B; b0 += 65535) {
+    const dim3 grid((unsigned)items, (unsigned)(B - b0 < 65535 ? B - b0 : 65535));
+    if (vec)
+      hipLaunchKernelGGL((flush_tiles_mfma_kernel<WT, true>), grid, dim3(256), 0, stream, y, c, e, l, u, g, lmap,
+                         umap, b0);
+    else
+      hipLaunchKernelGGL((flush_tiles_mfma_kernel<WT, false>), grid, dim3(256), 0, stream, y, c, e, l, u, g, lmap,
+                         umap, b0);
+  }
   return (int)hipGetLastError();
 }
 
