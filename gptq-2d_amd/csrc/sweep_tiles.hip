@@ -215,87 +215,28 @@ __device__ __forceinline__ void pull_product(floatx16& acc, const float* __restr
 // antidiagonal into one bank.
 constexpr int SP = 40;
 
-// One tile (I, J) of coarse stage T = I + J inside the outer block that starts at tile stage S0.
-//  1. Pull, on MFMA: the feedback of the tiles of this outer block swept before T, which no flush
-//     has delivered yet -- D = sum L[I,t] E[t,J] over t in [max(0, S0-J), I) and
-//     R = sum C[I,t] U[t,J] over t in [max(0, S0-I), J) -- the four waves taking every fourth
-//     k-tile and reducing through LDS.  Operands go straight from global memory into the MFMA
-//     layout (lane l: A(l%32, 16 (l/32) + s), B(16 (l/32) + s, l%32)).  Then C += D, Y += D + R.
-//  2. The tile's 63 antidiagonals in LDS, 8 lanes per row: each lane reads its 4 terms of the
-//     in-tile down and right feedback of its row's entry on the antidiagonal, and that entry's Y,
-//     C and quantizer inputs, all at once; the 8 partial sums meet through DPP; all 8 lanes round
-//     and one writes Y, E and C back; one barrier per antidiagonal.
-template <bool VEC, int KIND>
-__global__ __launch_bounds__(NTHREADS) void tile_pull_sweep_kernel(float* __restrict__ y, float* __restrict__ c,
-                                                                   float* __restrict__ e,
-                                                                   const float* __restrict__ l,
-                                                                   const float* __restrict__ u, int64_t m, int64_t n,
-                                                                   int64_t stage, int64_t S0, int64_t tile_lo,
-                                                                   BatchMap lmap, BatchMap umap, QSpec<float> qs,
-                                                                   int64_t nx, int64_t ny) {
-  __shared__ float red[4][2][TR][TR + 1];
-  __shared__ float Ys[TR][SP];
-  __shared__ float Cs[TR][SP];
-  __shared__ float Es[TR][SP];
-  __shared__ float Ls[TR][SP];
-  __shared__ float Us[TR][SP];
-  __shared__ float Ss[TR][SP];
-  __shared__ float Zs[TR][SP];
+// LDS image of one tile for the fp32 in-tile sweep: Y, C, E, the diagonal blocks L[I,I] (strictly
+// lower part) and U[J,J] (strictly upper part), and the quantizer inputs.
+struct TileLds {
+  float Ys[TR][SP];
+  float Cs[TR][SP];
+  float Es[TR][SP];
+  float Ls[TR][SP];
+  float Us[TR][SP];
+  float Ss[TR][SP];
+  float Zs[TR][SP];
+};
 
-  const GridIds id = grid_ids(nx, ny);
-  const int64_t b = id.b;
-  const int64_t I = tile_lo + id.x, J = stage - I;
-  const int64_t i0 = I * TR, j0 = J * TR;
-  const int64_t mat = b * m * n;
-  const float* lb = l + lmap.offset(b);
-  const float* ub = u + umap.offset(b);
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int li = lane & 31, hh = lane >> 5;
-
-  // ---- 1. pull
-  const int64_t dlo = S0 - J > 0 ? S0 - J : 0, rlo = S0 - I > 0 ? S0 - I : 0;
-  const bool any = dlo < I || rlo < J;
-  if (any) {
-    floatx16 accd, accr;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) accd[r] = accr[r] = 0.f;
-    pull_product<VEC>(accd, lb, m, m, m, e + mat, n, m, n, i0, j0, dlo, I, wave, li, hh);
-    pull_product<VEC>(accr, c + mat, n, m, n, ub, n, n, n, i0, j0, rlo, J, wave, li, hh);
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int row = 8 * (r >> 2) + 4 * hh + (r & 3);
-      red[wave][0][row][li] = accd[r];
-      red[wave][1][row][li] = accr[r];
-    }
-  }
-  __syncthreads();
-
-  // ---- load the tile
-  for (int t = tid; t < TR * TR; t += NTHREADS) {
-    const int r = t / TR, cc = t % TR;
-    const int64_t gi = i0 + r, gj = j0 + cc;
-    const bool in = gi < m && gj < n;
-    const int64_t off = mat + gi * n + gj;
-    float dd = 0.f, rr = 0.f;
-    if (any) {
-      dd = (red[0][0][r][cc] + red[1][0][r][cc]) + (red[2][0][r][cc] + red[3][0][r][cc]);
-      rr = (red[0][1][r][cc] + red[1][1][r][cc]) + (red[2][1][r][cc] + red[3][1][r][cc]);
-    }
-    Ys[r][cc] = in ? y[off] + (dd + rr) : 0.f;
-    Cs[r][cc] = in ? c[off] + dd : 0.f;
-    Es[r][cc] = 0.f;
-    Ls[r][cc] = (cc < r && gi < m) ? lb[gi * m + (i0 + cc)] : 0.f;
-    Us[r][cc] = (r < cc && j0 + cc < n) ? ub[(j0 + r) * n + (j0 + cc)] : 0.f;
-    if constexpr (KIND == Q_AFFINE) {
-      Ss[r][cc] = in ? qs.scale[qs.smap.offset(b) + gi * n + gj] : 1.f;
-      Zs[r][cc] = in ? qs.zp[qs.zmap.offset(b) + gi * n + gj] : 0.f;
-    } else if constexpr (KIND == Q_FORCED) {
-      Ss[r][cc] = in ? qs.scale[qs.smap.offset(b) + gi * n + gj] : 0.f;
-    }
-  }
-  __syncthreads();
-
-  // ---- 2. in-tile sweep
+// The tile's 63 antidiagonals in LDS, 8 lanes per row: each lane reads its 4 terms of the in-tile
+// down and right feedback of its row's entry on the antidiagonal, and that entry's Y, C and
+// quantizer inputs, all at once; the 8 partial sums meet through DPP; all 8 lanes round and one
+// writes Y, E and C back; one barrier per antidiagonal.  Then Y, C and E of the tile go to global
+// memory.  Expects the tile image complete in LDS (a barrier after it was written).
+template <int KIND>
+__device__ __forceinline__ void sweep_tile_lds(TileLds& tl, float* __restrict__ y, float* __restrict__ c,
+                                               float* __restrict__ e, const QSpec<float>& qs, int64_t m, int64_t n,
+                                               int64_t i0, int64_t j0, int64_t mat) {
+  const int tid = threadIdx.x;
   const int r = tid / PARTS, part = tid % PARTS;
   const int64_t gi = i0 + r;
   const int rows_in = m - i0 < TR ? (int)(m - i0) : TR;  // tile rows / columns inside the matrix
@@ -303,8 +244,9 @@ __global__ __launch_bounds__(NTHREADS) void tile_pull_sweep_kernel(float* __rest
   const bool row_in = r < rows_in;
   float lrow[TR / PARTS];
 #pragma unroll
-  for (int k = 0; k < TR / PARTS; ++k) lrow[k] = part + PARTS * k < r ? Ls[r][part + PARTS * k] : 0.f;
+  for (int k = 0; k < TR / PARTS; ++k) lrow[k] = part + PARTS * k < r ? tl.Ls[r][part + PARTS * k] : 0.f;
   float* ypre_row = qs.ypre ? qs.ypre + mat + gi * n + j0 : nullptr;
+#pragma unroll 1
   for (int t = 0; t < 2 * TR - 1; ++t) {
     const int cc = t - r;
     const bool active = row_in && cc >= 0 && cc < cols_in;
@@ -313,17 +255,17 @@ __global__ __launch_bounds__(NTHREADS) void tile_pull_sweep_kernel(float* __rest
 #pragma unroll
     for (int k = 0; k < TR / PARTS; ++k) {
       const int rr = part + PARTS * k;
-      ev[k] = Es[rr][ccs];
-      uv[k] = Us[rr][ccs];
-      cv[k] = Cs[r][rr];
+      ev[k] = tl.Es[rr][ccs];
+      uv[k] = tl.Us[rr][ccs];
+      cv[k] = tl.Cs[r][rr];
     }
-    const float y0 = Ys[r][ccs], c0 = Cs[r][ccs];
+    const float y0 = tl.Ys[r][ccs], c0 = tl.Cs[r][ccs];
     float sv = 0.f, zv = 0.f;
     if constexpr (KIND == Q_AFFINE) {
-      sv = Ss[r][ccs];
-      zv = Zs[r][ccs];
+      sv = tl.Ss[r][ccs];
+      zv = tl.Zs[r][ccs];
     } else if constexpr (KIND == Q_FORCED) {
-      sv = Ss[r][ccs];
+      sv = tl.Ss[r][ccs];
     }
     float down = 0.f, right = 0.f;
 #pragma unroll
@@ -337,9 +279,9 @@ __global__ __launch_bounds__(NTHREADS) void tile_pull_sweep_kernel(float* __rest
     const float z = quantize_entry<KIND>(yv, sv, zv, qs.qmin, qs.qmax);
     const float evn = z - yv;
     if (active && part == 0) {
-      Ys[r][cc] = z;
-      Es[r][cc] = evn;
-      Cs[r][cc] = (c0 + down) + evn;
+      tl.Ys[r][cc] = z;
+      tl.Es[r][cc] = evn;
+      tl.Cs[r][cc] = (c0 + down) + evn;
       if (ypre_row) ypre_row[cc] = yv;
     }
     __syncthreads();
@@ -350,11 +292,132 @@ __global__ __launch_bounds__(NTHREADS) void tile_pull_sweep_kernel(float* __rest
     const int64_t gi2 = i0 + rr, gj = j0 + cc;
     if (gi2 < m && gj < n) {
       const int64_t off = mat + gi2 * n + gj;
-      y[off] = Ys[rr][cc];
-      c[off] = Cs[rr][cc];
-      e[off] = Es[rr][cc];
+      y[off] = tl.Ys[rr][cc];
+      c[off] = tl.Cs[rr][cc];
+      e[off] = tl.Es[rr][cc];
     }
   }
+}
+
+// Own tile data of the fp32 kernels, read before the tile's feedback is complete (it does not
+// depend on it): entry q of this thread is (t / TR, t % TR) with t = threadIdx.x + NTHREADS q.
+template <int KIND>
+struct TileRegs {
+  static constexpr int NQ = TR * TR / NTHREADS;
+  float y[NQ], c[NQ], l[NQ], u[NQ], s[NQ], z[NQ];
+
+  __device__ __forceinline__ void load(const float* __restrict__ yg, const float* __restrict__ cg,
+                                       const float* __restrict__ lb, const float* __restrict__ ub,
+                                       const QSpec<float>& qs, int64_t b, int64_t m, int64_t n, int64_t i0,
+                                       int64_t j0, int64_t mat) {
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      const int t = threadIdx.x + NTHREADS * q;
+      const int r = t / TR, cc = t % TR;
+      const int64_t gi = i0 + r, gj = j0 + cc;
+      const bool in = gi < m && gj < n;
+      const int64_t off = mat + gi * n + gj;
+      y[q] = in ? yg[off] : 0.f;
+      c[q] = in ? cg[off] : 0.f;
+      // L[i0+r, i0+cc] strictly below the diagonal; U[j0+r, j0+cc] strictly above it
+      l[q] = (cc < r && gi < m) ? lb[gi * m + (i0 + cc)] : 0.f;
+      u[q] = (r < cc && j0 + cc < n) ? ub[(j0 + r) * n + (j0 + cc)] : 0.f;
+      if constexpr (KIND == Q_AFFINE) {
+        s[q] = in ? qs.scale[qs.smap.offset(b) + gi * n + gj] : 1.f;
+        z[q] = in ? qs.zp[qs.zmap.offset(b) + gi * n + gj] : 0.f;
+      } else if constexpr (KIND == Q_FORCED) {
+        s[q] = in ? qs.scale[qs.smap.offset(b) + gi * n + gj] : 0.f;
+      }
+    }
+  }
+
+  // LDS image of the tile with the pulled feedback D (down) and R (right) added: C + D, Y + (D + R).
+  // red holds the four waves' partial products (summed in a fixed order) when `pulled`.
+  __device__ __forceinline__ void store(TileLds& tl, const float (*red)[2][TR][TR + 1], bool pulled) const {
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      const int t = threadIdx.x + NTHREADS * q;
+      const int r = t / TR, cc = t % TR;
+      float dd = 0.f, rr = 0.f;
+      if (pulled) {
+        dd = (red[0][0][r][cc] + red[1][0][r][cc]) + (red[2][0][r][cc] + red[3][0][r][cc]);
+        rr = (red[0][1][r][cc] + red[1][1][r][cc]) + (red[2][1][r][cc] + red[3][1][r][cc]);
+      }
+      tl.Ys[r][cc] = y[q] + (dd + rr);
+      tl.Cs[r][cc] = c[q] + dd;
+      tl.Es[r][cc] = 0.f;
+      tl.Ls[r][cc] = l[q];
+      tl.Us[r][cc] = u[q];
+      if constexpr (KIND != Q_ROUND) tl.Ss[r][cc] = s[q];
+      if constexpr (KIND == Q_AFFINE) tl.Zs[r][cc] = z[q];
+    }
+  }
+};
+
+// Partial products of the four waves into red (layout of the 32 x 32 MFMA accumulator).
+__device__ __forceinline__ void stash_partials(float (*red)[2][TR][TR + 1], const floatx16& accd,
+                                               const floatx16& accr) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, li = lane & 31, hh = lane >> 5;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int row = 8 * (r >> 2) + 4 * hh + (r & 3);
+    red[wave][0][row][li] = accd[r];
+    red[wave][1][row][li] = accr[r];
+  }
+}
+
+// One tile (I, J) of coarse stage T = I + J inside the outer block that starts at tile stage S0,
+// one launch per coarse stage.
+//  1. Pull, on MFMA: the feedback of the tiles of this outer block swept before T, which no flush
+//     has delivered yet -- D = sum L[I,t] E[t,J] over t in [max(0, S0-J), I) and
+//     R = sum C[I,t] U[t,J] over t in [max(0, S0-I), J) -- the four waves taking every fourth
+//     k-tile and reducing through LDS.  Operands go straight from global memory into the MFMA
+//     layout (lane l: A(l%32, 16 (l/32) + s), B(16 (l/32) + s, l%32)).  Then C += D, Y += D + R.
+//  2. The tile's 63 antidiagonals in LDS (sweep_tile_lds).
+template <bool VEC, int KIND>
+__global__ __launch_bounds__(NTHREADS) void tile_pull_sweep_kernel(float* __restrict__ y, float* __restrict__ c,
+                                                                   float* __restrict__ e,
+                                                                   const float* __restrict__ l,
+                                                                   const float* __restrict__ u, int64_t m, int64_t n,
+                                                                   int64_t stage, int64_t S0, int64_t tile_lo,
+                                                                   BatchMap lmap, BatchMap umap, QSpec<float> qs,
+                                                                   int64_t nx, int64_t ny) {
+  __shared__ float red[4][2][TR][TR + 1];
+  __shared__ TileLds tl;
+
+  const GridIds id = grid_ids(nx, ny);
+  const int64_t b = id.b;
+  const int64_t I = tile_lo + id.x, J = stage - I;
+  const int64_t i0 = I * TR, j0 = J * TR;
+  const int64_t mat = b * m * n;
+  const float* lb = l + lmap.offset(b);
+  const float* ub = u + umap.offset(b);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int li = lane & 31, hh = lane >> 5;
+
+  // own tile data first: it does not depend on the pull, so its loads overlap the pull's
+  TileRegs<KIND> own;
+  own.load(y, c, lb, ub, qs, b, m, n, i0, j0, mat);
+
+  // ---- 1. pull
+  const int64_t dlo = S0 - J > 0 ? S0 - J : 0, rlo = S0 - I > 0 ? S0 - I : 0;
+  const bool any = dlo < I || rlo < J;
+  if (any) {
+    floatx16 accd, accr;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) accd[r] = accr[r] = 0.f;
+    pull_product<VEC>(accd, lb, m, m, m, e + mat, n, m, n, i0, j0, dlo, I, wave, li, hh);
+    pull_product<VEC>(accr, c + mat, n, m, n, ub, n, n, n, i0, j0, rlo, J, wave, li, hh);
+    stash_partials(red, accd, accr);
+  }
+  __syncthreads();
+
+  // ---- the tile image in LDS
+  own.store(tl, red, any);
+  __syncthreads();
+
+  // ---- 2. in-tile sweep
+  sweep_tile_lds<KIND>(tl, y, c, e, qs, m, n, i0, j0, mat);
 }
 
 template <bool VEC>
@@ -370,6 +433,14 @@ void launch_tile_pull(int32_t kind, dim3 grid, hipStream_t stream, float* y, flo
   else
     hipLaunchKernelGGL((tile_pull_sweep_kernel<VEC, Q_ROUND>), grid, dim3(NTHREADS), 0, stream, y, c, e, l, u, m, n,
                        st, S0, lo, lmap, umap, qs, nx, ny);
+}
+
+bool aligned16(const void* p) { return p == nullptr || ((uintptr_t)p & 15) == 0; }
+
+bool strides_mult4(const BatchMap& bm) {
+  for (int d = 0; d < bm.nd; ++d)
+    if (bm.stride[d] % 4) return false;
+  return true;
 }
 
 template <typename T>
@@ -398,6 +469,9 @@ int sweep_fused(T* y, T* c, T* e, const T* l, const T* u, int64_t m, int64_t n, 
   if (stage_begin < 0 || stage_begin > stage_end || stage_begin % outer_tiles) return GPTQ2D_EINVAL;
   int rc;
   if (stage_begin == 0 && (rc = gptq2d_fill<T>(c, T(0), B * m * n, stream))) return rc;
+  // 128-bit operand loads of the MFMA pull: rows, matrices and pointers 16-byte aligned
+  const bool vec = m % 4 == 0 && n % 4 == 0 && aligned16(y) && aligned16(c) && aligned16(e) && aligned16(l) &&
+                   aligned16(u) && strides_mult4(lmap) && strides_mult4(umap);
   for (int64_t S0 = stage_begin; S0 < stage_end; S0 += outer_tiles) {
     const int64_t S1 = S0 + outer_tiles < stages ? S0 + outer_tiles : stages;
     for (int64_t st = S0; st < S1; ++st) {
@@ -408,7 +482,7 @@ int sweep_fused(T* y, T* c, T* e, const T* l, const T* u, int64_t m, int64_t n, 
       if (prof) gptq2d_prof_begin(PROF_TILE_SWEEP, stream);
       if constexpr (sizeof(T) == 4) {
         // fp32: every tile pulls the feedback of this outer block's earlier tile stages itself
-        if (m % 4 == 0 && n % 4 == 0)
+        if (vec)
           launch_tile_pull<true>(qkind, g.grid, stream, y, c, e, l, u, m, n, st, S0, lo, lmap, umap, qs, g.nx, g.ny);
         else
           launch_tile_pull<false>(qkind, g.grid, stream, y, c, e, l, u, m, n, st, S0, lo, lmap, umap, qs, g.nx, g.ny);
