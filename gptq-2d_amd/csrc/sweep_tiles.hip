@@ -215,78 +215,139 @@ __device__ __forceinline__ void pull_product(floatx16& acc, const float* __restr
 // antidiagonal into one bank.
 constexpr int SP = 40;
 
-// LDS image of one tile for the fp32 in-tile sweep: Y, C, E, the diagonal blocks L[I,I] (strictly
-// lower part) and U[J,J] (strictly upper part), and the quantizer inputs.
+// LDS image of one tile for the fp32 in-tile sweep.  L[I,I] and U[J,J] are stored with zero
+// padding so that the sweep reads them at any offset in [-TR, 2 TR) without masks:
+// Lp[r][TR + k] = L[i0+r, i0+k] for 0 <= k < r (zero elsewhere), Up[TR + k][c] = U[j0+k, j0+c] for
+// k < c (zero elsewhere).  Ys, Cs, Ss, Zs: the tile's Y (feedback pulled in), C, quantizer inputs
+// on entry; Ys, Cs, Es the result.  Ed / Cr: errors (by column) and C (by row) of the entries
+// rounded on the current antidiagonal, double-buffered by its parity.
+constexpr int LPW = 3 * TR + 1;
+constexpr int UPW = TR + 1;
+
 struct TileLds {
+  float Lp[TR][LPW];
+  float Up[3 * TR][UPW];
   float Ys[TR][SP];
   float Cs[TR][SP];
   float Es[TR][SP];
-  float Ls[TR][SP];
-  float Us[TR][SP];
   float Ss[TR][SP];
   float Zs[TR][SP];
+  float Ed[2][TR];
+  float Cr[2][TR];
 };
 
-// The tile's 63 antidiagonals in LDS, 8 lanes per row: each lane reads its 4 terms of the in-tile
-// down and right feedback of its row's entry on the antidiagonal, and that entry's Y, C and
-// quantizer inputs, all at once; the 8 partial sums meet through DPP; all 8 lanes round and one
-// writes Y, E and C back; one barrier per antidiagonal.  Then Y, C and E of the tile go to global
-// memory.  Expects the tile image complete in LDS (a barrier after it was written).
+// Affine / round / forced quantizer of the in-tile sweep, given the precomputed correctly rounded
+// reciprocal rv = 1/sv and whether sv lies in [2^-60, 2^60] (affine only).  y / s is formed as
+// q0 = y rv, then one FMA correction with the exact remainder y - q0 s (Markstein's method): the
+// IEEE quotient whenever also |y| in [2^-60, 2^60] or y = 0 (then nothing over- or underflows),
+// the division itself otherwise.  This keeps the division's ten dependent operations off the
+// per-antidiagonal critical path.
 template <int KIND>
-__device__ __forceinline__ void sweep_tile_lds(TileLds& tl, float* __restrict__ y, float* __restrict__ c,
-                                               float* __restrict__ e, const QSpec<float>& qs, int64_t m, int64_t n,
-                                               int64_t i0, int64_t j0, int64_t mat) {
+__device__ __forceinline__ float quantize_entry_rcp(float yv, float sv, float zv, float rv, bool s_ok, float qmin,
+                                                    float qmax) {
+  // the dequantized value is rounded on its own (as the reference's plug-in writes it), so that the
+  // caller's error z - y is exactly that difference: no contraction into the caller's subtraction
+#pragma clang fp contract(off)
+  if constexpr (KIND == Q_AFFINE) {
+    const float q0 = yv * rv;
+    const float rem = __builtin_fmaf(-q0, sv, yv);
+    float q = __builtin_fmaf(rem, rv, q0);
+    const float ay = __builtin_fabsf(yv);
+    if (!(s_ok && ay <= 0x1p60f && (ay >= 0x1p-60f || yv == 0.f))) q = yv / sv;
+    const float code = clamp_val(round_even(q + zv), qmin, qmax);
+    return (code - zv) * sv;
+  } else if constexpr (KIND == Q_FORCED) {
+    return sv;
+  } else {
+    return round_even(yv);
+  }
+}
+
+// The tile's 63 antidiagonals, in push form.  Thread (r, part) = (tid / 8, tid % 8) owns the four
+// entries (r, c) of its row with (c + r) % 8 == part; register k holds the one with
+// ((c + r) / 8) % 4 == k.  Entries of antidiagonal t have c + r = t, so the entry rounded at step t
+// is register (t / 8) % 4 of thread part t % 8 in every row: a compile-time register in the
+// unrolled loop.  A step: the rounding threads quantize (their entries' feedback is complete) and
+// publish the error (by column) and final C (by row) to LDS; one barrier; then every thread adds
+// the step's feedback to its entries' sums -- down: L[r, t-c] E[t-c, c], right: C[r, t-r] U[t-r, c].
+// An entry is rounded at y = (Y + down) + right, and its C becomes (C + down) + error.  The
+// zero-padded diagonal blocks make the terms vanish for entries already rounded and for sources
+// outside the tile.  Then Y, C and E of the tile go to global memory.  Expects the tile image
+// complete in LDS (a barrier after it was written).
+template <int KIND>
+__device__ __forceinline__ void sweep_tile_push(TileLds& tl, float* __restrict__ y, float* __restrict__ c,
+                                                float* __restrict__ e, const QSpec<float>& qs, int64_t m, int64_t n,
+                                                int64_t i0, int64_t j0, int64_t mat) {
   const int tid = threadIdx.x;
   const int r = tid / PARTS, part = tid % PARTS;
-  const int64_t gi = i0 + r;
   const int rows_in = m - i0 < TR ? (int)(m - i0) : TR;  // tile rows / columns inside the matrix
   const int cols_in = n - j0 < TR ? (int)(n - j0) : TR;
   const bool row_in = r < rows_in;
-  float lrow[TR / PARTS];
+  const int qlo = (r - part + 7) >> 3;  // smallest q with 8 q + part >= r
+  int ck[4];
+  // per entry: Y and C on entry, the in-tile down and right feedback sums D and F (kept apart from
+  // Y, so that their rounding errors scale with the feedback, not with Y), the error E, the
+  // quantizer inputs S, Z and the reciprocal R of S
+  float Y[4], C[4], D[4], F[4], E[4], S[4], Z[4], R[4];
+  bool s_ok[4];
 #pragma unroll
-  for (int k = 0; k < TR / PARTS; ++k) lrow[k] = part + PARTS * k < r ? tl.Ls[r][part + PARTS * k] : 0.f;
-  float* ypre_row = qs.ypre ? qs.ypre + mat + gi * n + j0 : nullptr;
-#pragma unroll 1
-  for (int t = 0; t < 2 * TR - 1; ++t) {
-    const int cc = t - r;
-    const bool active = row_in && cc >= 0 && cc < cols_in;
-    const int ccs = active ? cc : 0;
-    float ev[TR / PARTS], uv[TR / PARTS], cv[TR / PARTS];
-#pragma unroll
-    for (int k = 0; k < TR / PARTS; ++k) {
-      const int rr = part + PARTS * k;
-      ev[k] = tl.Es[rr][ccs];
-      uv[k] = tl.Us[rr][ccs];
-      cv[k] = tl.Cs[r][rr];
-    }
-    const float y0 = tl.Ys[r][ccs], c0 = tl.Cs[r][ccs];
-    float sv = 0.f, zv = 0.f;
+  for (int k = 0; k < 4; ++k) {
+    ck[k] = 8 * (qlo + ((k - qlo) & 3)) + part - r;  // in [0, TR)
+    Y[k] = tl.Ys[r][ck[k]];
+    C[k] = tl.Cs[r][ck[k]];
+    D[k] = F[k] = E[k] = 0.f;
+    S[k] = Z[k] = R[k] = 0.f;
+    s_ok[k] = false;
     if constexpr (KIND == Q_AFFINE) {
-      sv = tl.Ss[r][ccs];
-      zv = tl.Zs[r][ccs];
+      S[k] = tl.Ss[r][ck[k]];
+      Z[k] = tl.Zs[r][ck[k]];
+      R[k] = 1.f / S[k];
+      const float as = __builtin_fabsf(S[k]);
+      s_ok[k] = as >= 0x1p-60f && as <= 0x1p60f;
     } else if constexpr (KIND == Q_FORCED) {
-      sv = tl.Ss[r][ccs];
+      S[k] = tl.Ss[r][ck[k]];
     }
-    float down = 0.f, right = 0.f;
+  }
+  float* ypre_row = qs.ypre ? qs.ypre + mat + (i0 + r) * n + j0 : nullptr;
+  // clamp bounds pinned in registers (an empty asm makes them opaque): otherwise the compiler
+  // re-reads them from the kernel arguments on every step
+  float qmin = qs.qmin, qmax = qs.qmax;
+  asm volatile("" : "+v"(qmin), "+v"(qmax));
 #pragma unroll
-    for (int k = 0; k < TR / PARTS; ++k) {
-      down += lrow[k] * ev[k];
-      right += (part + PARTS * k < ccs ? cv[k] : 0.f) * uv[k];
-    }
-    down = group8_sum(down);
-    right = group8_sum(right);
-    const float yv = (y0 + down) + right;
-    const float z = quantize_entry<KIND>(yv, sv, zv, qs.qmin, qs.qmax);
-    const float evn = z - yv;
-    if (active && part == 0) {
-      tl.Ys[r][cc] = z;
-      tl.Es[r][cc] = evn;
-      tl.Cs[r][cc] = (c0 + down) + evn;
-      if (ypre_row) ypre_row[cc] = yv;
+  for (int t = 0; t < 2 * TR - 1; ++t) {
+    const int ka = (t >> 3) & 3, buf = t & 1;
+    if (part == (t & 7) && row_in && t - r >= 0 && t - r < cols_in) {
+      const float yv = (Y[ka] + D[ka]) + F[ka];
+      const float z = quantize_entry_rcp<KIND>(yv, S[ka], Z[ka], R[ka], s_ok[ka], qmin, qmax);
+      const float ev = z - yv;
+      const float cf = (C[ka] + D[ka]) + ev;
+      Y[ka] = z;
+      E[ka] = ev;
+      C[ka] = cf;
+      tl.Ed[buf][t - r] = ev;
+      tl.Cr[buf][r] = cf;
+      if (ypre_row) ypre_row[t - r] = yv;
     }
     __syncthreads();
+    if (t == 2 * TR - 2) break;  // nothing left to receive feedback
+    const float cr = tl.Cr[buf][r];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const float lv = tl.Lp[r][TR + t - ck[k]];
+      const float ev = tl.Ed[buf][ck[k]];
+      const float uv = tl.Up[TR + t - r][ck[k]];
+      D[k] += lv * ev;
+      F[k] += cr * uv;
+    }
   }
 
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    tl.Ys[r][ck[k]] = Y[k];
+    tl.Cs[r][ck[k]] = C[k];
+    tl.Es[r][ck[k]] = E[k];
+  }
+  __syncthreads();
   for (int t = tid; t < TR * TR; t += NTHREADS) {
     const int rr = t / TR, cc = t % TR;
     const int64_t gi2 = i0 + rr, gj = j0 + cc;
@@ -331,8 +392,9 @@ struct TileRegs {
     }
   }
 
-  // LDS image of the tile with the pulled feedback D (down) and R (right) added: C + D, Y + (D + R).
-  // red holds the four waves' partial products (summed in a fixed order) when `pulled`.
+  // LDS image of the tile with the pulled feedback D (down) and R (right) added: C + D, Y + (D + R),
+  // and the zero padding of the diagonal blocks.  red holds the four waves' partial products
+  // (summed in a fixed order) when `pulled`.
   __device__ __forceinline__ void store(TileLds& tl, const float (*red)[2][TR][TR + 1], bool pulled) const {
 #pragma unroll
     for (int q = 0; q < NQ; ++q) {
@@ -345,11 +407,24 @@ struct TileRegs {
       }
       tl.Ys[r][cc] = y[q] + (dd + rr);
       tl.Cs[r][cc] = c[q] + dd;
-      tl.Es[r][cc] = 0.f;
-      tl.Ls[r][cc] = l[q];
-      tl.Us[r][cc] = u[q];
+      tl.Lp[r][TR + cc] = l[q];
+      tl.Up[TR + r][cc] = u[q];
       if constexpr (KIND != Q_ROUND) tl.Ss[r][cc] = s[q];
       if constexpr (KIND == Q_AFFINE) tl.Zs[r][cc] = z[q];
+    }
+    for (int i = threadIdx.x; i < TR * (LPW - TR); i += NTHREADS) {
+      const int r = i / (LPW - TR), k = i % (LPW - TR);
+      tl.Lp[r][k < TR ? k : k + TR] = 0.f;
+    }
+    for (int i = threadIdx.x; i < 2 * TR * UPW; i += NTHREADS) {
+      const int row = i / UPW, col = i % UPW;
+      tl.Up[row < TR ? row : row + TR][col] = 0.f;
+    }
+    // slots of antidiagonals that miss a row or column are read (times a zero factor) before any
+    // write: they must hold finite values, never leftover LDS contents
+    if (threadIdx.x < 2 * TR) {
+      tl.Ed[threadIdx.x / TR][threadIdx.x % TR] = 0.f;
+      tl.Cr[threadIdx.x / TR][threadIdx.x % TR] = 0.f;
     }
   }
 };
@@ -373,7 +448,7 @@ __device__ __forceinline__ void stash_partials(float (*red)[2][TR][TR + 1], cons
 //     R = sum C[I,t] U[t,J] over t in [max(0, S0-I), J) -- the four waves taking every fourth
 //     k-tile and reducing through LDS.  Operands go straight from global memory into the MFMA
 //     layout (lane l: A(l%32, 16 (l/32) + s), B(16 (l/32) + s, l%32)).  Then C += D, Y += D + R.
-//  2. The tile's 63 antidiagonals in LDS (sweep_tile_lds).
+//  2. The tile's 63 antidiagonals in LDS (sweep_tile_push).
 template <bool VEC, int KIND>
 __global__ __launch_bounds__(NTHREADS) void tile_pull_sweep_kernel(float* __restrict__ y, float* __restrict__ c,
                                                                    float* __restrict__ e,
@@ -417,7 +492,7 @@ __global__ __launch_bounds__(NTHREADS) void tile_pull_sweep_kernel(float* __rest
   __syncthreads();
 
   // ---- 2. in-tile sweep
-  sweep_tile_lds<KIND>(tl, y, c, e, qs, m, n, i0, j0, mat);
+  sweep_tile_push<KIND>(tl, y, c, e, qs, m, n, i0, j0, mat);
 }
 
 template <bool VEC>
