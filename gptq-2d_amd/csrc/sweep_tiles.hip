@@ -170,42 +170,42 @@ __device__ __forceinline__ float quantize_entry(float yv, float sv, float zv, fl
   }
 }
 
-// Pull one band product into acc: sum over k-tiles t in [lo, hi), t = lo + wave + 4 q, of
-// A[i0.., t] B[t, j0..] with A row-major (lda) and B row-major (ldb), both 32 x 32 tiles read
-// straight into the MFMA operand layout; per chunk of 16 k-tiles every load is issued first.
+// One wave's share of a band product on MFMA: acc += sum over the k-chunks ch in [c_lo, c_hi) with
+// ch = c_lo + half (mod 2) of A[i0 + 0..31, 8 ch + 0..7] B[8 ch + 0..7, j0 + 0..31], A and B
+// row-major (lda, ldb), read straight from global memory into the MFMA operand layout: lane l
+// supplies A(l % 32, 8 ch + 4 (l / 32) + s) and B(8 ch + 4 (l / 32) + s, l % 32) to MFMA s = 0..3 of
+// the chunk.  Loads of G chunks are issued before their MFMAs.
 template <bool VEC>
-__device__ __forceinline__ void pull_product(floatx16& acc, const float* __restrict__ A, int64_t lda, int64_t a_rows,
-                                             int64_t a_cols, const float* __restrict__ Bm, int64_t ldb,
-                                             int64_t b_rows, int64_t b_cols, int64_t i0, int64_t j0, int64_t lo,
-                                             int64_t hi, int wave, int li, int hh) {
+__device__ __forceinline__ void pull_chunks(floatx16& acc, const float* __restrict__ A, int64_t lda, int64_t a_rows,
+                                            int64_t a_cols, const float* __restrict__ Bm, int64_t ldb,
+                                            int64_t b_rows, int64_t b_cols, int64_t i0, int64_t j0, int64_t c_lo,
+                                            int64_t c_hi, int half, int li, int hh) {
   const int64_t ia = i0 + li, jb = j0 + li;
-  for (int64_t base = lo; base < hi; base += 4 * 4) {
-    float av[4][16], bv[4][16];
+  const bool arow = ia < a_rows, bcol = jb < b_cols;
+  constexpr int G = 4;
+  for (int64_t base = c_lo + half; base < c_hi; base += 2 * G) {
+    float av[G][4], bv[G][4];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int64_t t = base + wave + 4 * q;
-      const int64_t k0 = t * TR + 16 * hh;
-      const bool ok = t < hi;
+    for (int q = 0; q < G; ++q) {
+      const int64_t ch = base + 2 * q;
+      const int64_t k0 = 8 * ch + 4 * hh;
+      const bool ok = ch < c_hi;
       if (VEC) {
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const float4 f = (ok && ia < a_rows && k0 + 4 * v < a_cols)
-                               ? *reinterpret_cast<const float4*>(A + ia * lda + k0 + 4 * v)
-                               : make_float4(0.f, 0.f, 0.f, 0.f);
-          av[q][4 * v] = f.x, av[q][4 * v + 1] = f.y, av[q][4 * v + 2] = f.z, av[q][4 * v + 3] = f.w;
-        }
+        const float4 f = (ok && arow && k0 < a_cols) ? *reinterpret_cast<const float4*>(A + ia * lda + k0)
+                                                     : make_float4(0.f, 0.f, 0.f, 0.f);
+        av[q][0] = f.x, av[q][1] = f.y, av[q][2] = f.z, av[q][3] = f.w;
       } else {
 #pragma unroll
-        for (int s2 = 0; s2 < 16; ++s2) av[q][s2] = (ok && ia < a_rows && k0 + s2 < a_cols) ? A[ia * lda + k0 + s2] : 0.f;
+        for (int s2 = 0; s2 < 4; ++s2) av[q][s2] = (ok && arow && k0 + s2 < a_cols) ? A[ia * lda + k0 + s2] : 0.f;
       }
 #pragma unroll
-      for (int s2 = 0; s2 < 16; ++s2) bv[q][s2] = (ok && k0 + s2 < b_rows && jb < b_cols) ? Bm[(k0 + s2) * ldb + jb] : 0.f;
+      for (int s2 = 0; s2 < 4; ++s2) bv[q][s2] = (ok && bcol && k0 + s2 < b_rows) ? Bm[(k0 + s2) * ldb + jb] : 0.f;
     }
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      if (base + wave + 4 * q >= hi) break;
+    for (int q = 0; q < G; ++q) {
+      if (base + 2 * q >= c_hi) break;
 #pragma unroll
-      for (int s2 = 0; s2 < 16; ++s2) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[q][s2], bv[q][s2], acc, 0, 0, 0);
+      for (int s2 = 0; s2 < 4; ++s2) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[q][s2], bv[q][s2], acc, 0, 0, 0);
     }
   }
 }
@@ -393,8 +393,8 @@ struct TileRegs {
   }
 
   // LDS image of the tile with the pulled feedback D (down) and R (right) added: C + D, Y + (D + R),
-  // and the zero padding of the diagonal blocks.  red holds the four waves' partial products
-  // (summed in a fixed order) when `pulled`.
+  // and the zero padding of the diagonal blocks.  red[product][half] holds the two waves' partial
+  // sums of each product when `pulled`.
   __device__ __forceinline__ void store(TileLds& tl, const float (*red)[2][TR][TR + 1], bool pulled) const {
 #pragma unroll
     for (int q = 0; q < NQ; ++q) {
@@ -402,8 +402,8 @@ struct TileRegs {
       const int r = t / TR, cc = t % TR;
       float dd = 0.f, rr = 0.f;
       if (pulled) {
-        dd = (red[0][0][r][cc] + red[1][0][r][cc]) + (red[2][0][r][cc] + red[3][0][r][cc]);
-        rr = (red[0][1][r][cc] + red[1][1][r][cc]) + (red[2][1][r][cc] + red[3][1][r][cc]);
+        dd = red[0][0][r][cc] + red[0][1][r][cc];
+        rr = red[1][0][r][cc] + red[1][1][r][cc];
       }
       tl.Ys[r][cc] = y[q] + (dd + rr);
       tl.Cs[r][cc] = c[q] + dd;
@@ -429,40 +429,42 @@ struct TileRegs {
   }
 };
 
-// Partial products of the four waves into red (layout of the 32 x 32 MFMA accumulator).
-__device__ __forceinline__ void stash_partials(float (*red)[2][TR][TR + 1], const floatx16& accd,
-                                               const floatx16& accr) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, li = lane & 31, hh = lane >> 5;
+// A wave's partial product into red[product][half] (layout of the 32 x 32 MFMA accumulator).
+__device__ __forceinline__ void stash_partial(float (*red)[2][TR][TR + 1], const floatx16& acc, int product,
+                                              int half) {
+  const int lane = threadIdx.x & 63, li = lane & 31, hh = lane >> 5;
 #pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    const int row = 8 * (r >> 2) + 4 * hh + (r & 3);
-    red[wave][0][row][li] = accd[r];
-    red[wave][1][row][li] = accr[r];
-  }
+  for (int r = 0; r < 16; ++r) red[product][half][8 * (r >> 2) + 4 * hh + (r & 3)][li] = acc[r];
 }
 
-// One tile (I, J) of coarse stage T = I + J inside the outer block that starts at tile stage S0,
-// one launch per coarse stage.
-//  1. Pull, on MFMA: the feedback of the tiles of this outer block swept before T, which no flush
-//     has delivered yet -- D = sum L[I,t] E[t,J] over t in [max(0, S0-J), I) and
-//     R = sum C[I,t] U[t,J] over t in [max(0, S0-I), J) -- the four waves taking every fourth
-//     k-tile and reducing through LDS.  Operands go straight from global memory into the MFMA
-//     layout (lane l: A(l%32, 16 (l/32) + s), B(16 (l/32) + s, l%32)).  Then C += D, Y += D + R.
-//  2. The tile's 63 antidiagonals in LDS (sweep_tile_push).
+// One launch per coarse stage T of the fused fp32 sweep, inside the outer block of tile stages
+// [S0, S1).  The feedback a tile (I, J) needs from the tiles of its outer block swept before it
+// (no flush has delivered it yet) is D = sum L[I,t] E[t,J] over t in [max(0, S0-J), I) and
+// R = sum C[I,t] U[t,J] over t in [max(0, S0-I), J).  It is pulled on MFMA in two parts:
+//  * prep workgroups (blockIdx.x >= n_sweep) take the tiles of stage T+1 and add the part from
+//    the k-tiles before the last one (t < I-1, resp. t < J-1: stages up to T-1, all final) to
+//    their Y and C in global memory -- no tile of stage T touches those;
+//  * sweep workgroups take the tiles of stage T, pull the last k-tile (the tiles (I-1, J) and
+//    (I, J-1) of stage T-1) and sweep the tile's 63 antidiagonals in LDS (sweep_tile_push).
+// So only one k-tile of each product is on the stage-to-stage critical path; the rest runs beside
+// the previous stage's sweeps.  Waves 0-1 take the down product, waves 2-3 the right one, each
+// every second 8-deep k-chunk; the two halves meet in LDS.
 template <bool VEC, int KIND>
-__global__ __launch_bounds__(NTHREADS) void tile_pull_sweep_kernel(float* __restrict__ y, float* __restrict__ c,
-                                                                   float* __restrict__ e,
-                                                                   const float* __restrict__ l,
-                                                                   const float* __restrict__ u, int64_t m, int64_t n,
-                                                                   int64_t stage, int64_t S0, int64_t tile_lo,
-                                                                   BatchMap lmap, BatchMap umap, QSpec<float> qs,
-                                                                   int64_t nx, int64_t ny) {
-  __shared__ float red[4][2][TR][TR + 1];
+__global__ __launch_bounds__(NTHREADS, 2) void tile_stage_kernel(float* __restrict__ y, float* __restrict__ c,
+                                                                 float* __restrict__ e, const float* __restrict__ l,
+                                                                 const float* __restrict__ u, int64_t m, int64_t n,
+                                                                 int64_t stage, int64_t S0, int64_t tile_lo,
+                                                                 int64_t n_sweep, int64_t prep_lo, BatchMap lmap,
+                                                                 BatchMap umap, QSpec<float> qs, int64_t nx,
+                                                                 int64_t ny) {
+  __shared__ float red[2][2][TR][TR + 1];
   __shared__ TileLds tl;
 
   const GridIds id = grid_ids(nx, ny);
   const int64_t b = id.b;
-  const int64_t I = tile_lo + id.x, J = stage - I;
+  const bool sweep = id.x < n_sweep;
+  const int64_t st = sweep ? stage : stage + 1;
+  const int64_t I = sweep ? tile_lo + id.x : prep_lo + (id.x - n_sweep), J = st - I;
   const int64_t i0 = I * TR, j0 = J * TR;
   const int64_t mat = b * m * n;
   const float* lb = l + lmap.offset(b);
@@ -470,44 +472,73 @@ __global__ __launch_bounds__(NTHREADS) void tile_pull_sweep_kernel(float* __rest
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int li = lane & 31, hh = lane >> 5;
 
+  // k-chunk ranges (8 columns each) of this workgroup's part of the two products
+  const int64_t dlo = S0 - J > 0 ? S0 - J : 0, rlo = S0 - I > 0 ? S0 - I : 0;
+  int64_t d0, d1, r0, r1;
+  if (sweep) {
+    d0 = I - 1 >= dlo ? 4 * (I - 1) : 0, d1 = I - 1 >= dlo ? 4 * I : 0;
+    r0 = J - 1 >= rlo ? 4 * (J - 1) : 0, r1 = J - 1 >= rlo ? 4 * J : 0;
+  } else {
+    d0 = 4 * dlo, d1 = I - 1 > dlo ? 4 * (I - 1) : d0;
+    r0 = 4 * rlo, r1 = J - 1 > rlo ? 4 * (J - 1) : r0;
+  }
+  const bool pulled = d0 < d1 || r0 < r1;
+  if (!sweep && !pulled) return;
+
   // own tile data first: it does not depend on the pull, so its loads overlap the pull's
   TileRegs<KIND> own;
-  own.load(y, c, lb, ub, qs, b, m, n, i0, j0, mat);
+  if (sweep) own.load(y, c, lb, ub, qs, b, m, n, i0, j0, mat);
 
-  // ---- 1. pull
-  const int64_t dlo = S0 - J > 0 ? S0 - J : 0, rlo = S0 - I > 0 ? S0 - I : 0;
-  const bool any = dlo < I || rlo < J;
-  if (any) {
-    floatx16 accd, accr;
+  if (pulled) {
+    floatx16 acc;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) accd[r] = accr[r] = 0.f;
-    pull_product<VEC>(accd, lb, m, m, m, e + mat, n, m, n, i0, j0, dlo, I, wave, li, hh);
-    pull_product<VEC>(accr, c + mat, n, m, n, ub, n, n, n, i0, j0, rlo, J, wave, li, hh);
-    stash_partials(red, accd, accr);
+    for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+    const int product = wave >> 1, half = wave & 1;
+    if (product == 0)
+      pull_chunks<VEC>(acc, lb, m, m, m, e + mat, n, m, n, i0, j0, d0, d1, half, li, hh);
+    else
+      pull_chunks<VEC>(acc, c + mat, n, m, n, ub, n, n, n, i0, j0, r0, r1, half, li, hh);
+    stash_partial(red, acc, product, half);
   }
   __syncthreads();
 
-  // ---- the tile image in LDS
-  own.store(tl, red, any);
-  __syncthreads();
+  if (!sweep) {  // prep: Y += D + R, C += D in place
+#pragma unroll
+    for (int q = 0; q < TR * TR / NTHREADS; ++q) {
+      const int t = tid + NTHREADS * q;
+      const int r = t / TR, cc = t % TR;
+      const int64_t gi = i0 + r, gj = j0 + cc;
+      if (gi < m && gj < n) {
+        const int64_t off = mat + gi * n + gj;
+        const float dd = red[0][0][r][cc] + red[0][1][r][cc];
+        const float rr = red[1][0][r][cc] + red[1][1][r][cc];
+        y[off] = y[off] + (dd + rr);
+        c[off] = c[off] + dd;
+      }
+    }
+    return;
+  }
 
-  // ---- 2. in-tile sweep
+  // ---- the tile image in LDS, then the in-tile sweep
+  own.store(tl, red, pulled);
+  __syncthreads();
   sweep_tile_push<KIND>(tl, y, c, e, qs, m, n, i0, j0, mat);
 }
 
 template <bool VEC>
-void launch_tile_pull(int32_t kind, dim3 grid, hipStream_t stream, float* y, float* c, float* e, const float* l,
-                      const float* u, int64_t m, int64_t n, int64_t st, int64_t S0, int64_t lo, const BatchMap& lmap,
-                      const BatchMap& umap, const QSpec<float>& qs, int64_t nx, int64_t ny) {
+void launch_tile_stage(int32_t kind, dim3 grid, hipStream_t stream, float* y, float* c, float* e, const float* l,
+                       const float* u, int64_t m, int64_t n, int64_t st, int64_t S0, int64_t lo, int64_t n_sweep,
+                       int64_t prep_lo, const BatchMap& lmap, const BatchMap& umap, const QSpec<float>& qs, int64_t nx,
+                       int64_t ny) {
   if (kind == Q_AFFINE)
-    hipLaunchKernelGGL((tile_pull_sweep_kernel<VEC, Q_AFFINE>), grid, dim3(NTHREADS), 0, stream, y, c, e, l, u, m, n,
-                       st, S0, lo, lmap, umap, qs, nx, ny);
+    hipLaunchKernelGGL((tile_stage_kernel<VEC, Q_AFFINE>), grid, dim3(NTHREADS), 0, stream, y, c, e, l, u, m, n, st, S0,
+                       lo, n_sweep, prep_lo, lmap, umap, qs, nx, ny);
   else if (kind == Q_FORCED)
-    hipLaunchKernelGGL((tile_pull_sweep_kernel<VEC, Q_FORCED>), grid, dim3(NTHREADS), 0, stream, y, c, e, l, u, m, n,
-                       st, S0, lo, lmap, umap, qs, nx, ny);
+    hipLaunchKernelGGL((tile_stage_kernel<VEC, Q_FORCED>), grid, dim3(NTHREADS), 0, stream, y, c, e, l, u, m, n, st, S0,
+                       lo, n_sweep, prep_lo, lmap, umap, qs, nx, ny);
   else
-    hipLaunchKernelGGL((tile_pull_sweep_kernel<VEC, Q_ROUND>), grid, dim3(NTHREADS), 0, stream, y, c, e, l, u, m, n,
-                       st, S0, lo, lmap, umap, qs, nx, ny);
+    hipLaunchKernelGGL((tile_stage_kernel<VEC, Q_ROUND>), grid, dim3(NTHREADS), 0, stream, y, c, e, l, u, m, n, st, S0,
+                       lo, n_sweep, prep_lo, lmap, umap, qs, nx, ny);
 }
 
 bool aligned16(const void* p) { return p == nullptr || ((uintptr_t)p & 15) == 0; }
@@ -552,16 +583,24 @@ int sweep_fused(T* y, T* c, T* e, const T* l, const T* u, int64_t m, int64_t n, 
     for (int64_t st = S0; st < S1; ++st) {
       const int64_t lo = st - nt + 1 > 0 ? st - nt + 1 : 0;
       const int64_t hi = st < mt - 1 ? st : mt - 1;
-      Grid3 g = make_grid(hi - lo + 1, 1, B);
       const bool prof = gptq2d_prof_on(PROF_TILE_SWEEP);
       if (prof) gptq2d_prof_begin(PROF_TILE_SWEEP, stream);
       if constexpr (sizeof(T) == 4) {
-        // fp32: every tile pulls the feedback of this outer block's earlier tile stages itself
+        // fp32: this stage's sweeps plus the prep of the next stage of the outer block
+        int64_t plo = 0, pcount = 0;
+        if (st + 1 < S1) {
+          plo = st + 1 - nt + 1 > 0 ? st + 1 - nt + 1 : 0;
+          pcount = (st + 1 < mt - 1 ? st + 1 : mt - 1) - plo + 1;
+        }
+        const Grid3 g = make_grid(hi - lo + 1 + pcount, 1, B);
         if (vec)
-          launch_tile_pull<true>(qkind, g.grid, stream, y, c, e, l, u, m, n, st, S0, lo, lmap, umap, qs, g.nx, g.ny);
+          launch_tile_stage<true>(qkind, g.grid, stream, y, c, e, l, u, m, n, st, S0, lo, hi - lo + 1, plo, lmap, umap,
+                                  qs, g.nx, g.ny);
         else
-          launch_tile_pull<false>(qkind, g.grid, stream, y, c, e, l, u, m, n, st, S0, lo, lmap, umap, qs, g.nx, g.ny);
+          launch_tile_stage<false>(qkind, g.grid, stream, y, c, e, l, u, m, n, st, S0, lo, hi - lo + 1, plo, lmap, umap,
+                                   qs, g.nx, g.ny);
       } else {
+        const Grid3 g = make_grid(hi - lo + 1, 1, B);
         hipLaunchKernelGGL(sweep_tiles_kernel<T>, g.grid, dim3(NTHREADS), 0, stream, y, c, e, l, u, m, n, st, lo,
                            lmap, umap, qs, g.nx, g.ny);
       }
