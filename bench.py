@@ -41,6 +41,12 @@ HBM_PEAK_GBS = 8000.0
 # fp32 VALU without packed instructions (which this build does not use): half the published 157.3
 # TFLOP/s vector figure, i.e. 78.6 TFLOP/s of FMA = 39.3e12 single fp32 operations per second.
 VALU_FP32_OPS_PEAK = 39.3e12
+# Outer block of the fused sweep, in antidiagonals (32 tile stages).  A longer outer block moves
+# more of the cross-tile feedback into the few large outer flushes, which run closest to the MFMA
+# peak, at the price of more in-block prep work per tile stage; at 8192^2 on one MI355X: 512 ->
+# sweep 27.7 ms (flush 72.9 TFLOP/s), 1024 -> 26.1 ms (81.0), 2048 -> 28.0 ms (83.1).  It changes
+# the order of the fp32 additions only, not the algorithm.
+OUTER_BLOCK = 1024
 # fp32 VALU operations per trellis state evaluation: 2 sub, 2 mul, 1 add (the squared distance),
 # 1 add (the predecessor group's minimum), 1 min.
 OPS_PER_STATE_EVAL = 7
@@ -181,7 +187,7 @@ def main() -> int:
         lo, up = LDL.feedback_factors_of_grams(a, b, check=False)  # both factors, two streams
         if events:
             events[1].record()
-        z = G.gptq_2d(x, lo, up, quantizer=quant, quantizer_inputs=(scale, zp))
+        z = G.gptq_2d(x, lo, up, quantizer=quant, quantizer_inputs=(scale, zp), outer_block_size=OUTER_BLOCK)
         if events:
             events[2].record()
         return z, lo, up
@@ -249,6 +255,7 @@ def main() -> int:
             "workload": f"{cfg.name}: {m}x{n} INT4 symmetric per-row static bf16 scale, Wishart-like A, B "
                         f"(s_i = i^-{cfg.alpha:g}, 1e-2 damping); LDL(A) || LDL(B) + fused GPTQ-2D sweep",
             "m": m, "n": n, "stages": stages, "quantizer": "affine INT4 [-8, 7], zero point 0",
+            "outer_block_size": OUTER_BLOCK,
         },
         "breakdown": {
             **{k: round(v, 3) for k, v in parts.items()},

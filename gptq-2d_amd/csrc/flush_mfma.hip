@@ -341,9 +341,9 @@ __global__ __launch_bounds__(256, 2) void flush_tiles_mfma_kernel(float* __restr
   }
 }
 
+// Workgroups (target blocks of WT x WT tiles) of one launch, per batch entry.
 template <int WT>
-int launch(float* y, float* c, const float* e, const float* l, const float* u, const TileFlush& g,
-           const BatchMap& lmap, const BatchMap& umap, int64_t B, hipStream_t stream) {
+int64_t count_items(const TileFlush& g) {
   const int64_t rows_hi = g.S_end < g.mt ? g.S_end : g.mt;
   int64_t items = 0;
   for (int64_t by = 0; by * WT < rows_hi; ++by) {
@@ -351,6 +351,13 @@ int launch(float* y, float* c, const float* e, const float* l, const float* u, c
     row_block_span<WT>(g, by, first, count);
     items += count;
   }
+  return items;
+}
+
+template <int WT>
+int launch(float* y, float* c, const float* e, const float* l, const float* u, const TileFlush& g,
+           const BatchMap& lmap, const BatchMap& umap, int64_t B, hipStream_t stream) {
+  const int64_t items = count_items<WT>(g);
   if (items == 0 || B == 0) return 0;
   if (items > 0x7fffffff) return GPTQ2D_EUNSUPPORTED;
   const bool vec = g.m % 4 == 0 && g.n % 4 == 0;
@@ -368,12 +375,14 @@ int launch(float* y, float* c, const float* e, const float* l, const float* u, c
 
 }  // namespace
 
-// Flush of tile stages [S0, S1) into [S1, S_end) on MFMA; 4 x 4 tiles per workgroup for wide bands
-// of sources (outer flushes), 2 x 2 for single-stage bands.
+// Flush of tile stages [S0, S1) into [S1, S_end) on MFMA.
 int gptq2d_flush_tiles_mfma(float* y, float* c, const float* e, const float* l, const float* u, int64_t m, int64_t n,
                             int64_t S0, int64_t S1, int64_t S_end, const BatchMap& lmap, const BatchMap& umap,
                             int64_t B, hipStream_t stream) {
   TileFlush g{m, n, cdiv(m, TS), cdiv(n, TS), S0, S1, S_end};
-  if (S1 - S0 >= 4) return launch<4>(y, c, e, l, u, g, lmap, umap, B, stream);
+  // 4 x 4 tiles per workgroup when there are enough of them to fill the chip (two per CU); else
+  // 2 x 2, four times as many workgroups, each k-tile a quarter of the MFMAs (the first and last
+  // flushes of a sweep, where a few long items would otherwise set the launch time)
+  if (S1 - S0 >= 4 && count_items<4>(g) * B >= 512) return launch<4>(y, c, e, l, u, g, lmap, umap, B, stream);
   return launch<2>(y, c, e, l, u, g, lmap, umap, B, stream);
 }
