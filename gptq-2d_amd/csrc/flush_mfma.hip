@@ -12,11 +12,12 @@
 // A workgroup owns WT x WT target tiles and four waves, each wave (WT/2) x (WT/2) tiles with one
 // 16-register accumulator per tile.  The K loop walks the union of the tiles' k-tile ranges; each
 // k-tile's panels (A: the WG's rows x 32 of L, then of C; B: 32 x the WG's columns of E, then of U)
-// are prefetched into registers one k-tile ahead and stored to LDS, and a wave
-// issues a tile's 16 MFMAs only when the k-tile lies in that tile's own range -- no MFMA is spent
-// on a masked zero, and tiles that receive nothing are not read or written.  Staging loads are
-// masked to exactly the entries a product may read: L strictly below, U strictly above its
-// diagonal tiles, E and C on the band, nothing outside the matrix.
+// are prefetched into registers one k-tile ahead and stored to LDS.  Staging loads are masked to
+// exactly the entries a product may read: L strictly below, U strictly above its diagonal tiles,
+// E and C on the band, nothing outside the matrix -- so a tile whose own range does not contain
+// the k-tile multiplies zeros, and a wave runs its full MFMA block on every k-tile where any of
+// its tiles is active (the union adds WT - 1 k-tiles per phase to a tile's range).  Tiles that
+// receive nothing are not read or written.
 //
 // Operand layout (lane l, i = l % 32, h = l / 32): A(i, kslot = h), B(kslot = h, j = i); the 16
 // accumulators hold D(8 (r / 4) + 4 h + r % 4, i).  The k carried by slot h in MFMA s is 16 h + s
@@ -168,16 +169,17 @@ __device__ __forceinline__ void flush_phase(floatx16 (&acc)[WT / 2][WT / 2], flo
       store((t + 1) & 1);
       if (t + 2 < t_hi) load(t + 2);
     }
-    // tile masks as 32-bit scalar compares, so the MFMA branches are uniform; a step on which all
-    // of the wave's tiles are active (most of them) runs one straight MFMA block
+    // a wave skips a step on which none of its tiles is active; otherwise it runs the full MFMA
+    // block: the staging masks have already zeroed the operands of any tile outside its own range
+    // (L strictly below its diagonal tiles, E and C on the band), so the inactive tiles of a
+    // partial step accumulate exact zeros -- as fast as tile-by-tile issue, and branch-free
     const int ts = (int)t;
-    int mask = 0;
+    bool any = false;
 #pragma unroll
     for (int a = 0; a < H; ++a)
 #pragma unroll
-      for (int d = 0; d < H; ++d) mask |= (ts >= tlo[a][d] && ts < thi[a][d]) << (a * H + d);
-    mask = __builtin_amdgcn_readfirstlane(mask);
-    if (mask == 0) continue;
+      for (int d = 0; d < H; ++d) any |= ts >= tlo[a][d] && ts < thi[a][d];
+    if (!__builtin_amdgcn_readfirstlane((int)any)) continue;
     const float* as = As + (t & 1) * ABUF + (wi * TS + li) * AP + 16 * hh;
     const float* bsrc = Bs + (t & 1) * BBUF + (4 * hh * ROWS + wj * TS + li) * 4;
     float4 fa[2][H], fb[2][H];
@@ -187,36 +189,18 @@ __device__ __forceinline__ void flush_phase(floatx16 (&acc)[WT / 2][WT / 2], flo
 #pragma unroll
       for (int d = 0; d < H; ++d) fb[slot][d] = *reinterpret_cast<const float4*>(bsrc + (v * ROWS + d * TS) * 4);
     };
-    if (mask == (1 << (H * H)) - 1) {
-      frag(0, 0);
+    frag(0, 0);
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        if (v < 3) frag(v + 1, (v + 1) & 1);
+    for (int v = 0; v < 4; ++v) {
+      if (v < 3) frag(v + 1, (v + 1) & 1);
 #pragma unroll
-        for (int s2 = 0; s2 < 4; ++s2)
+      for (int s2 = 0; s2 < 4; ++s2)
 #pragma unroll
-          for (int a = 0; a < H; ++a)
+        for (int a = 0; a < H; ++a)
 #pragma unroll
-            for (int d = 0; d < H; ++d)
-              acc[a][d] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[v & 1][a][s2], fb[v & 1][d][s2], acc[a][d], 0, 0, 0);
-        __builtin_amdgcn_sched_barrier(0);
-      }
-    } else {
-      // partial step (first and last steps of a tile's range): tile by tile
-#pragma unroll
-      for (int a = 0; a < H; ++a)
-#pragma unroll
-        for (int d = 0; d < H; ++d)
-          if (mask >> (a * H + d) & 1) {
-#pragma unroll
-            for (int v = 0; v < 4; ++v) {
-              const float4 xa = *reinterpret_cast<const float4*>(as + a * TS * AP + 4 * v);
-              const float4 xb = *reinterpret_cast<const float4*>(bsrc + (v * ROWS + d * TS) * 4);
-#pragma unroll
-              for (int s2 = 0; s2 < 4; ++s2)
-                acc[a][d] = __builtin_amdgcn_mfma_f32_32x32x2f32(xa[s2], xb[s2], acc[a][d], 0, 0, 0);
-            }
-          }
+          for (int d = 0; d < H; ++d)
+            acc[a][d] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[v & 1][a][s2], fb[v & 1][d][s2], acc[a][d], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
 }

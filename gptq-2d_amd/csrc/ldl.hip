@@ -124,9 +124,11 @@ __device__ __forceinline__ void quad_solve(T (&x)[PB / 4], int q, const T* __res
 }
 
 // One panel of the blocked Cholesky.  Every workgroup factors the diagonal block W[j0.., j0..]
-// (n = min(PB, k - j0) rows) in LDS, right-looking with one barrier per column (the trailing update
-// uses the unscaled column, A(r, c2) -= A(r, c) A(c2, c) / A(c, c); the columns are scaled by
-// 1/sqrt(pivot) at the end); workgroup 0 writes it back.  Then the panel below is solved against it,
+// (n = min(PB, k - j0) rows; rows beyond n act as identity rows): the block is staged through LDS
+// with coalesced loads, then one wave factors it in registers, lane r holding row r, right-looking
+// column by column with no barrier -- the pivot and the scaled column entries reach the other
+// lanes by readlane (lane r's entries right of its diagonal take harmless updates and are never
+// read); workgroup 0 writes it back.  Then the panel below is solved against it,
 // W[r, j0:j0+PB] <- W[r, j0:j0+PB] C_jj^{-T}, in chunks of 64 rows staged through LDS (coalesced
 // loads and stores): four lanes share a row, lane q owning the columns c = q mod 4, and the
 // forward substitution runs column by column with the finished x_t broadcast inside the quad.
@@ -136,36 +138,33 @@ __global__ __launch_bounds__(256) void potrf_panel_kernel(T* __restrict__ w, int
   constexpr int CP = PB + 1;  // odd pitch: row and column walks are both conflict-free
   __shared__ T a[PB * CP];
   __shared__ T rs[64 * CP];
-  __shared__ T piv[PB];
-  const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
+  const int tid = threadIdx.x;
   for (int t = tid; t < PB * PB; t += 256) {
     const int r = t / PB, c = t % PB;
     a[r * CP + c] = (r < n && c <= r) ? w[(j0 + r) * ld + j0 + c] : (r == c ? T(1) : T(0));
   }
   __syncthreads();
-  for (int c = 0; c < PB; ++c) {
-    const T p = a[c * CP + c];
-    const T ip = T(1) / p;
-    if (tid == 0) piv[c] = p;
-    for (int r = c + 1 + ty; r < PB; r += 16) {
-      const T lrc = a[r * CP + c] * ip;
-      for (int c2 = c + 1 + tx; c2 <= r; c2 += 16) a[r * CP + c2] -= lrc * a[c2 * CP + c];
+  if (tid < 64) {
+    const int r = tid < PB ? tid : PB - 1;
+    T row[PB];
+#pragma unroll
+    for (int c = 0; c < PB; ++c) row[c] = a[r * CP + c];
+    int bad = 0;
+#pragma unroll
+    for (int c = 0; c < PB; ++c) {
+      const T d = bcast(row[c], c);
+      if (!(d > T(0)) && bad == 0) bad = c + 1;
+      const T sd = sqrt(d);
+      row[c] = tid == c ? sd : row[c] / sd;
+#pragma unroll
+      for (int c2 = c + 1; c2 < PB; ++c2) row[c2] -= row[c] * bcast(row[c], c2);
     }
-    __syncthreads();
+    if (tid < PB) {
+#pragma unroll
+      for (int c = 0; c < PB; ++c) a[r * CP + c] = row[c];
+    }
+    if (blockIdx.x == 0 && tid == 0 && bad && info[0] == 0) info[0] = (int)(j0 + bad);
   }
-  if (blockIdx.x == 0 && tid == 0 && info[0] == 0) {
-    for (int c = 0; c < n; ++c)
-      if (!(piv[c] > T(0))) {
-        info[0] = (int)(j0 + c + 1);
-        break;
-      }
-  }
-  for (int t = tid; t < PB * PB; t += 256) {
-    const int r = t / PB, c = t % PB;
-    if (c < r) a[r * CP + c] = a[r * CP + c] / sqrt(piv[c]);
-  }
-  __syncthreads();
-  if (tid < PB) a[tid * CP + tid] = sqrt(piv[tid]);
   __syncthreads();
   if (blockIdx.x == 0) {
     for (int t = tid; t < PB * PB; t += 256) {
