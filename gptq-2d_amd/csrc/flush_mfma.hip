@@ -12,7 +12,8 @@
 // A workgroup owns WT x WT target tiles and four waves, each wave (WT/2) x (WT/2) tiles with one
 // 16-register accumulator per tile.  The K loop walks the union of the tiles' k-tile ranges; each
 // k-tile's panels (A: the WG's rows x 32 of L, then of C; B: 32 x the WG's columns of E, then of U)
-// are prefetched into registers one k-tile ahead and stored to LDS.  Staging loads are masked to
+// are loaded one k-tile ahead straight into LDS (buffer loads with the LDS destination bit, no
+// register staging), double-buffered, one barrier per k-tile.  Staging loads are masked to
 // exactly the entries a product may read: L strictly below, U strictly above its diagonal tiles,
 // E and C on the band, nothing outside the matrix -- so a tile whose own range does not contain
 // the k-tile multiplies zeros, and a wave runs its full MFMA block on every k-tile where any of
@@ -27,17 +28,18 @@
 // _flush_right_kernel :936-1087 (fp32 `tl.dot` with input_precision="ieee"); one kernel here, with
 // one read-modify-write of Y and C per target tile.
 //
-// LDS: A as [row][k] (k fastest), B k-interleaved as [k / 4][j][k % 4], so that a lane's 16 values
-// of either operand for one k-tile are four 128-bit reads; both panels double-buffered, so one
-// barrier per k-tile; a k-tile's fragments are read before its MFMAs are issued.
+// LDS layouts are described at FlushLds: a lane reads its A values for one k-tile as four 128-bit
+// reads, its B values as 32-bit reads (one per MFMA, paired by the compiler); the next group's
+// fragments are read while the current group's MFMAs issue.
 #include "common.h"
+
+#include <type_traits>
 
 namespace {
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 constexpr int TS = 32;      // tile edge = MFMA block edge
-constexpr int AP = TS + 4;  // LDS pitch of the A panel rows (k fastest), 16-byte aligned
 
 struct TileFlush {
   int64_t m, n, mt, nt, S0, S1, S_end;
@@ -79,129 +81,152 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t matrix_rsrc(const float* base,
 }
 constexpr int OOB = 0x7ffffff0;  // a byte offset past every matrix the MFMA flush accepts
 
-__device__ __forceinline__ float4 buf_ld4(__amdgpu_buffer_rsrc_t r, int off, bool ok) {
-  return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, ok ? off : OOB, 0, 0));
+typedef __attribute__((address_space(3))) float lds_float;
+
+// LDS-direct load of W floats per lane (W = 4: 128 bits, W = 1: 32 bits) from byte offset `off` of
+// buffer r: lane l's data lands at dst + W l (dst uniform); an offset past the buffer writes zeros.
+// M0 carries the LDS address (one wait state before the load) and is restored afterwards.  Written
+// as assembly so that the compiler does not order the load before the LDS reads of the other
+// buffer; the caller orders it with wait_dma() and a barrier.
+template <int W>
+__device__ __forceinline__ void dma_load(__amdgpu_buffer_rsrc_t r, float* dst, int off) {
+  const unsigned lds = __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)(lds_float*)dst);
+  unsigned saved;
+  if constexpr (W == 4)
+    asm volatile(
+        "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "v"(off), "s"(r), "s"(lds)
+        : "memory");
+  else
+    asm volatile(
+        "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\tbuffer_load_dword %1, %2, 0 offen lds\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "v"(off), "s"(r), "s"(lds)
+        : "memory");
 }
-__device__ __forceinline__ float buf_ld1(__amdgpu_buffer_rsrc_t r, int off, bool ok) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, ok ? off : OOB, 0, 0));
-}
+// All of this wave's LDS-direct loads have landed.
+__device__ __forceinline__ void wait_dma() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// Panels in LDS, per k-tile (ROWS = 32 WT), both double-buffered:
+//   A (ROWS x 32 k; k contiguous in memory): float f holds row f / 32 and k = 4 (q ^ (row % 8)) + f % 4
+//     with q = (f % 32) / 4 -- the 16-byte k-quads XOR-swizzled by row, so that the 8 rows that 8
+//     lanes read at one k-quad lie in 8 different bank groups;
+//   B (32 k x ROWS columns; columns contiguous in memory): k-row k at k ROWS, plus BPAD floats per
+//     256-float group of rows, so that the lane halves (rows k and k + 16) fall 32 banks apart.
+template <int WT>
+struct FlushLds {
+  static constexpr int ROWS = WT * TS;
+  static constexpr int PANEL = ROWS * TS;
+  static constexpr int BPAD = 512 / ROWS;
+  static constexpr int BSZ = PANEL + PANEL / 256 * BPAD;
+  float a[2][PANEL];
+  float b[2][BSZ];
+};
 
 // One product phase (0: D = L E, 1: R = C U) of a workgroup, accumulated into acc.
 template <int WT, bool VEC, int PHASE>
-__device__ __forceinline__ void flush_phase(floatx16 (&acc)[WT / 2][WT / 2], float* As, float* Bs,
+__device__ __forceinline__ void flush_phase(floatx16 (&acc)[WT / 2][WT / 2], FlushLds<WT>& sm,
                                             __amdgpu_buffer_rsrc_t ra_src, __amdgpu_buffer_rsrc_t rb_src,
                                             const TileFlush& g, int64_t I0, int64_t J0, int wi, int wj,
                                             int64_t t_lo, int64_t t_hi, const int (&tlo)[WT / 2][WT / 2],
                                             const int (&thi)[WT / 2][WT / 2]) {
+  using L = FlushLds<WT>;
   constexpr int H = WT / 2;
-  constexpr int ROWS = WT * TS;
-  constexpr int NV = ROWS * TS / 4 / 256;
-  constexpr int ABUF = ROWS * AP;
-  constexpr int BBUF = TS * ROWS;
+  constexpr int ROWS = L::ROWS;
+  constexpr int W = VEC ? 4 : 1;          // floats per lane per load (rows of 4 k-multiples: 128 bits)
+  constexpr int PER = 64 * W;             // floats per wave load
+  constexpr int NI = L::PANEL / PER / 4;  // loads per wave per panel and k-tile
   const int tid = threadIdx.x, lane = tid & 63, li = lane & 31, hh = lane >> 5;
+  const int wave = tid >> 6;
   const int64_t kmax = PHASE == 0 ? g.m : g.n;  // k extent of both operands
   const int64_t alda = PHASE == 0 ? g.m : g.n;  // row stride of A (L or C)
+  const int s0 = (int)g.S0, s1 = (int)g.S1;
 
-  // staging geometry: A entry (row ar, k 4 akq..+3), B entries (k 4 bkg..+3, column bjc)
-  int aoff[NV], boff[NV];
-  bool arow_ok[NV], bcol_ok[NV];
-  int arow_t[NV], bcol_t[NV];
+  // loads of k-tile t into buffer buf, each masked to what a product may read (L strictly below its
+  // diagonal tiles, C and E on the band, U strictly above its diagonal tiles, nothing outside)
+  auto issue = [&](int64_t t, int buf) {
+    const int ts = (int)t, k0 = ts * TS;
 #pragma unroll
-  for (int q = 0; q < NV; ++q) {
-    const int f = tid + 256 * q;
-    const int64_t i = I0 * TS + f / (TS / 4), ka = 4 * (f % (TS / 4));
-    arow_ok[q] = i < g.m;
-    arow_t[q] = (int)(i >> 5);
-    aoff[q] = (int)((arow_ok[q] ? i * alda : 0) + ka) * 4;
-    const int64_t j = J0 * TS + f % ROWS, kb = 4 * (f / ROWS);
-    bcol_ok[q] = j < g.n;
-    bcol_t[q] = (int)(j >> 5);
-    boff[q] = (int)(kb * g.n + (bcol_ok[q] ? j : 0)) * 4;
-  }
-  float4 ra[NV], rb[NV];
-  auto load = [&](int64_t t) {
-    const int64_t k0 = t * TS;
-#pragma unroll
-    for (int q = 0; q < NV; ++q) {
-      const int f = tid + 256 * q;
-      const int64_t ka = k0 + 4 * (f % (TS / 4)), kb = k0 + 4 * (f / ROWS);
-      const int ts = (int)t, s0 = (int)g.S0, s1 = (int)g.S1;
-      const bool aband = PHASE == 0 ? ts < arow_t[q] : (arow_t[q] + ts >= s0 && arow_t[q] + ts < s1);
-      const bool bband = PHASE == 0 ? (ts + bcol_t[q] >= s0 && ts + bcol_t[q] < s1) : ts < bcol_t[q];
-      const bool aok = arow_ok[q] && aband, bok = bcol_ok[q] && bband;
-      const int ao = aoff[q] + (int)k0 * 4, bo = boff[q] + (int)(k0 * g.n) * 4, bs = (int)g.n * 4;
-      if (VEC) {
-        ra[q] = buf_ld4(ra_src, ao, aok && ka < kmax);
-        const bool bk = bok && kb < kmax;
-        rb[q].x = buf_ld1(rb_src, bo, bk);
-        rb[q].y = buf_ld1(rb_src, bo + bs, bk);
-        rb[q].z = buf_ld1(rb_src, bo + 2 * bs, bk);
-        rb[q].w = buf_ld1(rb_src, bo + 3 * bs, bk);
-      } else {
-        ra[q].x = buf_ld1(ra_src, ao, aok && ka < kmax);
-        ra[q].y = buf_ld1(ra_src, ao + 4, aok && ka + 1 < kmax);
-        ra[q].z = buf_ld1(ra_src, ao + 8, aok && ka + 2 < kmax);
-        ra[q].w = buf_ld1(ra_src, ao + 12, aok && ka + 3 < kmax);
-        rb[q].x = buf_ld1(rb_src, bo, bok && kb < kmax);
-        rb[q].y = buf_ld1(rb_src, bo + bs, bok && kb + 1 < kmax);
-        rb[q].z = buf_ld1(rb_src, bo + 2 * bs, bok && kb + 2 < kmax);
-        rb[q].w = buf_ld1(rb_src, bo + 3 * bs, bok && kb + 3 < kmax);
-      }
-    }
-  };
-  auto store = [&](int buf) {
-#pragma unroll
-    for (int q = 0; q < NV; ++q) {
-      const int f = tid + 256 * q;
-      *reinterpret_cast<float4*>(&As[buf * ABUF + (f / (TS / 4)) * AP + 4 * (f % (TS / 4))]) = ra[q];
-      *reinterpret_cast<float4*>(&Bs[buf * BBUF + 4 * f]) = rb[q];
+    for (int x = 0; x < NI; ++x) {
+      const int f0 = (wave + 4 * x) * PER, f = f0 + lane * W;
+      const int row = f / TS, kk = 4 * (((f % TS) / 4) ^ (row & 7)) + f % 4;
+      const int64_t i = I0 * TS + row;
+      const int at = (int)(i >> 5);
+      const bool aband = PHASE == 0 ? ts < at : (at + ts >= s0 && at + ts < s1);
+      const bool aok = i < g.m && aband && k0 + kk < kmax;
+      dma_load<W>(ra_src, &sm.a[buf][f0], aok ? (int)(i * alda + k0 + kk) * 4 : OOB);
+      const int kb = f / ROWS;
+      const int64_t j = J0 * TS + f % ROWS;
+      const int bt = (int)(j >> 5);
+      const bool bband = PHASE == 0 ? (ts + bt >= s0 && ts + bt < s1) : ts < bt;
+      const bool bok = j < g.n && bband && k0 + kb < kmax;
+      dma_load<W>(rb_src, &sm.b[buf][f0 + f0 / 256 * L::BPAD], bok ? (int)((k0 + kb) * g.n + j) * 4 : OOB);
     }
   };
 
-  if (t_lo >= t_hi) return;
-  __syncthreads();  // the previous phase's last reads of both buffers are done
-  load(t_lo);
-  store(t_lo & 1);
-  if (t_lo + 1 < t_hi) load(t_lo + 1);
-  for (int64_t t = t_lo; t < t_hi; ++t) {
-    __syncthreads();  // buffer t & 1 is complete; buffer (t + 1) & 1 is no longer read
-    if (t + 1 < t_hi) {
-      store((t + 1) & 1);
-      if (t + 2 < t_hi) load(t + 2);
-    }
-    // a wave skips a step on which none of its tiles is active; otherwise it runs the full MFMA
-    // block: the staging masks have already zeroed the operands of any tile outside its own range
-    // (L strictly below its diagonal tiles, E and C on the band), so the inactive tiles of a
-    // partial step accumulate exact zeros -- as fast as tile-by-tile issue, and branch-free
+  // fragments: A tile a, k-quad 4 hh + v of row (wi + a) 32 + li; B tile d, k = 16 hh + s, column
+  // (wj + d) 32 + li -- the k of MFMA s is 16 hh + s for both operands
+  const int a_base = (wi * TS + li) * TS;
+  const int sw = li & 7;
+  const int b_base = 16 * hh * ROWS + wj * TS + li + 16 * hh * ROWS / 256 * L::BPAD;
+
+  auto step = [&](int64_t t, auto cur_c) {
+    constexpr int cur = decltype(cur_c)::value;
+    __syncthreads();  // buffer cur is complete; buffer 1 - cur is no longer read
+    if (t + 1 < t_hi) issue(t + 1, 1 - cur);
+    // a wave skips a k-tile on which none of its tiles is active; otherwise it runs the full MFMA
+    // block -- the staging masks have zeroed the operands of any tile outside its own range, so
+    // the inactive tiles of a partial step accumulate exact zeros
     const int ts = (int)t;
     bool any = false;
 #pragma unroll
     for (int a = 0; a < H; ++a)
 #pragma unroll
       for (int d = 0; d < H; ++d) any |= ts >= tlo[a][d] && ts < thi[a][d];
-    if (!__builtin_amdgcn_readfirstlane((int)any)) continue;
-    const float* as = As + (t & 1) * ABUF + (wi * TS + li) * AP + 16 * hh;
-    const float* bsrc = Bs + (t & 1) * BBUF + (4 * hh * ROWS + wj * TS + li) * 4;
-    float4 fa[2][H], fb[2][H];
-    auto frag = [&](int v, int slot) {
-#pragma unroll
-      for (int a = 0; a < H; ++a) fa[slot][a] = *reinterpret_cast<const float4*>(as + a * TS * AP + 4 * v);
-#pragma unroll
-      for (int d = 0; d < H; ++d) fb[slot][d] = *reinterpret_cast<const float4*>(bsrc + (v * ROWS + d * TS) * 4);
-    };
-    frag(0, 0);
-#pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      if (v < 3) frag(v + 1, (v + 1) & 1);
-#pragma unroll
-      for (int s2 = 0; s2 < 4; ++s2)
+    if (__builtin_amdgcn_readfirstlane((int)any)) {
+      const float* as = &sm.a[cur][a_base];
+      const float* bs = &sm.b[cur][b_base];
+      float4 fa[2][H];
+      float fb[2][H][4];
+      auto frag = [&](int v, int slot) {
 #pragma unroll
         for (int a = 0; a < H; ++a)
+          fa[slot][a] = *reinterpret_cast<const float4*>(as + a * TS * TS + 4 * ((4 * hh + v) ^ sw));
 #pragma unroll
-          for (int d = 0; d < H; ++d)
-            acc[a][d] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[v & 1][a][s2], fb[v & 1][d][s2], acc[a][d], 0, 0, 0);
-      __builtin_amdgcn_sched_barrier(0);
+        for (int d = 0; d < H; ++d)
+#pragma unroll
+          for (int s2 = 0; s2 < 4; ++s2) {
+            const int s = 4 * v + s2;
+            fb[slot][d][s2] = bs[d * TS + s * ROWS + s * ROWS / 256 * L::BPAD];
+          }
+      };
+      frag(0, 0);
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        if (v < 3) frag(v + 1, (v + 1) & 1);
+#pragma unroll
+        for (int s2 = 0; s2 < 4; ++s2)
+#pragma unroll
+          for (int a = 0; a < H; ++a)
+#pragma unroll
+            for (int d = 0; d < H; ++d)
+              acc[a][d] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[v & 1][a][s2], fb[v & 1][d][s2], acc[a][d], 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+      }
     }
+    wait_dma();  // this wave's loads of k-tile t + 1 have landed before the next barrier
+  };
+
+  if (t_lo >= t_hi) return;
+  __syncthreads();  // the previous phase's last reads of both buffers are done
+  issue(t_lo, 0);
+  wait_dma();
+  for (int64_t t = t_lo; t < t_hi; t += 2) {
+    step(t, std::integral_constant<int, 0>{});
+    if (t + 1 < t_hi) step(t + 1, std::integral_constant<int, 1>{});
   }
 }
 
@@ -213,8 +238,7 @@ __global__ __launch_bounds__(256, 2) void flush_tiles_mfma_kernel(float* __restr
                                                                   BatchMap lmap, BatchMap umap, int64_t b0) {
   constexpr int H = WT / 2;        // tiles per wave per direction
   constexpr int ROWS = WT * TS;    // panel rows (A) / columns (B)
-  __shared__ __align__(16) float As[2 * ROWS * AP];  // A panel: [row][k], k fastest, pitch AP
-  __shared__ __align__(16) float Bs[2 * TS * ROWS];  // B panel: [k / 4][j][k % 4]
+  __shared__ __align__(16) FlushLds<WT> sm;
 
   // XCD-aware order: the hardware deals workgroup w to XCD w % 8; runs of XG consecutive work items
   // (neighbouring column blocks of a row block, which share L / C rows) go to one XCD and its L2,
@@ -295,10 +319,10 @@ __global__ __launch_bounds__(256, 2) void flush_tiles_mfma_kernel(float* __restr
   const __amdgpu_buffer_rsrc_t re = matrix_rsrc(e + mat, g.m * g.n);
   const __amdgpu_buffer_rsrc_t rc = matrix_rsrc(c + mat, g.m * g.n);
   const __amdgpu_buffer_rsrc_t ru = matrix_rsrc(u + umap.offset(b), g.n * g.n);
-  flush_phase<WT, VEC, 0>(acc, As, Bs, rl, re, g, I0, J0, wi, wj, lo0, hi0, tlo[0], thi[0]);
+  flush_phase<WT, VEC, 0>(acc, sm, rl, re, g, I0, J0, wi, wj, lo0, hi0, tlo[0], thi[0]);
 #pragma unroll
   for (int ph = 0; ph < 2; ++ph) {
-    if (ph == 1) flush_phase<WT, VEC, 1>(acc, As, Bs, rc, ru, g, I0, J0, wi, wj, lo1, hi1, tlo[1], thi[1]);
+    if (ph == 1) flush_phase<WT, VEC, 1>(acc, sm, rc, ru, g, I0, J0, wi, wj, lo1, hi1, tlo[1], thi[1]);
     // epilogue of the phase: C += D after the down products, Y += D + R after the right ones
 #pragma unroll
     for (int a = 0; a < H; ++a)
@@ -325,6 +349,14 @@ __global__ __launch_bounds__(256, 2) void flush_tiles_mfma_kernel(float* __restr
   }
 }
 
+bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+bool strides_mult4(const BatchMap& bm) {
+  for (int d = 0; d < bm.nd; ++d)
+    if (bm.stride[d] % 4) return false;
+  return true;
+}
+
 // Workgroups (target blocks of WT x WT tiles) of one launch, per batch entry.
 template <int WT>
 int64_t count_items(const TileFlush& g) {
@@ -338,21 +370,16 @@ int64_t count_items(const TileFlush& g) {
   return items;
 }
 
-template <int WT>
+template <int WT, bool VEC>
 int launch(float* y, float* c, const float* e, const float* l, const float* u, const TileFlush& g,
            const BatchMap& lmap, const BatchMap& umap, int64_t B, hipStream_t stream) {
   const int64_t items = count_items<WT>(g);
   if (items == 0 || B == 0) return 0;
   if (items > 0x7fffffff) return GPTQ2D_EUNSUPPORTED;
-  const bool vec = g.m % 4 == 0 && g.n % 4 == 0;
   for (int64_t b0 = 0; b0 < B; b0 += 65535) {
     const dim3 grid((unsigned)items, (unsigned)(B - b0 < 65535 ? B - b0 : 65535));
-    if (vec)
-      hipLaunchKernelGGL((flush_tiles_mfma_kernel<WT, true>), grid, dim3(256), 0, stream, y, c, e, l, u, g, lmap,
-                         umap, b0);
-    else
-      hipLaunchKernelGGL((flush_tiles_mfma_kernel<WT, false>), grid, dim3(256), 0, stream, y, c, e, l, u, g, lmap,
-                         umap, b0);
+    hipLaunchKernelGGL((flush_tiles_mfma_kernel<WT, VEC>), grid, dim3(256), 0, stream, y, c, e, l, u, g, lmap, umap,
+                       b0);
   }
   return (int)hipGetLastError();
 }
@@ -366,7 +393,12 @@ int gptq2d_flush_tiles_mfma(float* y, float* c, const float* e, const float* l, 
   TileFlush g{m, n, cdiv(m, TS), cdiv(n, TS), S0, S1, S_end};
   // 4 x 4 tiles per workgroup when there are enough of them to fill the chip (two per CU); else
   // 2 x 2, four times as many workgroups, each k-tile a quarter of the MFMAs (the first and last
-  // flushes of a sweep, where a few long items would otherwise set the launch time)
-  if (S1 - S0 >= 4 && count_items<4>(g) * B >= 512) return launch<4>(y, c, e, l, u, g, lmap, umap, B, stream);
-  return launch<2>(y, c, e, l, u, g, lmap, umap, B, stream);
+  // flushes of a sweep, where a few long items would otherwise set the launch time).  Rows whose
+  // length is not a multiple of 4 (or matrices not 16-byte aligned) are staged 32 bits at a time,
+  // in 2 x 2 blocks only.
+  const bool vec = m % 4 == 0 && n % 4 == 0 && aligned16(y) && aligned16(c) && aligned16(e) && aligned16(l) &&
+                   aligned16(u) && strides_mult4(lmap) && strides_mult4(umap);
+  if (!vec) return launch<2, false>(y, c, e, l, u, g, lmap, umap, B, stream);
+  if (S1 - S0 >= 4 && count_items<4>(g) * B >= 512) return launch<4, true>(y, c, e, l, u, g, lmap, umap, B, stream);
+  return launch<2, true>(y, c, e, l, u, g, lmap, umap, B, stream);
 }
