@@ -33,6 +33,9 @@ COMMON_FLAGS = [
     f"-I{CSRC}",
 ]
 
+# Libraries linked in: rocBLAS's fp32 GEMM serves the dense products of the triangular inverse.
+LINK_LIBS = ["-L/opt/rocm/lib", "-lrocblas"]
+
 # Per-file extra flags.  The trellis search must not contract a*b+c into fma: its costs are
 # compared for exact ties and must equal the reference's unfused sums.
 EXTRA_FLAGS = {
@@ -59,7 +62,7 @@ def build(verbose: bool = False) -> pathlib.Path:
     with concurrent.futures.ThreadPoolExecutor(workers) as pool:
         objs = list(pool.map(_compile, sources))
     tmp = LIB.with_suffix(".so.tmp")
-    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
+    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), *LINK_LIBS, "-o", str(tmp)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stdout}\n{res.stderr}")

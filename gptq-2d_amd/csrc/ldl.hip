@@ -7,7 +7,8 @@
 // its diagonal (size 1) or, for size p, (L_raw - D) D^{-1} + I with D the p x p block diagonal.
 // ldl(M, size) is the same normalisation applied to the Cholesky factor of M itself.
 //
-// Device work, all on the caller's stream, no host synchronisation, no allocation:
+// Device work, all on the caller's stream, no host synchronisation, no device allocation by this
+// library:
 //   1. W = J M J: the reversal of the flat array.
 //   2. Right-looking blocked Cholesky of W in place, panels of NB columns: one launch factors the
 //      diagonal block (redundantly in every workgroup, in LDS) and solves the panel below against
@@ -16,7 +17,12 @@
 //   3. ldl_of_inverse only: C^{-1} in place by recursive doubling.  Diagonal NB blocks are inverted
 //      by one wave each; then for s = NB, 2 NB, ... every pair of inverted s-blocks A^{-1}, D^{-1}
 //      with off-diagonal block B becomes one inverted 2s-block through -D^{-1} (B A^{-1}) -- two
-//      triangular GEMMs per level, all pairs of a level in one batched launch.
+//      triangular GEMMs per level, all pairs of a level in one batched launch.  For fp32 and
+//      k >= 512 these are rocBLAS's strided-batched sgemm (a plain library GEMM: dense, on
+//      triangles padded with the zeros of W's cleared upper triangle; at k = 8192 that is twice the
+//      triangular flops at ~130 TFLOP/s, against ~40 TFLOP/s for the triangular MFMA kernel of
+//      gemm.hip), with the unused part of the output buffer as the GEMM's workspace; the rocBLAS
+//      handle of a device and host thread is created on first use.
 //   4. Normalisation into L (LDS-tiled transposed read for ldl_of_inverse).
 //
 // A non-positive (or NaN) pivot records its 1-based column in `info` (device int, 0 when the
@@ -25,6 +31,10 @@
 // Reference: IST-DASLab/GPTQ-2D gptq_2d_reference.py:29-55 (_unit_diagonal_blocks, ldl_of_inverse,
 // ldl), which call torch.linalg.cholesky and solve_triangular.
 #include "linalg.h"
+
+#include <rocblas/rocblas.h>
+
+#include <unordered_map>
 
 namespace {
 
@@ -403,13 +413,67 @@ int cholesky_inplace(T* w, int64_t k, int* info, hipStream_t stream) {
   return 0;
 }
 
-// In-place inverse of the lower triangular W (k x k); tmp holds >= k*k/4 + k elements.
+// Zero the strict upper triangle of W (k x k), one row per workgroup.
+template <typename T>
+__global__ __launch_bounds__(256) void zero_upper_kernel(T* __restrict__ w, int64_t k) {
+  for (int64_t i = blockIdx.x; i < k; i += gridDim.x)
+    for (int64_t j = i + 1 + threadIdx.x; j < k; j += 256) w[i * k + j] = T(0);
+}
+
+// rocBLAS handle of the current device for this host thread, created on first use and kept until
+// the process ends.
+rocblas_handle blas_handle() {
+  thread_local std::unordered_map<int, rocblas_handle> handles;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return nullptr;
+  const auto it = handles.find(dev);
+  if (it != handles.end()) return it->second;
+  rocblas_handle h = nullptr;
+  if (rocblas_create_handle(&h) != rocblas_status_success) return nullptr;
+  handles.emplace(dev, h);
+  return h;
+}
+
+// Row-major, strided-batched D = alpha A B + beta D (A: M x K, B: K x N) on rocBLAS's fp32 GEMM,
+// as the column-major product D^T = B^T A^T; `ws` (ws_bytes) is the GEMM's workspace, so that
+// rocBLAS allocates nothing.
+int blas_gemm_rm(int64_t M, int64_t N, int64_t K, int64_t batch, const float* A, int64_t lda, int64_t sa,
+                 const float* B, int64_t ldb, int64_t sb, float* D, int64_t ldd, int64_t sd, float alpha, float beta,
+                 void* ws, size_t ws_bytes, hipStream_t stream) {
+  rocblas_handle h = blas_handle();
+  if (!h || rocblas_set_stream(h, stream) != rocblas_status_success ||
+      rocblas_set_workspace(h, ws, ws_bytes) != rocblas_status_success)
+    return GPTQ2D_EUNSUPPORTED;
+  const rocblas_status st = rocblas_sgemm_strided_batched(
+      h, rocblas_operation_none, rocblas_operation_none, (rocblas_int)N, (rocblas_int)M, (rocblas_int)K, &alpha, B,
+      (rocblas_int)ldb, sb, A, (rocblas_int)lda, sa, &beta, D, (rocblas_int)ldd, sd, (rocblas_int)batch);
+  return st == rocblas_status_success ? 0 : GPTQ2D_EUNSUPPORTED;
+}
+
+// In-place inverse of the lower triangular W (k x k); tmp holds >= k*k/4 + k elements, and for
+// fp32 the rest of a k x k buffer behind it serves as GEMM workspace.
 template <typename T>
 int trtri_inplace(T* w, int64_t k, T* tmp, hipStream_t stream) {
   constexpr int NB = LdlBlock<T>::NB;
   int rc;
   hipLaunchKernelGGL((trtri_leaf_kernel<T, NB>), dim3((unsigned)cdiv(k, NB)), dim3(64), 0, stream, w, k, k);
   if ((rc = (int)hipGetLastError())) return rc;
+  // fp32 from k = 512 on: every level's two products run as dense GEMMs on rocBLAS, the triangular
+  // operands padded with the zeros of W's cleared upper triangle; the GEMM workspace (up to 64 MiB)
+  // is the part of the k x k buffer behind tmp that the levels do not use
+  void* ws = nullptr;
+  size_t ws_bytes = 0;
+  bool blas = false;
+  if constexpr (sizeof(T) == 4) {
+    const uintptr_t lo = ((uintptr_t)(tmp + k * k / 4 + k) + 255) & ~(uintptr_t)255, hi = (uintptr_t)(tmp + k * k);
+    blas = k >= 512 && hi > lo;
+    if (blas) {
+      ws = (void*)lo;
+      ws_bytes = hi - lo < ((size_t)64 << 20) ? hi - lo : ((size_t)64 << 20);
+      hipLaunchKernelGGL(zero_upper_kernel<T>, dim3((unsigned)(k < 8192 ? k : 8192)), dim3(256), 0, stream, w, k);
+      if ((rc = (int)hipGetLastError())) return rc;
+    }
+  }
   for (int64_t s = NB; s < k; s *= 2) {
     const int64_t full = k / (2 * s);                  // pairs with two full s-blocks
     const int64_t tail_r1 = full * 2 * s + s;          // a last, short pair starts its D block here
@@ -419,6 +483,19 @@ int trtri_inplace(T* w, int64_t k, T* tmp, hipStream_t stream) {
       if (pairs == 0) continue;
       const int64_t r0 = part == 0 ? 0 : full * 2 * s;
       const int64_t s2 = part == 0 ? s : tail;
+      if constexpr (sizeof(T) == 4) {
+        if (blas) {
+          const int64_t bs = 2 * s * k + 2 * s;
+          // T = B A^{-1}, then B <- -D^{-1} T
+          if ((rc = blas_gemm_rm(s2, s, s, pairs, w + (r0 + s) * k + r0, k, bs, w + r0 * k + r0, k, bs, tmp, s,
+                                 s2 * s, 1.f, 0.f, ws, ws_bytes, stream)))
+            return rc;
+          if ((rc = blas_gemm_rm(s2, s, s2, pairs, w + (r0 + s) * k + (r0 + s), k, bs, tmp, s, s2 * s,
+                                 w + (r0 + s) * k + r0, k, bs, -1.f, 0.f, ws, ws_bytes, stream)))
+            return rc;
+          continue;
+        }
+      }
       // T = B A^{-1}: (s2 x s) = (s2 x s) (s x s, lower)
       GemmProblem<T> g{};
       g.M = s2;

@@ -92,9 +92,11 @@ def _check_factor(got, m, size, inverse, tol):
     assert off.item() < 50 * tol, off.item()
 
 
-@pytest.mark.parametrize("k", [1, 5, 64, 65, 100, 257, 600])
+@pytest.mark.parametrize("k", [1, 5, 64, 65, 100, 257, 600, 777, 1536])
 @pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
 def test_ldl_of_inverse(k, dtype):
+    """Sizes from 512 on take the fp32 path whose inverse levels run on rocBLAS (600, 777: short
+    last pairs; 1536: three full levels and a short one)."""
     print(f"ldl_of_inverse k={k} {dtype}", flush=True)
     m = instances.wishart_factor(k, .5, 10 + k).to(dtype).to(DEV)
     got = LDL.ldl_of_inverse(m)
