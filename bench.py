@@ -47,6 +47,14 @@ VALU_FP32_OPS_PEAK = 39.3e12
 # sweep 27.7 ms (flush 72.9 TFLOP/s), 1024 -> 26.1 ms (81.0), 2048 -> 28.0 ms (83.1).  It changes
 # the order of the fp32 additions only, not the algorithm.
 OUTER_BLOCK = 1024
+# HBM bytes per outer-flush launch at OUTER_BLOCK on the headline layer, mean over a step's 15
+# launches: rocprofv3 FETCH_SIZE and WRITE_SIZE passes (one counter per run) over this benchmark,
+# each scaled by what the same counter reads for a plain 256 MiB copy kernel in the same run
+# (x1.9998 and x1.0000).  Counters cannot be read inside the timed run, so the figure is the
+# measured one, with the command and per-kernel values in profiles/flush_traffic_H_int4.md; the
+# algorithmic minimum (every operand once) is FLUSH_ALGORITHMIC_BYTES.
+FLUSH_TRAFFIC_BYTES = 1.839e9
+FLUSH_ALGORITHMIC_BYTES = 0.525e9
 # fp32 VALU operations per trellis state evaluation: 2 sub, 2 mul, 1 add (the squared distance),
 # 1 add (the predecessor group's minimum), 1 min.
 OPS_PER_STATE_EVAL = 7
@@ -231,7 +239,9 @@ def main() -> int:
         "peak": FP32_MFMA_PEAK_TFLOPS,
         "unit": "TFLOP/s",
         "frac": achieved / FP32_MFMA_PEAK_TFLOPS if achieved else None,
-        "traffic": None,
+        "traffic": FLUSH_TRAFFIC_BYTES if (m, n) == (8192, 8192) and OUTER_BLOCK == 1024 else None,
+        "traffic_unit": "B per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-calibrated)",
+        "traffic_algorithmic": FLUSH_ALGORITHMIC_BYTES if (m, n) == (8192, 8192) and OUTER_BLOCK == 1024 else None,
         "kernel": "cross-tile feedback panels (flush), fp32",
         "launches": flush_n // max(1, args.steps),
         "avg_launch_us": avg_us,

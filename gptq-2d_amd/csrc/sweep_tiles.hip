@@ -5,11 +5,12 @@
 // stages T = I + J of tiles: the tiles of one coarse stage do not depend on each other, and each
 // is swept by one workgroup entirely in LDS -- its 2*TR-1 antidiagonals one after another, every
 // entry of an antidiagonal at once, the in-tile error feedback through the diagonal blocks
-// L[I,I] and U[J,J], the quantizer applied in place.  Feedback between tiles is the block flush
-// of flush.hip with P = Q = TR: after each coarse stage into the rest of its outer block, and after
-// each outer block of `outer_tiles` coarse stages into all later stages.  The host loop below
-// issues every launch of the sweep from C++ in one call, so a whole layer is one C-ABI call and
-// one capturable stream of kernels.
+// L[I,I] and U[J,J], the quantizer applied in place.  Feedback between tiles: after each outer
+// block of `outer_tiles` coarse stages, the block flush of flush.hip with P = Q = TR (on MFMA for
+// fp32) into all later stages; inside an outer block, fp32 tiles pull the feedback of the block's
+// earlier tiles on MFMA (tile_stage_kernel), fp64 stages are flushed into the rest of the block
+// after each coarse stage.  The host loop below issues every launch of the sweep from C++ in one
+// call, so a whole layer is one C-ABI call and one capturable stream of kernels.
 //
 // In exact arithmetic the result equals the reference's blocked sweep (gptq_2d.py:1295-1375) and
 // Algorithm 1 on vec(X) (GPTQ-2D paper, Theorem 1); in floating point the sums are accumulated in
