@@ -140,10 +140,39 @@ __device__ __forceinline__ void flush_phase(floatx16 (&acc)[WT / 2][WT / 2], Flu
   constexpr int PER = 64 * W;             // floats per wave load
   constexpr int NI = L::PANEL / PER / 4;  // loads per wave per panel and k-tile
   const int tid = threadIdx.x, lane = tid & 63, li = lane & 31, hh = lane >> 5;
-  const int wave = tid >> 6;
-  const int64_t kmax = PHASE == 0 ? g.m : g.n;  // k extent of both operands
-  const int64_t alda = PHASE == 0 ? g.m : g.n;  // row stride of A (L or C)
-  const int s0 = (int)g.S0, s1 = (int)g.S1;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: LDS bases in scalar registers
+  const int kmax = (int)(PHASE == 0 ? g.m : g.n);  // k extent of both operands
+  const int alda = (int)(PHASE == 0 ? g.m : g.n);  // row stride of A (L or C)
+  const int gm = (int)g.m, gn = (int)g.n, s0 = (int)g.S0, s1 = (int)g.S1;  // < 2^15: 32-bit index math
+
+  // per-lane staging geometry of load x: A row i (tile at, k offset akk), B column j (tile bt, k row
+  // kb); loop-invariant, so kept in registers for the 128-bit path (NI = 4) and recomputed for the
+  // 32-bit one
+  struct Geo {
+    int a_off, a_t, a_kk, b_off, b_t, b_kb;
+    bool a_in, b_in;
+  };
+  auto geo = [&](int x) {
+    Geo o;
+    const int f = (wave + 4 * x) * PER + lane * W;
+    const int row = f / TS;
+    o.a_kk = 4 * (((f % TS) / 4) ^ (row & 7)) + f % 4;
+    const int i = (int)I0 * TS + row;
+    o.a_in = i < gm;
+    o.a_t = i >> 5;
+    o.a_off = ((o.a_in ? i * alda : 0) + o.a_kk) * 4;
+    o.b_kb = f / ROWS;
+    const int j = (int)J0 * TS + f % ROWS;
+    o.b_in = j < gn;
+    o.b_t = j >> 5;
+    o.b_off = (o.b_kb * gn + (o.b_in ? j : 0)) * 4;
+    return o;
+  };
+  Geo pre[VEC ? NI : 1];
+  if constexpr (VEC) {
+#pragma unroll
+    for (int x = 0; x < NI; ++x) pre[x] = geo(x);
+  }
 
   // loads of k-tile t into buffer buf, each masked to what a product may read (L strictly below its
   // diagonal tiles, C and E on the band, U strictly above its diagonal tiles, nothing outside)
@@ -151,19 +180,14 @@ __device__ __forceinline__ void flush_phase(floatx16 (&acc)[WT / 2][WT / 2], Flu
     const int ts = (int)t, k0 = ts * TS;
 #pragma unroll
     for (int x = 0; x < NI; ++x) {
-      const int f0 = (wave + 4 * x) * PER, f = f0 + lane * W;
-      const int row = f / TS, kk = 4 * (((f % TS) / 4) ^ (row & 7)) + f % 4;
-      const int64_t i = I0 * TS + row;
-      const int at = (int)(i >> 5);
-      const bool aband = PHASE == 0 ? ts < at : (at + ts >= s0 && at + ts < s1);
-      const bool aok = i < g.m && aband && k0 + kk < kmax;
-      dma_load<W>(ra_src, &sm.a[buf][f0], aok ? (int)(i * alda + k0 + kk) * 4 : OOB);
-      const int kb = f / ROWS;
-      const int64_t j = J0 * TS + f % ROWS;
-      const int bt = (int)(j >> 5);
-      const bool bband = PHASE == 0 ? (ts + bt >= s0 && ts + bt < s1) : ts < bt;
-      const bool bok = j < g.n && bband && k0 + kb < kmax;
-      dma_load<W>(rb_src, &sm.b[buf][f0 + f0 / 256 * L::BPAD], bok ? (int)((k0 + kb) * g.n + j) * 4 : OOB);
+      const Geo o = VEC ? pre[x] : geo(x);
+      const int f0 = (wave + 4 * x) * PER;
+      const bool aband = PHASE == 0 ? ts < o.a_t : (o.a_t + ts >= s0 && o.a_t + ts < s1);
+      const bool aok = o.a_in && aband && k0 + o.a_kk < kmax;
+      dma_load<W>(ra_src, &sm.a[buf][f0], aok ? o.a_off + k0 * 4 : OOB);
+      const bool bband = PHASE == 0 ? (ts + o.b_t >= s0 && ts + o.b_t < s1) : ts < o.b_t;
+      const bool bok = o.b_in && bband && k0 + o.b_kb < kmax;
+      dma_load<W>(rb_src, &sm.b[buf][f0 + f0 / 256 * L::BPAD], bok ? o.b_off + k0 * gn * 4 : OOB);
     }
   };
 
