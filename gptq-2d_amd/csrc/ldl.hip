@@ -10,10 +10,14 @@
 // Device work, all on the caller's stream, no host synchronisation, no device allocation by this
 // library:
 //   1. W = J M J: the reversal of the flat array.
-//   2. Right-looking blocked Cholesky of W in place, panels of NB columns: one launch factors the
-//      diagonal block (redundantly in every workgroup, in LDS) and solves the panel below against
-//      it, one thread per row (potrf_panel_kernel); the trailing lower triangle takes the rank-NB
-//      update on the GEMM (fp32: MFMA).
+//   2. Right-looking blocked Cholesky of W in place, panels of NB columns: a panel's diagonal
+//      block is factored (redundantly in every workgroup) and the panel below solved against it;
+//      the trailing lower triangle takes the rank-NB update.  fp32 runs it with a look-ahead of one
+//      panel on the one stream: after a panel, a strip launch updates only the next panel's
+//      columns, and the next panel's factorisation shares one launch (panel_step_kernel) with the
+//      rest of the previous trailing update, on disjoint columns -- the latency-bound panel runs
+//      beside the MFMA update instead of after it.  fp64 (and fp32 with k % 4 != 0) keep the plain
+//      sequence, the update on gemm.hip.
 //   3. ldl_of_inverse only: C^{-1} in place by recursive doubling.  Diagonal NB blocks are inverted
 //      by one wave each; then for s = NB, 2 NB, ... every pair of inverted s-blocks A^{-1}, D^{-1}
 //      with off-diagonal block B becomes one inverted 2s-block through -D^{-1} (B A^{-1}) -- two
@@ -143,11 +147,20 @@ __device__ __forceinline__ void quad_solve(T (&x)[PB / 4], int q, const T* __res
 // loads and stores): four lanes share a row, lane q owning the columns c = q mod 4, and the
 // forward substitution runs column by column with the finished x_t broadcast inside the quad.
 template <typename T, int PB>
-__global__ __launch_bounds__(256) void potrf_panel_kernel(T* __restrict__ w, int64_t ld, int64_t j0, int n,
-                                                          int64_t k, int* __restrict__ info) {
-  constexpr int CP = PB + 1;  // odd pitch: row and column walks are both conflict-free
-  __shared__ T a[PB * CP];
-  __shared__ T rs[64 * CP];
+struct PotrfLds {
+  static constexpr int CP = PB + 1;  // odd pitch: row and column walks are both conflict-free
+  T a[PB * CP];
+  T rs[64 * CP];
+};
+
+// Panel j0 as above, for workgroup `bid` of `nblk` taking part (the panel's row chunks are dealt
+// over them).
+template <typename T, int PB>
+__device__ __forceinline__ void potrf_panel(PotrfLds<T, PB>& sm, T* __restrict__ w, int64_t ld, int64_t j0, int n,
+                                            int64_t k, int* __restrict__ info, int64_t bid, int64_t nblk) {
+  constexpr int CP = PB + 1;
+  T* a = sm.a;
+  T* rs = sm.rs;
   const int tid = threadIdx.x;
   for (int t = tid; t < PB * PB; t += 256) {
     const int r = t / PB, c = t % PB;
@@ -173,10 +186,10 @@ __global__ __launch_bounds__(256) void potrf_panel_kernel(T* __restrict__ w, int
 #pragma unroll
       for (int c = 0; c < PB; ++c) a[r * CP + c] = row[c];
     }
-    if (blockIdx.x == 0 && tid == 0 && bad && info[0] == 0) info[0] = (int)(j0 + bad);
+    if (bid == 0 && tid == 0 && bad && info[0] == 0) info[0] = (int)(j0 + bad);
   }
   __syncthreads();
-  if (blockIdx.x == 0) {
+  if (bid == 0) {
     for (int t = tid; t < PB * PB; t += 256) {
       const int r = t / PB, c = t % PB;
       if (r < n && c <= r) w[(j0 + r) * ld + j0 + c] = a[r * CP + c];
@@ -185,7 +198,7 @@ __global__ __launch_bounds__(256) void potrf_panel_kernel(T* __restrict__ w, int
   if (n < PB) return;
   const int64_t first = j0 + PB;
   const int q = tid & 3, rr = tid >> 2;
-  for (int64_t r0 = first + (int64_t)blockIdx.x * 64; r0 < k; r0 += (int64_t)gridDim.x * 64) {
+  for (int64_t r0 = first + bid * 64; r0 < k; r0 += nblk * 64) {
     __syncthreads();
     for (int t = tid; t < 64 * PB; t += 256) {
       const int i = t / PB, c = t % PB;
@@ -204,6 +217,13 @@ __global__ __launch_bounds__(256) void potrf_panel_kernel(T* __restrict__ w, int
       if (r0 + i < k) w[(r0 + i) * ld + j0 + c] = rs[i * CP + c];
     }
   }
+}
+
+template <typename T, int PB>
+__global__ __launch_bounds__(256) void potrf_panel_kernel(T* __restrict__ w, int64_t ld, int64_t j0, int n,
+                                                          int64_t k, int* __restrict__ info) {
+  __shared__ PotrfLds<T, PB> sm;
+  potrf_panel<T, PB>(sm, w, ld, j0, n, k, info, blockIdx.x, gridDim.x);
 }
 
 // One wave per diagonal NB block of the lower triangular W: replace it by its inverse.
@@ -309,30 +329,30 @@ __global__ __launch_bounds__(256) void normalize_block_kernel(T* __restrict__ ou
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
-// Trailing update of one Cholesky panel on fp32 MFMA: D -= P P^T on the lower triangle of the
-// trailing square D = W[r0.., r0..] (R x R), P = W[r0.., r0-K .. r0) the solved panel.  One
-// workgroup per 64 x 64 lower tile, numbered along the triangle and re-numbered so that each XCD
-// (own L2) runs a contiguous share; it issues all its loads at once -- its D block into the
-// accumulators, both 64 x K panels through LDS as float4 -- then 16 MFMAs (32x32x2) per 32 k,
+// Trailing update of one Cholesky panel on fp32 MFMA: D -= P P^T on the lower triangle of a
+// trailing square D = W[r0.., r0..] (R x R), P = W[r0.., pc .. pc + K) the solved panel.  One
+// workgroup per 64 x 64 lower tile (ti, tj); it issues all its loads at once -- its D block into
+// the accumulators, both 64 x K panels through LDS as float4 -- then 16 MFMAs (32x32x2) per 32 k,
 // A negated so that the accumulation is D - P P^T directly.  Lane layout as in gemm.hip.
 template <int K>
-__global__ __launch_bounds__(256) void syrk_lower_kernel(float* __restrict__ w, int64_t ld, int64_t r0, int64_t R) {
-  constexpr int TP = 64, PP = K + 4;
-  __shared__ __align__(16) float As[TP * PP];
-  __shared__ __align__(16) float Bs[TP * PP];
-  const int64_t n = gridDim.x, lin = blockIdx.x;
-  const int64_t base = n / 8, extra = n % 8, xcd = lin % 8;
-  const int64_t id = xcd * base + (xcd < extra ? xcd : extra) + lin / 8;
-  int64_t ti = (int64_t)((sqrt(8.0 * (double)id + 1.0) - 1.0) * 0.5);
-  while ((ti + 1) * (ti + 2) / 2 <= id) ++ti;
-  while (ti * (ti + 1) / 2 > id) --ti;
-  const int64_t tj = id - ti * (ti + 1) / 2;
+struct SyrkLds {
+  static constexpr int PP = K + 4;
+  float a[64 * PP];
+  float b[64 * PP];
+};
+
+template <int K>
+__device__ __forceinline__ void syrk_tile(SyrkLds<K>& sm, float* __restrict__ w, int64_t ld, int64_t r0, int64_t R,
+                                          int64_t pc, int64_t ti, int64_t tj) {
+  constexpr int TP = 64, PP = SyrkLds<K>::PP;
+  float* As = sm.a;
+  float* Bs = sm.b;
   const int64_t i0 = ti * TP, j0 = tj * TP;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wy = wave >> 1, wx = wave & 1, li = lane & 31, hh = lane >> 5;
   const bool active = !(ti == tj && wy < wx);  // the upper block of a diagonal tile has nothing to do
   float* d = w + r0 * ld + r0;
-  const float* P = w + r0 * ld + (r0 - K);
+  const float* P = w + r0 * ld + pc;
   floatx16 acc;
 #pragma unroll
   for (int e = 0; e < 16; ++e) {
@@ -371,10 +391,87 @@ __global__ __launch_bounds__(256) void syrk_lower_kernel(float* __restrict__ w, 
   }
 }
 
+// Tile (ti, tj) of workgroup lin of n covering a lower triangle of tiles, numbered along the
+// triangle and re-numbered so that each XCD (own L2) runs a contiguous share.
+__device__ __forceinline__ void triangle_tile(int64_t lin, int64_t n, int64_t& ti, int64_t& tj) {
+  const int64_t base = n / 8, extra = n % 8, xcd = lin % 8;
+  const int64_t id = xcd * base + (xcd < extra ? xcd : extra) + lin / 8;
+  ti = (int64_t)((sqrt(8.0 * (double)id + 1.0) - 1.0) * 0.5);
+  while ((ti + 1) * (ti + 2) / 2 <= id) ++ti;
+  while (ti * (ti + 1) / 2 > id) --ti;
+  tj = id - ti * (ti + 1) / 2;
+}
+
+// Whole trailing update of the panel just before r0 (P = W[r0.., r0-K .. r0)).
+template <int K>
+__global__ __launch_bounds__(256) void syrk_lower_kernel(float* __restrict__ w, int64_t ld, int64_t r0, int64_t R) {
+  __shared__ __align__(16) SyrkLds<K> sm;
+  int64_t ti, tj;
+  triangle_tile(blockIdx.x, gridDim.x, ti, tj);
+  syrk_tile<K>(sm, w, ld, r0, R, r0 - K, ti, tj);
+}
+
+// The first K columns of a trailing update (the next panel's columns, every row): tile (x, 0).
+template <int K>
+__global__ __launch_bounds__(256) void syrk_strip_kernel(float* __restrict__ w, int64_t ld, int64_t r0, int64_t R,
+                                                         int64_t pc) {
+  __shared__ __align__(16) SyrkLds<K> sm;
+  syrk_tile<K>(sm, w, ld, r0, R, pc, blockIdx.x, 0);
+}
+
+// Look-ahead step of the fp32 Cholesky: workgroups [0, n_potrf) factor and solve panel j0; the
+// others apply the rest of the previous panel's trailing update (the square W[r0.., r0..], R x R,
+// P = W[r0.., pc .. pc + K), its first K columns -- panel j0 -- already updated by the strip
+// kernel).  The two touch disjoint columns, so the panel's latency-bound factorisation runs beside
+// the throughput-bound update.
+template <int PB>
+__global__ __launch_bounds__(256) void panel_step_kernel(float* __restrict__ w, int64_t ld, int64_t j0, int n,
+                                                         int64_t k, int* __restrict__ info, int64_t n_potrf,
+                                                         int64_t r0, int64_t R, int64_t pc) {
+  __shared__ __align__(16) union {
+    PotrfLds<float, PB> p;
+    SyrkLds<PB> s;
+  } sm;
+  if ((int64_t)blockIdx.x < n_potrf) {
+    potrf_panel<float, PB>(sm.p, w, ld, j0, n, k, info, blockIdx.x, n_potrf);
+    return;
+  }
+  int64_t ti, tj;
+  triangle_tile(blockIdx.x - n_potrf, gridDim.x - n_potrf, ti, tj);
+  syrk_tile<PB>(sm.s, w, ld, r0, R, pc, ti, tj);
+}
+
 template <typename T>
 int cholesky_inplace(T* w, int64_t k, int* info, hipStream_t stream) {
   constexpr int PB = LdlBlock<T>::PB;
   int rc;
+  if constexpr (sizeof(T) == 4) {
+    if (k % 4 == 0) {
+      // look-ahead: panel j0's update of the next panel's columns runs on its own (strip); the rest
+      // of its trailing update runs in the launch that factors the next panel
+      int64_t pr0 = 0, pR = 0, ppc = 0;  // rest update still to apply
+      for (int64_t j0 = 0; j0 < k; j0 += PB) {
+        const int n = k - j0 < PB ? (int)(k - j0) : PB;
+        const int64_t rest = k - j0 - PB;
+        const int64_t blocks = rest > 0 ? (cdiv(rest, 64) < 256 ? cdiv(rest, 64) : 256) : 1;
+        const int64_t nt = pR > 0 ? cdiv(pR, 64) : 0;
+        hipLaunchKernelGGL((panel_step_kernel<PB>), dim3((unsigned)(blocks + nt * (nt + 1) / 2)), dim3(256), 0, stream,
+                           (float*)w, k, j0, n, k, info, blocks, pr0, pR, ppc);
+        if ((rc = (int)hipGetLastError())) return rc;
+        pR = 0;
+        if (rest <= 0) break;
+        hipLaunchKernelGGL((syrk_strip_kernel<PB>), dim3((unsigned)cdiv(rest, 64)), dim3(256), 0, stream, (float*)w,
+                           k, j0 + PB, rest, j0);
+        if ((rc = (int)hipGetLastError())) return rc;
+        if (rest > PB) {
+          pr0 = j0 + 2 * PB;
+          pR = rest - PB;
+          ppc = j0;
+        }
+      }
+      return 0;
+    }
+  }
   for (int64_t j0 = 0; j0 < k; j0 += PB) {
     const int n = k - j0 < PB ? (int)(k - j0) : PB;
     const int64_t rest = k - j0 - PB;
@@ -383,15 +480,6 @@ int cholesky_inplace(T* w, int64_t k, int* info, hipStream_t stream) {
     if ((rc = (int)hipGetLastError())) return rc;
     if (rest <= 0) break;
     // trailing lower triangle: W22 -= P P^T with P = W[j0+PB:, j0:j0+PB]
-    if constexpr (sizeof(T) == 4) {
-      if (k % 4 == 0) {
-        const int64_t nt = cdiv(rest, 64);
-        hipLaunchKernelGGL((syrk_lower_kernel<PB>), dim3((unsigned)(nt * (nt + 1) / 2)), dim3(256), 0, stream, w, k,
-                           j0 + PB, rest);
-        if ((rc = (int)hipGetLastError())) return rc;
-        continue;
-      }
-    }
     GemmProblem<T> g{};
     g.M = g.N = rest;
     g.K = PB;
