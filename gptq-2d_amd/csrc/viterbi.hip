@@ -8,10 +8,12 @@
 // closest path ends in the first argmin of cost_{last}, and each earlier state is the first
 // argmin over h of cost_{t-1}(h G + (state_t >> KV)).
 //
-// One workgroup (1024 threads) per sequence runs every step of both tail-biting passes: the group
-// minima of the previous step sit in LDS (double-buffered, or read back from the history when 2 G
-// values do not fit), each thread evaluates the 2^KV predecessors of its groups in order, and every
-// step's minima are also stored in an HBM history [steps - 1][G] per sequence.  The final argmin is a
+// One workgroup (1024 threads) per one or two sequences runs every step of both tail-biting passes
+// (two when 512 rows or more fill the chip and their minima fit in LDS: each table entry, read from
+// L2 once per step, then serves both -- the table reads, not the arithmetic, bound the search): the
+// group minima of the previous step sit in LDS (double-buffered, or read back from the history when
+// 2 G values do not fit), each thread evaluates the 2^KV predecessors of its groups in order, and
+// every step's minima are also stored in an HBM history [steps - 1][G] per sequence.  The final argmin is a
 // block reduction; the walk back is done by one wave that recomputes the 2^KV candidate costs of the
 // path's group at each step from the history -- the exact operations of the forward pass, so it picks
 // the predecessor the search picked.  Tail-biting: pass 1 reads x rotated by half a sequence
@@ -98,71 +100,102 @@ struct Sequence {
   }
 };
 
-// Forward pass: history[t][j] = best_t(j) for t < steps - 1; returns (in *state_out, shared) the
-// first argmin of cost_{last} under the masks.  prev_lds: 2 G values of LDS or nullptr.
-template <typename T, int V>
-__device__ void forward_pass(const Sequence<T, V>& seq, const T* __restrict__ table, T* __restrict__ hist,
-                             T* prev_lds, const SearchGeom& g, int roll, bool masked, int64_t overlap,
-                             int64_t* best_state, T* red_v, int64_t* red_i) {
+// Forward pass of NS sequences in lockstep (the workgroup's): history_k[t][j] = best_t(j) of sequence
+// k for t < steps - 1, and best_state[k] the first argmin of its cost_{last} under the masks.  Each
+// table entry is loaded once per step for all NS sequences.  prev_lds: NS x 2 G values of LDS, or
+// nullptr (then the previous step's minima are read back from the history).  Sequences with
+// live[k] false are computed on a valid stand-in (their x pointer) but write nothing.
+template <typename T, int V, int NS>
+__device__ void forward_pass(const Sequence<T, V> (&seq)[NS], const bool (&live)[NS], const T* __restrict__ table,
+                             T* const (&hist)[NS], T* prev_lds, const SearchGeom& g, int roll, bool masked,
+                             const int64_t (&overlap)[NS], int64_t* best_state, T* red_v, int64_t* red_i) {
   const int tid = threadIdx.x;
   const int64_t G = g.G, H = (int64_t)1 << g.KV;
   const T inf = inf_value<T>();
   for (int t = 0; t + 1 < g.steps; ++t) {
-    T x0, x1;
-    seq.at(t, roll, x0, x1);
-    const T* prev = t == 0 ? nullptr : (prev_lds ? prev_lds + ((t - 1) & 1) * G : hist + (int64_t)(t - 1) * G);
-    T* cur_lds = prev_lds ? prev_lds + (t & 1) * G : nullptr;
-    T* cur_hist = hist + (int64_t)t * G;
-    for (int64_t j = tid; j < G; j += VT_THREADS) {
-      T best = inf;
-      for (int64_t h = 0; h < H; ++h) {
-        const int64_t s = h * G + j;
-        T c = local_cost<T, V>(table, s, x0, x1);
-        if (t == 0) {
-          if (masked && (s >> g.KV) != overlap) c = inf;
-        } else {
-          c = prev[s >> g.KV] + c;
+    T x0[NS], x1[NS];
+    const T* prev[NS];
+    T* cur_lds[NS];
+#pragma unroll
+    for (int k = 0; k < NS; ++k) {
+      seq[k].at(t, roll, x0[k], x1[k]);
+      T* pl = prev_lds ? prev_lds + k * 2 * G : nullptr;
+      // at t = 0 a readable stand-in (its values are not used): the branch-free step below reads it
+      prev[k] = t == 0 ? (pl ? pl : hist[k]) : (pl ? pl + ((t - 1) & 1) * G : hist[k] + (int64_t)(t - 1) * G);
+      cur_lds[k] = pl ? pl + (t & 1) * G : nullptr;
+    }
+    // 32-bit state arithmetic (2^L <= 2^24 states)
+    const int G32 = (int)G, H32 = (int)H, kv = g.KV;
+    for (int j = tid; j < G32; j += VT_THREADS) {
+      T best[NS];
+#pragma unroll
+      for (int k = 0; k < NS; ++k) best[k] = inf;
+      const bool first = t == 0;
+#pragma unroll 16
+      for (int h = 0; h < H32; ++h) {
+        const int s = h * G32 + j;
+        const T t0 = table[s * V];
+        const T t1 = V == 2 ? table[s * V + 1] : T(0);
+        const int ps = s >> kv;
+#pragma unroll
+        for (int k = 0; k < NS; ++k) {
+          const T d0 = t0 - x0[k];
+          T c = d0 * d0;
+          if constexpr (V == 2) {
+            const T d1 = t1 - x1[k];
+            c = c + d1 * d1;
+          }
+          const T pv = prev[k][ps];
+          c = first ? (masked && ps != overlap[k] ? inf : c) : pv + c;
+          best[k] = fmin(c, best[k]);  // costs are never NaN: the same value as c < best ? c : best
         }
-        best = c < best ? c : best;
       }
-      cur_hist[j] = best;
-      if (cur_lds) cur_lds[j] = best;
+#pragma unroll
+      for (int k = 0; k < NS; ++k) {
+        if (live[k]) hist[k][(int64_t)t * G + j] = best[k];
+        if (cur_lds[k]) cur_lds[k][j] = best[k];
+      }
     }
     __syncthreads();
   }
-  // final step: first argmin over all states
-  T x0, x1;
-  seq.at(g.steps - 1, roll, x0, x1);
+  // final step: first argmin over all states, per sequence
   const int last = g.steps - 1;
-  const T* prev = last == 0 ? nullptr : (prev_lds ? prev_lds + ((last - 1) & 1) * G : hist + (int64_t)(last - 1) * G);
-  T bv = inf;
-  int64_t bi = INT64_MAX;
   const int64_t S = G << g.KV;
-  for (int64_t s = tid; s < S; s += VT_THREADS) {
-    T c = local_cost<T, V>(table, s, x0, x1);
-    if (last == 0) {
-      if (masked && (s >> g.KV) != overlap) c = inf;
-    } else {
-      c = prev[s >> g.KV] + c;
-    }
-    if (masked && (s & (G - 1)) != overlap) c = inf;
-    if (c < bv || bi == INT64_MAX) {  // increasing s per thread: the first, then strictly smaller ones
-      bv = c;
-      bi = s;
-    }
-  }
-  wave_argmin(bv, bi);
   const int wave = tid >> 6, lane = tid & 63;
-  if (lane == 0) {
-    red_v[wave] = bv;
-    red_i[wave] = bi;
+#pragma unroll
+  for (int k = 0; k < NS; ++k) {
+    T x0, x1;
+    seq[k].at(last, roll, x0, x1);
+    T* pl = prev_lds ? prev_lds + k * 2 * G : nullptr;
+    const T* prev = last == 0 ? nullptr : (pl ? pl + ((last - 1) & 1) * G : hist[k] + (int64_t)(last - 1) * G);
+    T bv = inf;
+    int64_t bi = INT64_MAX;
+    for (int64_t s = tid; s < S; s += VT_THREADS) {
+      T c = local_cost<T, V>(table, s, x0, x1);
+      if (last == 0) {
+        if (masked && (s >> g.KV) != overlap[k]) c = inf;
+      } else {
+        c = prev[s >> g.KV] + c;
+      }
+      if (masked && (s & (G - 1)) != overlap[k]) c = inf;
+      if (c < bv || bi == INT64_MAX) {  // increasing s per thread: the first, then strictly smaller ones
+        bv = c;
+        bi = s;
+      }
+    }
+    wave_argmin(bv, bi);
+    if (lane == 0) {
+      red_v[k * (VT_THREADS / 64) + wave] = bv;
+      red_i[k * (VT_THREADS / 64) + wave] = bi;
+    }
   }
   __syncthreads();
-  if (tid == 0) {
-    T v = red_v[0];
-    int64_t i = red_i[0];
-    for (int w = 1; w < VT_THREADS / 64; ++w) arg_better(v, i, red_v[w], red_i[w]);
-    *best_state = i & (S - 1);  // every state is a candidate, so i < S; the mask only keeps reads in bounds
+  if (tid < NS) {
+    const int k = tid;
+    T v = red_v[k * (VT_THREADS / 64)];
+    int64_t i = red_i[k * (VT_THREADS / 64)];
+    for (int w = 1; w < VT_THREADS / 64; ++w) arg_better(v, i, red_v[k * (VT_THREADS / 64) + w], red_i[k * (VT_THREADS / 64) + w]);
+    best_state[k] = i & (S - 1);  // every state is a candidate, so i < S; the mask only keeps reads in bounds
   }
   __syncthreads();
 }
@@ -211,39 +244,66 @@ __device__ int64_t backtrack(const Sequence<T, V>& seq, const T* __restrict__ ta
   return state;
 }
 
-template <typename T, int V>
+// NS sequences per workgroup: rows NS blockIdx.x + k; wave k walks sequence k back.
+template <typename T, int V, int NS>
 __global__ __launch_bounds__(VT_THREADS) void viterbi_kernel(const T* __restrict__ x, const T* __restrict__ table,
                                                              T* __restrict__ hist_all, const T* __restrict__ scale,
                                                              T* __restrict__ out, int64_t* __restrict__ states,
-                                                             int L, int KV, int steps, int tail_biting,
+                                                             int64_t rows, int L, int KV, int steps, int tail_biting,
                                                              int prev_in_lds) {
   extern __shared__ __align__(16) unsigned char smem[];
-  __shared__ T red_v[VT_THREADS / 64];
-  __shared__ int64_t red_i[VT_THREADS / 64];
-  __shared__ int64_t sh_state, sh_overlap;
-  const int64_t row = blockIdx.x;
+  __shared__ T red_v[NS * (VT_THREADS / 64)];
+  __shared__ int64_t red_i[NS * (VT_THREADS / 64)];
+  __shared__ int64_t sh_state[NS], sh_overlap[NS];
   SearchGeom g{L, KV, steps, (int64_t)1 << (L - KV)};
-  Sequence<T, V> seq{x + row * (int64_t)steps * V, steps};
-  T* hist = hist_all + row * (int64_t)(steps > 1 ? steps - 1 : 1) * g.G;
+  Sequence<T, V> seq[NS];
+  bool live[NS];
+  T* hist[NS];
+#pragma unroll
+  for (int k = 0; k < NS; ++k) {
+    const int64_t row = (int64_t)blockIdx.x * NS + k;
+    live[k] = row < rows;
+    const int64_t r = live[k] ? row : rows - 1;  // a valid stand-in for the reads
+    seq[k] = Sequence<T, V>{x + r * (int64_t)steps * V, steps};
+    hist[k] = hist_all + r * (int64_t)(steps > 1 ? steps - 1 : 1) * g.G;
+  }
   T* prev_lds = prev_in_lds ? reinterpret_cast<T*>(smem) : nullptr;
-  const T sc = scale ? scale[row] : T(1);
-  T* orow = out ? out + row * (int64_t)steps * V : nullptr;
-  int64_t* srow = states ? states + row * (int64_t)steps : nullptr;
-  int64_t overlap = 0;
+  const int wave = threadIdx.x >> 6;
+  int64_t overlap[NS];
+#pragma unroll
+  for (int k = 0; k < NS; ++k) overlap[k] = 0;
   if (tail_biting) {
     const int half = steps / 2;
-    forward_pass<T, V>(seq, table, hist, prev_lds, g, steps - half, false, 0, &sh_state, red_v, red_i);
-    if (threadIdx.x < 64) {
-      const int64_t st = backtrack<T, V>(seq, table, hist, g, steps - half, false, 0, sh_state, half, T(1), nullptr,
-                                         nullptr);
-      if (threadIdx.x == 0) sh_overlap = st >> KV;
-    }
+    forward_pass<T, V, NS>(seq, live, table, hist, prev_lds, g, steps - half, false, overlap, sh_state, red_v, red_i);
+#pragma unroll
+    for (int k = 0; k < NS; ++k)
+      if (wave == k && live[k]) {
+        const int64_t st = backtrack<T, V>(seq[k], table, hist[k], g, steps - half, false, 0, sh_state[k], half, T(1),
+                                           nullptr, nullptr);
+        if ((threadIdx.x & 63) == 0) sh_overlap[k] = st >> KV;
+      }
     __syncthreads();
-    overlap = sh_overlap;
+#pragma unroll
+    for (int k = 0; k < NS; ++k) overlap[k] = live[k] ? sh_overlap[k] : 0;
   }
-  forward_pass<T, V>(seq, table, hist, prev_lds, g, 0, tail_biting != 0, overlap, &sh_state, red_v, red_i);
-  if (threadIdx.x < 64)
-    backtrack<T, V>(seq, table, hist, g, 0, tail_biting != 0, overlap, sh_state, 0, sc, orow, srow);
+  forward_pass<T, V, NS>(seq, live, table, hist, prev_lds, g, 0, tail_biting != 0, overlap, sh_state, red_v, red_i);
+#pragma unroll
+  for (int k = 0; k < NS; ++k)
+    if (wave == k && live[k]) {
+      const int64_t row = (int64_t)blockIdx.x * NS + k;
+      const T sc = scale ? scale[row] : T(1);
+      T* orow = out ? out + row * (int64_t)steps * V : nullptr;
+      int64_t* srow = states ? states + row * (int64_t)steps : nullptr;
+      backtrack<T, V>(seq[k], table, hist[k], g, 0, tail_biting != 0, overlap[k], sh_state[k], 0, sc, orow, srow);
+    }
+}
+
+template <typename T, int V, int NS>
+void launch_viterbi(size_t lds, bool in_lds, hipStream_t stream, const T* x, const T* table, T* hist, const T* scale,
+                    T* out, int64_t* states, int64_t rows, int L, int KV, int steps, int tail_biting) {
+  const dim3 grid((unsigned)((rows + NS - 1) / NS));
+  hipLaunchKernelGGL((viterbi_kernel<T, V, NS>), grid, dim3(VT_THREADS), in_lds ? lds : 0, stream, x, table, hist,
+                     scale, out, states, rows, L, KV, steps, tail_biting, in_lds ? 1 : 0);
 }
 
 template <typename T>
@@ -254,16 +314,27 @@ int viterbi(const T* x, const T* table, T* hist, const T* scale, T* out, int64_t
   if (rows == 0) return 0;
   if (rows > 0x7fffffff || steps > 0x7fffffff) return GPTQ2D_EUNSUPPORTED;
   const int64_t G = (int64_t)1 << (L - KV);
-  const size_t lds = 2 * G * sizeof(T);
-  const int in_lds = lds <= 96 * 1024;
-  const size_t dyn = in_lds ? lds : 0;
-  const dim3 grid((unsigned)rows);
-  if (V == 1)
-    hipLaunchKernelGGL((viterbi_kernel<T, 1>), grid, dim3(VT_THREADS), dyn, stream, x, table, hist, scale, out, states,
-                       L, KV, (int)steps, tail_biting, in_lds);
-  else
-    hipLaunchKernelGGL((viterbi_kernel<T, 2>), grid, dim3(VT_THREADS), dyn, stream, x, table, hist, scale, out, states,
-                       L, KV, (int)steps, tail_biting, in_lds);
+  // two sequences per workgroup (each table load serves both) when their minima fit in LDS and
+  // there are enough rows to fill the chip, else one
+  const size_t lds1 = 2 * G * sizeof(T), lds2 = 2 * lds1;
+  const bool two = lds2 <= 96 * 1024 && rows >= 512;
+  const size_t lds = two ? lds2 : lds1;
+  const bool in_lds = lds <= 96 * 1024;
+  if (two) {
+    if (V == 1)
+      launch_viterbi<T, 1, 2>(lds, in_lds, stream, x, table, hist, scale, out, states, rows, L, KV, (int)steps,
+                              tail_biting);
+    else
+      launch_viterbi<T, 2, 2>(lds, in_lds, stream, x, table, hist, scale, out, states, rows, L, KV, (int)steps,
+                              tail_biting);
+  } else {
+    if (V == 1)
+      launch_viterbi<T, 1, 1>(lds, in_lds, stream, x, table, hist, scale, out, states, rows, L, KV, (int)steps,
+                              tail_biting);
+    else
+      launch_viterbi<T, 2, 1>(lds, in_lds, stream, x, table, hist, scale, out, states, rows, L, KV, (int)steps,
+                              tail_biting);
+  }
   return (int)hipGetLastError();
 }
 
