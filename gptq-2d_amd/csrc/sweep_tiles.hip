@@ -314,6 +314,14 @@ __device__ __forceinline__ void sweep_tile_push(TileLds& tl, float* __restrict__
   // re-reads them from the kernel arguments on every step
   float qmin = qs.qmin, qmax = qs.qmax;
   asm volatile("" : "+v"(qmin), "+v"(qmax));
+  // L and U coefficients of the next step, read a step ahead (they do not depend on the sweep), so
+  // that only the published errors and C are read between a barrier and the feedback update
+  float LV[4], UV[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    LV[k] = tl.Lp[r][TR - ck[k]];
+    UV[k] = tl.Up[TR - r][ck[k]];
+  }
 #pragma unroll
   for (int t = 0; t < 2 * TR - 1; ++t) {
     const int ka = (t >> 3) & 3, buf = t & 1;
@@ -332,13 +340,28 @@ __device__ __forceinline__ void sweep_tile_push(TileLds& tl, float* __restrict__
     __syncthreads();
     if (t == 2 * TR - 2) break;  // nothing left to receive feedback
     const float cr = tl.Cr[buf][r];
+    float ev[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) ev[k] = tl.Ed[buf][ck[k]];
+    float LN[4], UN[4];
+    if (t + 1 < 2 * TR - 2) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        LN[k] = tl.Lp[r][TR + t + 1 - ck[k]];
+        UN[k] = tl.Up[TR + t + 1 - r][ck[k]];
+      }
+    }
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-      const float lv = tl.Lp[r][TR + t - ck[k]];
-      const float ev = tl.Ed[buf][ck[k]];
-      const float uv = tl.Up[TR + t - r][ck[k]];
-      D[k] += lv * ev;
-      F[k] += cr * uv;
+      D[k] += LV[k] * ev[k];
+      F[k] += cr * UV[k];
+    }
+    if (t + 1 < 2 * TR - 2) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        LV[k] = LN[k];
+        UV[k] = UN[k];
+      }
     }
   }
 
