@@ -157,7 +157,8 @@ struct PotrfLds {
 // over them).
 template <typename T, int PB>
 __device__ __forceinline__ void potrf_panel(PotrfLds<T, PB>& sm, T* __restrict__ w, int64_t ld, int64_t j0, int n,
-                                            int64_t k, int* __restrict__ info, int64_t bid, int64_t nblk) {
+                                            int64_t k, int* __restrict__ info, T* __restrict__ stage, int64_t bid,
+                                            int64_t nblk) {
   constexpr int CP = PB + 1;
   T* a = sm.a;
   T* rs = sm.rs;
@@ -189,10 +190,13 @@ __device__ __forceinline__ void potrf_panel(PotrfLds<T, PB>& sm, T* __restrict__
     if (bid == 0 && tid == 0 && bad && info[0] == 0) info[0] = (int)(j0 + bad);
   }
   __syncthreads();
+  // the factored block goes to the staging block, not back into W: workgroups of this launch that
+  // start late (the GPU busy with other work) still read the unfactored block from W; a later
+  // launch copies it into W (stage_to_w)
   if (bid == 0) {
     for (int t = tid; t < PB * PB; t += 256) {
       const int r = t / PB, c = t % PB;
-      if (r < n && c <= r) w[(j0 + r) * ld + j0 + c] = a[r * CP + c];
+      if (r < n && c <= r) stage[r * n + c] = a[r * CP + c];  // pitch n: fits any k x k buffer
     }
   }
   if (n < PB) return;
@@ -221,9 +225,25 @@ __device__ __forceinline__ void potrf_panel(PotrfLds<T, PB>& sm, T* __restrict__
 
 template <typename T, int PB>
 __global__ __launch_bounds__(256) void potrf_panel_kernel(T* __restrict__ w, int64_t ld, int64_t j0, int n,
-                                                          int64_t k, int* __restrict__ info) {
+                                                          int64_t k, int* __restrict__ info, T* __restrict__ stage) {
   __shared__ PotrfLds<T, PB> sm;
-  potrf_panel<T, PB>(sm, w, ld, j0, n, k, info, blockIdx.x, gridDim.x);
+  potrf_panel<T, PB>(sm, w, ld, j0, n, k, info, stage, blockIdx.x, gridDim.x);
+}
+
+// The staged factored diagonal block of panel j0 (n rows) into W, by one workgroup.
+template <typename T, int PB>
+__device__ __forceinline__ void stage_to_w(T* __restrict__ w, int64_t ld, int64_t j0, int n,
+                                           const T* __restrict__ stage) {
+  for (int t = threadIdx.x; t < PB * PB; t += blockDim.x) {
+    const int r = t / PB, c = t % PB;
+    if (r < n && c <= r) w[(j0 + r) * ld + j0 + c] = stage[r * n + c];
+  }
+}
+
+template <typename T, int PB>
+__global__ __launch_bounds__(256) void stage_to_w_kernel(T* __restrict__ w, int64_t ld, int64_t j0, int n,
+                                                         const T* __restrict__ stage) {
+  stage_to_w<T, PB>(w, ld, j0, n, stage);
 }
 
 // One wave per diagonal NB block of the lower triangular W: replace it by its inverse.
@@ -411,11 +431,16 @@ __global__ __launch_bounds__(256) void syrk_lower_kernel(float* __restrict__ w, 
   syrk_tile<K>(sm, w, ld, r0, R, r0 - K, ti, tj);
 }
 
-// The first K columns of a trailing update (the next panel's columns, every row): tile (x, 0).
+// The first K columns of a trailing update (the next panel's columns, every row): tile (x, 0); the
+// last workgroup copies panel pc's staged diagonal block into W.
 template <int K>
 __global__ __launch_bounds__(256) void syrk_strip_kernel(float* __restrict__ w, int64_t ld, int64_t r0, int64_t R,
-                                                         int64_t pc) {
+                                                         int64_t pc, const float* __restrict__ stage) {
   __shared__ __align__(16) SyrkLds<K> sm;
+  if (blockIdx.x == gridDim.x - 1) {
+    stage_to_w<float, K>(w, ld, pc, K, stage);
+    return;
+  }
   syrk_tile<K>(sm, w, ld, r0, R, pc, blockIdx.x, 0);
 }
 
@@ -426,14 +451,14 @@ __global__ __launch_bounds__(256) void syrk_strip_kernel(float* __restrict__ w, 
 // the throughput-bound update.
 template <int PB>
 __global__ __launch_bounds__(256) void panel_step_kernel(float* __restrict__ w, int64_t ld, int64_t j0, int n,
-                                                         int64_t k, int* __restrict__ info, int64_t n_potrf,
-                                                         int64_t r0, int64_t R, int64_t pc) {
+                                                         int64_t k, int* __restrict__ info, float* __restrict__ stage,
+                                                         int64_t n_potrf, int64_t r0, int64_t R, int64_t pc) {
   __shared__ __align__(16) union {
     PotrfLds<float, PB> p;
     SyrkLds<PB> s;
   } sm;
   if ((int64_t)blockIdx.x < n_potrf) {
-    potrf_panel<float, PB>(sm.p, w, ld, j0, n, k, info, blockIdx.x, n_potrf);
+    potrf_panel<float, PB>(sm.p, w, ld, j0, n, k, info, stage, blockIdx.x, n_potrf);
     return;
   }
   int64_t ti, tj;
@@ -442,26 +467,37 @@ __global__ __launch_bounds__(256) void panel_step_kernel(float* __restrict__ w, 
 }
 
 template <typename T>
-int cholesky_inplace(T* w, int64_t k, int* info, hipStream_t stream) {
+int cholesky_inplace(T* w, int64_t k, int* info, T* stage, hipStream_t stream, int64_t col_begin = 0,
+                     int64_t col_end = -1) {
+  // panels [col_begin, col_end) (multiples of PB; col_end < 0: to the end).  Between calls, every
+  // earlier panel's update has been applied to the whole trailing matrix and every factored
+  // diagonal block is in W.  stage: PB x PB elements of scratch (a panel's factored diagonal block
+  // between its launch and the next).
   constexpr int PB = LdlBlock<T>::PB;
   int rc;
+  if (col_end < 0 || col_end > k) col_end = k;
   if constexpr (sizeof(T) == 4) {
     if (k % 4 == 0) {
       // look-ahead: panel j0's update of the next panel's columns runs on its own (strip); the rest
       // of its trailing update runs in the launch that factors the next panel
       int64_t pr0 = 0, pR = 0, ppc = 0;  // rest update still to apply
-      for (int64_t j0 = 0; j0 < k; j0 += PB) {
+      for (int64_t j0 = col_begin; j0 < col_end; j0 += PB) {
         const int n = k - j0 < PB ? (int)(k - j0) : PB;
         const int64_t rest = k - j0 - PB;
         const int64_t blocks = rest > 0 ? (cdiv(rest, 64) < 256 ? cdiv(rest, 64) : 256) : 1;
         const int64_t nt = pR > 0 ? cdiv(pR, 64) : 0;
         hipLaunchKernelGGL((panel_step_kernel<PB>), dim3((unsigned)(blocks + nt * (nt + 1) / 2)), dim3(256), 0, stream,
-                           (float*)w, k, j0, n, k, info, blocks, pr0, pR, ppc);
+                           (float*)w, k, j0, n, k, info, (float*)stage, blocks, pr0, pR, ppc);
         if ((rc = (int)hipGetLastError())) return rc;
         pR = 0;
-        if (rest <= 0) break;
-        hipLaunchKernelGGL((syrk_strip_kernel<PB>), dim3((unsigned)cdiv(rest, 64)), dim3(256), 0, stream, (float*)w,
-                           k, j0 + PB, rest, j0);
+        if (rest <= 0) {  // the last panel: its staged block into W on its own
+          hipLaunchKernelGGL((stage_to_w_kernel<float, PB>), dim3(1), dim3(256), 0, stream, (float*)w, k, j0, n,
+                             (const float*)stage);
+          if ((rc = (int)hipGetLastError())) return rc;
+          break;
+        }
+        hipLaunchKernelGGL((syrk_strip_kernel<PB>), dim3((unsigned)cdiv(rest, 64) + 1), dim3(256), 0, stream,
+                           (float*)w, k, j0 + PB, rest, j0, (const float*)stage);
         if ((rc = (int)hipGetLastError())) return rc;
         if (rest > PB) {
           pr0 = j0 + 2 * PB;
@@ -469,14 +505,22 @@ int cholesky_inplace(T* w, int64_t k, int* info, hipStream_t stream) {
           ppc = j0;
         }
       }
+      if (pR > 0) {  // a range that stops early: apply the last panel's rest on its own
+        const int64_t nt = cdiv(pR, 64);
+        hipLaunchKernelGGL((panel_step_kernel<PB>), dim3((unsigned)(nt * (nt + 1) / 2)), dim3(256), 0, stream,
+                           (float*)w, k, (int64_t)0, 0, k, info, (float*)stage, (int64_t)0, pr0, pR, ppc);
+        if ((rc = (int)hipGetLastError())) return rc;
+      }
       return 0;
     }
   }
-  for (int64_t j0 = 0; j0 < k; j0 += PB) {
+  for (int64_t j0 = col_begin; j0 < col_end; j0 += PB) {
     const int n = k - j0 < PB ? (int)(k - j0) : PB;
     const int64_t rest = k - j0 - PB;
     const unsigned blocks = rest > 0 ? (unsigned)(cdiv(rest, 64) < 256 ? cdiv(rest, 64) : 256) : 1u;
-    hipLaunchKernelGGL((potrf_panel_kernel<T, PB>), dim3(blocks), dim3(256), 0, stream, w, k, j0, n, k, info);
+    hipLaunchKernelGGL((potrf_panel_kernel<T, PB>), dim3(blocks), dim3(256), 0, stream, w, k, j0, n, k, info, stage);
+    if ((rc = (int)hipGetLastError())) return rc;
+    hipLaunchKernelGGL((stage_to_w_kernel<T, PB>), dim3(1), dim3(256), 0, stream, w, k, j0, n, (const T*)stage);
     if ((rc = (int)hipGetLastError())) return rc;
     if (rest <= 0) break;
     // trailing lower triangle: W22 -= P P^T with P = W[j0+PB:, j0:j0+PB]
@@ -518,6 +562,12 @@ rocblas_handle blas_handle() {
   if (it != handles.end()) return it->second;
   rocblas_handle h = nullptr;
   if (rocblas_create_handle(&h) != rocblas_status_success) return nullptr;
+  // no atomics (rocBLAS's default, set explicitly): split-sum GEMMs with atomic accumulation would
+  // make the last bits of the result change from run to run
+  if (rocblas_set_atomics_mode(h, rocblas_atomics_not_allowed) != rocblas_status_success) {
+    rocblas_destroy_handle(h);
+    return nullptr;
+  }
   handles.emplace(dev, h);
   return h;
 }
@@ -648,6 +698,35 @@ int normalize(T* out, const T* w, int64_t k, int64_t size, int64_t base, int64_t
   return (int)hipGetLastError();
 }
 
+// One matrix of ldl_of_inverse in parts: col_begin == 0 starts it (the reversed copy into work);
+// Cholesky panels [col_begin, col_end) (multiples of the panel width, col_end < 0 or >= k: to the
+// end); finish: the triangular inverse and the normalisation into out.
+template <typename T>
+int ldl_of_inverse_part(const T* m, T* out, T* work, int* info, int64_t k, int64_t size, int64_t col_begin,
+                        int64_t col_end, bool finish, hipStream_t stream) {
+  constexpr int PB = LdlBlock<T>::PB;
+  if (k < 0 || size <= 0 || (k > 0 && k % size)) return GPTQ2D_EINVAL;
+  if (size > 1 && size > LdlBlock<T>::NB) return GPTQ2D_EUNSUPPORTED;
+  if (col_begin < 0 || col_begin % PB || (col_end >= 0 && col_end < col_begin) || (col_end >= 0 && col_end % PB &&
+                                                                                     col_end < k))
+    return GPTQ2D_EINVAL;
+  if (k == 0) return 0;
+  int rc;
+  const int64_t kk = k * k;
+  if (col_begin == 0) {
+    const int64_t blocks = cdiv(kk, 256) < 8192 ? cdiv(kk, 256) : 8192;
+    hipLaunchKernelGGL(copy_kernel<T>, dim3((unsigned)blocks), dim3(256), 0, stream, work, m, kk, 1);
+    if ((rc = (int)hipGetLastError())) return rc;
+  }
+  // out is free until the inverse: its first elements stage the factored diagonal blocks
+  if (col_begin < k && (rc = cholesky_inplace<T>(work, k, info, out, stream, col_begin, col_end))) return rc;
+  if (finish) {
+    if ((rc = trtri_inplace<T>(work, k, out, stream))) return rc;
+    if ((rc = normalize<T>(out, work, k, size, (k - 1) * k + (k - 1), -1, -k, stream))) return rc;
+  }
+  return 0;
+}
+
 // inverse != 0: ldl_of_inverse; else ldl.  m, out, work: [batch, k, k] contiguous; info: [batch].
 template <typename T>
 int ldl_impl(bool inverse, const T* m, T* out, T* work, int* info, int64_t batch, int64_t k, int64_t size,
@@ -665,7 +744,9 @@ int ldl_impl(bool inverse, const T* m, T* out, T* work, int* info, int64_t batch
     const int64_t blocks = cdiv(kk, 256) < 8192 ? cdiv(kk, 256) : 8192;
     hipLaunchKernelGGL(copy_kernel<T>, dim3((unsigned)blocks), dim3(256), 0, stream, wb, mb, kk, inverse ? 1 : 0);
     if ((rc = (int)hipGetLastError())) return rc;
-    if ((rc = cholesky_inplace<T>(wb, k, ib, stream))) return rc;
+    // ob is free until the inverse / normalisation: its first elements stage the factored diagonal
+    // blocks
+    if ((rc = cholesky_inplace<T>(wb, k, ib, ob, stream))) return rc;
     if (inverse) {
       if ((rc = trtri_inplace<T>(wb, k, ob, stream))) return rc;  // out is free scratch until normalisation
       // L_raw(i, j) = Cinv(k-1-j, k-1-i) = w[(k-1-j)*k + (k-1-i)]
@@ -693,5 +774,14 @@ extern "C" {
 
 GPTQ2D_LDL_ABI(f32, float)
 GPTQ2D_LDL_ABI(f64, double)
+
+#define GPTQ2D_LDL_PART_ABI(SUF, T)                                                                                 \
+  int gptq2d_ldl_of_inverse_part_##SUF(const T* m, T* out, T* work, int* info, int64_t k, int64_t size,            \
+                                       int64_t col_begin, int64_t col_end, int32_t finish, hipStream_t stream) {  \
+    return ldl_of_inverse_part<T>(m, out, work, info, k, size, col_begin, col_end, finish != 0, stream);            \
+  }
+
+GPTQ2D_LDL_PART_ABI(f32, float)
+GPTQ2D_LDL_PART_ABI(f64, double)
 
 }  // extern "C"

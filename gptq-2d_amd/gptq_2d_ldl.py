@@ -69,19 +69,56 @@ def ldl(M: torch.Tensor, size: int = 1, *, check: bool = True) -> torch.Tensor:
     return _factor("ldl", M, size, check)
 
 
+def _part(m, out, work, info, k, size, col_begin, col_end, finish):
+    """One part of ldl_of_inverse of the k x k matrix m on the current stream (see the C ABI)."""
+    _hip.call("ldl_of_inverse_part", m.dtype, _hip.ptr(m), _hip.ptr(out), _hip.ptr(work), _hip.ptr(info), k, size,
+              col_begin, col_end, finish, _hip.stream(m.device))
+
+
 def feedback_factors_of_grams(G: torch.Tensor, H: torch.Tensor, super_entry_shape=(1, 1), *, check: bool = True):
     """(L, U) = (ldl_of_inverse(G, p), ldl_of_inverse(H, q)^T) from the Grams themselves, the two
-    factorisations running concurrently on two side streams of the current device (each is a
-    sequence of latency-bound panel steps, so they fill each other's gaps).  No counterpart in the
-    reference, whose callers compute the two factors one after the other (demo.ipynb cell 5)."""
+    Cholesky factorisations running concurrently on two side streams of the current device (each is a
+    sequence of latency-bound panel steps, so they fill each other's gaps); the triangular inverses,
+    throughput-bound GEMMs on rocBLAS, one after the other (as fast as running them together).  No
+    counterpart in the reference, whose callers compute the two factors one after the other
+    (demo.ipynb cell 5)."""
     p, q = super_entry_shape
     main = torch.cuda.current_stream(G.device)
     streams = _side_streams(G.device)
-    out = []
-    for s, (m, size) in zip(streams, ((G, p), (H, q))):
+    for s in streams:
         s.wait_stream(main)
-        with torch.cuda.stream(s):
-            out.append(ldl_of_inverse(m, size=size, check=False))
+    jobs = []
+    for m, size in ((G, p), (H, q)):
+        assert m.dim() >= 2 and m.size(-1) == m.size(-2), "expected square matrices [..., k, k]"
+        assert m.dtype in (torch.float32, torch.float64), "expected float32 or float64"
+        _hip.require_device(m)
+        k = m.size(-1)
+        assert size > 0 and k % size == 0, "the block size must divide the matrix size"
+        assert size <= MAX_BLOCK[m.dtype], f"diagonal blocks up to {MAX_BLOCK[m.dtype]} are supported for {m.dtype}"
+        jobs.append((m, size, k))
+    out = []
+    with torch.cuda.device(G.device):
+        # buffers on their stream's pool; the Cholesky parts concurrently
+        bufs = []
+        for s, (m, size, k) in zip(streams, jobs):
+            with torch.cuda.stream(s):
+                src = m.reshape(-1, k, k).contiguous()
+                o = torch.empty_like(src)
+                w = torch.empty_like(src)
+                info = torch.zeros(src.size(0), dtype=torch.int32, device=m.device)
+                for b in range(src.size(0)):
+                    _part(src[b], o[b], w[b], info[b:b + 1], k, size, 0, -1, 0)
+            bufs.append((src, o, w, info))
+        # the inverses (rocBLAS) one after the other
+        done = torch.cuda.Event()
+        for i, (s, (m, size, k), (src, o, w, info)) in enumerate(zip(streams, jobs, bufs)):
+            if i:
+                s.wait_event(done)
+            with torch.cuda.stream(s):
+                for b in range(src.size(0)):
+                    _part(src[b], o[b], w[b], info[b:b + 1], k, size, k, -1, 1)
+                done.record(s)
+            out.append(o.reshape(m.shape))
     for s, t in zip(streams, out):
         main.wait_stream(s)
         t.record_stream(main)

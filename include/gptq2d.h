@@ -109,6 +109,15 @@ extern "C" {
    * (ldl_of_inverse, gptq_2d_reference.py:29-49).  size <= 64 (f32) or 32 (f64). */                 \
   int gptq2d_ldl_of_inverse_##SUF(const T* m, T* out, T* work, int* info, int64_t batch, int64_t k, int64_t size,  \
                                   void* stream);                                                                    \
+  /* ldl_of_inverse of one k x k matrix in parts, so that the Cholesky and the inverse of two          \
+   * factorisations can be scheduled apart on two streams (the reference computes its factors one     \
+   * after the other, demo.ipynb cell 5):                                                             \
+   * col_begin == 0 starts (copies m into work); Cholesky panels of columns [col_begin, col_end)        \
+   * (multiples of 64 for f32, 32 for f64; col_end < 0: to k); finish != 0: the inverse and the        \
+   * normalisation into out.  One call with col_begin = 0, col_end = -1, finish = 1 equals             \
+   * gptq2d_ldl_of_inverse with batch 1.  info[0] as there. */                                          \
+  int gptq2d_ldl_of_inverse_part_##SUF(const T* m, T* out, T* work, int* info, int64_t k, int64_t size,            \
+                                       int64_t col_begin, int64_t col_end, int32_t finish, void* stream);          \
   /* Unit lower (block) triangular L with M = L Lambda L^T (ldl, gptq_2d_reference.py:52-55). */       \
   int gptq2d_ldl_##SUF(const T* m, T* out, T* work, int* info, int64_t batch, int64_t k, int64_t size,              \
                        void* stream);                                                                               \

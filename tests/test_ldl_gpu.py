@@ -144,6 +144,20 @@ def test_not_positive_definite():
         LDL.ldl(m)
 
 
+def test_concurrent_factors_deterministic():
+    """Regression: the two factorisations of feedback_factors_of_grams run concurrently on two streams, so a
+    panel launch's workgroups may start late, behind the other stream's work.  They must still read the
+    unfactored diagonal block (the factored one is staged and copied into place by a later launch): every
+    run equals the single-stream ldl_of_inverse of each factor, bitwise."""
+    a = instances.wishart_factor(8192, .5, 1, device=DEV).float()
+    b = instances.wishart_factor(8192, .5, 2, device=DEV).float()
+    ref_l = LDL.ldl_of_inverse(a, check=False)
+    ref_u = LDL.ldl_of_inverse(b, check=False).t()
+    for rep in range(24):
+        lo, up = LDL.feedback_factors_of_grams(a, b, check=False)
+        assert lo.equal(ref_l) and up.equal(ref_u), rep
+
+
 def test_headline_size_fp32():
     """8192 x 8192 fp32 factor of the headline layer: structure, and agreement with the fp64 oracle on a
     sampled set of rows (the full fp64 CPU reference takes too long here)."""
