@@ -168,28 +168,50 @@ __device__ __forceinline__ void potrf_panel(PotrfLds<T, PB>& sm, T* __restrict__
     a[r * CP + c] = (r < n && c <= r) ? w[(j0 + r) * ld + j0 + c] : (r == c ? T(1) : T(0));
   }
   __syncthreads();
-  if (tid < 64) {
-    const int r = tid < PB ? tid : PB - 1;
-    T row[PB];
+  // blocked right-looking factorisation of the diagonal block, 16 columns at a time: one wave
+  // factors the 16 columns (lane r holds row r's 16 entries; pivot and column entries by
+  // readlane: 120 per block instead of 2016 for the whole block in one go -- lane r's entries
+  // right of its diagonal take harmless updates and are never read), which also solves the rows
+  // below within the block; then all four waves apply the rank-16 update to the rest of the block
+  constexpr int CB = 16;
+  int bad = 0;
 #pragma unroll
-    for (int c = 0; c < PB; ++c) row[c] = a[r * CP + c];
-    int bad = 0;
+  for (int c0 = 0; c0 < PB; c0 += CB) {
+    if (tid < 64) {
+      const int r = tid < PB ? tid : PB - 1;
+      T x[CB];
 #pragma unroll
-    for (int c = 0; c < PB; ++c) {
-      const T d = bcast(row[c], c);
-      if (!(d > T(0)) && bad == 0) bad = c + 1;
-      const T sd = sqrt(d);
-      row[c] = tid == c ? sd : row[c] / sd;
+      for (int c = 0; c < CB; ++c) x[c] = a[r * CP + c0 + c];
 #pragma unroll
-      for (int c2 = c + 1; c2 < PB; ++c2) row[c2] -= row[c] * bcast(row[c], c2);
+      for (int c = 0; c < CB; ++c) {
+        const T d = bcast(x[c], c0 + c);
+        if (!(d > T(0)) && bad == 0) bad = c0 + c + 1;
+        const T sd = sqrt(d);
+        x[c] = tid == c0 + c ? sd : x[c] / sd;
+#pragma unroll
+        for (int c2 = c + 1; c2 < CB; ++c2) x[c2] -= x[c] * bcast(x[c], c0 + c2);
+      }
+      if (tid < PB && tid >= c0) {
+#pragma unroll
+        for (int c = 0; c < CB; ++c) a[r * CP + c0 + c] = x[c];
+      }
     }
-    if (tid < PB) {
+    __syncthreads();
+    if (c0 + CB < PB) {
+      // a[r][c2] -= sum_{c in block} a[r][c] a[c2][c] for c0 + CB <= c2 <= r < PB
+      constexpr int NR = PB;  // rows of the block
+      for (int e = tid; e < NR * NR; e += 256) {
+        const int r = e / NR, c2 = e % NR;
+        if (c2 < c0 + CB || c2 > r) continue;
+        T acc = a[r * CP + c2];
 #pragma unroll
-      for (int c = 0; c < PB; ++c) a[r * CP + c] = row[c];
+        for (int c = 0; c < CB; ++c) acc -= a[r * CP + c0 + c] * a[c2 * CP + c0 + c];
+        a[r * CP + c2] = acc;
+      }
+      __syncthreads();
     }
-    if (bid == 0 && tid == 0 && bad && info[0] == 0) info[0] = (int)(j0 + bad);
   }
-  __syncthreads();
+  if (bid == 0 && tid == 0 && bad && info[0] == 0) info[0] = (int)(j0 + bad);
   // the factored block goes to the staging block, not back into W: workgroups of this launch that
   // start late (the GPU busy with other work) still read the unfactored block from W; a later
   // launch copies it into W (stage_to_w)
