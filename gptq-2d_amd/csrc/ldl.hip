@@ -10,14 +10,17 @@
 // Device work, all on the caller's stream, no host synchronisation, no device allocation by this
 // library:
 //   1. W = J M J: the reversal of the flat array.
-//   2. Right-looking blocked Cholesky of W in place, panels of NB columns: a panel's diagonal
+//   2. Right-looking blocked Cholesky of W in place, panels of PB columns: a panel's diagonal
 //      block is factored (redundantly in every workgroup) and the panel below solved against it;
-//      the trailing lower triangle takes the rank-NB update.  fp32 runs it with a look-ahead of one
+//      the trailing lower triangle takes the rank-PB update.  fp32 (k % 4 == 0) blocks it on two
+//      levels: strips of four panels, where each panel updates only its strip's later columns and
+//      a strip's end brings one rank-256 update of the whole trailing triangle (MFMA-bound, where
+//      rank-64 updates are bound by moving the triangle through HBM), with a look-ahead of one
 //      panel on the one stream: after a panel, a strip launch updates only the next panel's
 //      columns, and the next panel's factorisation shares one launch (panel_step_kernel) with the
-//      rest of the previous trailing update, on disjoint columns -- the latency-bound panel runs
-//      beside the MFMA update instead of after it.  fp64 (and fp32 with k % 4 != 0) keep the plain
-//      sequence, the update on gemm.hip.
+//      rest of the update, on disjoint columns -- the latency-bound panel runs beside the MFMA
+//      update instead of after it.  fp64 (and fp32 with k % 4 != 0) keep the plain sequence, the
+//      update on gemm.hip.
 //   3. ldl_of_inverse only: C^{-1} in place by recursive doubling.  Diagonal NB blocks are inverted
 //      by one wave each; then for s = NB, 2 NB, ... every pair of inverted s-blocks A^{-1}, D^{-1}
 //      with off-diagonal block B becomes one inverted 2s-block through -D^{-1} (B A^{-1}) -- two
@@ -35,17 +38,21 @@
 // Reference: IST-DASLab/GPTQ-2D gptq_2d_reference.py:29-55 (_unit_diagonal_blocks, ldl_of_inverse,
 // ldl), which call torch.linalg.cholesky and solve_triangular.
 #include "linalg.h"
+#include "lds_dma.h"
 
 #include <rocblas/rocblas.h>
 
+#include <type_traits>
 #include <unordered_map>
 
 namespace {
 
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
 template <typename T>
 struct LdlBlock;
 // NB: diagonal blocks inverted by one wave in registers (trtri leaves, block normalisation);
-// PB: Cholesky panel width (the diagonal block is factored in LDS, the trailing update has K = PB).
+// PB: Cholesky panel width (the diagonal block is factored in LDS).
 template <>
 struct LdlBlock<float> {
   static constexpr int NB = 64;
@@ -115,11 +122,13 @@ __device__ __forceinline__ double quad_bcast(double v) {
 }
 
 template <int T0, int PB, typename T>
-__device__ __forceinline__ void quad_solve_step(T (&x)[PB / 4], int q, const T* __restrict__ a, int cp) {
-  // column T0: its owner (lane q == T0 % 4, slot T0 / 4) finalises x_T0, the quad shares it, and every
-  // lane removes it from its own later columns c = 4 idx + q > T0
+__device__ __forceinline__ void quad_solve_step(T (&x)[PB / 4], int q, const T* __restrict__ a, int cp,
+                                                const T* __restrict__ rinv) {
+  // column T0: its owner (lane q == T0 % 4, slot T0 / 4) finalises x_T0 (times the pivot's
+  // reciprocal), the quad shares it, and every lane removes it from its own later columns
+  // c = 4 idx + q > T0
   constexpr int O = T0 & 3, IT = T0 >> 2;
-  T xt = x[IT] / a[T0 * cp + T0];
+  T xt = x[IT] * rinv[T0];
   xt = quad_bcast<O>(xt);
   if (q == O) x[IT] = xt;
 #pragma unroll
@@ -130,27 +139,45 @@ __device__ __forceinline__ void quad_solve_step(T (&x)[PB / 4], int q, const T* 
 }
 
 template <int T0, int PB, typename T>
-__device__ __forceinline__ void quad_solve(T (&x)[PB / 4], int q, const T* __restrict__ a, int cp) {
+__device__ __forceinline__ void quad_solve(T (&x)[PB / 4], int q, const T* __restrict__ a, int cp,
+                                           const T* __restrict__ rinv) {
   if constexpr (T0 < PB) {
-    quad_solve_step<T0, PB, T>(x, q, a, cp);
-    quad_solve<T0 + 1, PB, T>(x, q, a, cp);
+    quad_solve_step<T0, PB, T>(x, q, a, cp, rinv);
+    quad_solve<T0 + 1, PB, T>(x, q, a, cp, rinv);
   }
+}
+
+// Pivot of a Cholesky column: sd = sqrt(d) and inv = 1 / sd.  fp32: the hardware reciprocal square
+// root refined by one Newton step, y (3 - d y^2) / 2, so that the column is scaled by a product, not a
+// quotient (the dependent chain of every column is the panel's critical path).
+__device__ __forceinline__ void pivot(float d, float& sd, float& inv) {
+  const float y = __builtin_amdgcn_rsqf(d);
+  inv = y * fmaf(-0.5f * d * y, y, 1.5f);
+  sd = d * inv;
+}
+__device__ __forceinline__ void pivot(double d, double& sd, double& inv) {
+  sd = sqrt(d);
+  inv = 1.0 / sd;
 }
 
 // One panel of the blocked Cholesky.  Every workgroup factors the diagonal block W[j0.., j0..]
 // (n = min(PB, k - j0) rows; rows beyond n act as identity rows): the block is staged through LDS
-// with coalesced loads, then one wave factors it in registers, lane r holding row r, right-looking
-// column by column with no barrier -- the pivot and the scaled column entries reach the other
-// lanes by readlane (lane r's entries right of its diagonal take harmless updates and are never
-// read); workgroup 0 writes it back.  Then the panel below is solved against it,
-// W[r, j0:j0+PB] <- W[r, j0:j0+PB] C_jj^{-T}, in chunks of 64 rows staged through LDS (coalesced
-// loads and stores): four lanes share a row, lane q owning the columns c = q mod 4, and the
-// forward substitution runs column by column with the finished x_t broadcast inside the quad.
+// with coalesced loads and factored 16 columns at a time -- one wave factors the 16 columns in
+// registers, lane r holding row r, column by column with no barrier (the pivot and the scaled
+// column entries reach the other lanes by readlane; lane r's entries right of its diagonal take
+// harmless updates and are never read), then the workgroup applies the rank-16 update to the
+// block's later columns (fp32: one 32 x 32 MFMA tile per wave); workgroup 0 stages the factored
+// block.  Then the panel below is solved against it, W[r, j0:j0+PB] <- W[r, j0:j0+PB] C_jj^{-T}, in
+// chunks of 64 rows staged through LDS (coalesced loads and stores; a workgroup's first chunk is
+// loaded into registers before the factorisation, so the load overlaps it): four lanes share a
+// row, lane q owning the columns c = q mod 4, and the forward substitution runs column by column
+// with the finished x_t broadcast inside the quad.
 template <typename T, int PB>
 struct PotrfLds {
   static constexpr int CP = PB + 1;  // odd pitch: row and column walks are both conflict-free
   T a[PB * CP];
   T rs[64 * CP];
+  T rinv[PB];  // reciprocals of the factored block's diagonal
 };
 
 // Panel j0 as above, for workgroup `bid` of `nblk` taking part (the panel's row chunks are dealt
@@ -167,46 +194,80 @@ __device__ __forceinline__ void potrf_panel(PotrfLds<T, PB>& sm, T* __restrict__
     const int r = t / PB, c = t % PB;
     a[r * CP + c] = (r < n && c <= r) ? w[(j0 + r) * ld + j0 + c] : (r == c ? T(1) : T(0));
   }
+  // this workgroup's first chunk of the panel below, in flight during the factorisation
+  const int64_t first = j0 + PB;
+  constexpr int PRE = 64 * PB / 256;
+  T pre[PRE];
+  if (n == PB) {
+    const int64_t r0 = first + bid * 64;
+#pragma unroll
+    for (int u = 0; u < PRE; ++u) {
+      const int t = tid + 256 * u, i = t / PB, c = t % PB;
+      pre[u] = r0 + i < k ? w[(r0 + i) * ld + j0 + c] : T(0);
+    }
+  }
   __syncthreads();
-  // blocked right-looking factorisation of the diagonal block, 16 columns at a time: one wave
-  // factors the 16 columns (lane r holds row r's 16 entries; pivot and column entries by
-  // readlane: 120 per block instead of 2016 for the whole block in one go -- lane r's entries
-  // right of its diagonal take harmless updates and are never read), which also solves the rows
-  // below within the block; then all four waves apply the rank-16 update to the rest of the block
   constexpr int CB = 16;
   int bad = 0;
 #pragma unroll
   for (int c0 = 0; c0 < PB; c0 += CB) {
     if (tid < 64) {
       const int r = tid < PB ? tid : PB - 1;
-      T x[CB];
+      T x[CB], myinv = T(0);
 #pragma unroll
       for (int c = 0; c < CB; ++c) x[c] = a[r * CP + c0 + c];
 #pragma unroll
       for (int c = 0; c < CB; ++c) {
         const T d = bcast(x[c], c0 + c);
         if (!(d > T(0)) && bad == 0) bad = c0 + c + 1;
-        const T sd = sqrt(d);
-        x[c] = tid == c0 + c ? sd : x[c] / sd;
+        T sd, inv;
+        pivot(d, sd, inv);
+        if (tid == c0 + c) myinv = inv;
+        x[c] = tid == c0 + c ? sd : x[c] * inv;
 #pragma unroll
         for (int c2 = c + 1; c2 < CB; ++c2) x[c2] -= x[c] * bcast(x[c], c0 + c2);
       }
       if (tid < PB && tid >= c0) {
 #pragma unroll
         for (int c = 0; c < CB; ++c) a[r * CP + c0 + c] = x[c];
+        if (tid < c0 + CB) sm.rinv[tid] = myinv;
       }
     }
     __syncthreads();
     if (c0 + CB < PB) {
-      // a[r][c2] -= sum_{c in block} a[r][c] a[c2][c] for c0 + CB <= c2 <= r < PB
-      constexpr int NR = PB;  // rows of the block
-      for (int e = tid; e < NR * NR; e += 256) {
-        const int r = e / NR, c2 = e % NR;
-        if (c2 < c0 + CB || c2 > r) continue;
-        T acc = a[r * CP + c2];
+      // a[r][c2] -= sum_{c in block} a[r][c] a[c2][c] for the later columns c2 >= c0 + CB (every row:
+      // the entries above the diagonal take harmless updates)
+      if constexpr (sizeof(T) == 4 && PB == 64) {
+        // wave (wy, wx): the 32 x 32 tile at rows 32 wy, columns 32 wx; 8 MFMAs of k-depth 2, lane
+        // (i, h) feeding k = c0 + 2 s + h of row 32 wy + i (A) and of row 32 wx + i (B)
+        const int lane = tid & 63, li = lane & 31, hh = lane >> 5;
+        const int wy = tid >> 7, wx = (tid >> 6) & 1;
+        if (32 * wx + 31 >= c0 + CB) {
+          floatx16 acc;
 #pragma unroll
-        for (int c = 0; c < CB; ++c) acc -= a[r * CP + c0 + c] * a[c2 * CP + c0 + c];
-        a[r * CP + c2] = acc;
+          for (int e = 0; e < 16; ++e) acc[e] = 0.f;
+#pragma unroll
+          for (int s2 = 0; s2 < CB / 2; ++s2)
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[(32 * wy + li) * CP + c0 + 2 * s2 + hh],
+                                                       a[(32 * wx + li) * CP + c0 + 2 * s2 + hh], acc, 0, 0, 0);
+          const int col = 32 * wx + li;
+          if (col >= c0 + CB) {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+              const int row = 32 * wy + 8 * (e >> 2) + 4 * hh + (e & 3);
+              a[row * CP + col] -= acc[e];
+            }
+          }
+        }
+      } else {
+        for (int e = tid; e < PB * PB; e += 256) {
+          const int r = e / PB, c2 = e % PB;
+          if (c2 < c0 + CB || c2 > r) continue;
+          T acc = a[r * CP + c2];
+#pragma unroll
+          for (int c = 0; c < CB; ++c) acc -= a[r * CP + c0 + c] * a[c2 * CP + c0 + c];
+          a[r * CP + c2] = acc;
+        }
       }
       __syncthreads();
     }
@@ -222,19 +283,26 @@ __device__ __forceinline__ void potrf_panel(PotrfLds<T, PB>& sm, T* __restrict__
     }
   }
   if (n < PB) return;
-  const int64_t first = j0 + PB;
   const int q = tid & 3, rr = tid >> 2;
   for (int64_t r0 = first + bid * 64; r0 < k; r0 += nblk * 64) {
     __syncthreads();
-    for (int t = tid; t < 64 * PB; t += 256) {
-      const int i = t / PB, c = t % PB;
-      rs[i * CP + c] = r0 + i < k ? w[(r0 + i) * ld + j0 + c] : T(0);
+    if (r0 == first + bid * 64) {
+#pragma unroll
+      for (int u = 0; u < PRE; ++u) {
+        const int t = tid + 256 * u, i = t / PB, c = t % PB;
+        rs[i * CP + c] = pre[u];
+      }
+    } else {
+      for (int t = tid; t < 64 * PB; t += 256) {
+        const int i = t / PB, c = t % PB;
+        rs[i * CP + c] = r0 + i < k ? w[(r0 + i) * ld + j0 + c] : T(0);
+      }
     }
     __syncthreads();
     T x[PB / 4];
 #pragma unroll
     for (int idx = 0; idx < PB / 4; ++idx) x[idx] = rs[rr * CP + 4 * idx + q];
-    quad_solve<0, PB, T>(x, q, a, CP);
+    quad_solve<0, PB, T>(x, q, a, CP, sm.rinv);
 #pragma unroll
     for (int idx = 0; idx < PB / 4; ++idx) rs[rr * CP + 4 * idx + q] = x[idx];
     __syncthreads();
@@ -369,123 +437,193 @@ __global__ __launch_bounds__(256) void normalize_block_kernel(T* __restrict__ ou
   }
 }
 
-typedef float floatx16 __attribute__((ext_vector_type(16)));
+// Rank-K update of a lower trapezoid on fp32 MFMA (v_mfma_f32_32x32x2_f32):
+//   D -= P P^T  on  D = W[r0.., r0..] (R x R; lower triangle, columns < C),  P = W[r0.., pc .. pc + K)
+// with K a multiple of 32.  One workgroup per 128 x 128 block (bi, bj), four waves of 64 x 64 (2 x 2
+// MFMA blocks each).  The K loop walks k-tiles of 32: both panels of a k-tile (the block's 128 rows
+// of P, and the 128 rows that are its columns) are loaded one k-tile ahead straight into LDS
+// (buffer loads with the LDS destination bit), double-buffered, one barrier per k-tile; rows past R
+// (A) or past min(R, C) (B) load as zeros.  Both panels use the same layout -- P's k runs along a row
+// for both operands of D = P P^T: float f of a panel holds row f / 32 and k = 4 (q ^ (row % 8)) +
+// f % 4, q = (f % 32) / 4 (16-byte k-quads XOR-swizzled by row, so that 8 lanes reading one quad of
+// 8 rows hit 8 bank groups), and every fragment read is 128 bits.  Lane l (i = l % 32, h = l / 32)
+// feeds A(i, 16 h + s) and B(16 h + s, i) to MFMA s; the accumulators hold
+// D(8 (r / 4) + 4 h + r % 4, i).  The epilogue subtracts the products from D in place (read all
+// 16 entries of a block, then write), masked to the lower triangle, to i < R and to j < C.
+//
+// The same kernel serves the three updates of the two-level Cholesky below: a panel's update of the
+// next panel's columns (C = 64), its update of the rest of its 256-column strip (rank 64), and a
+// strip's rank-256 update of the whole trailing triangle.
+constexpr int WB = 128;  // block edge
+constexpr int WK = 32;   // k-tile depth
 
-// Trailing update of one Cholesky panel on fp32 MFMA: D -= P P^T on the lower triangle of a
-// trailing square D = W[r0.., r0..] (R x R), P = W[r0.., pc .. pc + K) the solved panel.  One
-// workgroup per 64 x 64 lower tile (ti, tj); it issues all its loads at once -- its D block into
-// the accumulators, both 64 x K panels through LDS as float4 -- then 16 MFMAs (32x32x2) per 32 k,
-// A negated so that the accumulation is D - P P^T directly.  Lane layout as in gemm.hip.
-template <int K>
-struct SyrkLds {
-  static constexpr int PP = K + 4;
-  float a[64 * PP];
-  float b[64 * PP];
+struct WideLds {
+  float a[2][WB * WK];
+  float b[2][WB * WK];
 };
 
-template <int K>
-__device__ __forceinline__ void syrk_tile(SyrkLds<K>& sm, float* __restrict__ w, int64_t ld, int64_t r0, int64_t R,
-                                          int64_t pc, int64_t ti, int64_t tj) {
-  constexpr int TP = 64, PP = SyrkLds<K>::PP;
-  float* As = sm.a;
-  float* Bs = sm.b;
-  const int64_t i0 = ti * TP, j0 = tj * TP;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wy = wave >> 1, wx = wave & 1, li = lane & 31, hh = lane >> 5;
-  const bool active = !(ti == tj && wy < wx);  // the upper block of a diagonal tile has nothing to do
-  float* d = w + r0 * ld + r0;
-  const float* P = w + r0 * ld + pc;
-  floatx16 acc;
+__device__ __forceinline__ void syrk_wide_block(WideLds& sm, float* __restrict__ w, int64_t ld, int64_t r0, int R,
+                                                int C, int64_t pc, int K, int bi, int bj) {
+  const int tid = threadIdx.x, lane = tid & 63, li = lane & 31, hh = lane >> 5;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wy = wave >> 1, wx = wave & 1;
+  const int I0 = bi * WB, J0 = bj * WB;
+  const int ild = (int)ld;
+  const int CR = C < R ? C : R;
+  // offsets below ld * R * 4 < 2^31 (checked by the host)
+  const __amdgpu_buffer_rsrc_t rp = matrix_rsrc(w + r0 * ld + pc, (int64_t)(R - 1) * ld + K);
+
+  // per-lane staging offsets of the wave's four 128-bit loads per panel and k-tile
+  int aoff[4], boff[4];
 #pragma unroll
-  for (int e = 0; e < 16; ++e) {
-    const int64_t i = i0 + 32 * wy + 8 * (e >> 2) + 4 * hh + (e & 3), j = j0 + 32 * wx + li;
-    acc[e] = (active && i < R && j < R) ? d[i * ld + j] : 0.f;
+  for (int x = 0; x < 4; ++x) {
+    const int f = (wave + 4 * x) * 256 + 4 * lane;
+    const int row = f >> 5, kq = ((f >> 2) & 7) ^ (row & 7);
+    const int ia = I0 + row, ib = J0 + row;
+    aoff[x] = ia < R ? (ia * ild + 4 * kq) * 4 : OOB;
+    boff[x] = ib < CR ? (ib * ild + 4 * kq) * 4 : OOB;
   }
+  auto issue = [&](int t, int buf) {
 #pragma unroll
-  for (int q = 0; q < TP * K / 4 / 256; ++q) {
-    const int f = tid + 256 * q;
-    const int r = f / (K / 4), kq = f % (K / 4);
-    const int64_t ia = i0 + r, ib = j0 + r;
-    const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
-    *reinterpret_cast<float4*>(&As[r * PP + 4 * kq]) =
-        ia < R ? *reinterpret_cast<const float4*>(P + ia * ld + 4 * kq) : z;
-    *reinterpret_cast<float4*>(&Bs[r * PP + 4 * kq]) =
-        ib < R ? *reinterpret_cast<const float4*>(P + ib * ld + 4 * kq) : z;
-  }
-  __syncthreads();
-  if (!active) return;
-#pragma unroll
-  for (int kc = 0; kc < K / 32; ++kc) {
-    float4 af[4], bf[4];
-#pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      af[v] = *reinterpret_cast<const float4*>(&As[(32 * wy + li) * PP + 32 * kc + 16 * hh + 4 * v]);
-      bf[v] = *reinterpret_cast<const float4*>(&Bs[(32 * wx + li) * PP + 32 * kc + 16 * hh + 4 * v]);
+    for (int x = 0; x < 4; ++x) {
+      const int f0 = (wave + 4 * x) * 256;
+      dma_load<4>(rp, &sm.a[buf][f0], aoff[x] == OOB ? OOB : aoff[x] + t * WK * 4);
+      dma_load<4>(rp, &sm.b[buf][f0], boff[x] == OOB ? OOB : boff[x] + t * WK * 4);
     }
+  };
+
+  // a wave with nothing to write (above the diagonal, right of C or below R) still loads and waits
+  const bool act = !(bi == bj && wy < wx) && J0 + 64 * wx < C && I0 + 64 * wy < R;
+  floatx16 acc[2][2];
 #pragma unroll
-    for (int s2 = 0; s2 < 16; ++s2)
-      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(-af[s2 >> 2][s2 & 3], bf[s2 >> 2][s2 & 3], acc, 0, 0, 0);
-  }
+  for (int a = 0; a < 2; ++a)
 #pragma unroll
-  for (int e = 0; e < 16; ++e) {
-    const int64_t i = i0 + 32 * wy + 8 * (e >> 2) + 4 * hh + (e & 3), j = j0 + 32 * wx + li;
-    if (i < R && j < R && j <= i) d[i * ld + j] = acc[e];
+    for (int d = 0; d < 2; ++d)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[a][d][r] = 0.f;
+
+  const int sw = li & 7;
+  const int a_base = (64 * wy + li) * WK, b_base = (64 * wx + li) * WK;
+  auto step = [&](int t, auto cur_c) {
+    constexpr int cur = decltype(cur_c)::value;
+    __syncthreads();  // buffer cur is complete; buffer 1 - cur is no longer read
+    if (t + 1 < K / WK) issue(t + 1, 1 - cur);
+    if (act) {
+      const float* as = &sm.a[cur][a_base];
+      const float* bs = &sm.b[cur][b_base];
+      float4 fa[2][2], fb[2][2];
+      auto frag = [&](int v, int slot) {
+#pragma unroll
+        for (int a = 0; a < 2; ++a) {
+          fa[slot][a] = *reinterpret_cast<const float4*>(as + a * 32 * WK + 4 * ((4 * hh + v) ^ sw));
+          fb[slot][a] = *reinterpret_cast<const float4*>(bs + a * 32 * WK + 4 * ((4 * hh + v) ^ sw));
+        }
+      };
+      frag(0, 0);
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        if (v < 3) frag(v + 1, (v + 1) & 1);
+#pragma unroll
+        for (int s2 = 0; s2 < 4; ++s2)
+#pragma unroll
+          for (int a = 0; a < 2; ++a)
+#pragma unroll
+            for (int d = 0; d < 2; ++d)
+              acc[a][d] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[v & 1][a][s2], fb[v & 1][d][s2], acc[a][d], 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    wait_dma();  // this wave's loads of k-tile t + 1 have landed before the next barrier
+  };
+  issue(0, 0);
+  wait_dma();
+  for (int t = 0; t < K / WK; t += 2) {
+    step(t, std::integral_constant<int, 0>{});
+    if (t + 1 < K / WK) step(t + 1, std::integral_constant<int, 1>{});
   }
+  if (!act) return;
+  const __amdgpu_buffer_rsrc_t rd = matrix_rsrc(w + r0 * ld + r0, (int64_t)(R - 1) * ld + R);
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int d = 0; d < 2; ++d) {
+      int off[16];
+      float cur[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int i = I0 + 64 * wy + 32 * a + 8 * (r >> 2) + 4 * hh + (r & 3), j = J0 + 64 * wx + 32 * d + li;
+        off[r] = (i < R && j < C && j <= i) ? (i * ild + j) * 4 : OOB;
+        cur[r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rd, off[r], 0, 0));
+      }
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, cur[r] - acc[a][d][r]), rd, off[r], 0, 0);
+    }
 }
 
-// Tile (ti, tj) of workgroup lin of n covering a lower triangle of tiles, numbered along the
-// triangle and re-numbered so that each XCD (own L2) runs a contiguous share.
-__device__ __forceinline__ void triangle_tile(int64_t lin, int64_t n, int64_t& ti, int64_t& tj) {
+// Workgroup lin of n renumbered so that each XCD (own L2) runs a contiguous share of the blocks: the
+// hardware deals workgroup w to XCD w % 8.
+__device__ __forceinline__ int64_t xcd_contiguous(int64_t lin, int64_t n) {
   const int64_t base = n / 8, extra = n % 8, xcd = lin % 8;
-  const int64_t id = xcd * base + (xcd < extra ? xcd : extra) + lin / 8;
-  ti = (int64_t)((sqrt(8.0 * (double)id + 1.0) - 1.0) * 0.5);
-  while ((ti + 1) * (ti + 2) / 2 <= id) ++ti;
-  while (ti * (ti + 1) / 2 > id) --ti;
-  tj = id - ti * (ti + 1) / 2;
+  return xcd * base + (xcd < extra ? xcd : extra) + lin / 8;
 }
 
-// Whole trailing update of the panel just before r0 (P = W[r0.., r0-K .. r0)).
-template <int K>
-__global__ __launch_bounds__(256) void syrk_lower_kernel(float* __restrict__ w, int64_t ld, int64_t r0, int64_t R) {
-  __shared__ __align__(16) SyrkLds<K> sm;
-  int64_t ti, tj;
-  triangle_tile(blockIdx.x, gridDim.x, ti, tj);
-  syrk_tile<K>(sm, w, ld, r0, R, r0 - K, ti, tj);
-}
-
-// The first K columns of a trailing update (the next panel's columns, every row): tile (x, 0); the
-// last workgroup copies panel pc's staged diagonal block into W.
-template <int K>
-__global__ __launch_bounds__(256) void syrk_strip_kernel(float* __restrict__ w, int64_t ld, int64_t r0, int64_t R,
-                                                         int64_t pc, const float* __restrict__ stage) {
-  __shared__ __align__(16) SyrkLds<K> sm;
-  if (blockIdx.x == gridDim.x - 1) {
-    stage_to_w<float, K>(w, ld, pc, K, stage);
+// Block (bi, bj) number id of a lower trapezoid of blocks with nbc block columns, numbered row by
+// row: the triangle of the first nbc block rows, then nbc blocks per row.
+__device__ __forceinline__ void trapezoid_block(int64_t id, int64_t nbc, int& bi, int& bj) {
+  const int64_t tri = nbc * (nbc + 1) / 2;
+  if (id >= tri) {
+    bi = (int)(nbc + (id - tri) / nbc);
+    bj = (int)((id - tri) % nbc);
     return;
   }
-  syrk_tile<K>(sm, w, ld, r0, R, pc, blockIdx.x, 0);
+  int64_t ti = (int64_t)((sqrt(8.0 * (double)id + 1.0) - 1.0) * 0.5);
+  while ((ti + 1) * (ti + 2) / 2 <= id) ++ti;
+  while (ti * (ti + 1) / 2 > id) --ti;
+  bi = (int)ti;
+  bj = (int)(id - ti * (ti + 1) / 2);
+}
+
+// Workgroups of a trapezoid update (R x R lower triangle, columns < C; C <= R).
+__host__ __device__ inline int64_t trapezoid_blocks(int64_t R, int64_t C) {
+  const int64_t nb = (R + WB - 1) / WB, nbc = (C + WB - 1) / WB;
+  return nbc * (nbc + 1) / 2 + (nb - nbc) * nbc;
+}
+
+// A panel's update of the next panel's columns (D's first PB columns, every row: blocks (x, 0));
+// the last workgroup copies the staged diagonal block of panel `sc` (PB rows) into W.
+template <int PB>
+__global__ __launch_bounds__(256, 2) void syrk_strip_kernel(float* __restrict__ w, int64_t ld, int64_t r0, int R,
+                                                            int64_t pc, int K, int64_t sc,
+                                                            const float* __restrict__ stage) {
+  __shared__ __align__(16) WideLds sm;
+  if (blockIdx.x == gridDim.x - 1) {
+    stage_to_w<float, PB>(w, ld, sc, PB, stage);
+    return;
+  }
+  syrk_wide_block(sm, w, ld, r0, R, PB, pc, K, (int)blockIdx.x, 0);
 }
 
 // Look-ahead step of the fp32 Cholesky: workgroups [0, n_potrf) factor and solve panel j0; the
-// others apply the rest of the previous panel's trailing update (the square W[r0.., r0..], R x R,
-// P = W[r0.., pc .. pc + K), its first K columns -- panel j0 -- already updated by the strip
-// kernel).  The two touch disjoint columns, so the panel's latency-bound factorisation runs beside
-// the throughput-bound update.
+// others apply a pending trapezoid update (square W[r0.., r0..], R x R, columns < C, rank K from
+// P = W[r0.., pc .. pc + K)).  The two touch disjoint columns, so the panel's latency-bound
+// factorisation runs beside the throughput-bound update.
 template <int PB>
-__global__ __launch_bounds__(256) void panel_step_kernel(float* __restrict__ w, int64_t ld, int64_t j0, int n,
-                                                         int64_t k, int* __restrict__ info, float* __restrict__ stage,
-                                                         int64_t n_potrf, int64_t r0, int64_t R, int64_t pc) {
+__global__ __launch_bounds__(256, 2) void panel_step_kernel(float* __restrict__ w, int64_t ld, int64_t j0, int n,
+                                                            int64_t k, int* __restrict__ info,
+                                                            float* __restrict__ stage, int64_t n_potrf, int64_t r0,
+                                                            int R, int C, int64_t pc, int K) {
   __shared__ __align__(16) union {
     PotrfLds<float, PB> p;
-    SyrkLds<PB> s;
+    WideLds s;
   } sm;
   if ((int64_t)blockIdx.x < n_potrf) {
     potrf_panel<float, PB>(sm.p, w, ld, j0, n, k, info, stage, blockIdx.x, n_potrf);
     return;
   }
-  int64_t ti, tj;
-  triangle_tile(blockIdx.x - n_potrf, gridDim.x - n_potrf, ti, tj);
-  syrk_tile<PB>(sm.s, w, ld, r0, R, pc, ti, tj);
+  int bi, bj;
+  trapezoid_block(xcd_contiguous(blockIdx.x - n_potrf, gridDim.x - n_potrf), (C + WB - 1) / WB, bi, bj);
+  syrk_wide_block(sm.s, w, ld, r0, R, C, pc, K, bi, bj);
 }
 
 template <typename T>
@@ -499,38 +637,58 @@ int cholesky_inplace(T* w, int64_t k, int* info, T* stage, hipStream_t stream, i
   int rc;
   if (col_end < 0 || col_end > k) col_end = k;
   if constexpr (sizeof(T) == 4) {
-    if (k % 4 == 0) {
-      // look-ahead: panel j0's update of the next panel's columns runs on its own (strip); the rest
-      // of its trailing update runs in the launch that factors the next panel
-      int64_t pr0 = 0, pR = 0, ppc = 0;  // rest update still to apply
+    if (k % 4 == 0 && k * k < (int64_t)1 << 29) {
+      // two-level: strips of SW columns (aligned to multiples of SW, cut at the range ends).  Inside
+      // a strip, each panel updates only the strip's later columns (rank PB); after a strip's last
+      // panel, one rank-(strip width) update covers everything to its right -- four times the
+      // arithmetic per byte of the trailing triangle that a rank-PB update moves.  Look-ahead: the
+      // update of the next panel's columns runs on its own (strip kernel), the rest of the update
+      // runs in the launch that factors the next panel.
+      constexpr int64_t SW = 4 * PB;
+      int64_t pr0 = 0, pC = 0, ppc = 0;  // pending trapezoid update (columns < pC of W[pr0.., pr0..])
+      int pK = 0;
       for (int64_t j0 = col_begin; j0 < col_end; j0 += PB) {
         const int n = k - j0 < PB ? (int)(k - j0) : PB;
         const int64_t rest = k - j0 - PB;
         const int64_t blocks = rest > 0 ? (cdiv(rest, 64) < 256 ? cdiv(rest, 64) : 256) : 1;
-        const int64_t nt = pR > 0 ? cdiv(pR, 64) : 0;
-        hipLaunchKernelGGL((panel_step_kernel<PB>), dim3((unsigned)(blocks + nt * (nt + 1) / 2)), dim3(256), 0, stream,
-                           (float*)w, k, j0, n, k, info, (float*)stage, blocks, pr0, pR, ppc);
+        const int64_t pR = pC > 0 ? k - pr0 : 0;
+        const int64_t upd = pC > 0 ? trapezoid_blocks(pR, pC) : 0;
+        hipLaunchKernelGGL((panel_step_kernel<PB>), dim3((unsigned)(blocks + upd)), dim3(256), 0, stream, (float*)w,
+                           k, j0, n, k, info, (float*)stage, blocks, pr0, (int)pR, (int)pC, ppc, pK);
         if ((rc = (int)hipGetLastError())) return rc;
-        pR = 0;
+        pC = 0;
         if (rest <= 0) {  // the last panel: its staged block into W on its own
           hipLaunchKernelGGL((stage_to_w_kernel<float, PB>), dim3(1), dim3(256), 0, stream, (float*)w, k, j0, n,
                              (const float*)stage);
           if ((rc = (int)hipGetLastError())) return rc;
           break;
         }
-        hipLaunchKernelGGL((syrk_strip_kernel<PB>), dim3((unsigned)cdiv(rest, 64) + 1), dim3(256), 0, stream,
-                           (float*)w, k, j0 + PB, rest, j0, (const float*)stage);
+        // the strip of panel j0: [s_lo, s_hi)
+        const int64_t s_al = j0 / SW * SW;
+        const int64_t s_lo = s_al > col_begin ? s_al : col_begin;
+        const int64_t s_hi = s_al + SW < col_end ? s_al + SW : col_end;
+        const bool strip_end = j0 + PB >= s_hi;
+        // the strip's rank: panel j0 alone inside the strip, the whole strip at its end
+        const int64_t pc = strip_end ? s_lo : j0;
+        const int K = (int)(j0 + PB - pc);
+        hipLaunchKernelGGL((syrk_strip_kernel<PB>), dim3((unsigned)cdiv(rest, WB) + 1), dim3(256), 0, stream, (float*)w,
+                           k, j0 + PB, (int)rest, pc, K, j0, (const float*)stage);
         if ((rc = (int)hipGetLastError())) return rc;
-        if (rest > PB) {
-          pr0 = j0 + 2 * PB;
-          pR = rest - PB;
-          ppc = j0;
+        // the rest: the strip's later columns, or everything to the right at a strip's end
+        const int64_t r0 = j0 + 2 * PB, R = rest - PB;
+        const int64_t C = strip_end ? R : (s_hi - r0 < R ? s_hi - r0 : R);
+        if (R > 0 && C > 0) {
+          pr0 = r0;
+          pC = C;
+          ppc = pc;
+          pK = K;
         }
       }
-      if (pR > 0) {  // a range that stops early: apply the last panel's rest on its own
-        const int64_t nt = cdiv(pR, 64);
-        hipLaunchKernelGGL((panel_step_kernel<PB>), dim3((unsigned)(nt * (nt + 1) / 2)), dim3(256), 0, stream,
-                           (float*)w, k, (int64_t)0, 0, k, info, (float*)stage, (int64_t)0, pr0, pR, ppc);
+      if (pC > 0) {  // a range that stops early: apply the pending update on its own
+        const int64_t pR = k - pr0;
+        hipLaunchKernelGGL((panel_step_kernel<PB>), dim3((unsigned)trapezoid_blocks(pR, pC)), dim3(256), 0, stream,
+                           (float*)w, k, (int64_t)0, 0, k, info, (float*)stage, (int64_t)0, pr0, (int)pR, (int)pC,
+                           ppc, pK);
         if ((rc = (int)hipGetLastError())) return rc;
       }
       return 0;
@@ -729,8 +887,9 @@ int ldl_of_inverse_part(const T* m, T* out, T* work, int* info, int64_t k, int64
   constexpr int PB = LdlBlock<T>::PB;
   if (k < 0 || size <= 0 || (k > 0 && k % size)) return GPTQ2D_EINVAL;
   if (size > 1 && size > LdlBlock<T>::NB) return GPTQ2D_EUNSUPPORTED;
-  if (col_begin < 0 || col_begin % PB || (col_end >= 0 && col_end < col_begin) || (col_end >= 0 && col_end % PB &&
-                                                                                     col_end < k))
+  // range ends on panel boundaries, or at k (col_begin = k: nothing left to factor)
+  if (col_begin < 0 || (col_begin % PB && col_begin != k) || (col_end >= 0 && col_end < col_begin) ||
+      (col_end >= 0 && col_end % PB && col_end < k))
     return GPTQ2D_EINVAL;
   if (k == 0) return 0;
   int rc;

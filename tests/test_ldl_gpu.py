@@ -158,6 +158,42 @@ def test_concurrent_factors_deterministic():
         assert lo.equal(ref_l) and up.equal(ref_u), rep
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+@pytest.mark.parametrize("ka,kb", [(777, 600), (100, 257), (65, 64)])
+def test_feedback_factors_of_grams_ragged(ka, kb, dtype):
+    """Sizes that are not multiples of the panel width: the factor pair equals the single-stream factors
+    bitwise (the inverse-only part starts at column k, past the last panel)."""
+    print(f"feedback_factors_of_grams {ka} {kb} {dtype}", flush=True)
+    a = instances.wishart_factor(ka, .5, 40 + ka).to(dtype).to(DEV)
+    b = instances.wishart_factor(kb, .5, 50 + kb).to(dtype).to(DEV)
+    lo, up = LDL.feedback_factors_of_grams(a, b, (1, 1))
+    assert lo.equal(LDL.ldl_of_inverse(a)) and up.equal(LDL.ldl_of_inverse(b).t())
+    _check_factor(lo, a, 1, True, 1e-9 if dtype == torch.float64 else 2e-4)
+
+
+@pytest.mark.parametrize("k,cuts", [(1536, (192, 640)), (600, (64, 320, 512)), (8192, (4160,))])
+def test_cholesky_in_parts(k, cuts):
+    """The Cholesky split over calls at panel boundaries that cut the 256-column strips of the fp32 path:
+    each call ends with the update of everything right of its range, so the parts make the same factor
+    (up to rounding: the strips' rank-256 updates are grouped differently)."""
+    print(f"cholesky in parts k={k} cuts={cuts}", flush=True)
+    m = instances.wishart_factor(k, .5, 60 + k).float().to(DEV)
+    out, work = torch.empty_like(m), torch.empty_like(m)
+    info = torch.zeros(1, dtype=torch.int32, device=DEV)
+    bounds = (0,) + cuts + (-1,)
+    for c0, c1 in zip(bounds[:-1], bounds[1:]):
+        LDL._part(m, out, work, info, k, 1, c0, c1, 0)
+    LDL._part(m, out, work, info, k, 1, k, -1, 1)
+    torch.cuda.synchronize()
+    assert info.item() == 0
+    ref = LDL.ldl_of_inverse(m)
+    err = ((out - ref).abs().max() / ref.abs().max()).item()
+    print(f"  parts vs one call: max rel diff {err:.2e}", flush=True)
+    assert err < 1e-4
+    if k <= 2048:
+        _check_factor(out, m, 1, True, 2e-4)
+
+
 def test_headline_size_fp32():
     """8192 x 8192 fp32 factor of the headline layer: structure, and agreement with the fp64 oracle on a
     sampled set of rows (the full fp64 CPU reference takes too long here)."""
