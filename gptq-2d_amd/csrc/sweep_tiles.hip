@@ -243,9 +243,11 @@ struct TileLds {
 // IEEE quotient whenever also |y| in [2^-60, 2^60] or y = 0 (then nothing over- or underflows),
 // the division itself otherwise.  This keeps the division's ten dependent operations off the
 // per-antidiagonal critical path.
+// Every lane evaluates it (no divergent branch on the per-step critical path); the division runs
+// only when a lane with `active` set needs it, behind a branch that is uniform over the wave.
 template <int KIND>
 __device__ __forceinline__ float quantize_entry_rcp(float yv, float sv, float zv, float rv, bool s_ok, float qmin,
-                                                    float qmax) {
+                                                    float qmax, bool active) {
   // the dequantized value is rounded on its own (as the reference's plug-in writes it), so that the
   // caller's error z - y is exactly that difference: no contraction into the caller's subtraction
 #pragma clang fp contract(off)
@@ -254,7 +256,11 @@ __device__ __forceinline__ float quantize_entry_rcp(float yv, float sv, float zv
     const float rem = __builtin_fmaf(-q0, sv, yv);
     float q = __builtin_fmaf(rem, rv, q0);
     const float ay = __builtin_fabsf(yv);
-    if (!(s_ok && ay <= 0x1p60f && (ay >= 0x1p-60f || yv == 0.f))) q = yv / sv;
+    const bool exact = s_ok && ay <= 0x1p60f && (ay >= 0x1p-60f || yv == 0.f);
+    if (__builtin_amdgcn_ballot_w64(active && !exact)) {
+      asm volatile("");  // keeps the division behind the branch (no speculation into a select)
+      if (!exact) q = yv / sv;
+    }
     const float code = clamp_val(round_even(q + zv), qmin, qmax);
     return (code - zv) * sv;
   } else if constexpr (KIND == Q_FORCED) {
@@ -309,7 +315,8 @@ __device__ __forceinline__ void sweep_tile_push(TileLds& tl, float* __restrict__
       S[k] = tl.Ss[r][ck[k]];
     }
   }
-  float* ypre_row = qs.ypre ? qs.ypre + mat + (i0 + r) * n + j0 : nullptr;
+  const bool has_ypre = qs.ypre != nullptr;
+  float* ypre_row = has_ypre ? qs.ypre + mat + (i0 + r) * n + j0 : nullptr;
   // clamp bounds pinned in registers (an empty asm makes them opaque): otherwise the compiler
   // re-reads them from the kernel arguments on every step
   float qmin = qs.qmin, qmax = qs.qmax;
@@ -325,17 +332,21 @@ __device__ __forceinline__ void sweep_tile_push(TileLds& tl, float* __restrict__
 #pragma unroll
   for (int t = 0; t < 2 * TR - 1; ++t) {
     const int ka = (t >> 3) & 3, buf = t & 1;
-    if (part == (t & 7) && row_in && t - r >= 0 && t - r < cols_in) {
+    // every lane evaluates its step-t register; only the rounding lanes keep and publish it
+    const bool rnd = part == (t & 7) && row_in && t - r >= 0 && t - r < cols_in;
+    {
       const float yv = (Y[ka] + D[ka]) + F[ka];
-      const float z = quantize_entry_rcp<KIND>(yv, S[ka], Z[ka], R[ka], s_ok[ka], qmin, qmax);
+      const float z = quantize_entry_rcp<KIND>(yv, S[ka], Z[ka], R[ka], s_ok[ka], qmin, qmax, rnd);
       const float ev = z - yv;
       const float cf = (C[ka] + D[ka]) + ev;
-      Y[ka] = z;
-      E[ka] = ev;
-      C[ka] = cf;
-      tl.Ed[buf][t - r] = ev;
-      tl.Cr[buf][r] = cf;
-      if (ypre_row) ypre_row[t - r] = yv;
+      if (rnd) {
+        Y[ka] = z;
+        E[ka] = ev;
+        C[ka] = cf;
+        tl.Ed[buf][t - r] = ev;
+        tl.Cr[buf][r] = cf;
+      }
+      if (has_ypre && rnd) ypre_row[t - r] = yv;
     }
     __syncthreads();
     if (t == 2 * TR - 2) break;  // nothing left to receive feedback
