@@ -42,6 +42,7 @@
 
 #include <rocblas/rocblas.h>
 
+#include <array>
 #include <type_traits>
 #include <unordered_map>
 
@@ -626,75 +627,101 @@ __global__ __launch_bounds__(256, 2) void panel_step_kernel(float* __restrict__ 
   syrk_wide_block(sm.s, w, ld, r0, R, C, pc, K, bi, bj);
 }
 
+// Launch sequence of the blocked Cholesky of W (k x k) in place over the panels [col_begin, col_end)
+// (multiples of PB; col_end < 0: to the end), one panel per step() so that one host thread can
+// interleave two factorisations on two streams.  Between runs (and after finish()), every earlier
+// panel's update has been applied to the whole trailing matrix and every factored diagonal block
+// is in W.  stage: PB x PB elements of scratch (a panel's factored diagonal block between its
+// launch and the next).
 template <typename T>
-int cholesky_inplace(T* w, int64_t k, int* info, T* stage, hipStream_t stream, int64_t col_begin = 0,
-                     int64_t col_end = -1) {
-  // panels [col_begin, col_end) (multiples of PB; col_end < 0: to the end).  Between calls, every
-  // earlier panel's update has been applied to the whole trailing matrix and every factored
-  // diagonal block is in W.  stage: PB x PB elements of scratch (a panel's factored diagonal block
-  // between its launch and the next).
-  constexpr int PB = LdlBlock<T>::PB;
-  int rc;
-  if (col_end < 0 || col_end > k) col_end = k;
-  if constexpr (sizeof(T) == 4) {
-    if (k % 4 == 0 && k * k < (int64_t)1 << 29) {
-      // two-level: strips of SW columns (aligned to multiples of SW, cut at the range ends).  Inside
-      // a strip, each panel updates only the strip's later columns (rank PB); after a strip's last
-      // panel, one rank-(strip width) update covers everything to its right -- four times the
-      // arithmetic per byte of the trailing triangle that a rank-PB update moves.  Look-ahead: the
-      // update of the next panel's columns runs on its own (strip kernel), the rest of the update
-      // runs in the launch that factors the next panel.
-      constexpr int64_t SW = 4 * PB;
-      int64_t pr0 = 0, pC = 0, ppc = 0;  // pending trapezoid update (columns < pC of W[pr0.., pr0..])
-      int pK = 0;
-      for (int64_t j0 = col_begin; j0 < col_end; j0 += PB) {
-        const int n = k - j0 < PB ? (int)(k - j0) : PB;
-        const int64_t rest = k - j0 - PB;
-        const int64_t blocks = rest > 0 ? (cdiv(rest, 64) < 256 ? cdiv(rest, 64) : 256) : 1;
-        const int64_t pR = pC > 0 ? k - pr0 : 0;
-        const int64_t upd = pC > 0 ? trapezoid_blocks(pR, pC) : 0;
-        hipLaunchKernelGGL((panel_step_kernel<PB>), dim3((unsigned)(blocks + upd)), dim3(256), 0, stream, (float*)w,
-                           k, j0, n, k, info, (float*)stage, blocks, pr0, (int)pR, (int)pC, ppc, pK);
-        if ((rc = (int)hipGetLastError())) return rc;
-        pC = 0;
-        if (rest <= 0) {  // the last panel: its staged block into W on its own
-          hipLaunchKernelGGL((stage_to_w_kernel<float, PB>), dim3(1), dim3(256), 0, stream, (float*)w, k, j0, n,
-                             (const float*)stage);
-          if ((rc = (int)hipGetLastError())) return rc;
-          break;
-        }
-        // the strip of panel j0: [s_lo, s_hi)
-        const int64_t s_al = j0 / SW * SW;
-        const int64_t s_lo = s_al > col_begin ? s_al : col_begin;
-        const int64_t s_hi = s_al + SW < col_end ? s_al + SW : col_end;
-        const bool strip_end = j0 + PB >= s_hi;
-        // the strip's rank: panel j0 alone inside the strip, the whole strip at its end
-        const int64_t pc = strip_end ? s_lo : j0;
-        const int K = (int)(j0 + PB - pc);
-        hipLaunchKernelGGL((syrk_strip_kernel<PB>), dim3((unsigned)cdiv(rest, WB) + 1), dim3(256), 0, stream, (float*)w,
-                           k, j0 + PB, (int)rest, pc, K, j0, (const float*)stage);
-        if ((rc = (int)hipGetLastError())) return rc;
-        // the rest: the strip's later columns, or everything to the right at a strip's end
-        const int64_t r0 = j0 + 2 * PB, R = rest - PB;
-        const int64_t C = strip_end ? R : (s_hi - r0 < R ? s_hi - r0 : R);
-        if (R > 0 && C > 0) {
-          pr0 = r0;
-          pC = C;
-          ppc = pc;
-          pK = K;
-        }
-      }
-      if (pC > 0) {  // a range that stops early: apply the pending update on its own
-        const int64_t pR = k - pr0;
-        hipLaunchKernelGGL((panel_step_kernel<PB>), dim3((unsigned)trapezoid_blocks(pR, pC)), dim3(256), 0, stream,
-                           (float*)w, k, (int64_t)0, 0, k, info, (float*)stage, (int64_t)0, pr0, (int)pR, (int)pC,
-                           ppc, pK);
-        if ((rc = (int)hipGetLastError())) return rc;
-      }
-      return 0;
-    }
+struct CholeskyRun {
+  static constexpr int PB = LdlBlock<T>::PB;
+  static constexpr int64_t SW = 4 * PB;  // strip width of the two-level fp32 path
+  T* w;
+  int64_t k;
+  int* info;
+  T* stage;
+  hipStream_t stream;
+  int64_t col_begin, col_end, j0;
+  bool two_level, done = false;
+  int64_t pr0 = 0, pC = 0, ppc = 0;  // pending trapezoid update (columns < pC of W[pr0.., pr0..])
+  int pK = 0;
+
+  CholeskyRun(T* w_, int64_t k_, int* info_, T* stage_, hipStream_t s, int64_t cb = 0, int64_t ce = -1)
+      : w(w_), k(k_), info(info_), stage(stage_), stream(s), col_begin(cb), col_end(ce < 0 || ce > k_ ? k_ : ce),
+        j0(cb) {
+    two_level = sizeof(T) == 4 && k % 4 == 0 && k * k < (int64_t)1 << 29;
+    done = j0 >= col_end;
   }
-  for (int64_t j0 = col_begin; j0 < col_end; j0 += PB) {
+
+  // The launches of panel j0, then j0 += PB.
+  int step() {
+    if (done) return 0;
+    int rc;
+    if constexpr (sizeof(T) == 4)
+      rc = two_level ? step_two_level() : step_plain();
+    else
+      rc = step_plain();
+    if (rc) return rc;
+    j0 += PB;
+    if (!done && j0 >= col_end) {
+      done = true;
+      return finish();
+    }
+    return 0;
+  }
+
+ private:
+  // fp32, two levels: strips of SW columns (aligned to multiples of SW, cut at the range ends).
+  // Inside a strip, each panel updates only the strip's later columns (rank PB); after a strip's
+  // last panel, one rank-(strip width) update covers everything to its right -- four times the
+  // arithmetic per byte of the trailing triangle that a rank-PB update moves.  Look-ahead: the
+  // update of the next panel's columns runs on its own (strip kernel), the rest of the update runs
+  // in the launch that factors the next panel.
+  int step_two_level() {
+    int rc;
+    float* wf = (float*)w;
+    const int n = k - j0 < PB ? (int)(k - j0) : PB;
+    const int64_t rest = k - j0 - PB;
+    const int64_t blocks = rest > 0 ? (cdiv(rest, 64) < 256 ? cdiv(rest, 64) : 256) : 1;
+    const int64_t pR = pC > 0 ? k - pr0 : 0;
+    const int64_t upd = pC > 0 ? trapezoid_blocks(pR, pC) : 0;
+    hipLaunchKernelGGL((panel_step_kernel<PB>), dim3((unsigned)(blocks + upd)), dim3(256), 0, stream, wf, k, j0, n, k,
+                       info, (float*)stage, blocks, pr0, (int)pR, (int)pC, ppc, pK);
+    if ((rc = (int)hipGetLastError())) return rc;
+    pC = 0;
+    if (rest <= 0) {  // the last panel: its staged block into W on its own
+      hipLaunchKernelGGL((stage_to_w_kernel<float, PB>), dim3(1), dim3(256), 0, stream, wf, k, j0, n,
+                         (const float*)stage);
+      done = true;
+      return (int)hipGetLastError();
+    }
+    // the strip of panel j0: [s_lo, s_hi)
+    const int64_t s_al = j0 / SW * SW;
+    const int64_t s_lo = s_al > col_begin ? s_al : col_begin;
+    const int64_t s_hi = s_al + SW < col_end ? s_al + SW : col_end;
+    const bool strip_end = j0 + PB >= s_hi;
+    // the update's rank: panel j0 alone inside the strip, the whole strip at its end
+    const int64_t pc = strip_end ? s_lo : j0;
+    const int K = (int)(j0 + PB - pc);
+    hipLaunchKernelGGL((syrk_strip_kernel<PB>), dim3((unsigned)cdiv(rest, WB) + 1), dim3(256), 0, stream, wf, k,
+                       j0 + PB, (int)rest, pc, K, j0, (const float*)stage);
+    if ((rc = (int)hipGetLastError())) return rc;
+    // the rest: the strip's later columns, or everything to the right at a strip's end
+    const int64_t r0 = j0 + 2 * PB, R = rest - PB;
+    const int64_t C = strip_end ? R : (s_hi - r0 < R ? s_hi - r0 : R);
+    if (R > 0 && C > 0) {
+      pr0 = r0;
+      pC = C;
+      ppc = pc;
+      pK = K;
+    }
+    return 0;
+  }
+
+  // fp64 (and fp32 with k % 4 != 0): panel, staged block into W, trailing update on gemm.hip.
+  int step_plain() {
+    int rc;
     const int n = k - j0 < PB ? (int)(k - j0) : PB;
     const int64_t rest = k - j0 - PB;
     const unsigned blocks = rest > 0 ? (unsigned)(cdiv(rest, 64) < 256 ? cdiv(rest, 64) : 256) : 1u;
@@ -702,7 +729,10 @@ int cholesky_inplace(T* w, int64_t k, int* info, T* stage, hipStream_t stream, i
     if ((rc = (int)hipGetLastError())) return rc;
     hipLaunchKernelGGL((stage_to_w_kernel<T, PB>), dim3(1), dim3(256), 0, stream, w, k, j0, n, (const T*)stage);
     if ((rc = (int)hipGetLastError())) return rc;
-    if (rest <= 0) break;
+    if (rest <= 0) {
+      done = true;
+      return 0;
+    }
     // trailing lower triangle: W22 -= P P^T with P = W[j0+PB:, j0:j0+PB]
     GemmProblem<T> g{};
     g.M = g.N = rest;
@@ -720,16 +750,49 @@ int cholesky_inplace(T* w, int64_t k, int* info, T* stage, hipStream_t stream, i
     g.alpha = T(-1);
     g.beta = T(1);
     g.d_tri = TRI_LOWER;
-    if ((rc = gptq2d_gemm<T>(g, stream))) return rc;
+    return gptq2d_gemm<T>(g, stream);
   }
+
+  // A range that stops early: the pending update on its own.
+  int finish() {
+    if constexpr (sizeof(T) == 4) {
+      if (pC <= 0) return 0;
+      const int64_t pR = k - pr0;
+      hipLaunchKernelGGL((panel_step_kernel<PB>), dim3((unsigned)trapezoid_blocks(pR, pC)), dim3(256), 0, stream,
+                         (float*)w, k, (int64_t)0, 0, k, info, (float*)stage, (int64_t)0, pr0, (int)pR, (int)pC,
+                         ppc, pK);
+      pC = 0;
+      return (int)hipGetLastError();
+    }
+    return 0;
+  }
+};
+
+template <typename T>
+int cholesky_inplace(T* w, int64_t k, int* info, T* stage, hipStream_t stream, int64_t col_begin = 0,
+                     int64_t col_end = -1) {
+  CholeskyRun<T> run(w, k, info, stage, stream, col_begin, col_end);
+  int rc;
+  while (!run.done)
+    if ((rc = run.step())) return rc;
   return 0;
 }
 
-// Zero the strict upper triangle of W (k x k), one row per workgroup.
+// Elements from the start of `out` where the Cholesky stages its factored diagonal blocks: the
+// buffer's last PB x PB elements, away from what the triangular inverse's first part writes while
+// the factorisation still runs.
 template <typename T>
-__global__ __launch_bounds__(256) void zero_upper_kernel(T* __restrict__ w, int64_t k) {
-  for (int64_t i = blockIdx.x; i < k; i += gridDim.x)
-    for (int64_t j = i + 1 + threadIdx.x; j < k; j += 256) w[i * k + j] = T(0);
+int64_t stage_offset(int64_t k) {
+  constexpr int64_t PB = LdlBlock<T>::PB;
+  return k * k > PB * PB ? k * k - PB * PB : 0;
+}
+
+// Zero the strict upper triangle of the n x n diagonal block at w (row stride ld), one row per
+// workgroup.
+template <typename T>
+__global__ __launch_bounds__(256) void zero_upper_kernel(T* __restrict__ w, int64_t ld, int64_t n) {
+  for (int64_t i = blockIdx.x; i < n; i += gridDim.x)
+    for (int64_t j = i + 1 + threadIdx.x; j < n; j += 256) w[i * ld + j] = T(0);
 }
 
 // rocBLAS handle of the current device for this host thread, created on first use and kept until
@@ -768,48 +831,50 @@ int blas_gemm_rm(int64_t M, int64_t N, int64_t K, int64_t batch, const float* A,
   return st == rocblas_status_success ? 0 : GPTQ2D_EUNSUPPORTED;
 }
 
-// In-place inverse of the lower triangular W (k x k); tmp holds >= k*k/4 + k elements, and for
-// fp32 the rest of a k x k buffer behind it serves as GEMM workspace.
+// A level product of the triangular inverse: the MFMA kernel that skips the zero triangle of the
+// inverted block (tri = 1: B lower, 2: A lower), or rocBLAS's dense GEMM where that kernel's layout
+// conditions do not hold (rows not on 16-byte boundaries).
+int level_gemm(int64_t M, int64_t N, int64_t K, int64_t batch, const float* A, int64_t lda, int64_t sa,
+               const float* B, int64_t ldb, int64_t sb, float* D, int64_t ldd, int64_t sd, float alpha, int tri,
+               void* ws, size_t ws_bytes, hipStream_t stream) {
+  TriGemm g{M, N, K, batch, A, lda, sa, B, ldb, sb, D, ldd, sd, alpha, tri};
+  const int rc = gptq2d_tri_gemm_f32(g, stream);
+  if (rc != GPTQ2D_EUNSUPPORTED) return rc;
+  return blas_gemm_rm(M, N, K, batch, A, lda, sa, B, ldb, sb, D, ldd, sd, alpha, 0.f, ws, ws_bytes, stream);
+}
+
+// In-place inverse of the lower triangular n x n diagonal block at w (row stride ld): leaves, then
+// the levels.  tmp: >= n*n/4 + n elements for the levels' products.  blas (fp32): the levels on
+// rocBLAS with workspace ws; the block's strict upper triangle is zeroed first (the dense GEMMs
+// read it as the triangles' padding).
 template <typename T>
-int trtri_inplace(T* w, int64_t k, T* tmp, hipStream_t stream) {
+int trtri_block(T* w, int64_t ld, int64_t n, T* tmp, bool blas, void* ws, size_t ws_bytes, hipStream_t stream) {
   constexpr int NB = LdlBlock<T>::NB;
   int rc;
-  hipLaunchKernelGGL((trtri_leaf_kernel<T, NB>), dim3((unsigned)cdiv(k, NB)), dim3(64), 0, stream, w, k, k);
+  hipLaunchKernelGGL((trtri_leaf_kernel<T, NB>), dim3((unsigned)cdiv(n, NB)), dim3(64), 0, stream, w, ld, n);
   if ((rc = (int)hipGetLastError())) return rc;
-  // fp32 from k = 512 on: every level's two products run as dense GEMMs on rocBLAS, the triangular
-  // operands padded with the zeros of W's cleared upper triangle; the GEMM workspace (up to 64 MiB)
-  // is the part of the k x k buffer behind tmp that the levels do not use
-  void* ws = nullptr;
-  size_t ws_bytes = 0;
-  bool blas = false;
-  if constexpr (sizeof(T) == 4) {
-    const uintptr_t lo = ((uintptr_t)(tmp + k * k / 4 + k) + 255) & ~(uintptr_t)255, hi = (uintptr_t)(tmp + k * k);
-    blas = k >= 512 && hi > lo;
-    if (blas) {
-      ws = (void*)lo;
-      ws_bytes = hi - lo < ((size_t)64 << 20) ? hi - lo : ((size_t)64 << 20);
-      hipLaunchKernelGGL(zero_upper_kernel<T>, dim3((unsigned)(k < 8192 ? k : 8192)), dim3(256), 0, stream, w, k);
-      if ((rc = (int)hipGetLastError())) return rc;
-    }
+  if (blas) {
+    hipLaunchKernelGGL(zero_upper_kernel<T>, dim3((unsigned)(n < 8192 ? n : 8192)), dim3(256), 0, stream, w, ld, n);
+    if ((rc = (int)hipGetLastError())) return rc;
   }
-  for (int64_t s = NB; s < k; s *= 2) {
-    const int64_t full = k / (2 * s);                  // pairs with two full s-blocks
-    const int64_t tail_r1 = full * 2 * s + s;          // a last, short pair starts its D block here
-    const int64_t tail = tail_r1 < k ? k - tail_r1 : 0;
+  for (int64_t s = NB; s < n; s *= 2) {
+    const int64_t full = n / (2 * s);          // pairs with two full s-blocks
+    const int64_t tail_r1 = full * 2 * s + s;  // a last, short pair starts its D block here
+    const int64_t tail = tail_r1 < n ? n - tail_r1 : 0;
     for (int part = 0; part < 2; ++part) {
       const int64_t pairs = part == 0 ? full : (tail > 0 ? 1 : 0);
       if (pairs == 0) continue;
       const int64_t r0 = part == 0 ? 0 : full * 2 * s;
       const int64_t s2 = part == 0 ? s : tail;
+      const int64_t bs = 2 * s * ld + 2 * s;
       if constexpr (sizeof(T) == 4) {
         if (blas) {
-          const int64_t bs = 2 * s * k + 2 * s;
           // T = B A^{-1}, then B <- -D^{-1} T
-          if ((rc = blas_gemm_rm(s2, s, s, pairs, w + (r0 + s) * k + r0, k, bs, w + r0 * k + r0, k, bs, tmp, s,
-                                 s2 * s, 1.f, 0.f, ws, ws_bytes, stream)))
+          if ((rc = level_gemm(s2, s, s, pairs, w + (r0 + s) * ld + r0, ld, bs, w + r0 * ld + r0, ld, bs, tmp, s,
+                               s2 * s, 1.f, 1, ws, ws_bytes, stream)))
             return rc;
-          if ((rc = blas_gemm_rm(s2, s, s2, pairs, w + (r0 + s) * k + (r0 + s), k, bs, tmp, s, s2 * s,
-                                 w + (r0 + s) * k + r0, k, bs, -1.f, 0.f, ws, ws_bytes, stream)))
+          if ((rc = level_gemm(s2, s, s2, pairs, w + (r0 + s) * ld + (r0 + s), ld, bs, tmp, s, s2 * s,
+                               w + (r0 + s) * ld + r0, ld, bs, -1.f, 2, ws, ws_bytes, stream)))
             return rc;
           continue;
         }
@@ -820,14 +885,14 @@ int trtri_inplace(T* w, int64_t k, T* tmp, hipStream_t stream) {
       g.N = s;
       g.K = s;
       g.batch = pairs;
-      g.A = w + (r0 + s) * k + r0;  // B block
-      g.a_rs = k;
+      g.A = w + (r0 + s) * ld + r0;  // B block
+      g.a_rs = ld;
       g.a_cs = 1;
-      g.a_bs = 2 * s * k + 2 * s;
-      g.B = w + r0 * k + r0;  // A^{-1}
-      g.b_rs = k;
+      g.a_bs = bs;
+      g.B = w + r0 * ld + r0;  // A^{-1}
+      g.b_rs = ld;
       g.b_cs = 1;
-      g.b_bs = 2 * s * k + 2 * s;
+      g.b_bs = bs;
       g.b_tri = TRI_LOWER;
       g.D = tmp;
       g.d_rs = s;
@@ -842,25 +907,129 @@ int trtri_inplace(T* w, int64_t k, T* tmp, hipStream_t stream) {
       h.N = s;
       h.K = s2;
       h.batch = pairs;
-      h.A = w + (r0 + s) * k + (r0 + s);  // D^{-1}
-      h.a_rs = k;
+      h.A = w + (r0 + s) * ld + (r0 + s);  // D^{-1}
+      h.a_rs = ld;
       h.a_cs = 1;
-      h.a_bs = 2 * s * k + 2 * s;
+      h.a_bs = bs;
       h.a_tri = TRI_LOWER;
       h.B = tmp;
       h.b_rs = s;
       h.b_cs = 1;
       h.b_bs = s2 * s;
-      h.D = w + (r0 + s) * k + r0;
-      h.d_rs = k;
+      h.D = w + (r0 + s) * ld + r0;
+      h.d_rs = ld;
       h.d_cs = 1;
-      h.d_bs = 2 * s * k + 2 * s;
+      h.d_bs = bs;
       h.alpha = T(-1);
       h.beta = T(0);
       if ((rc = gptq2d_gemm<T>(h, stream))) return rc;
     }
   }
   return 0;
+}
+
+// Split point of the triangular inverse of a k x k factor: s = NB 2^j, the largest below k, for
+// fp32 from k = 2048 (levels on rocBLAS); 0: no split.  With a split, the inverse of C = [A 0; B D]
+// (A: s x s) runs in three parts:
+//   1. A^{-1} in place and T = B A^{-1} -- these read only the Cholesky's columns < s, so they can
+//      run while the factorisation of the columns >= s goes on;
+//   2. D^{-1} in place, once the factorisation is complete;
+//   3. B <- -D^{-1} T, and the normalisation into out.
+// The levels below s are the same whether or not the inverse is split (the recursive doubling pairs
+// blocks aligned to multiples of their size, and s is a multiple of every lower level's pair size).
+template <typename T>
+int64_t trtri_split(int64_t k) {
+  if constexpr (sizeof(T) != 4) {
+    return 0;
+  } else {
+    if (k < 2048) return 0;
+    int64_t s = LdlBlock<T>::NB;
+    while (2 * s < k) s *= 2;
+    return s;
+  }
+}
+
+// Where the three parts keep their data in `out` (k x k elements, free until the normalisation; its
+// last PB x PB elements stage the Cholesky's diagonal blocks while part 1 runs): T (n2 x s, and
+// before it part 1's level products), part 2's level products, then one rocBLAS workspace for part
+// 1 and one for parts 2 and 3 -- disjoint, as parts 1 and 2 may run at the same time.
+struct TrtriLayout {
+  int64_t s, n2, t_off, tmp2_off;
+  void *ws1, *ws2;
+  size_t ws_bytes;
+};
+
+template <typename T>
+TrtriLayout trtri_layout(T* out, int64_t k, int64_t s) {
+  TrtriLayout L{};
+  L.s = s;
+  L.n2 = k - s;
+  L.t_off = 0;
+  const int64_t t_end = L.n2 * s > s * s / 4 + s ? L.n2 * s : s * s / 4 + s;
+  L.tmp2_off = t_end;
+  const int64_t tmp2_end = L.tmp2_off + L.n2 * L.n2 / 4 + L.n2;
+  const uintptr_t lo = ((uintptr_t)(out + tmp2_end) + 255) & ~(uintptr_t)255;
+  const uintptr_t hi = (uintptr_t)(out + stage_offset<T>(k)) & ~(uintptr_t)255;
+  size_t half = hi > lo ? ((hi - lo) / 2) & ~(size_t)255 : 0;
+  if (half > ((size_t)64 << 20)) half = (size_t)64 << 20;
+  L.ws1 = (void*)lo;
+  L.ws2 = (void*)(lo + half);
+  L.ws_bytes = half;
+  return L;
+}
+
+// In-place inverse of the lower triangular W (k x k) in one sequence; tmp: a k x k buffer (its
+// first k*k/4 + k elements hold the levels' products, for fp32 the rest serves as GEMM workspace).
+template <typename T>
+int trtri_inplace(T* w, int64_t k, T* tmp, hipStream_t stream) {
+  void* ws = nullptr;
+  size_t ws_bytes = 0;
+  bool blas = false;
+  if constexpr (sizeof(T) == 4) {
+    const uintptr_t lo = ((uintptr_t)(tmp + k * k / 4 + k) + 255) & ~(uintptr_t)255, hi = (uintptr_t)(tmp + k * k);
+    blas = k >= 512 && hi > lo;
+    if (blas) {
+      ws = (void*)lo;
+      ws_bytes = hi - lo < ((size_t)64 << 20) ? hi - lo : ((size_t)64 << 20);
+    }
+  }
+  return trtri_block<T>(w, k, k, tmp, blas, ws, ws_bytes, stream);
+}
+
+template <typename T>
+int normalize(T* out, const T* w, int64_t k, int64_t size, int64_t base, int64_t rs, int64_t cs, hipStream_t stream);
+
+// Part `phase` (1, 2, 3 as at trtri_split) of the inverse of the Cholesky factor in work and the
+// normalisation into out (L_raw(i, j) = C^{-1}(k-1-j, k-1-i) = work[(k-1-j) k + (k-1-i)]).  Without
+// a split, part 1 does nothing, part 2 is the whole inverse and part 3 the normalisation.
+template <typename T>
+int trtri_part(T* out, T* w, int64_t k, int64_t size, int phase, hipStream_t stream) {
+  const int64_t s = trtri_split<T>(k);
+  int rc = 0;
+  if (s == 0) {
+    if (phase == 2) return trtri_inplace<T>(w, k, out, stream);
+    if (phase == 3) return normalize<T>(out, w, k, size, (k - 1) * k + (k - 1), -1, -k, stream);
+    return 0;
+  }
+  if constexpr (sizeof(T) == 4) {
+    const TrtriLayout L = trtri_layout<T>(out, k, s);
+    if (L.ws_bytes == 0) return GPTQ2D_EUNSUPPORTED;
+    if (phase == 1) {
+      if ((rc = trtri_block<T>(w, k, s, out + L.t_off, true, L.ws1, L.ws_bytes, stream))) return rc;
+      // T = B A^{-1}: (n2 x s) = (n2 x s) (s x s)
+      return level_gemm(L.n2, s, s, 1, w + s * k, k, 0, w, k, 0, out + L.t_off, s, 0, 1.f, 1, L.ws1, L.ws_bytes,
+                        stream);
+    }
+    if (phase == 2) return trtri_block<T>(w + s * k + s, k, L.n2, out + L.tmp2_off, true, L.ws2, L.ws_bytes, stream);
+    if (phase == 3) {
+      // B <- -D^{-1} T: (n2 x s) = (n2 x n2) (n2 x s)
+      if ((rc = level_gemm(L.n2, s, L.n2, 1, w + s * k + s, k, 0, out + L.t_off, s, 0, w + s * k, k, 0, -1.f, 2,
+                           L.ws2, L.ws_bytes, stream)))
+        return rc;
+      return normalize<T>(out, w, k, size, (k - 1) * k + (k - 1), -1, -k, stream);
+    }
+  }
+  return rc;
 }
 
 template <typename T>
@@ -880,7 +1049,7 @@ int normalize(T* out, const T* w, int64_t k, int64_t size, int64_t base, int64_t
 
 // One matrix of ldl_of_inverse in parts: col_begin == 0 starts it (the reversed copy into work);
 // Cholesky panels [col_begin, col_end) (multiples of the panel width, col_end < 0 or >= k: to the
-// end); finish: the triangular inverse and the normalisation into out.
+// end); finish: the triangular inverse and the normalisation into out (its three parts in order).
 template <typename T>
 int ldl_of_inverse_part(const T* m, T* out, T* work, int* info, int64_t k, int64_t size, int64_t col_begin,
                         int64_t col_end, bool finish, hipStream_t stream) {
@@ -899,11 +1068,83 @@ int ldl_of_inverse_part(const T* m, T* out, T* work, int* info, int64_t k, int64
     hipLaunchKernelGGL(copy_kernel<T>, dim3((unsigned)blocks), dim3(256), 0, stream, work, m, kk, 1);
     if ((rc = (int)hipGetLastError())) return rc;
   }
-  // out is free until the inverse: its first elements stage the factored diagonal blocks
-  if (col_begin < k && (rc = cholesky_inplace<T>(work, k, info, out, stream, col_begin, col_end))) return rc;
-  if (finish) {
-    if ((rc = trtri_inplace<T>(work, k, out, stream))) return rc;
-    if ((rc = normalize<T>(out, work, k, size, (k - 1) * k + (k - 1), -1, -k, stream))) return rc;
+  if (col_begin < k &&
+      (rc = cholesky_inplace<T>(work, k, info, out + stage_offset<T>(k), stream, col_begin, col_end)))
+    return rc;
+  if (finish)
+    for (int phase = 1; phase <= 3; ++phase)
+      if ((rc = trtri_part<T>(out, work, k, size, phase, stream))) return rc;
+  return 0;
+}
+
+// Four events of the current device for this host thread (no timing), created on first use and
+// kept until the process ends.
+int pair_events(hipEvent_t (&ev)[4]) {
+  thread_local std::unordered_map<int, std::array<hipEvent_t, 4>> cache;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return GPTQ2D_EUNSUPPORTED;
+  auto it = cache.find(dev);
+  if (it == cache.end()) {
+    std::array<hipEvent_t, 4> e{};
+    for (auto& x : e)
+      if (hipEventCreateWithFlags(&x, hipEventDisableTiming) != hipSuccess) return GPTQ2D_EUNSUPPORTED;
+    it = cache.emplace(dev, e).first;
+  }
+  for (int i = 0; i < 4; ++i) ev[i] = it->second[i];
+  return 0;
+}
+
+// ldl_of_inverse of two matrices at once (m[f], k[f] x k[f], block size size[f]; outputs out[f],
+// scratch work[f], info[f]), on the caller's streams: factor f on stream[f], the first parts of the
+// triangular inverses on stream[2].  One host loop enqueues the two Cholesky factorisations panel by
+// panel, alternating, so that both chains of latency-bound panel launches are in flight together
+// from the start; when a factorisation has passed its inverse's split point, part 1 of that inverse
+// goes to stream[2] (after an event on stream[f]), where it runs beside the rest of both
+// factorisations; parts 2 and 3 follow on stream[f], part 3 after an event on stream[2].  The
+// results equal two ldl_of_inverse calls bit for bit (the same launches, in another order).
+template <typename T>
+int ldl_of_inverse_pair(const T* const* m, T* const* out, T* const* work, int* const* info, const int64_t* k,
+                        const int64_t* size, hipStream_t const* stream) {
+  for (int f = 0; f < 2; ++f) {
+    if (k[f] < 0 || size[f] <= 0 || (k[f] > 0 && k[f] % size[f])) return GPTQ2D_EINVAL;
+    if (size[f] > 1 && size[f] > LdlBlock<T>::NB) return GPTQ2D_EUNSUPPORTED;
+  }
+  if (stream[0] == stream[1] || stream[0] == stream[2] || stream[1] == stream[2]) return GPTQ2D_EINVAL;
+  hipEvent_t ev[4];  // per factor: Cholesky past the split (on stream[f]), part 1 done (on stream[2])
+  int rc;
+  if ((rc = pair_events(ev))) return rc;
+  int64_t split[2];
+  for (int f = 0; f < 2; ++f) {
+    split[f] = k[f] > 0 ? trtri_split<T>(k[f]) : 0;
+    if (k[f] == 0) continue;
+    const int64_t kk = k[f] * k[f];
+    const int64_t blocks = cdiv(kk, 256) < 8192 ? cdiv(kk, 256) : 8192;
+    hipLaunchKernelGGL(copy_kernel<T>, dim3((unsigned)blocks), dim3(256), 0, stream[f], work[f], m[f], kk, 1);
+    if ((rc = (int)hipGetLastError())) return rc;
+  }
+  CholeskyRun<T> run[2] = {
+      CholeskyRun<T>(work[0], k[0], info[0], out[0] + stage_offset<T>(k[0]), stream[0]),
+      CholeskyRun<T>(work[1], k[1], info[1], out[1] + stage_offset<T>(k[1]), stream[1])};
+  bool lead[2] = {split[0] == 0, split[1] == 0};  // part 1 enqueued (or none)
+  while (!run[0].done || !run[1].done || !lead[0] || !lead[1]) {
+    for (int f = 0; f < 2; ++f) {
+      if ((rc = run[f].step())) return rc;
+      // columns < split final: every panel before the split factored and its block copied into W
+      // (the strip launch of the panel before the split does the copy)
+      if (!lead[f] && (run[f].done || run[f].j0 >= split[f])) {
+        if (hipEventRecord(ev[f], stream[f]) != hipSuccess || hipStreamWaitEvent(stream[2], ev[f], 0) != hipSuccess)
+          return GPTQ2D_EUNSUPPORTED;
+        if ((rc = trtri_part<T>(out[f], work[f], k[f], size[f], 1, stream[2]))) return rc;
+        if (hipEventRecord(ev[2 + f], stream[2]) != hipSuccess) return GPTQ2D_EUNSUPPORTED;
+        lead[f] = true;
+      }
+    }
+  }
+  for (int f = 0; f < 2; ++f) {
+    if (k[f] == 0) continue;
+    if ((rc = trtri_part<T>(out[f], work[f], k[f], size[f], 2, stream[f]))) return rc;
+    if (split[f] && hipStreamWaitEvent(stream[f], ev[2 + f], 0) != hipSuccess) return GPTQ2D_EUNSUPPORTED;
+    if ((rc = trtri_part<T>(out[f], work[f], k[f], size[f], 3, stream[f]))) return rc;
   }
   return 0;
 }
@@ -925,13 +1166,12 @@ int ldl_impl(bool inverse, const T* m, T* out, T* work, int* info, int64_t batch
     const int64_t blocks = cdiv(kk, 256) < 8192 ? cdiv(kk, 256) : 8192;
     hipLaunchKernelGGL(copy_kernel<T>, dim3((unsigned)blocks), dim3(256), 0, stream, wb, mb, kk, inverse ? 1 : 0);
     if ((rc = (int)hipGetLastError())) return rc;
-    // ob is free until the inverse / normalisation: its first elements stage the factored diagonal
+    // ob is free until the inverse / normalisation: its last elements stage the factored diagonal
     // blocks
-    if ((rc = cholesky_inplace<T>(wb, k, ib, ob, stream))) return rc;
+    if ((rc = cholesky_inplace<T>(wb, k, ib, ob + stage_offset<T>(k), stream))) return rc;
     if (inverse) {
-      if ((rc = trtri_inplace<T>(wb, k, ob, stream))) return rc;  // out is free scratch until normalisation
-      // L_raw(i, j) = Cinv(k-1-j, k-1-i) = w[(k-1-j)*k + (k-1-i)]
-      if ((rc = normalize<T>(ob, wb, k, size, (k - 1) * k + (k - 1), -1, -k, stream))) return rc;
+      for (int phase = 1; phase <= 3; ++phase)
+        if ((rc = trtri_part<T>(ob, wb, k, size, phase, stream))) return rc;
     } else {
       if ((rc = normalize<T>(ob, wb, k, size, 0, k, 1, stream))) return rc;
     }
@@ -960,6 +1200,17 @@ GPTQ2D_LDL_ABI(f64, double)
   int gptq2d_ldl_of_inverse_part_##SUF(const T* m, T* out, T* work, int* info, int64_t k, int64_t size,            \
                                        int64_t col_begin, int64_t col_end, int32_t finish, hipStream_t stream) {  \
     return ldl_of_inverse_part<T>(m, out, work, info, k, size, col_begin, col_end, finish != 0, stream);            \
+  }                                                                                                                 \
+  int gptq2d_ldl_of_inverse_pair_##SUF(const T* m0, T* out0, T* work0, int* info0, int64_t k0, int64_t size0,      \
+                                       const T* m1, T* out1, T* work1, int* info1, int64_t k1, int64_t size1,      \
+                                       hipStream_t stream0, hipStream_t stream1, hipStream_t stream2) {            \
+    const T* m[2] = {m0, m1};                                                                                       \
+    T* out[2] = {out0, out1};                                                                                       \
+    T* work[2] = {work0, work1};                                                                                    \
+    int* info[2] = {info0, info1};                                                                                  \
+    const int64_t k[2] = {k0, k1}, size[2] = {size0, size1};                                                        \
+    const hipStream_t st[3] = {stream0, stream1, stream2};                                                          \
+    return ldl_of_inverse_pair<T>(m, out, work, info, k, size, st);                                                  \
   }
 
 GPTQ2D_LDL_PART_ABI(f32, float)

@@ -31,3 +31,23 @@ struct GemmProblem {
 
 template <typename T>
 int gptq2d_gemm(const GemmProblem<T>& p, hipStream_t stream);
+
+// Row-major fp32 D = alpha A B (no beta) for `batch` strided problems with one lower triangular
+// operand whose other triangle holds zeros: tri = 1: B (B(k, j) = 0 for k < j), tri = 2: A
+// (A(i, k) = 0 for k > i), 0: dense.  A: M x K (row stride lda, batch stride sa), B: K x N, D: M x N.
+// On MFMA, skipping the k-tiles that meet only the zero triangle (trmm_mfma.hip).  Needs K, N, lda,
+// ldb, sa, sb multiples of 4, A and B on 16-byte boundaries and each operand under 2^29 elements;
+// returns GPTQ2D_EUNSUPPORTED otherwise (nothing launched).
+struct TriGemm {
+  int64_t M, N, K, batch;
+  const float* A;
+  int64_t lda, sa;
+  const float* B;
+  int64_t ldb, sb;
+  float* D;
+  int64_t ldd, sd;
+  float alpha;
+  int32_t tri;
+};
+
+int gptq2d_tri_gemm_f32(const TriGemm& g, hipStream_t stream);

@@ -13,6 +13,8 @@ parts on fp32 MFMA).  A matrix that is not positive definite raises
 
 from __future__ import annotations
 
+import ctypes
+
 import torch
 
 import _hip
@@ -20,7 +22,7 @@ import _hip
 # p x p diagonal blocks up to this size are normalised on the GPU (fp32; fp64: 32).
 MAX_BLOCK = {torch.float32: 64, torch.float64: 32}
 
-# Two side streams per device for feedback_factors_of_grams (created once: a new stream per call
+# Three side streams per device for feedback_factors_of_grams (created once: a new stream per call
 # would cost a stream creation and defeat the caching allocator's reuse of its blocks).
 _SIDE_STREAMS: dict = {}
 
@@ -28,7 +30,7 @@ _SIDE_STREAMS: dict = {}
 def _side_streams(device: torch.device):
     key = torch.device(device).index if torch.device(device).index is not None else torch.cuda.current_device()
     if key not in _SIDE_STREAMS:
-        _SIDE_STREAMS[key] = tuple(torch.cuda.Stream(device=key) for _ in range(2))
+        _SIDE_STREAMS[key] = tuple(torch.cuda.Stream(device=key) for _ in range(3))
     return _SIDE_STREAMS[key]
 
 
@@ -76,12 +78,12 @@ def _part(m, out, work, info, k, size, col_begin, col_end, finish):
 
 
 def feedback_factors_of_grams(G: torch.Tensor, H: torch.Tensor, super_entry_shape=(1, 1), *, check: bool = True):
-    """(L, U) = (ldl_of_inverse(G, p), ldl_of_inverse(H, q)^T) from the Grams themselves, the two
-    Cholesky factorisations running concurrently on two side streams of the current device (each is a
-    sequence of latency-bound panel steps, so they fill each other's gaps); the triangular inverses,
-    throughput-bound GEMMs on rocBLAS, one after the other (as fast as running them together).  No
-    counterpart in the reference, whose callers compute the two factors one after the other
-    (demo.ipynb cell 5)."""
+    """(L, U) = (ldl_of_inverse(G, p), ldl_of_inverse(H, q)^T) from the Grams themselves, both at once on
+    three side streams of the current device (gptq2d_ldl_of_inverse_pair): the two Cholesky
+    factorisations -- each a chain of latency-bound panel launches -- run together, and the first part
+    of each triangular inverse runs beside the rest of the factorisations.  Bitwise equal to the two
+    ldl_of_inverse calls.  No counterpart in the reference, whose callers compute the two factors one
+    after the other (demo.ipynb cell 5)."""
     p, q = super_entry_shape
     main = torch.cuda.current_stream(G.device)
     streams = _side_streams(G.device)
@@ -98,27 +100,28 @@ def feedback_factors_of_grams(G: torch.Tensor, H: torch.Tensor, super_entry_shap
         jobs.append((m, size, k))
     out = []
     with torch.cuda.device(G.device):
-        # buffers on their stream's pool; the Cholesky parts concurrently
+        # each factor's buffers on its stream's pool
         bufs = []
         for s, (m, size, k) in zip(streams, jobs):
             with torch.cuda.stream(s):
                 src = m.reshape(-1, k, k).contiguous()
-                o = torch.empty_like(src)
-                w = torch.empty_like(src)
-                info = torch.zeros(src.size(0), dtype=torch.int32, device=m.device)
-                for b in range(src.size(0)):
-                    _part(src[b], o[b], w[b], info[b:b + 1], k, size, 0, -1, 0)
-            bufs.append((src, o, w, info))
-        # the inverses (rocBLAS) one after the other
-        done = torch.cuda.Event()
-        for i, (s, (m, size, k), (src, o, w, info)) in enumerate(zip(streams, jobs, bufs)):
-            if i:
-                s.wait_event(done)
-            with torch.cuda.stream(s):
-                for b in range(src.size(0)):
-                    _part(src[b], o[b], w[b], info[b:b + 1], k, size, k, -1, 1)
-                done.record(s)
-            out.append(o.reshape(m.shape))
+                bufs.append((src, torch.empty_like(src), torch.empty_like(src),
+                             torch.zeros(src.size(0), dtype=torch.int32, device=m.device)))
+        (sa, oa, wa, ia), (sb, ob, wb, ib) = bufs
+        (_, pa, ka), (_, pb, kb) = jobs
+        if sa.dtype == sb.dtype and sa.size(0) == sb.size(0):
+            sp = [ctypes.c_void_p(s.cuda_stream) for s in streams]
+            for b in range(sa.size(0)):
+                _hip.call("ldl_of_inverse_pair", sa.dtype, _hip.ptr(sa[b]), _hip.ptr(oa[b]), _hip.ptr(wa[b]),
+                          _hip.ptr(ia[b:b + 1]), ka, pa, _hip.ptr(sb[b]), _hip.ptr(ob[b]), _hip.ptr(wb[b]),
+                          _hip.ptr(ib[b:b + 1]), kb, pb, *sp)
+        else:  # different dtypes or batch counts: each factor on its own stream, in one sequence
+            for s, (m, size, k), (src, o, w, info) in zip(streams, jobs, bufs):
+                with torch.cuda.stream(s):
+                    for b in range(src.size(0)):
+                        _part(src[b], o[b], w[b], info[b:b + 1], k, size, 0, -1, 1)
+        out = [oa.reshape(G.shape), ob.reshape(H.shape)]
+    # streams[2]'s work is ordered before the last launches of streams[0] and [1] (events)
     for s, t in zip(streams, out):
         main.wait_stream(s)
         t.record_stream(main)

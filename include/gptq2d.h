@@ -118,6 +118,17 @@ extern "C" {
    * gptq2d_ldl_of_inverse with batch 1.  info[0] as there. */                                          \
   int gptq2d_ldl_of_inverse_part_##SUF(const T* m, T* out, T* work, int* info, int64_t k, int64_t size,            \
                                        int64_t col_begin, int64_t col_end, int32_t finish, void* stream);          \
+  /* ldl_of_inverse of two matrices at once (the Kronecker factors of one layer; no reference         \
+   * counterpart -- the reference computes them one after the other, demo.ipynb cell 5): matrix f      \
+   * (m_f, k_f x k_f, block size size_f, outputs out_f, scratch work_f, info_f as above) on stream_f,   \
+   * with the first part of each triangular inverse on stream2 (three distinct streams of one          \
+   * device).  The two Cholesky factorisations are enqueued panel by panel, alternating, and the       \
+   * inverse of a factor's leading block starts on stream2 as soon as its factorisation has passed     \
+   * it; stream0 and stream1 wait for stream2 before their normalisations.  Results equal two          \
+   * gptq2d_ldl_of_inverse calls bit for bit. */                                                     \
+  int gptq2d_ldl_of_inverse_pair_##SUF(const T* m0, T* out0, T* work0, int* info0, int64_t k0, int64_t size0,      \
+                                       const T* m1, T* out1, T* work1, int* info1, int64_t k1, int64_t size1,      \
+                                       void* stream0, void* stream1, void* stream2);                               \
   /* Unit lower (block) triangular L with M = L Lambda L^T (ldl, gptq_2d_reference.py:52-55). */       \
   int gptq2d_ldl_##SUF(const T* m, T* out, T* work, int* info, int64_t batch, int64_t k, int64_t size,              \
                        void* stream);                                                                               \

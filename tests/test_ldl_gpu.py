@@ -92,11 +92,12 @@ def _check_factor(got, m, size, inverse, tol):
     assert off.item() < 50 * tol, off.item()
 
 
-@pytest.mark.parametrize("k", [1, 5, 64, 65, 100, 257, 600, 777, 1536])
+@pytest.mark.parametrize("k", [1, 5, 64, 65, 100, 257, 600, 777, 1000, 1536, 2052])
 @pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
 def test_ldl_of_inverse(k, dtype):
-    """Sizes from 512 on take the fp32 path whose inverse levels run on rocBLAS (600, 777: short
-    last pairs; 1536: three full levels and a short one)."""
+    """fp32 from k = 512 on: the inverse's level products on the triangular MFMA kernel (600, 1000:
+    short last pairs and ragged 128-blocks; 1536: three full levels and a short one; 2052: the inverse
+    split at its top level), or on rocBLAS where rows are not 16-byte aligned (777)."""
     print(f"ldl_of_inverse k={k} {dtype}", flush=True)
     m = instances.wishart_factor(k, .5, 10 + k).to(dtype).to(DEV)
     got = LDL.ldl_of_inverse(m)
