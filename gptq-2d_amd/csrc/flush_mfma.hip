@@ -58,21 +58,39 @@ __device__ __forceinline__ void tile_range(const TileFlush& g, int phase, int64_
   hi = g.S1 - a < b ? g.S1 - a : b;
 }
 
+// The launch geometry in 32 bits for the kernel's work-item arithmetic (tile counts and stages stay
+// below 2^15): the scalar unit compares 32-bit values itself, while 64-bit signed compares go
+// through the vector unit and back -- a per-workgroup walk over the row blocks in 64 bits cost
+// microseconds beside the MFMA waves of other workgroups.
+struct TileGeo32 {
+  int mt, nt, S0, S1, S_end;
+};
+
+__device__ __forceinline__ bool is_target(const TileGeo32& g, int I, int J) {
+  return I < g.mt && J < g.nt && I + J >= g.S1 && I + J < g.S_end;
+}
+
+__device__ __forceinline__ void tile_range(const TileGeo32& g, int phase, int I, int J, int& lo, int& hi) {
+  const int a = phase == 0 ? J : I, b = phase == 0 ? I : J;
+  lo = g.S0 - a > 0 ? g.S0 - a : 0;
+  hi = g.S1 - a < b ? g.S1 - a : b;
+}
+
 // Workgroups of a launch are exactly the (row block, column block) pairs that can hold targets:
 // row block `by` (tile rows WT by ..) spans the column blocks [first, last] below.  Launching no
 // empty workgroups matters: the dispatcher hands workgroups to the XCDs and shader engines in
 // turn, and a stride of empty ones leaves whole engines idle while others queue.
-template <int WT>
-__host__ __device__ inline void row_block_span(const TileFlush& g, int64_t by, int64_t& first, int64_t& count) {
-  const int64_t I0 = by * WT;
-  int64_t jt_lo = g.S1 - (I0 + WT - 1);
+template <int WT, typename G, typename Int>
+__host__ __device__ inline void row_block_span(const G& g, Int by, Int& first, Int& count) {
+  const Int I0 = by * WT;
+  Int jt_lo = (Int)g.S1 - (I0 + WT - 1);
   if (jt_lo < 0) jt_lo = 0;
-  int64_t jt_hi = g.S_end - 1 - I0;  // inclusive
-  if (jt_hi > g.nt - 1) jt_hi = g.nt - 1;
+  Int jt_hi = (Int)g.S_end - 1 - I0;  // inclusive
+  if (jt_hi > (Int)g.nt - 1) jt_hi = (Int)g.nt - 1;
   // a tile with I, J >= S1 receives nothing (its down range needs J < S1, its right range I < S1)
-  if (I0 >= g.S1 && jt_hi > g.S1 - 1) jt_hi = g.S1 - 1;
+  if (I0 >= (Int)g.S1 && jt_hi > (Int)g.S1 - 1) jt_hi = (Int)g.S1 - 1;
   first = jt_lo / WT;
-  count = (I0 < g.mt && jt_hi >= jt_lo) ? jt_hi / WT - first + 1 : 0;
+  count = (I0 < (Int)g.mt && jt_hi >= jt_lo) ? jt_hi / WT - first + 1 : 0;
 }
 
 // Panels in LDS, per k-tile (ROWS = 32 WT), both double-buffered:
@@ -232,39 +250,40 @@ __global__ __launch_bounds__(256, 2) void flush_tiles_mfma_kernel(float* __restr
   // XCD-aware order: the hardware deals workgroup w to XCD w % 8; runs of XG consecutive work items
   // (neighbouring column blocks of a row block, which share L / C rows) go to one XCD and its L2,
   // and the XCDs take turns run by run, so that all of them see the same mix of item sizes
-  constexpr int64_t XG = 16;
-  const int64_t nwg = gridDim.x, w = blockIdx.x;
-  const int64_t full = nwg / (8 * XG) * (8 * XG);
-  int64_t item = w;
+  constexpr int XG = 16;
+  const int nwg = (int)gridDim.x, w = (int)blockIdx.x;
+  const int full = nwg / (8 * XG) * (8 * XG);
+  int item = w;
   if (w < full) {
-    const int64_t within = w % (8 * XG);
+    const int within = w % (8 * XG);
     item = w - within + (within % 8) * XG + within / 8;
   }
   const int64_t b = b0 + blockIdx.y;
-  int64_t by = 0, first = 0, count = 0;
-  for (; by * WT < g.mt; ++by) {
-    row_block_span<WT>(g, by, first, count);
+  const TileGeo32 q{(int)g.mt, (int)g.nt, (int)g.S0, (int)g.S1, (int)g.S_end};
+  int by = 0, first = 0, count = 0;
+  for (; by * WT < q.mt; ++by) {
+    row_block_span<WT>(q, by, first, count);
     if (item < count) break;
     item -= count;
   }
-  if (by * WT >= g.mt) return;
-  const int64_t I0 = by * WT;
-  const int64_t J0 = (first + item) * WT;
-  if (J0 >= g.nt || I0 + J0 >= g.S_end || I0 + J0 + 2 * WT - 2 < g.S1) return;
+  if (by * WT >= q.mt) return;
+  const int I0 = by * WT;
+  const int J0 = (first + item) * WT;
+  if (J0 >= q.nt || I0 + J0 >= q.S_end || I0 + J0 + 2 * WT - 2 < q.S1) return;
 
   // workgroup-wide k ranges; nothing to do -> no memory touched
-  int64_t lo0 = INT64_MAX, hi0 = 0, lo1 = INT64_MAX, hi1 = 0;
+  int lo0 = INT32_MAX, hi0 = 0, lo1 = INT32_MAX, hi1 = 0;
   for (int a = 0; a < WT; ++a)
     for (int d = 0; d < WT; ++d) {
-      const int64_t I = I0 + a, J = J0 + d;
-      if (!is_target(g, I, J)) continue;
-      int64_t lo, hi;
-      tile_range(g, 0, I, J, lo, hi);
+      const int I = I0 + a, J = J0 + d;
+      if (!is_target(q, I, J)) continue;
+      int lo, hi;
+      tile_range(q, 0, I, J, lo, hi);
       if (lo < hi) {
         lo0 = lo < lo0 ? lo : lo0;
         hi0 = hi > hi0 ? hi : hi0;
       }
-      tile_range(g, 1, I, J, lo, hi);
+      tile_range(q, 1, I, J, lo, hi);
       if (lo < hi) {
         lo1 = lo < lo1 ? lo : lo1;
         hi1 = hi > hi1 ? hi : hi1;
@@ -284,14 +303,14 @@ __global__ __launch_bounds__(256, 2) void flush_tiles_mfma_kernel(float* __restr
   for (int a = 0; a < H; ++a)
 #pragma unroll
     for (int d = 0; d < H; ++d) {
-      const int64_t I = I0 + wi + a, J = J0 + wj + d;
-      const bool tgt = is_target(g, I, J);
+      const int I = I0 + wi + a, J = J0 + wj + d;
+      const bool tgt = is_target(q, I, J);
 #pragma unroll
       for (int p = 0; p < 2; ++p) {
-        int64_t lo, hi;
-        tile_range(g, p, I, J, lo, hi);
-        tlo[p][a][d] = (int)lo;
-        thi[p][a][d] = tgt ? (int)hi : (int)lo;
+        int lo, hi;
+        tile_range(q, p, I, J, lo, hi);
+        tlo[p][a][d] = lo;
+        thi[p][a][d] = tgt ? hi : lo;
       }
     }
 
