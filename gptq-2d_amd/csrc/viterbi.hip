@@ -87,6 +87,7 @@ __device__ __forceinline__ void wave_argmin(T& v, int64_t& i) {
 struct SearchGeom {
   int L, KV, steps;
   int64_t G;
+  bool vec4;  // fp32, G % 4 == 0, KV >= 2, table and history on 16-byte boundaries
 };
 
 template <typename T, int V>
@@ -126,6 +127,60 @@ __device__ void forward_pass(const Sequence<T, V> (&seq)[NS], const bool (&live)
     }
     // 32-bit state arithmetic (2^L <= 2^24 states)
     const int G32 = (int)G, H32 = (int)H, kv = g.KV;
+    if constexpr (sizeof(T) == 4) {
+      if (g.vec4) {
+        // four consecutive groups j .. j + 3 per thread: for each h their states h G + j .. + 3 are
+        // consecutive, so their table entries come in 128-bit loads (one per 4 V floats), and with
+        // KV >= 2 they share the predecessor group s >> KV, whose minimum is read once per sequence;
+        // the operations of each state evaluation are those of the loop below
+        for (int j = 4 * tid; j < G32; j += 4 * VT_THREADS) {
+          T best[NS][4];
+#pragma unroll
+          for (int k = 0; k < NS; ++k)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) best[k][e] = inf;
+          const bool first = t == 0;
+#pragma unroll 4
+          for (int h = 0; h < H32; ++h) {
+            const int s = h * G32 + j;
+            T tv[4 * V];
+#pragma unroll
+            for (int q = 0; q < V; ++q) {
+              const float4 f = *reinterpret_cast<const float4*>(table + (int64_t)s * V + 4 * q);
+              tv[4 * q] = f.x;
+              tv[4 * q + 1] = f.y;
+              tv[4 * q + 2] = f.z;
+              tv[4 * q + 3] = f.w;
+            }
+            const int ps = s >> kv;
+#pragma unroll
+            for (int k = 0; k < NS; ++k) {
+              const T pv = prev[k][ps];
+              const bool masked_out = masked && ps != overlap[k];
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                const T d0 = tv[V * e] - x0[k];
+                T c = d0 * d0;
+                if constexpr (V == 2) {
+                  const T d1 = tv[V * e + 1] - x1[k];
+                  c = c + d1 * d1;
+                }
+                c = first ? (masked_out ? inf : c) : pv + c;
+                best[k][e] = fmin(c, best[k][e]);
+              }
+            }
+          }
+#pragma unroll
+          for (int k = 0; k < NS; ++k) {
+            const float4 b4 = make_float4(best[k][0], best[k][1], best[k][2], best[k][3]);
+            if (live[k]) *reinterpret_cast<float4*>(hist[k] + (int64_t)t * G + j) = b4;
+            if (cur_lds[k]) *reinterpret_cast<float4*>(cur_lds[k] + j) = b4;
+          }
+        }
+        __syncthreads();
+        continue;
+      }
+    }
     for (int j = tid; j < G32; j += VT_THREADS) {
       T best[NS];
 #pragma unroll
@@ -250,12 +305,12 @@ __global__ __launch_bounds__(VT_THREADS) void viterbi_kernel(const T* __restrict
                                                              T* __restrict__ hist_all, const T* __restrict__ scale,
                                                              T* __restrict__ out, int64_t* __restrict__ states,
                                                              int64_t rows, int L, int KV, int steps, int tail_biting,
-                                                             int prev_in_lds) {
+                                                             int prev_in_lds, int vec4) {
   extern __shared__ __align__(16) unsigned char smem[];
   __shared__ T red_v[NS * (VT_THREADS / 64)];
   __shared__ int64_t red_i[NS * (VT_THREADS / 64)];
   __shared__ int64_t sh_state[NS], sh_overlap[NS];
-  SearchGeom g{L, KV, steps, (int64_t)1 << (L - KV)};
+  SearchGeom g{L, KV, steps, (int64_t)1 << (L - KV), vec4 != 0};
   Sequence<T, V> seq[NS];
   bool live[NS];
   T* hist[NS];
@@ -302,8 +357,10 @@ template <typename T, int V, int NS>
 void launch_viterbi(size_t lds, bool in_lds, hipStream_t stream, const T* x, const T* table, T* hist, const T* scale,
                     T* out, int64_t* states, int64_t rows, int L, int KV, int steps, int tail_biting) {
   const dim3 grid((unsigned)((rows + NS - 1) / NS));
+  const bool vec4 = sizeof(T) == 4 && L - KV >= 2 && KV >= 2 && ((uintptr_t)table & 15) == 0 &&
+                    ((uintptr_t)hist & 15) == 0;
   hipLaunchKernelGGL((viterbi_kernel<T, V, NS>), grid, dim3(VT_THREADS), in_lds ? lds : 0, stream, x, table, hist,
-                     scale, out, states, rows, L, KV, steps, tail_biting, in_lds ? 1 : 0);
+                     scale, out, states, rows, L, KV, steps, tail_biting, in_lds ? 1 : 0, vec4 ? 1 : 0);
 }
 
 template <typename T>
