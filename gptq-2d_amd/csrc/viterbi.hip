@@ -29,6 +29,8 @@
 // (the same search as 2 x (T/V + 1) launches per call).
 #include "common.h"
 
+#include <type_traits>
+
 namespace {
 
 constexpr int VT_THREADS = 1024;
@@ -133,13 +135,15 @@ __device__ void forward_pass(const Sequence<T, V> (&seq)[NS], const bool (&live)
         // consecutive, so their table entries come in 128-bit loads (one per 4 V floats), and with
         // KV >= 2 they share the predecessor group s >> KV, whose minimum is read once per sequence;
         // the operations of each state evaluation are those of the loop below
+        // the first step and the others as separate loops (no per-evaluation select on t == 0)
+        auto groups = [&](auto first_c) {
+        constexpr bool first = decltype(first_c)::value;
         for (int j = 4 * tid; j < G32; j += 4 * VT_THREADS) {
           T best[NS][4];
 #pragma unroll
           for (int k = 0; k < NS; ++k)
 #pragma unroll
             for (int e = 0; e < 4; ++e) best[k][e] = inf;
-          const bool first = t == 0;
 #pragma unroll 4
           for (int h = 0; h < H32; ++h) {
             const int s = h * G32 + j;
@@ -155,8 +159,8 @@ __device__ void forward_pass(const Sequence<T, V> (&seq)[NS], const bool (&live)
             const int ps = s >> kv;
 #pragma unroll
             for (int k = 0; k < NS; ++k) {
-              const T pv = prev[k][ps];
-              const bool masked_out = masked && ps != overlap[k];
+              const T pv = first ? T(0) : prev[k][ps];
+              const bool masked_out = first && masked && ps != overlap[k];
 #pragma unroll
               for (int e = 0; e < 4; ++e) {
                 const T d0 = tv[V * e] - x0[k];
@@ -165,7 +169,10 @@ __device__ void forward_pass(const Sequence<T, V> (&seq)[NS], const bool (&live)
                   const T d1 = tv[V * e + 1] - x1[k];
                   c = c + d1 * d1;
                 }
-                c = first ? (masked_out ? inf : c) : pv + c;
+                if constexpr (first)
+                  c = masked_out ? inf : c;
+                else
+                  c = pv + c;
                 best[k][e] = fmin(c, best[k][e]);
               }
             }
@@ -177,6 +184,11 @@ __device__ void forward_pass(const Sequence<T, V> (&seq)[NS], const bool (&live)
             if (cur_lds[k]) *reinterpret_cast<float4*>(cur_lds[k] + j) = b4;
           }
         }
+        };
+        if (t == 0)
+          groups(std::true_type{});
+        else
+          groups(std::false_type{});
         __syncthreads();
         continue;
       }
