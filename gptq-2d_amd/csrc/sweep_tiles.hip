@@ -181,26 +181,31 @@ __device__ __forceinline__ void pull_chunks(floatx16& acc, const float* __restri
                                             int64_t a_cols, const float* __restrict__ Bm, int64_t ldb,
                                             int64_t b_rows, int64_t b_cols, int64_t i0, int64_t j0, int64_t c_lo,
                                             int64_t c_hi, int half, int li, int hh) {
+  // this lane's row of A and column of B as pointers (64-bit arithmetic once); k offsets in 32 bits
   const int64_t ia = i0 + li, jb = j0 + li;
   const bool arow = ia < a_rows, bcol = jb < b_cols;
+  const float* ap = A + (arow ? ia : 0) * lda;
+  const float* bp = Bm + (bcol ? jb : 0);
+  const int clo = (int)c_lo, chi = (int)c_hi, acols = (int)a_cols, brows = (int)b_rows;
   constexpr int G = 4;
-  for (int64_t base = c_lo + half; base < c_hi; base += 2 * G) {
+  for (int base = clo + half; base < chi; base += 2 * G) {
     float av[G][4], bv[G][4];
 #pragma unroll
     for (int q = 0; q < G; ++q) {
-      const int64_t ch = base + 2 * q;
-      const int64_t k0 = 8 * ch + 4 * hh;
-      const bool ok = ch < c_hi;
+      const int ch = base + 2 * q;
+      const int k0 = 8 * ch + 4 * hh;
+      const bool ok = ch < chi;
       if (VEC) {
-        const float4 f = (ok && arow && k0 < a_cols) ? *reinterpret_cast<const float4*>(A + ia * lda + k0)
-                                                     : make_float4(0.f, 0.f, 0.f, 0.f);
+        const float4 f = (ok && arow && k0 < acols) ? *reinterpret_cast<const float4*>(ap + k0)
+                                                    : make_float4(0.f, 0.f, 0.f, 0.f);
         av[q][0] = f.x, av[q][1] = f.y, av[q][2] = f.z, av[q][3] = f.w;
       } else {
 #pragma unroll
-        for (int s2 = 0; s2 < 4; ++s2) av[q][s2] = (ok && arow && k0 + s2 < a_cols) ? A[ia * lda + k0 + s2] : 0.f;
+        for (int s2 = 0; s2 < 4; ++s2) av[q][s2] = (ok && arow && k0 + s2 < acols) ? ap[k0 + s2] : 0.f;
       }
+      const float* bk = bp + (int64_t)k0 * ldb;
 #pragma unroll
-      for (int s2 = 0; s2 < 4; ++s2) bv[q][s2] = (ok && bcol && k0 + s2 < b_rows) ? Bm[(k0 + s2) * ldb + jb] : 0.f;
+      for (int s2 = 0; s2 < 4; ++s2) bv[q][s2] = (ok && bcol && k0 + s2 < brows) ? bk[s2 * ldb] : 0.f;
     }
 #pragma unroll
     for (int q = 0; q < G; ++q) {
@@ -383,14 +388,16 @@ __device__ __forceinline__ void sweep_tile_push(TileLds& tl, float* __restrict__
     tl.Es[r][ck[k]] = E[k];
   }
   __syncthreads();
+  float* yt = y + mat + i0 * n + j0;
+  float* ct = c + mat + i0 * n + j0;
+  float* et = e + mat + i0 * n + j0;
   for (int t = tid; t < TR * TR; t += NTHREADS) {
     const int rr = t / TR, cc = t % TR;
-    const int64_t gi2 = i0 + rr, gj = j0 + cc;
-    if (gi2 < m && gj < n) {
-      const int64_t off = mat + gi2 * n + gj;
-      y[off] = tl.Ys[rr][cc];
-      c[off] = tl.Cs[rr][cc];
-      e[off] = tl.Es[rr][cc];
+    if (rr < rows_in && cc < cols_in) {
+      const int off = rr * (int)n + cc;
+      yt[off] = tl.Ys[rr][cc];
+      ct[off] = tl.Cs[rr][cc];
+      et[off] = tl.Es[rr][cc];
     }
   }
 }
@@ -406,23 +413,33 @@ struct TileRegs {
                                        const float* __restrict__ lb, const float* __restrict__ ub,
                                        const QSpec<float>& qs, int64_t b, int64_t m, int64_t n, int64_t i0,
                                        int64_t j0, int64_t mat) {
+    // the tile's corner in every operand (64-bit arithmetic once, uniform), then 32-bit offsets in
+    // the tile (32 rows of at most 2^26 elements)
+    const int rows_in = m - i0 < TR ? (int)(m - i0) : TR, cols_in = n - j0 < TR ? (int)(n - j0) : TR;
+    const int ni = (int)n, mi = (int)m;
+    const int64_t corner = i0 * n + j0;
+    const float* yt = yg + mat + corner;
+    const float* ct = cg + mat + corner;
+    const float* lt = lb + i0 * m + i0;  // L[i0 + r, i0 + cc] at r m + cc
+    const float* ut = ub + j0 * n + j0;  // U[j0 + r, j0 + cc] at r n + cc
+    const float* st = KIND != Q_ROUND ? qs.scale + qs.smap.offset(b) + corner : nullptr;
+    const float* zt = KIND == Q_AFFINE ? qs.zp + qs.zmap.offset(b) + corner : nullptr;
 #pragma unroll
     for (int q = 0; q < NQ; ++q) {
       const int t = threadIdx.x + NTHREADS * q;
       const int r = t / TR, cc = t % TR;
-      const int64_t gi = i0 + r, gj = j0 + cc;
-      const bool in = gi < m && gj < n;
-      const int64_t off = mat + gi * n + gj;
-      y[q] = in ? yg[off] : 0.f;
-      c[q] = in ? cg[off] : 0.f;
+      const bool in = r < rows_in && cc < cols_in;
+      const int off = r * ni + cc;
+      y[q] = in ? yt[off] : 0.f;
+      c[q] = in ? ct[off] : 0.f;
       // L[i0+r, i0+cc] strictly below the diagonal; U[j0+r, j0+cc] strictly above it
-      l[q] = (cc < r && gi < m) ? lb[gi * m + (i0 + cc)] : 0.f;
-      u[q] = (r < cc && j0 + cc < n) ? ub[(j0 + r) * n + (j0 + cc)] : 0.f;
+      l[q] = (cc < r && r < rows_in) ? lt[r * mi + cc] : 0.f;
+      u[q] = (r < cc && cc < cols_in) ? ut[off] : 0.f;
       if constexpr (KIND == Q_AFFINE) {
-        s[q] = in ? qs.scale[qs.smap.offset(b) + gi * n + gj] : 1.f;
-        z[q] = in ? qs.zp[qs.zmap.offset(b) + gi * n + gj] : 0.f;
+        s[q] = in ? st[off] : 1.f;
+        z[q] = in ? zt[off] : 0.f;
       } else if constexpr (KIND == Q_FORCED) {
-        s[q] = in ? qs.scale[qs.smap.offset(b) + gi * n + gj] : 0.f;
+        s[q] = in ? st[off] : 0.f;
       }
     }
   }
@@ -538,17 +555,19 @@ __global__ __launch_bounds__(NTHREADS, 2) void tile_stage_kernel(float* __restri
   __syncthreads();
 
   if (!sweep) {  // prep: Y += D + R, C += D in place
+    const int rows_in = m - i0 < TR ? (int)(m - i0) : TR, cols_in = n - j0 < TR ? (int)(n - j0) : TR;
+    float* yt = y + mat + i0 * n + j0;
+    float* ct = c + mat + i0 * n + j0;
 #pragma unroll
     for (int q = 0; q < TR * TR / NTHREADS; ++q) {
       const int t = tid + NTHREADS * q;
       const int r = t / TR, cc = t % TR;
-      const int64_t gi = i0 + r, gj = j0 + cc;
-      if (gi < m && gj < n) {
-        const int64_t off = mat + gi * n + gj;
+      if (r < rows_in && cc < cols_in) {
+        const int off = r * (int)n + cc;
         const float dd = red[0][0][r][cc] + red[0][1][r][cc];
         const float rr = red[1][0][r][cc] + red[1][1][r][cc];
-        y[off] = y[off] + (dd + rr);
-        c[off] = c[off] + dd;
+        yt[off] = yt[off] + (dd + rr);
+        ct[off] = ct[off] + dd;
       }
     }
     return;
@@ -592,6 +611,8 @@ int sweep_fused(T* y, T* c, T* e, const T* l, const T* u, int64_t m, int64_t n, 
   BatchMap lmap, umap;
   if (!make_batch_map(lmap, bnd, bshape, lstride) || !make_batch_map(umap, bnd, bshape, ustride)) return GPTQ2D_EINVAL;
   if (m <= 0 || n <= 0 || outer_tiles < 1) return GPTQ2D_EINVAL;
+  // the fp32 tile kernels index inside a tile with 32-bit offsets (32 rows of a row length < 2^26)
+  if (sizeof(T) == 4 && (m >= ((int64_t)1 << 26) || n >= ((int64_t)1 << 26))) return GPTQ2D_EUNSUPPORTED;
   if (qkind != Q_ROUND && qkind != Q_AFFINE && qkind != Q_FORCED) return GPTQ2D_EINVAL;
   if ((qkind == Q_AFFINE && (!qa || !qb)) || (qkind == Q_FORCED && !qa)) return GPTQ2D_EINVAL;
   QSpec<T> qs;
