@@ -464,13 +464,23 @@ struct TileRegs {
       if constexpr (KIND != Q_ROUND) tl.Ss[r][cc] = s[q];
       if constexpr (KIND == Q_AFFINE) tl.Zs[r][cc] = z[q];
     }
-    for (int i = threadIdx.x; i < TR * (LPW - TR); i += NTHREADS) {
-      const int r = i / (LPW - TR), k = i % (LPW - TR);
-      tl.Lp[r][k < TR ? k : k + TR] = 0.f;
-    }
-    for (int i = threadIdx.x; i < 2 * TR * UPW; i += NTHREADS) {
-      const int row = i / UPW, col = i % UPW;
-      tl.Up[row < TR ? row : row + TR][col] = 0.f;
+    // zero padding without divisions: 8 threads per row of Lp (its 65 padding columns), 4 per padding
+    // row of Up (33 columns each); a strided column walk per thread
+    {
+      static_assert(NTHREADS == 8 * TR && LPW - TR <= 72 && UPW <= 36, "padding walk shape");
+      const int r = threadIdx.x >> 3, sub = threadIdx.x & 7;
+#pragma unroll
+      for (int i = 0; i < 9; ++i) {
+        const int k = sub + 8 * i;
+        if (k < LPW - TR) tl.Lp[r][k < TR ? k : k + TR] = 0.f;
+      }
+      const int row = threadIdx.x >> 2, sub4 = threadIdx.x & 3;
+      float* up_row = tl.Up[row < TR ? row : row + TR];
+#pragma unroll
+      for (int i = 0; i < 9; ++i) {
+        const int col = sub4 + 4 * i;
+        if (col < UPW) up_row[col] = 0.f;
+      }
     }
     // slots of antidiagonals that miss a row or column are read (times a zero factor) before any
     // write: they must hold finite values, never leftover LDS contents
