@@ -261,12 +261,15 @@ __device__ __forceinline__ float quantize_entry_rcp(float yv, float sv, float zv
     const float rem = __builtin_fmaf(-q0, sv, yv);
     float q = __builtin_fmaf(rem, rv, q0);
     const float ay = __builtin_fabsf(yv);
+    // s_ok also holds only when the zero point is not NaN and qmin <= qmax: then q is the IEEE
+    // quotient, round(q + z) is not NaN, and the median of (x, qmin, qmax) is the clamp, in one
+    // operation on the per-step critical path
     const bool exact = s_ok && ay <= 0x1p60f && (ay >= 0x1p-60f || yv == 0.f);
+    float code = __builtin_amdgcn_fmed3f(round_even(q + zv), qmin, qmax);
     if (__builtin_amdgcn_ballot_w64(active && !exact)) {
       asm volatile("");  // keeps the division behind the branch (no speculation into a select)
-      if (!exact) q = yv / sv;
+      if (!exact) code = clamp_val(round_even(yv / sv + zv), qmin, qmax);
     }
-    const float code = clamp_val(round_even(q + zv), qmin, qmax);
     return (code - zv) * sv;
   } else if constexpr (KIND == Q_FORCED) {
     return sv;
@@ -302,6 +305,7 @@ __device__ __forceinline__ void sweep_tile_push(TileLds& tl, float* __restrict__
   // quantizer inputs S, Z and the reciprocal R of S
   float Y[4], C[4], D[4], F[4], E[4], S[4], Z[4], R[4];
   bool s_ok[4];
+  const bool qmin_le_qmax = qs.qmin <= qs.qmax;
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
     ck[k] = 8 * (qlo + ((k - qlo) & 3)) + part - r;  // in [0, TR)
@@ -315,7 +319,7 @@ __device__ __forceinline__ void sweep_tile_push(TileLds& tl, float* __restrict__
       Z[k] = tl.Zs[r][ck[k]];
       R[k] = 1.f / S[k];
       const float as = __builtin_fabsf(S[k]);
-      s_ok[k] = as >= 0x1p-60f && as <= 0x1p60f;
+      s_ok[k] = as >= 0x1p-60f && as <= 0x1p60f && Z[k] == Z[k] && qmin_le_qmax;
     } else if constexpr (KIND == Q_FORCED) {
       S[k] = tl.Ss[r][ck[k]];
     }
