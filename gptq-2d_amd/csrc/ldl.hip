@@ -179,35 +179,91 @@ struct PotrfLds {
   T a[PB * CP];
   T rs[64 * CP];
   T rinv[PB];  // reciprocals of the factored block's diagonal
+  T pd[PB * CP];  // the update's source panel: the rows of the diagonal block
+  T px[64 * CP];  // and the rows of the current chunk
 };
+
+// Lane layout of a 64 x 64 product on MFMA (v_mfma_f32_32x32x2_f32) from row-major LDS operands
+// with pitch cp: wave (wy, wx) forms the 32 x 32 tile at rows 32 wy, columns 32 wx of A B^T (K = 64,
+// k = 2 s + h for MFMA s), acc[e] = tile(8 (e / 4) + 4 h + e % 4, lane % 32).
+__device__ __forceinline__ floatx16 tile_abt64(const float* __restrict__ A, const float* __restrict__ B, int cp,
+                                               int wy, int wx, int li, int hh) {
+  floatx16 acc;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) acc[e] = 0.f;
+#pragma unroll
+  for (int s2 = 0; s2 < 32; ++s2)
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(A[(32 * wy + li) * cp + 2 * s2 + hh], B[(32 * wx + li) * cp + 2 * s2 + hh],
+                                               acc, 0, 0, 0);
+  return acc;
+}
 
 // Panel j0 as above, for workgroup `bid` of `nblk` taking part (the panel's row chunks are dealt
 // over them).
 template <typename T, int PB>
 __device__ __forceinline__ void potrf_panel(PotrfLds<T, PB>& sm, T* __restrict__ w, int64_t ld, int64_t j0, int n,
                                             int64_t k, int* __restrict__ info, T* __restrict__ stage, int64_t bid,
-                                            int64_t nblk) {
+                                            int64_t nblk, int64_t upc = -1) {
+  // upc >= 0 (fp32): the panel's columns still lack the rank-PB update of the panel at columns
+  // [upc, upc + PB); the workgroup applies it to the diagonal block and to each of its chunks (on
+  // MFMA, before the factorisation and before each solve) instead of a launch of its own
   constexpr int CP = PB + 1;
+  constexpr bool kFuse = sizeof(T) == 4 && PB == 64;
+  const bool fuse = kFuse && upc >= 0;
   T* a = sm.a;
   T* rs = sm.rs;
   const int tid = threadIdx.x;
-  for (int t = tid; t < PB * PB; t += 256) {
-    const int r = t / PB, c = t % PB;
-    a[r * CP + c] = (r < n && c <= r) ? w[(j0 + r) * ld + j0 + c] : (r == c ? T(1) : T(0));
+  const int lane = tid & 63, li = lane & 31, hh = lane >> 5, wy = tid >> 7, wx = (tid >> 6) & 1;
+  // every load of the prologue is issued before any is waited for (into registers, unrolled): a
+  // load-then-store loop would wait out one memory latency per element.  The diagonal block and the
+  // update source's rows of it come first -- loads return in issue order, so the factorisation
+  // waits for these and not for the chunk loads issued after them.
+  constexpr int NL = PB * PB / 256;
+  T dv[NL], pv[NL];
+#pragma unroll
+  for (int u = 0; u < NL; ++u) {
+    const int t = tid + 256 * u, r = t / PB, c = t % PB;
+    dv[u] = (r < n && c <= r) ? w[(j0 + r) * ld + j0 + c] : (r == c ? T(1) : T(0));
   }
-  // this workgroup's first chunk of the panel below, in flight during the factorisation
+  if (fuse) {
+#pragma unroll
+    for (int u = 0; u < NL; ++u) {
+      const int t = tid + 256 * u, r = t / PB, c = t % PB;
+      pv[u] = r < n ? w[(j0 + r) * ld + upc + c] : T(0);
+    }
+  }
+  // this workgroup's first chunk of the panel below (and of the update's source panel), in flight
+  // during the factorisation
   const int64_t first = j0 + PB;
   constexpr int PRE = 64 * PB / 256;
-  T pre[PRE];
+  T pre[PRE], xpre[PRE];
   if (n == PB) {
     const int64_t r0 = first + bid * 64;
 #pragma unroll
     for (int u = 0; u < PRE; ++u) {
       const int t = tid + 256 * u, i = t / PB, c = t % PB;
       pre[u] = r0 + i < k ? w[(r0 + i) * ld + j0 + c] : T(0);
+      if (fuse) xpre[u] = r0 + i < k ? w[(r0 + i) * ld + upc + c] : T(0);
     }
   }
+#pragma unroll
+  for (int u = 0; u < NL; ++u) {
+    const int t = tid + 256 * u, r = t / PB, c = t % PB;
+    a[r * CP + c] = dv[u];
+    if (fuse) sm.pd[r * CP + c] = pv[u];
+  }
   __syncthreads();
+  if constexpr (kFuse) {
+    if (fuse) {
+      // the diagonal block: a -= Pd Pd^T (the tile above the diagonal is not needed)
+      if (wy >= wx) {
+        const floatx16 acc = tile_abt64(sm.pd, sm.pd, CP, wy, wx, li, hh);
+#pragma unroll
+        for (int e = 0; e < 16; ++e) a[(32 * wy + 8 * (e >> 2) + 4 * hh + (e & 3)) * CP + 32 * wx + li] -= acc[e];
+      }
+      __syncthreads();
+    }
+  }
   constexpr int CB = 16;
   int bad = 0;
 #pragma unroll
@@ -292,14 +348,25 @@ __device__ __forceinline__ void potrf_panel(PotrfLds<T, PB>& sm, T* __restrict__
       for (int u = 0; u < PRE; ++u) {
         const int t = tid + 256 * u, i = t / PB, c = t % PB;
         rs[i * CP + c] = pre[u];
+        if (fuse) sm.px[i * CP + c] = xpre[u];
       }
     } else {
       for (int t = tid; t < 64 * PB; t += 256) {
         const int i = t / PB, c = t % PB;
         rs[i * CP + c] = r0 + i < k ? w[(r0 + i) * ld + j0 + c] : T(0);
+        if (fuse) sm.px[i * CP + c] = r0 + i < k ? w[(r0 + i) * ld + upc + c] : T(0);
       }
     }
     __syncthreads();
+    if constexpr (kFuse) {
+      if (fuse) {
+        // the chunk: X -= Px Pd^T
+        const floatx16 acc = tile_abt64(sm.px, sm.pd, CP, wy, wx, li, hh);
+#pragma unroll
+        for (int e = 0; e < 16; ++e) rs[(32 * wy + 8 * (e >> 2) + 4 * hh + (e & 3)) * CP + 32 * wx + li] -= acc[e];
+        __syncthreads();
+      }
+    }
     T x[PB / 4];
 #pragma unroll
     for (int idx = 0; idx < PB / 4; ++idx) x[idx] = rs[rr * CP + 4 * idx + q];
@@ -325,9 +392,19 @@ __global__ __launch_bounds__(256) void potrf_panel_kernel(T* __restrict__ w, int
 template <typename T, int PB>
 __device__ __forceinline__ void stage_to_w(T* __restrict__ w, int64_t ld, int64_t j0, int n,
                                            const T* __restrict__ stage) {
-  for (int t = threadIdx.x; t < PB * PB; t += blockDim.x) {
-    const int r = t / PB, c = t % PB;
-    if (r < n && c <= r) w[(j0 + r) * ld + j0 + c] = stage[r * n + c];
+  // all loads issued before the first store (256 threads; a load-then-store loop would wait out one
+  // memory latency per element)
+  constexpr int NL = PB * PB / 256;
+  T v[NL];
+#pragma unroll
+  for (int u = 0; u < NL; ++u) {
+    const int t = threadIdx.x + 256 * u, r = t / PB, c = t % PB;
+    v[u] = (r < n && c <= r) ? stage[r * n + c] : T(0);
+  }
+#pragma unroll
+  for (int u = 0; u < NL; ++u) {
+    const int t = threadIdx.x + 256 * u, r = t / PB, c = t % PB;
+    if (r < n && c <= r) w[(j0 + r) * ld + j0 + c] = v[u];
   }
 }
 
@@ -609,21 +686,30 @@ __global__ __launch_bounds__(256, 2) void syrk_strip_kernel(float* __restrict__ 
 // others apply a pending trapezoid update (square W[r0.., r0..], R x R, columns < C, rank K from
 // P = W[r0.., pc .. pc + K)).  The two touch disjoint columns, so the panel's latency-bound
 // factorisation runs beside the throughput-bound update.
+// upc >= 0: the panel first takes the rank-PB update of the panel at columns [upc, upc + PB) itself.
+// copy_stage != nullptr: the last workgroup moves that earlier panel's staged diagonal block (at
+// column copy_j0, PB rows) into W.
 template <int PB>
 __global__ __launch_bounds__(256, 2) void panel_step_kernel(float* __restrict__ w, int64_t ld, int64_t j0, int n,
                                                             int64_t k, int* __restrict__ info,
                                                             float* __restrict__ stage, int64_t n_potrf, int64_t r0,
-                                                            int R, int C, int64_t pc, int K) {
+                                                            int R, int C, int64_t pc, int K, int64_t upc,
+                                                            const float* __restrict__ copy_stage, int64_t copy_j0) {
   __shared__ __align__(16) union {
     PotrfLds<float, PB> p;
     WideLds s;
   } sm;
+  const int64_t n_upd = gridDim.x - n_potrf - (copy_stage ? 1 : 0);
+  if (copy_stage && (int64_t)blockIdx.x == gridDim.x - 1) {
+    stage_to_w<float, PB>(w, ld, copy_j0, PB, copy_stage);
+    return;
+  }
   if ((int64_t)blockIdx.x < n_potrf) {
-    potrf_panel<float, PB>(sm.p, w, ld, j0, n, k, info, stage, blockIdx.x, n_potrf);
+    potrf_panel<float, PB>(sm.p, w, ld, j0, n, k, info, stage, blockIdx.x, n_potrf, upc);
     return;
   }
   int bi, bj;
-  trapezoid_block(xcd_contiguous(blockIdx.x - n_potrf, gridDim.x - n_potrf), (C + WB - 1) / WB, bi, bj);
+  trapezoid_block(xcd_contiguous(blockIdx.x - n_potrf, n_upd), (C + WB - 1) / WB, bi, bj);
   syrk_wide_block(sm.s, w, ld, r0, R, C, pc, K, bi, bj);
 }
 
@@ -643,7 +729,7 @@ struct CholeskyRun {
   T* stage;
   hipStream_t stream;
   int64_t col_begin, col_end, j0;
-  bool two_level, done = false;
+  bool two_level, fuse, done = false;
   int64_t pr0 = 0, pC = 0, ppc = 0;  // pending trapezoid update (columns < pC of W[pr0.., pr0..])
   int pK = 0;
 
@@ -651,8 +737,13 @@ struct CholeskyRun {
       : w(w_), k(k_), info(info_), stage(stage_), stream(s), col_begin(cb), col_end(ce < 0 || ce > k_ ? k_ : ce),
         j0(cb) {
     two_level = sizeof(T) == 4 && k % 4 == 0 && k * k < (int64_t)1 << 29;
+    fuse = two_level && k * k >= 2 * (int64_t)PB * PB;
     done = j0 >= col_end;
   }
+
+  // Staging block of panel j (two alternating ones when fused: a panel's launch copies the previous
+  // panel's block into W while its own workgroup 0 stages the new one).
+  T* slot(int64_t j) const { return fuse && ((j / PB) & 1) ? stage + (int64_t)PB * PB : stage; }
 
   // The launches of panel j0, then j0 += PB.
   int step() {
@@ -686,27 +777,34 @@ struct CholeskyRun {
     const int64_t blocks = rest > 0 ? (cdiv(rest, 64) < 256 ? cdiv(rest, 64) : 256) : 1;
     const int64_t pR = pC > 0 ? k - pr0 : 0;
     const int64_t upd = pC > 0 ? trapezoid_blocks(pR, pC) : 0;
-    hipLaunchKernelGGL((panel_step_kernel<PB>), dim3((unsigned)(blocks + upd)), dim3(256), 0, stream, wf, k, j0, n, k,
-                       info, (float*)stage, blocks, pr0, (int)pR, (int)pC, ppc, pK);
-    if ((rc = (int)hipGetLastError())) return rc;
-    pC = 0;
-    if (rest <= 0) {  // the last panel: its staged block into W on its own
-      hipLaunchKernelGGL((stage_to_w_kernel<float, PB>), dim3(1), dim3(256), 0, stream, wf, k, j0, n,
-                         (const float*)stage);
-      done = true;
-      return (int)hipGetLastError();
-    }
     // the strip of panel j0: [s_lo, s_hi)
     const int64_t s_al = j0 / SW * SW;
     const int64_t s_lo = s_al > col_begin ? s_al : col_begin;
     const int64_t s_hi = s_al + SW < col_end ? s_al + SW : col_end;
+    // fused: a panel after the first of its strip takes the previous panel's rank-PB update itself
+    // (no launch of its own for it), and its launch moves the previous panel's staged block into W
+    const bool in_strip = fuse && j0 > s_lo;
+    const float* copy = in_strip ? (const float*)slot(j0 - PB) : nullptr;
+    hipLaunchKernelGGL((panel_step_kernel<PB>), dim3((unsigned)(blocks + upd + (copy ? 1 : 0))), dim3(256), 0, stream,
+                       wf, k, j0, n, k, info, (float*)slot(j0), blocks, pr0, (int)pR, (int)pC, ppc, pK,
+                       in_strip ? j0 - PB : (int64_t)-1, copy, j0 - PB);
+    if ((rc = (int)hipGetLastError())) return rc;
+    pC = 0;
+    if (rest <= 0) {  // the last panel: its staged block into W on its own
+      hipLaunchKernelGGL((stage_to_w_kernel<float, PB>), dim3(1), dim3(256), 0, stream, wf, k, j0, n,
+                         (const float*)slot(j0));
+      done = true;
+      return (int)hipGetLastError();
+    }
     const bool strip_end = j0 + PB >= s_hi;
     // the update's rank: panel j0 alone inside the strip, the whole strip at its end
     const int64_t pc = strip_end ? s_lo : j0;
     const int K = (int)(j0 + PB - pc);
-    hipLaunchKernelGGL((syrk_strip_kernel<PB>), dim3((unsigned)cdiv(rest, WB) + 1), dim3(256), 0, stream, wf, k,
-                       j0 + PB, (int)rest, pc, K, j0, (const float*)stage);
-    if ((rc = (int)hipGetLastError())) return rc;
+    if (strip_end || !fuse) {
+      hipLaunchKernelGGL((syrk_strip_kernel<PB>), dim3((unsigned)cdiv(rest, WB) + 1), dim3(256), 0, stream, wf, k,
+                         j0 + PB, (int)rest, pc, K, j0, (const float*)slot(j0));
+      if ((rc = (int)hipGetLastError())) return rc;
+    }
     // the rest: the strip's later columns, or everything to the right at a strip's end
     const int64_t r0 = j0 + 2 * PB, R = rest - PB;
     const int64_t C = strip_end ? R : (s_hi - r0 < R ? s_hi - r0 : R);
@@ -760,7 +858,7 @@ struct CholeskyRun {
       const int64_t pR = k - pr0;
       hipLaunchKernelGGL((panel_step_kernel<PB>), dim3((unsigned)trapezoid_blocks(pR, pC)), dim3(256), 0, stream,
                          (float*)w, k, (int64_t)0, 0, k, info, (float*)stage, (int64_t)0, pr0, (int)pR, (int)pC,
-                         ppc, pK);
+                         ppc, pK, (int64_t)-1, (const float*)nullptr, (int64_t)0);
       pC = 0;
       return (int)hipGetLastError();
     }
@@ -779,12 +877,13 @@ int cholesky_inplace(T* w, int64_t k, int* info, T* stage, hipStream_t stream, i
 }
 
 // Elements from the start of `out` where the Cholesky stages its factored diagonal blocks: the
-// buffer's last PB x PB elements, away from what the triangular inverse's first part writes while
+// buffer's last 2 PB x PB elements (two alternating blocks; one, at the start, for k^2 < 2 PB^2 --
+// CholeskyRun then does not fuse), away from what the triangular inverse's first part writes while
 // the factorisation still runs.
 template <typename T>
 int64_t stage_offset(int64_t k) {
   constexpr int64_t PB = LdlBlock<T>::PB;
-  return k * k > PB * PB ? k * k - PB * PB : 0;
+  return k * k >= 2 * PB * PB ? k * k - 2 * PB * PB : 0;
 }
 
 // Zero the strict upper triangle of the n x n diagonal block at w (row stride ld), one row per
