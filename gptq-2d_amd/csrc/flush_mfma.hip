@@ -413,18 +413,18 @@ int gptq2d_flush_tiles_mfma(float* y, float* c, const float* e, const float* l, 
                             int64_t S0, int64_t S1, int64_t S_end, const BatchMap& lmap, const BatchMap& umap,
                             int64_t B, hipStream_t stream) {
   TileFlush g{m, n, cdiv(m, TS), cdiv(n, TS), S0, S1, S_end};
-  // 4 x 4 tiles per workgroup, two resident per CU, unless the 4 x 4 items would run in fewer than
-  // two rounds over the chip, or fewer than four with a last round under a fifth full: then 2 x 2
-  // (four times as many workgroups, each k-tile a quarter of the MFMAs, four resident per CU), whose
-  // finer grain evens out the last round (at 8192^2 this picks 2 x 2 for 6 of the 15 outer
-  // flushes, 2.2% less flush time).  Rows whose length is not a multiple of 4 (or matrices not
+  // 2 x 2 tiles per workgroup (four resident per CU), whose fine grain evens out the launch's last
+  // round over the chip, unless the 4 x 4 items (two resident per CU; each k-tile's panels serve
+  // four times the MFMAs) would fill six rounds or more, where the last round weighs little.  At
+  // 8192^2 every outer flush takes 2 x 2: 99 TFLOP/s over a layer's 15 flushes against 96-98 when
+  // the 4 x 4 grain was kept from two rounds on (with the work-item lookup in 32 bits, a small
+  // workgroup's prologue costs little).  Rows whose length is not a multiple of 4 (or matrices not
   // 16-byte aligned) are staged 32 bits at a time, in 2 x 2 blocks only.
   const bool vec = m % 4 == 0 && n % 4 == 0 && aligned16(y) && aligned16(c) && aligned16(e) && aligned16(l) &&
                    aligned16(u) && strides_mult4(lmap) && strides_mult4(umap);
   if (!vec) return launch<2, false>(y, c, e, l, u, g, lmap, umap, B, stream);
   const double rounds = (double)(count_items<4>(g) * B) / (2.0 * device_cus());
-  const double last = rounds - (double)(int64_t)rounds;
-  if (S1 - S0 >= 4 && rounds >= 2 && !(rounds < 4 && last < 0.2))
+  if (S1 - S0 >= 4 && rounds >= 6)
     return launch<4, true>(y, c, e, l, u, g, lmap, umap, B, stream);
   return launch<2, true>(y, c, e, l, u, g, lmap, umap, B, stream);
 }
