@@ -45,6 +45,7 @@
 #include <array>
 #include <type_traits>
 #include <unordered_map>
+#include <utility>
 
 namespace {
 
@@ -148,6 +149,24 @@ __device__ __forceinline__ void quad_solve(T (&x)[PB / 4], int q, const T* __res
   }
 }
 
+// fp32 step T0 (0 .. 15) of a 16-column block of the solve below, with the block's coefficients in
+// registers: cf[j][t] = C(c, c0 + t) for the lane's column c = c0 + 4 j + q when c > c0 + t, else 0
+// (so the finished entries and the owner's own entry take x - xt * 0 = x), ri[t] = 1 / C(t, t).
+template <int T0>
+__device__ __forceinline__ void block16_step(float (&x)[4], const float (&cf)[4][16], const float (&ri)[16], int q) {
+  constexpr int O = T0 & 3, IT = T0 >> 2;
+  float xt = x[IT] * ri[T0];
+  xt = quad_bcast<O>(xt);
+  if (q == O) x[IT] = xt;
+#pragma unroll
+  for (int j = IT; j < 4; ++j) x[j] -= xt * cf[j][T0];
+}
+template <int... Ts>
+__device__ __forceinline__ void block16_steps(float (&x)[4], const float (&cf)[4][16], const float (&ri)[16], int q,
+                                              std::integer_sequence<int, Ts...>) {
+  (block16_step<Ts>(x, cf, ri, q), ...);
+}
+
 // Pivot of a Cholesky column: sd = sqrt(d) and inv = 1 / sd.  fp32: the hardware reciprocal square
 // root refined by one Newton step, y (3 - d y^2) / 2, so that the column is scaled by a product, not a
 // quotient (the dependent chain of every column is the panel's critical path).
@@ -172,7 +191,8 @@ __device__ __forceinline__ void pivot(double d, double& sd, double& inv) {
 // chunks of 64 rows staged through LDS (coalesced loads and stores; a workgroup's first chunk is
 // loaded into registers before the factorisation, so the load overlaps it): four lanes share a
 // row, lane q owning the columns c = q mod 4, and the forward substitution runs column by column
-// with the finished x_t broadcast inside the quad.
+// with the finished x_t broadcast inside the quad (fp32: in blocks of 16 columns with the block's
+// coefficients in registers and the updates between blocks on MFMA, solve_chunk16).
 template <typename T, int PB>
 struct PotrfLds {
   static constexpr int CP = PB + 1;  // odd pitch: row and column walks are both conflict-free
@@ -196,6 +216,54 @@ __device__ __forceinline__ floatx16 tile_abt64(const float* __restrict__ A, cons
     acc = __builtin_amdgcn_mfma_f32_32x32x2f32(A[(32 * wy + li) * cp + 2 * s2 + hh], B[(32 * wx + li) * cp + 2 * s2 + hh],
                                                acc, 0, 0, 0);
   return acc;
+}
+
+// fp32 solve of a 64-row chunk, X <- X C^{-T} (X: 64 x 64 in rs, C: the factored 64 x 64 block in a,
+// rinv: its diagonal's reciprocals), in four blocks of 16 columns.  Inside a block, the forward
+// substitution of quad_solve (four lanes per row, lane q owning the columns c = q mod 4) with the
+// block's coefficients read into registers first, so that no LDS read sits in its 16-step chain;
+// then the block's rank-16 update of the later columns, X[:, later] -= X[:, block] C[later, block]^T,
+// on MFMA (wave (wy, wx): the 32 x 32 tile at rows 32 wy, columns 32 wx, when it holds later
+// columns).  Expects rs complete (a barrier after it was written); ends with a barrier.
+__device__ __forceinline__ void solve_chunk16(float* __restrict__ rs, const float* __restrict__ a,
+                                              const float* __restrict__ rinv, int tid) {
+  constexpr int CP = 65;
+  const int q = tid & 3, rr = tid >> 2;
+  const int lane = tid & 63, li = lane & 31, hh = lane >> 5, wy = tid >> 7, wx = (tid >> 6) & 1;
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    const int c0 = 16 * b;
+    float x[4], cf[4][16], ri[16];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) x[j] = rs[rr * CP + c0 + 4 * j + q];
+#pragma unroll
+    for (int t = 0; t < 16; ++t) ri[t] = rinv[c0 + t];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int t = 0; t < 4 * j + 4; ++t) cf[j][t] = 4 * j + q > t ? a[(c0 + 4 * j + q) * CP + c0 + t] : 0.f;
+    block16_steps(x, cf, ri, q, std::make_integer_sequence<int, 16>{});
+#pragma unroll
+    for (int j = 0; j < 4; ++j) rs[rr * CP + c0 + 4 * j + q] = x[j];
+    __syncthreads();
+    if (b < 3) {
+      if (32 * wx + 31 >= c0 + 16) {
+        floatx16 acc;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[e] = 0.f;
+#pragma unroll
+        for (int s2 = 0; s2 < 8; ++s2)
+          acc = __builtin_amdgcn_mfma_f32_32x32x2f32(rs[(32 * wy + li) * CP + c0 + 2 * s2 + hh],
+                                                     a[(32 * wx + li) * CP + c0 + 2 * s2 + hh], acc, 0, 0, 0);
+        const int col = 32 * wx + li;
+        if (col >= c0 + 16) {
+#pragma unroll
+          for (int e = 0; e < 16; ++e) rs[(32 * wy + 8 * (e >> 2) + 4 * hh + (e & 3)) * CP + col] -= acc[e];
+        }
+      }
+      __syncthreads();
+    }
+  }
 }
 
 // Panel j0 as above, for workgroup `bid` of `nblk` taking part (the panel's row chunks are dealt
@@ -367,13 +435,17 @@ __device__ __forceinline__ void potrf_panel(PotrfLds<T, PB>& sm, T* __restrict__
         __syncthreads();
       }
     }
-    T x[PB / 4];
+    if constexpr (kFuse) {
+      solve_chunk16(rs, a, sm.rinv, tid);
+    } else {
+      T x[PB / 4];
 #pragma unroll
-    for (int idx = 0; idx < PB / 4; ++idx) x[idx] = rs[rr * CP + 4 * idx + q];
-    quad_solve<0, PB, T>(x, q, a, CP, sm.rinv);
+      for (int idx = 0; idx < PB / 4; ++idx) x[idx] = rs[rr * CP + 4 * idx + q];
+      quad_solve<0, PB, T>(x, q, a, CP, sm.rinv);
 #pragma unroll
-    for (int idx = 0; idx < PB / 4; ++idx) rs[rr * CP + 4 * idx + q] = x[idx];
-    __syncthreads();
+      for (int idx = 0; idx < PB / 4; ++idx) rs[rr * CP + 4 * idx + q] = x[idx];
+      __syncthreads();
+    }
     for (int t = tid; t < 64 * PB; t += 256) {
       const int i = t / PB, c = t % PB;
       if (r0 + i < k) w[(r0 + i) * ld + j0 + c] = rs[i * CP + c];
@@ -670,16 +742,26 @@ __host__ __device__ inline int64_t trapezoid_blocks(int64_t R, int64_t C) {
 
 // A panel's update of the next panel's columns (D's first PB columns, every row: blocks (x, 0));
 // the last workgroup copies the staged diagonal block of panel `sc` (PB rows) into W.
+// The matrix of a launch of the fp32 Cholesky (blockIdx.y selects one of two, see CholeskyRun):
+// W, its info word, the staging block of the launch's panel and the staged block to copy into W
+// (nullptr: none).
+struct PanelPtrs {
+  float* w;
+  int* info;
+  float* stage;
+  const float* copy;
+};
+
 template <int PB>
-__global__ __launch_bounds__(256, 2) void syrk_strip_kernel(float* __restrict__ w, int64_t ld, int64_t r0, int R,
-                                                            int64_t pc, int K, int64_t sc,
-                                                            const float* __restrict__ stage) {
+__global__ __launch_bounds__(256, 2) void syrk_strip_kernel(PanelPtrs p0, PanelPtrs p1, int64_t ld, int64_t r0,
+                                                            int R, int64_t pc, int K, int64_t sc) {
   __shared__ __align__(16) WideLds sm;
+  const PanelPtrs& p = blockIdx.y ? p1 : p0;
   if (blockIdx.x == gridDim.x - 1) {
-    stage_to_w<float, PB>(w, ld, sc, PB, stage);
+    stage_to_w<float, PB>(p.w, ld, sc, PB, p.stage);
     return;
   }
-  syrk_wide_block(sm, w, ld, r0, R, PB, pc, K, (int)blockIdx.x, 0);
+  syrk_wide_block(sm, p.w, ld, r0, R, PB, pc, K, (int)blockIdx.x, 0);
 }
 
 // Look-ahead step of the fp32 Cholesky: workgroups [0, n_potrf) factor and solve panel j0; the
@@ -687,30 +769,29 @@ __global__ __launch_bounds__(256, 2) void syrk_strip_kernel(float* __restrict__ 
 // P = W[r0.., pc .. pc + K)).  The two touch disjoint columns, so the panel's latency-bound
 // factorisation runs beside the throughput-bound update.
 // upc >= 0: the panel first takes the rank-PB update of the panel at columns [upc, upc + PB) itself.
-// copy_stage != nullptr: the last workgroup moves that earlier panel's staged diagonal block (at
-// column copy_j0, PB rows) into W.
+// copy != nullptr: the last workgroup moves that earlier panel's staged diagonal block (at column
+// copy_j0, PB rows) into W.  The matrix: p0 or p1 by blockIdx.y (the copy set in both or neither).
 template <int PB>
-__global__ __launch_bounds__(256, 2) void panel_step_kernel(float* __restrict__ w, int64_t ld, int64_t j0, int n,
-                                                            int64_t k, int* __restrict__ info,
-                                                            float* __restrict__ stage, int64_t n_potrf, int64_t r0,
-                                                            int R, int C, int64_t pc, int K, int64_t upc,
-                                                            const float* __restrict__ copy_stage, int64_t copy_j0) {
+__global__ __launch_bounds__(256, 2) void panel_step_kernel(PanelPtrs p0, PanelPtrs p1, int64_t ld, int64_t j0,
+                                                            int n, int64_t k, int64_t n_potrf, int64_t r0, int R,
+                                                            int C, int64_t pc, int K, int64_t upc, int64_t copy_j0) {
   __shared__ __align__(16) union {
     PotrfLds<float, PB> p;
     WideLds s;
   } sm;
-  const int64_t n_upd = gridDim.x - n_potrf - (copy_stage ? 1 : 0);
-  if (copy_stage && (int64_t)blockIdx.x == gridDim.x - 1) {
-    stage_to_w<float, PB>(w, ld, copy_j0, PB, copy_stage);
+  const PanelPtrs& p = blockIdx.y ? p1 : p0;
+  const int64_t n_upd = gridDim.x - n_potrf - (p.copy ? 1 : 0);
+  if (p.copy && (int64_t)blockIdx.x == gridDim.x - 1) {
+    stage_to_w<float, PB>(p.w, ld, copy_j0, PB, p.copy);
     return;
   }
   if ((int64_t)blockIdx.x < n_potrf) {
-    potrf_panel<float, PB>(sm.p, w, ld, j0, n, k, info, stage, blockIdx.x, n_potrf, upc);
+    potrf_panel<float, PB>(sm.p, p.w, ld, j0, n, k, p.info, p.stage, blockIdx.x, n_potrf, upc);
     return;
   }
   int bi, bj;
   trapezoid_block(xcd_contiguous(blockIdx.x - n_potrf, n_upd), (C + WB - 1) / WB, bi, bj);
-  syrk_wide_block(sm.s, w, ld, r0, R, C, pc, K, bi, bj);
+  syrk_wide_block(sm.s, p.w, ld, r0, R, C, pc, K, bi, bj);
 }
 
 // Launch sequence of the blocked Cholesky of W (k x k) in place over the panels [col_begin, col_end)
@@ -718,7 +799,9 @@ __global__ __launch_bounds__(256, 2) void panel_step_kernel(float* __restrict__ 
 // interleave two factorisations on two streams.  Between runs (and after finish()), every earlier
 // panel's update has been applied to the whole trailing matrix and every factored diagonal block
 // is in W.  stage: PB x PB elements of scratch (a panel's factored diagonal block between its
-// launch and the next).
+// launch and the next).  twin() (two-level path only): a second k x k matrix factored by the same
+// launches, as blockIdx.y = 1 of each -- one chain of latency-bound panel launches for both, and
+// twice the work in each throughput-bound update; each matrix sees the launches it would see alone.
 template <typename T>
 struct CholeskyRun {
   static constexpr int PB = LdlBlock<T>::PB;
@@ -732,6 +815,9 @@ struct CholeskyRun {
   bool two_level, fuse, done = false;
   int64_t pr0 = 0, pC = 0, ppc = 0;  // pending trapezoid update (columns < pC of W[pr0.., pr0..])
   int pK = 0;
+  T* w1 = nullptr;  // the twin, if any
+  int* info1 = nullptr;
+  T* stage1 = nullptr;
 
   CholeskyRun(T* w_, int64_t k_, int* info_, T* stage_, hipStream_t s, int64_t cb = 0, int64_t ce = -1)
       : w(w_), k(k_), info(info_), stage(stage_), stream(s), col_begin(cb), col_end(ce < 0 || ce > k_ ? k_ : ce),
@@ -741,9 +827,22 @@ struct CholeskyRun {
     done = j0 >= col_end;
   }
 
-  // Staging block of panel j (two alternating ones when fused: a panel's launch copies the previous
-  // panel's block into W while its own workgroup 0 stages the new one).
-  T* slot(int64_t j) const { return fuse && ((j / PB) & 1) ? stage + (int64_t)PB * PB : stage; }
+  // Factor a second matrix (same k, its own info word and staging blocks) in the same launches; false
+  // (nothing changed) off the two-level path or once a step was taken.
+  bool twin(T* w_, int* info_, T* stage_) {
+    if (!two_level || j0 != col_begin || done) return false;
+    w1 = w_;
+    info1 = info_;
+    stage1 = stage_;
+    return true;
+  }
+
+  // Staging block of panel j of matrix f (two alternating ones when fused: a panel's launch copies
+  // the previous panel's block into W while its own workgroup 0 stages the new one).
+  T* slot(int64_t j, int f = 0) const {
+    T* st = f ? stage1 : stage;
+    return fuse && ((j / PB) & 1) ? st + (int64_t)PB * PB : st;
+  }
 
   // The launches of panel j0, then j0 += PB.
   int step() {
@@ -771,7 +870,6 @@ struct CholeskyRun {
   // in the launch that factors the next panel.
   int step_two_level() {
     int rc;
-    float* wf = (float*)w;
     const int n = k - j0 < PB ? (int)(k - j0) : PB;
     const int64_t rest = k - j0 - PB;
     const int64_t blocks = rest > 0 ? (cdiv(rest, 64) < 256 ? cdiv(rest, 64) : 256) : 1;
@@ -784,25 +882,34 @@ struct CholeskyRun {
     // fused: a panel after the first of its strip takes the previous panel's rank-PB update itself
     // (no launch of its own for it), and its launch moves the previous panel's staged block into W
     const bool in_strip = fuse && j0 > s_lo;
-    const float* copy = in_strip ? (const float*)slot(j0 - PB) : nullptr;
-    hipLaunchKernelGGL((panel_step_kernel<PB>), dim3((unsigned)(blocks + upd + (copy ? 1 : 0))), dim3(256), 0, stream,
-                       wf, k, j0, n, k, info, (float*)slot(j0), blocks, pr0, (int)pR, (int)pC, ppc, pK,
-                       in_strip ? j0 - PB : (int64_t)-1, copy, j0 - PB);
+    const unsigned ny = w1 ? 2u : 1u;
+    PanelPtrs pp[2];
+    for (int f = 0; f < 2; ++f) {
+      const int g = f < (int)ny ? f : 0;
+      pp[f] = PanelPtrs{(float*)(g ? w1 : w), g ? info1 : info, (float*)slot(j0, g),
+                        in_strip ? (const float*)slot(j0 - PB, g) : nullptr};
+    }
+    hipLaunchKernelGGL((panel_step_kernel<PB>), dim3((unsigned)(blocks + upd + (in_strip ? 1 : 0)), ny), dim3(256), 0,
+                       stream, pp[0], pp[1], k, j0, n, k, blocks, pr0, (int)pR, (int)pC, ppc, pK,
+                       in_strip ? j0 - PB : (int64_t)-1, j0 - PB);
     if ((rc = (int)hipGetLastError())) return rc;
     pC = 0;
     if (rest <= 0) {  // the last panel: its staged block into W on its own
-      hipLaunchKernelGGL((stage_to_w_kernel<float, PB>), dim3(1), dim3(256), 0, stream, wf, k, j0, n,
-                         (const float*)slot(j0));
+      for (unsigned f = 0; f < ny; ++f) {
+        hipLaunchKernelGGL((stage_to_w_kernel<float, PB>), dim3(1), dim3(256), 0, stream, pp[f].w, k, j0, n,
+                           (const float*)pp[f].stage);
+        if ((rc = (int)hipGetLastError())) return rc;
+      }
       done = true;
-      return (int)hipGetLastError();
+      return 0;
     }
     const bool strip_end = j0 + PB >= s_hi;
     // the update's rank: panel j0 alone inside the strip, the whole strip at its end
     const int64_t pc = strip_end ? s_lo : j0;
     const int K = (int)(j0 + PB - pc);
     if (strip_end || !fuse) {
-      hipLaunchKernelGGL((syrk_strip_kernel<PB>), dim3((unsigned)cdiv(rest, WB) + 1), dim3(256), 0, stream, wf, k,
-                         j0 + PB, (int)rest, pc, K, j0, (const float*)slot(j0));
+      hipLaunchKernelGGL((syrk_strip_kernel<PB>), dim3((unsigned)cdiv(rest, WB) + 1, ny), dim3(256), 0, stream, pp[0],
+                         pp[1], k, j0 + PB, (int)rest, pc, K, j0);
       if ((rc = (int)hipGetLastError())) return rc;
     }
     // the rest: the strip's later columns, or everything to the right at a strip's end
@@ -856,9 +963,11 @@ struct CholeskyRun {
     if constexpr (sizeof(T) == 4) {
       if (pC <= 0) return 0;
       const int64_t pR = k - pr0;
-      hipLaunchKernelGGL((panel_step_kernel<PB>), dim3((unsigned)trapezoid_blocks(pR, pC)), dim3(256), 0, stream,
-                         (float*)w, k, (int64_t)0, 0, k, info, (float*)stage, (int64_t)0, pr0, (int)pR, (int)pC,
-                         ppc, pK, (int64_t)-1, (const float*)nullptr, (int64_t)0);
+      const PanelPtrs p0{(float*)w, info, (float*)stage, nullptr};
+      const PanelPtrs p1 = w1 ? PanelPtrs{(float*)w1, info1, (float*)stage1, nullptr} : p0;
+      hipLaunchKernelGGL((panel_step_kernel<PB>), dim3((unsigned)trapezoid_blocks(pR, pC), w1 ? 2u : 1u), dim3(256),
+                         0, stream, p0, p1, k, (int64_t)0, 0, k, (int64_t)0, pr0, (int)pR, (int)pC, ppc, pK,
+                         (int64_t)-1, (int64_t)0);
       pC = 0;
       return (int)hipGetLastError();
     }
@@ -1199,8 +1308,10 @@ int pair_events(hipEvent_t (&ev)[4]) {
 // panel, alternating, so that both chains of latency-bound panel launches are in flight together
 // from the start; when a factorisation has passed its inverse's split point, part 1 of that inverse
 // goes to stream[2] (after an event on stream[f]), where it runs beside the rest of both
-// factorisations; parts 2 and 3 follow on stream[f], part 3 after an event on stream[2].  The
-// results equal two ldl_of_inverse calls bit for bit (the same launches, in another order).
+// factorisations; parts 2 and 3 follow on stream[f], part 3 after an event on stream[2].  Two fp32
+// matrices of one size on the two-level path share every Cholesky launch instead (CholeskyRun's
+// twin).  The results equal two ldl_of_inverse calls bit for bit (each matrix sees the same
+// workgroups' arithmetic, in another order of launches).
 template <typename T>
 int ldl_of_inverse_pair(const T* const* m, T* const* out, T* const* work, int* const* info, const int64_t* k,
                         const int64_t* size, hipStream_t const* stream) {
@@ -1213,13 +1324,43 @@ int ldl_of_inverse_pair(const T* const* m, T* const* out, T* const* work, int* c
   int rc;
   if ((rc = pair_events(ev))) return rc;
   int64_t split[2];
+  CholeskyRun<T> twin(work[0], k[0], info[0], out[0] + stage_offset<T>(k[0]), stream[0]);
+  const bool twinned = k[0] == k[1] && k[0] > 0 && twin.twin(work[1], info[1], out[1] + stage_offset<T>(k[1]));
   for (int f = 0; f < 2; ++f) {
     split[f] = k[f] > 0 ? trtri_split<T>(k[f]) : 0;
     if (k[f] == 0) continue;
     const int64_t kk = k[f] * k[f];
     const int64_t blocks = cdiv(kk, 256) < 8192 ? cdiv(kk, 256) : 8192;
-    hipLaunchKernelGGL(copy_kernel<T>, dim3((unsigned)blocks), dim3(256), 0, stream[f], work[f], m[f], kk, 1);
+    hipLaunchKernelGGL(copy_kernel<T>, dim3((unsigned)blocks), dim3(256), 0, stream[twinned ? 0 : f], work[f], m[f],
+                       kk, 1);
     if ((rc = (int)hipGetLastError())) return rc;
+  }
+  if (twinned) {
+    // both factorisations in one chain of launches on stream[0]; past the split, part 1 of the
+    // inverses on stream[2] (factor 0) and stream[1] (factor 1), beside the rest of the chain; parts 2
+    // and 3 of factor f on stream[f] after the chain (an event for stream[1]), part 3 of factor 0
+    // after its part 1 (an event on stream[2])
+    bool lead = split[0] == 0;
+    while (!twin.done || !lead) {
+      if ((rc = twin.step())) return rc;
+      if (!lead && (twin.done || twin.j0 >= split[0])) {
+        if (hipEventRecord(ev[0], stream[0]) != hipSuccess || hipStreamWaitEvent(stream[2], ev[0], 0) != hipSuccess ||
+            hipStreamWaitEvent(stream[1], ev[0], 0) != hipSuccess)
+          return GPTQ2D_EUNSUPPORTED;
+        if ((rc = trtri_part<T>(out[0], work[0], k[0], size[0], 1, stream[2]))) return rc;
+        if (hipEventRecord(ev[2], stream[2]) != hipSuccess) return GPTQ2D_EUNSUPPORTED;
+        if ((rc = trtri_part<T>(out[1], work[1], k[1], size[1], 1, stream[1]))) return rc;
+        lead = true;
+      }
+    }
+    if (hipEventRecord(ev[1], stream[0]) != hipSuccess || hipStreamWaitEvent(stream[1], ev[1], 0) != hipSuccess)
+      return GPTQ2D_EUNSUPPORTED;
+    for (int f = 0; f < 2; ++f) {
+      if ((rc = trtri_part<T>(out[f], work[f], k[f], size[f], 2, stream[f]))) return rc;
+      if (f == 0 && split[0] && hipStreamWaitEvent(stream[0], ev[2], 0) != hipSuccess) return GPTQ2D_EUNSUPPORTED;
+      if ((rc = trtri_part<T>(out[f], work[f], k[f], size[f], 3, stream[f]))) return rc;
+    }
+    return 0;
   }
   CholeskyRun<T> run[2] = {
       CholeskyRun<T>(work[0], k[0], info[0], out[0] + stage_offset<T>(k[0]), stream[0]),

@@ -245,37 +245,39 @@ struct TileLds {
 // Affine / round / forced quantizer of the in-tile sweep, given the precomputed correctly rounded
 // reciprocal rv = 1/sv and whether sv lies in [2^-60, 2^60] (affine only).  y / s is formed as
 // q0 = y rv, then one FMA correction with the exact remainder y - q0 s (Markstein's method): the
-// IEEE quotient whenever also |y| in [2^-60, 2^60] or y = 0 (then nothing over- or underflows),
-// the division itself otherwise.  This keeps the division's ten dependent operations off the
-// per-antidiagonal critical path.
-// Every lane evaluates it (no divergent branch on the per-step critical path); the division runs
-// only when a lane with `active` set needs it, behind a branch that is uniform over the wave.
+// IEEE quotient whenever also |y| in [2^-60, 2^60] or y = 0 (then nothing over- or underflows);
+// `exact` says whether that holds, and otherwise quantize_entry_div (the division itself) gives the
+// value.  This keeps the division's ten dependent operations off the per-antidiagonal critical path.
 template <int KIND>
 __device__ __forceinline__ float quantize_entry_rcp(float yv, float sv, float zv, float rv, bool s_ok, float qmin,
-                                                    float qmax, bool active) {
+                                                    float qmax, bool& exact) {
   // the dequantized value is rounded on its own (as the reference's plug-in writes it), so that the
   // caller's error z - y is exactly that difference: no contraction into the caller's subtraction
 #pragma clang fp contract(off)
   if constexpr (KIND == Q_AFFINE) {
     const float q0 = yv * rv;
     const float rem = __builtin_fmaf(-q0, sv, yv);
-    float q = __builtin_fmaf(rem, rv, q0);
+    const float q = __builtin_fmaf(rem, rv, q0);
     const float ay = __builtin_fabsf(yv);
     // s_ok also holds only when the zero point is not NaN and qmin <= qmax: then q is the IEEE
     // quotient, round(q + z) is not NaN, and the median of (x, qmin, qmax) is the clamp, in one
     // operation on the per-step critical path
-    const bool exact = s_ok && ay <= 0x1p60f && (ay >= 0x1p-60f || yv == 0.f);
-    float code = __builtin_amdgcn_fmed3f(round_even(q + zv), qmin, qmax);
-    if (__builtin_amdgcn_ballot_w64(active && !exact)) {
-      asm volatile("");  // keeps the division behind the branch (no speculation into a select)
-      if (!exact) code = clamp_val(round_even(yv / sv + zv), qmin, qmax);
-    }
+    exact = s_ok && ay <= 0x1p60f && (ay >= 0x1p-60f || yv == 0.f);
+    const float code = __builtin_amdgcn_fmed3f(round_even(q + zv), qmin, qmax);
     return (code - zv) * sv;
   } else if constexpr (KIND == Q_FORCED) {
+    exact = true;
     return sv;
   } else {
+    exact = true;
     return round_even(yv);
   }
+}
+
+__device__ __forceinline__ float quantize_entry_div(float yv, float sv, float zv, float qmin, float qmax) {
+#pragma clang fp contract(off)
+  const float code = clamp_val(round_even(yv / sv + zv), qmin, qmax);
+  return (code - zv) * sv;
 }
 
 // The tile's 63 antidiagonals, in push form.  Thread (r, part) = (tid / 8, tid % 8) owns the four
@@ -343,22 +345,40 @@ __device__ __forceinline__ void sweep_tile_push(TileLds& tl, float* __restrict__
     const int ka = (t >> 3) & 3, buf = t & 1;
     // every lane evaluates its step-t register; only the rounding lanes keep and publish it
     const bool rnd = part == (t & 7) && row_in && t - r >= 0 && t - r < cols_in;
+    const float yv = (Y[ka] + D[ka]) + F[ka];
     {
-      const float yv = (Y[ka] + D[ka]) + F[ka];
-      const float z = quantize_entry_rcp<KIND>(yv, S[ka], Z[ka], R[ka], s_ok[ka], qmin, qmax, rnd);
-      const float ev = z - yv;
-      const float cf = (C[ka] + D[ka]) + ev;
+      bool exact;
+      float z = quantize_entry_rcp<KIND>(yv, S[ka], Z[ka], R[ka], s_ok[ka], qmin, qmax, exact);
+      float ev = z - yv;
+      const float cd = C[ka] + D[ka];
+      float cf = cd + ev;
       if (rnd) {
+        // published at once; a lane whose quotient needs the division writes again (same address:
+        // the later write stands), behind a branch taken only when some lane of the wave needs it
+        tl.Ed[buf][t - r] = ev;
+        tl.Cr[buf][r] = cf;
+        if constexpr (KIND == Q_AFFINE) {
+          if (__builtin_amdgcn_ballot_w64(!exact)) {
+            asm volatile("");  // keeps the division behind the branch (no speculation into a select)
+            if (!exact) {
+              z = quantize_entry_div(yv, S[ka], Z[ka], qmin, qmax);
+              ev = z - yv;
+              cf = cd + ev;
+              tl.Ed[buf][t - r] = ev;
+              tl.Cr[buf][r] = cf;
+            }
+          }
+        }
         Y[ka] = z;
         E[ka] = ev;
         C[ka] = cf;
-        tl.Ed[buf][t - r] = ev;
-        tl.Cr[buf][r] = cf;
       }
-      if (has_ypre && rnd) ypre_row[t - r] = yv;
     }
     __syncthreads();
-    if (t == 2 * TR - 2) break;  // nothing left to receive feedback
+    if (t == 2 * TR - 2) {
+      if (has_ypre && rnd) ypre_row[t - r] = yv;
+      break;  // nothing left to receive feedback
+    }
     const float cr = tl.Cr[buf][r];
     float ev[4];
 #pragma unroll
@@ -371,6 +391,8 @@ __device__ __forceinline__ void sweep_tile_push(TileLds& tl, float* __restrict__
         UN[k] = tl.Up[TR + t + 1 - r][ck[k]];
       }
     }
+    // the pre-quantization value out while this step's published values are read back
+    if (has_ypre && rnd) ypre_row[t - r] = yv;
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
       D[k] += LV[k] * ev[k];

@@ -160,10 +160,11 @@ def test_concurrent_factors_deterministic():
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
-@pytest.mark.parametrize("ka,kb", [(777, 600), (100, 257), (65, 64)])
+@pytest.mark.parametrize("ka,kb", [(777, 600), (100, 257), (65, 64), (600, 600), (2052, 2052)])
 def test_feedback_factors_of_grams_ragged(ka, kb, dtype):
     """Sizes that are not multiples of the panel width: the factor pair equals the single-stream factors
-    bitwise (the inverse-only part starts at column k, past the last panel)."""
+    bitwise (the inverse-only part starts at column k, past the last panel).  Equal fp32 sizes share
+    every Cholesky launch (the second matrix as blockIdx.y = 1); 2052 also splits the inverse."""
     print(f"feedback_factors_of_grams {ka} {kb} {dtype}", flush=True)
     a = instances.wishart_factor(ka, .5, 40 + ka).to(dtype).to(DEV)
     b = instances.wishart_factor(kb, .5, 50 + kb).to(dtype).to(DEV)
