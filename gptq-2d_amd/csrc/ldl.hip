@@ -186,7 +186,7 @@ __device__ __forceinline__ void pivot(double d, double& sd, double& inv) {
 // registers, lane r holding row r, column by column with no barrier (the pivot and the scaled
 // column entries reach the other lanes by readlane; lane r's entries right of its diagonal take
 // harmless updates and are never read), then the workgroup applies the rank-16 update to the
-// block's later columns (fp32: one 32 x 32 MFMA tile per wave); workgroup 0 stages the factored
+// block's later columns (fp32: one 32 x 32 MFMA tile per wave); the workgroups stage the factored
 // block.  Then the panel below is solved against it, W[r, j0:j0+PB] <- W[r, j0:j0+PB] C_jj^{-T}, in
 // chunks of 64 rows staged through LDS (coalesced loads and stores; a workgroup's first chunk is
 // loaded into registers before the factorisation, so the load overlaps it): four lanes share a
@@ -208,13 +208,18 @@ struct PotrfLds {
 // k = 2 s + h for MFMA s), acc[e] = tile(8 (e / 4) + 4 h + e % 4, lane % 32).
 __device__ __forceinline__ floatx16 tile_abt64(const float* __restrict__ A, const float* __restrict__ B, int cp,
                                                int wy, int wx, int li, int hh) {
+  // every operand read before the first MFMA: no LDS latency between MFMAs
+  float av[32], bv[32];
+#pragma unroll
+  for (int s2 = 0; s2 < 32; ++s2) {
+    av[s2] = A[(32 * wy + li) * cp + 2 * s2 + hh];
+    bv[s2] = B[(32 * wx + li) * cp + 2 * s2 + hh];
+  }
   floatx16 acc;
 #pragma unroll
   for (int e = 0; e < 16; ++e) acc[e] = 0.f;
 #pragma unroll
-  for (int s2 = 0; s2 < 32; ++s2)
-    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(A[(32 * wy + li) * cp + 2 * s2 + hh], B[(32 * wx + li) * cp + 2 * s2 + hh],
-                                               acc, 0, 0, 0);
+  for (int s2 = 0; s2 < 32; ++s2) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[s2], bv[s2], acc, 0, 0, 0);
   return acc;
 }
 
@@ -248,13 +253,17 @@ __device__ __forceinline__ void solve_chunk16(float* __restrict__ rs, const floa
     __syncthreads();
     if (b < 3) {
       if (32 * wx + 31 >= c0 + 16) {
+        float av[8], bv[8];
+#pragma unroll
+        for (int s2 = 0; s2 < 8; ++s2) {
+          av[s2] = rs[(32 * wy + li) * CP + c0 + 2 * s2 + hh];
+          bv[s2] = a[(32 * wx + li) * CP + c0 + 2 * s2 + hh];
+        }
         floatx16 acc;
 #pragma unroll
         for (int e = 0; e < 16; ++e) acc[e] = 0.f;
 #pragma unroll
-        for (int s2 = 0; s2 < 8; ++s2)
-          acc = __builtin_amdgcn_mfma_f32_32x32x2f32(rs[(32 * wy + li) * CP + c0 + 2 * s2 + hh],
-                                                     a[(32 * wx + li) * CP + c0 + 2 * s2 + hh], acc, 0, 0, 0);
+        for (int s2 = 0; s2 < 8; ++s2) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[s2], bv[s2], acc, 0, 0, 0);
         const int col = 32 * wx + li;
         if (col >= c0 + 16) {
 #pragma unroll
@@ -283,35 +292,28 @@ __device__ __forceinline__ void potrf_panel(PotrfLds<T, PB>& sm, T* __restrict__
   const int tid = threadIdx.x;
   const int lane = tid & 63, li = lane & 31, hh = lane >> 5, wy = tid >> 7, wx = (tid >> 6) & 1;
   // every load of the prologue is issued before any is waited for (into registers, unrolled): a
-  // load-then-store loop would wait out one memory latency per element.  The diagonal block and the
-  // update source's rows of it come first -- loads return in issue order, so the factorisation
-  // waits for these and not for the chunk loads issued after them.
-  constexpr int NL = PB * PB / 256;
+  // load-then-store loop would wait out one memory latency per element.
+  // Lane (rl, cl) = (tid / PB, tid % PB) loads rows rl + RS u of column cl.  A full panel (n = PB)
+  // loads unconditionally along one pointer (the upper triangle's values are read and dropped);
+  // the last, short panel takes the guarded walk.
+  constexpr int NL = PB * PB / 256, RS = 256 / PB;
+  const int rl = tid / PB, cl = tid % PB;
   T dv[NL], pv[NL];
+  if (n == PB) {
+    const T* src = w + (j0 + rl) * ld + j0 + cl;
+    const T* psrc = w + (j0 + rl) * ld + upc + cl;
 #pragma unroll
-  for (int u = 0; u < NL; ++u) {
-    const int t = tid + 256 * u, r = t / PB, c = t % PB;
-    dv[u] = (r < n && c <= r) ? w[(j0 + r) * ld + j0 + c] : (r == c ? T(1) : T(0));
-  }
-  if (fuse) {
+    for (int u = 0; u < NL; ++u) {
+      const T v = src[(int64_t)u * RS * ld];
+      dv[u] = cl <= rl + RS * u ? v : T(0);
+      if (fuse) pv[u] = psrc[(int64_t)u * RS * ld];
+    }
+  } else {
 #pragma unroll
     for (int u = 0; u < NL; ++u) {
       const int t = tid + 256 * u, r = t / PB, c = t % PB;
-      pv[u] = r < n ? w[(j0 + r) * ld + upc + c] : T(0);
-    }
-  }
-  // this workgroup's first chunk of the panel below (and of the update's source panel), in flight
-  // during the factorisation
-  const int64_t first = j0 + PB;
-  constexpr int PRE = 64 * PB / 256;
-  T pre[PRE], xpre[PRE];
-  if (n == PB) {
-    const int64_t r0 = first + bid * 64;
-#pragma unroll
-    for (int u = 0; u < PRE; ++u) {
-      const int t = tid + 256 * u, i = t / PB, c = t % PB;
-      pre[u] = r0 + i < k ? w[(r0 + i) * ld + j0 + c] : T(0);
-      if (fuse) xpre[u] = r0 + i < k ? w[(r0 + i) * ld + upc + c] : T(0);
+      dv[u] = (r < n && c <= r) ? w[(j0 + r) * ld + j0 + c] : (r == c ? T(1) : T(0));
+      if (fuse) pv[u] = r < n ? w[(j0 + r) * ld + upc + c] : T(0);
     }
   }
 #pragma unroll
@@ -321,6 +323,32 @@ __device__ __forceinline__ void potrf_panel(PotrfLds<T, PB>& sm, T* __restrict__
     if (fuse) sm.pd[r * CP + c] = pv[u];
   }
   __syncthreads();
+  // this workgroup's first chunk of the panel below (and of the update's source panel), in flight
+  // during the factorisation.  Issued only now: every workgroup of the launch reads the same
+  // diagonal block (cache hits after the first) but a chunk of its own, and chunk loads issued
+  // beside the block's would hold the factorisation's start behind the whole launch's chunk traffic
+  const int64_t first = j0 + PB;
+  constexpr int PRE = 64 * PB / 256;
+  T pre[PRE], xpre[PRE];
+  if (n == PB) {
+    const int64_t r0 = first + bid * 64;
+    if (r0 + 64 <= k) {
+      const T* src = w + (r0 + rl) * ld + j0 + cl;
+      const T* psrc = w + (r0 + rl) * ld + upc + cl;
+#pragma unroll
+      for (int u = 0; u < PRE; ++u) {
+        pre[u] = src[(int64_t)u * RS * ld];
+        if (fuse) xpre[u] = psrc[(int64_t)u * RS * ld];
+      }
+    } else {
+#pragma unroll
+      for (int u = 0; u < PRE; ++u) {
+        const int t = tid + 256 * u, i = t / PB, c = t % PB;
+        pre[u] = r0 + i < k ? w[(r0 + i) * ld + j0 + c] : T(0);
+        if (fuse) xpre[u] = r0 + i < k ? w[(r0 + i) * ld + upc + c] : T(0);
+      }
+    }
+  }
   if constexpr (kFuse) {
     if (fuse) {
       // the diagonal block: a -= Pd Pd^T (the tile above the diagonal is not needed)
@@ -368,13 +396,17 @@ __device__ __forceinline__ void potrf_panel(PotrfLds<T, PB>& sm, T* __restrict__
         const int lane = tid & 63, li = lane & 31, hh = lane >> 5;
         const int wy = tid >> 7, wx = (tid >> 6) & 1;
         if (32 * wx + 31 >= c0 + CB) {
+          float av[CB / 2], bv[CB / 2];
+#pragma unroll
+          for (int s2 = 0; s2 < CB / 2; ++s2) {
+            av[s2] = a[(32 * wy + li) * CP + c0 + 2 * s2 + hh];
+            bv[s2] = a[(32 * wx + li) * CP + c0 + 2 * s2 + hh];
+          }
           floatx16 acc;
 #pragma unroll
           for (int e = 0; e < 16; ++e) acc[e] = 0.f;
 #pragma unroll
-          for (int s2 = 0; s2 < CB / 2; ++s2)
-            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[(32 * wy + li) * CP + c0 + 2 * s2 + hh],
-                                                       a[(32 * wx + li) * CP + c0 + 2 * s2 + hh], acc, 0, 0, 0);
+          for (int s2 = 0; s2 < CB / 2; ++s2) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[s2], bv[s2], acc, 0, 0, 0);
           const int col = 32 * wx + li;
           if (col >= c0 + CB) {
 #pragma unroll
@@ -401,12 +433,9 @@ __device__ __forceinline__ void potrf_panel(PotrfLds<T, PB>& sm, T* __restrict__
   // the factored block goes to the staging block, not back into W: workgroups of this launch that
   // start late (the GPU busy with other work) still read the unfactored block from W; a later
   // launch copies it into W (stage_to_w)
-  if (bid == 0) {
-    for (int t = tid; t < PB * PB; t += 256) {
-      const int r = t / PB, c = t % PB;
-      if (r < n && c <= r) stage[r * n + c] = a[r * CP + c];  // pitch n: fits any k x k buffer
-    }
-  }
+  // (its rows dealt over the launch's workgroups: row r by workgroup r mod nblk)
+  for (int r = (int)(bid % PB); r < n; r += (int)(nblk < PB ? nblk : PB))
+    if (bid < PB && tid <= r) stage[r * n + tid] = a[r * CP + tid];  // pitch n: fits any k x k buffer
   if (n < PB) return;
   const int q = tid & 3, rr = tid >> 2;
   for (int64_t r0 = first + bid * 64; r0 < k; r0 += nblk * 64) {
@@ -838,7 +867,7 @@ struct CholeskyRun {
   }
 
   // Staging block of panel j of matrix f (two alternating ones when fused: a panel's launch copies
-  // the previous panel's block into W while its own workgroup 0 stages the new one).
+  // the previous panel's block into W while its own workgroups stage the new one).
   T* slot(int64_t j, int f = 0) const {
     T* st = f ? stage1 : stage;
     return fuse && ((j / PB) & 1) ? st + (int64_t)PB * PB : st;
@@ -1341,9 +1370,10 @@ int ldl_of_inverse_pair(const T* const* m, T* const* out, T* const* work, int* c
     // and 3 of factor f on stream[f] after the chain (an event for stream[1]), part 3 of factor 0
     // after its part 1 (an event on stream[2])
     bool lead = split[0] == 0;
+    const int64_t lead_col = getenv("GPTQ2D_LEAD") ? split[0] + atoll(getenv("GPTQ2D_LEAD")) : split[0];  // EXPERIMENT
     while (!twin.done || !lead) {
       if ((rc = twin.step())) return rc;
-      if (!lead && (twin.done || twin.j0 >= split[0])) {
+      if (!lead && (twin.done || twin.j0 >= lead_col)) {
         if (hipEventRecord(ev[0], stream[0]) != hipSuccess || hipStreamWaitEvent(stream[2], ev[0], 0) != hipSuccess ||
             hipStreamWaitEvent(stream[1], ev[0], 0) != hipSuccess)
           return GPTQ2D_EUNSUPPORTED;
