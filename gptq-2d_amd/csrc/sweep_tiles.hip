@@ -172,7 +172,7 @@ __device__ __forceinline__ float quantize_entry(float yv, float sv, float zv, fl
 }
 
 // One wave's share of a band product on MFMA: acc += sum over the k-chunks ch in [c_lo, c_hi) with
-// ch = c_lo + half (mod 2) of A[i0 + 0..31, 8 ch + 0..7] B[8 ch + 0..7, j0 + 0..31], A and B
+// ch = c_lo + part (mod nparts) of A[i0 + 0..31, 8 ch + 0..7] B[8 ch + 0..7, j0 + 0..31], A and B
 // row-major (lda, ldb), read straight from global memory into the MFMA operand layout: lane l
 // supplies A(l % 32, 8 ch + 4 (l / 32) + s) and B(8 ch + 4 (l / 32) + s, l % 32) to MFMA s = 0..3 of
 // the chunk.  Loads of G chunks are issued before their MFMAs.
@@ -180,7 +180,7 @@ template <bool VEC>
 __device__ __forceinline__ void pull_chunks(floatx16& acc, const float* __restrict__ A, int64_t lda, int64_t a_rows,
                                             int64_t a_cols, const float* __restrict__ Bm, int64_t ldb,
                                             int64_t b_rows, int64_t b_cols, int64_t i0, int64_t j0, int64_t c_lo,
-                                            int64_t c_hi, int half, int li, int hh) {
+                                            int64_t c_hi, int part, int nparts, int li, int hh) {
   // this lane's row of A and column of B as pointers (64-bit arithmetic once); k offsets in 32 bits
   const int64_t ia = i0 + li, jb = j0 + li;
   const bool arow = ia < a_rows, bcol = jb < b_cols;
@@ -188,11 +188,11 @@ __device__ __forceinline__ void pull_chunks(floatx16& acc, const float* __restri
   const float* bp = Bm + (bcol ? jb : 0);
   const int clo = (int)c_lo, chi = (int)c_hi, acols = (int)a_cols, brows = (int)b_rows;
   constexpr int G = 4;
-  for (int base = clo + half; base < chi; base += 2 * G) {
+  for (int base = clo + part; base < chi; base += nparts * G) {
     float av[G][4], bv[G][4];
 #pragma unroll
     for (int q = 0; q < G; ++q) {
-      const int ch = base + 2 * q;
+      const int ch = base + nparts * q;
       const int k0 = 8 * ch + 4 * hh;
       const bool ok = ch < chi;
       if (VEC) {
@@ -209,7 +209,7 @@ __device__ __forceinline__ void pull_chunks(floatx16& acc, const float* __restri
     }
 #pragma unroll
     for (int q = 0; q < G; ++q) {
-      if (base + 2 * q >= c_hi) break;
+      if (base + nparts * q >= chi) break;
 #pragma unroll
       for (int s2 = 0; s2 < 4; ++s2) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[q][s2], bv[q][s2], acc, 0, 0, 0);
     }
@@ -430,6 +430,15 @@ __device__ __forceinline__ void sweep_tile_push(TileLds& tl, float* __restrict__
 
 // Own tile data of the fp32 kernels, read before the tile's feedback is complete (it does not
 // depend on it): entry q of this thread is (t / TR, t % TR) with t = threadIdx.x + NTHREADS q.
+// The pulled feedback at (r, cc) from the four waves' partial sums (wave w's in red[w / 2][w % 2]):
+// waves [0, wd) summed the down product D, the others the right product R (in wave order).
+__device__ __forceinline__ void pulled_sums(const float (*red)[2][TR][TR + 1], int wd, int r, int cc, float& dd,
+                                            float& rr) {
+  const float s0 = red[0][0][r][cc], s1 = red[0][1][r][cc], s2 = red[1][0][r][cc], s3 = red[1][1][r][cc];
+  dd = (wd > 0 ? s0 : 0.f) + (wd > 1 ? s1 : 0.f) + (wd > 2 ? s2 : 0.f) + (wd > 3 ? s3 : 0.f);
+  rr = (wd > 0 ? 0.f : s0) + (wd > 1 ? 0.f : s1) + (wd > 2 ? 0.f : s2) + (wd > 3 ? 0.f : s3);
+}
+
 template <int KIND>
 struct TileRegs {
   static constexpr int NQ = TR * TR / NTHREADS;
@@ -471,18 +480,15 @@ struct TileRegs {
   }
 
   // LDS image of the tile with the pulled feedback D (down) and R (right) added: C + D, Y + (D + R),
-  // and the zero padding of the diagonal blocks.  red[product][half] holds the two waves' partial
-  // sums of each product when `pulled`.
-  __device__ __forceinline__ void store(TileLds& tl, const float (*red)[2][TR][TR + 1], bool pulled) const {
+  // and the zero padding of the diagonal blocks.  red holds the waves' partial sums when `pulled`
+  // (pulled_sums: the first wd waves' are D's).
+  __device__ __forceinline__ void store(TileLds& tl, const float (*red)[2][TR][TR + 1], bool pulled, int wd) const {
 #pragma unroll
     for (int q = 0; q < NQ; ++q) {
       const int t = threadIdx.x + NTHREADS * q;
       const int r = t / TR, cc = t % TR;
       float dd = 0.f, rr = 0.f;
-      if (pulled) {
-        dd = red[0][0][r][cc] + red[0][1][r][cc];
-        rr = red[1][0][r][cc] + red[1][1][r][cc];
-      }
+      if (pulled) pulled_sums(red, wd, r, cc, dd, rr);
       tl.Ys[r][cc] = y[q] + (dd + rr);
       tl.Cs[r][cc] = c[q] + dd;
       tl.Lp[r][TR + cc] = l[q];
@@ -577,16 +583,21 @@ __global__ __launch_bounds__(NTHREADS, 2) void tile_stage_kernel(float* __restri
   TileRegs<KIND> own;
   if (sweep) own.load(y, c, lb, ub, qs, b, m, n, i0, j0, mat);
 
+  // the four waves dealt to the two products in proportion to their chunk counts (a tile near its
+  // outer block's edge has nearly all its history in one of them), each product's chunks
+  // interleaved over its waves
+  const int64_t nd = d1 - d0, nr = r1 - r0;
+  int wd = nd == 0 ? 0 : (nr == 0 ? 4 : (int)((4 * nd + (nd + nr) / 2) / (nd + nr)));
+  if (nd > 0 && nr > 0) wd = wd < 1 ? 1 : (wd > 3 ? 3 : wd);
   if (pulled) {
     floatx16 acc;
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[r] = 0.f;
-    const int product = wave >> 1, half = wave & 1;
-    if (product == 0)
-      pull_chunks<VEC>(acc, lb, m, m, m, e + mat, n, m, n, i0, j0, d0, d1, half, li, hh);
+    if (wave < wd)
+      pull_chunks<VEC>(acc, lb, m, m, m, e + mat, n, m, n, i0, j0, d0, d1, wave, wd, li, hh);
     else
-      pull_chunks<VEC>(acc, c + mat, n, m, n, ub, n, n, n, i0, j0, r0, r1, half, li, hh);
-    stash_partial(red, acc, product, half);
+      pull_chunks<VEC>(acc, c + mat, n, m, n, ub, n, n, n, i0, j0, r0, r1, wave - wd, 4 - wd, li, hh);
+    stash_partial(red, acc, wave >> 1, wave & 1);
   }
   __syncthreads();
 
@@ -600,8 +611,8 @@ __global__ __launch_bounds__(NTHREADS, 2) void tile_stage_kernel(float* __restri
       const int r = t / TR, cc = t % TR;
       if (r < rows_in && cc < cols_in) {
         const int off = r * (int)n + cc;
-        const float dd = red[0][0][r][cc] + red[0][1][r][cc];
-        const float rr = red[1][0][r][cc] + red[1][1][r][cc];
+        float dd, rr;
+        pulled_sums(red, wd, r, cc, dd, rr);
         yt[off] = yt[off] + (dd + rr);
         ct[off] = ct[off] + dd;
       }
@@ -610,7 +621,7 @@ __global__ __launch_bounds__(NTHREADS, 2) void tile_stage_kernel(float* __restri
   }
 
   // ---- the tile image in LDS, then the in-tile sweep
-  own.store(tl, red, pulled);
+  own.store(tl, red, pulled, wd);
   __syncthreads();
   sweep_tile_push<KIND>(tl, y, c, e, qs, m, n, i0, j0, mat);
 }
