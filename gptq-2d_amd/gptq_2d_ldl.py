@@ -80,8 +80,9 @@ def _part(m, out, work, info, k, size, col_begin, col_end, finish):
 def feedback_factors_of_grams(G: torch.Tensor, H: torch.Tensor, super_entry_shape=(1, 1), *, check: bool = True):
     """(L, U) = (ldl_of_inverse(G, p), ldl_of_inverse(H, q)^T) from the Grams themselves, both at once on
     three side streams of the current device (gptq2d_ldl_of_inverse_pair): the two Cholesky
-    factorisations -- each a chain of latency-bound panel launches -- run together, and the first part
-    of each triangular inverse runs beside the rest of the factorisations.  Bitwise equal to the two
+    factorisations -- chains of latency-bound panel launches -- share every launch when the factors are
+    fp32 of one size (else they run together on two streams), and the first part of each triangular
+    inverse runs beside the rest of the factorisations.  Bitwise equal to the two
     ldl_of_inverse calls.  No counterpart in the reference, whose callers compute the two factors one
     after the other (demo.ipynb cell 5)."""
     p, q = super_entry_shape

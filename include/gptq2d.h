@@ -121,10 +121,10 @@ extern "C" {
   /* ldl_of_inverse of two matrices at once (the Kronecker factors of one layer; no reference         \
    * counterpart -- the reference computes them one after the other, demo.ipynb cell 5): matrix f      \
    * (m_f, k_f x k_f, block size size_f, outputs out_f, scratch work_f, info_f as above) on stream_f,   \
-   * with the first part of each triangular inverse on stream2 (three distinct streams of one          \
-   * device).  The two Cholesky factorisations are enqueued panel by panel, alternating, and the       \
-   * inverse of a factor's leading block starts on stream2 as soon as its factorisation has passed     \
-   * it; stream0 and stream1 wait for stream2 before their normalisations.  Results equal two          \
+   * the first parts of the triangular inverses beside the factorisations (three distinct streams of  \
+   * one device).  Two fp32 matrices of one size share every Cholesky launch; other pairs are         \
+   * enqueued panel by panel, alternating.  The inverse of a factor's leading block starts as soon as \
+   * its factorisation has passed it, and the normalisations wait for it.  Results equal two          \
    * gptq2d_ldl_of_inverse calls bit for bit. */                                                     \
   int gptq2d_ldl_of_inverse_pair_##SUF(const T* m0, T* out0, T* work0, int* info0, int64_t k0, int64_t size0,      \
                                        const T* m1, T* out1, T* work1, int* info1, int64_t k1, int64_t size1,      \
