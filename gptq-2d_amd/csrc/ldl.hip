@@ -235,19 +235,27 @@ __device__ __forceinline__ void solve_chunk16(float* __restrict__ rs, const floa
   constexpr int CP = 65;
   const int q = tid & 3, rr = tid >> 2;
   const int lane = tid & 63, li = lane & 31, hh = lane >> 5, wy = tid >> 7, wx = (tid >> 6) & 1;
-#pragma unroll
-  for (int b = 0; b < 4; ++b) {
+  // block b's coefficients, read one block ahead (they do not depend on the chunk)
+  float cf[2][4][16], ri[2][16];
+  auto coefs = [&](int b, int slot) {
     const int c0 = 16 * b;
-    float x[4], cf[4][16], ri[16];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) x[j] = rs[rr * CP + c0 + 4 * j + q];
-#pragma unroll
-    for (int t = 0; t < 16; ++t) ri[t] = rinv[c0 + t];
+    for (int t = 0; t < 16; ++t) ri[slot][t] = rinv[c0 + t];
 #pragma unroll
     for (int j = 0; j < 4; ++j)
 #pragma unroll
-      for (int t = 0; t < 4 * j + 4; ++t) cf[j][t] = 4 * j + q > t ? a[(c0 + 4 * j + q) * CP + c0 + t] : 0.f;
-    block16_steps(x, cf, ri, q, std::make_integer_sequence<int, 16>{});
+      for (int t = 0; t < 4 * j + 4; ++t)
+        cf[slot][j][t] = 4 * j + q > t ? a[(c0 + 4 * j + q) * CP + c0 + t] : 0.f;
+  };
+  coefs(0, 0);
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    const int c0 = 16 * b;
+    float x[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) x[j] = rs[rr * CP + c0 + 4 * j + q];
+    if (b < 3) coefs(b + 1, (b + 1) & 1);
+    block16_steps(x, cf[b & 1], ri[b & 1], q, std::make_integer_sequence<int, 16>{});
 #pragma unroll
     for (int j = 0; j < 4; ++j) rs[rr * CP + c0 + 4 * j + q] = x[j];
     __syncthreads();
@@ -376,7 +384,8 @@ __device__ __forceinline__ void potrf_panel(PotrfLds<T, PB>& sm, T* __restrict__
         T sd, inv;
         pivot(d, sd, inv);
         if (tid == c0 + c) myinv = inv;
-        x[c] = tid == c0 + c ? sd : x[c] * inv;
+        // fp32: the pivot lane's x[c] is d, and d * inv is sd bit for bit (pivot), so no select
+        x[c] = (sizeof(T) == 4 || tid != c0 + c) ? x[c] * inv : sd;
 #pragma unroll
         for (int c2 = c + 1; c2 < CB; ++c2) x[c2] -= x[c] * bcast(x[c], c0 + c2);
       }
