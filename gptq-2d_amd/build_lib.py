@@ -33,8 +33,8 @@ COMMON_FLAGS = [
     f"-I{CSRC}",
 ]
 
-# Libraries linked in: rocBLAS's fp32 GEMM serves the dense products of the triangular inverse.
-LINK_LIBS = ["-L/opt/rocm/lib", "-lrocblas"]
+# No libraries beyond the HIP runtime hipcc links by itself.
+LINK_LIBS: list[str] = []
 
 # Per-file extra flags.  The trellis search must not contract a*b+c into fma: its costs are
 # compared for exact ties and must equal the reference's unfused sums.

@@ -40,7 +40,6 @@
 #include "linalg.h"
 #include "lds_dma.h"
 
-#include <rocblas/rocblas.h>
 
 #include <array>
 #include <type_traits>
@@ -101,11 +100,20 @@ __device__ __forceinline__ void wave_trtri(const T (&a)[NB], T (&x)[NB], int lan
   for (int c = 0; c < NB; ++c) x[c] = c <= lane ? ((c == lane ? T(1) : T(0)) - acc[c]) * inv : T(0);
 }
 
-// dst = src (rev = 0) or dst = the reversal of the flat src (rev = 1), which is J M J for a matrix.
+// dst = src (rev = 0) or dst = the reversal of the flat src (rev = 1), which is J M J for a matrix;
+// info[0..n_info) = 0 (the pivot report of the factorisation that follows on the same stream).
 template <typename T>
-__global__ void copy_kernel(T* __restrict__ dst, const T* __restrict__ src, int64_t count, int rev) {
+__global__ void copy_kernel(T* __restrict__ dst, const T* __restrict__ src, int64_t count, int rev,
+                            int* __restrict__ info, int n_info) {
+  if (blockIdx.x == 0 && (int)threadIdx.x < n_info) info[threadIdx.x] = 0;
   for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < count; t += (int64_t)gridDim.x * blockDim.x)
     dst[t] = src[rev ? count - 1 - t : t];
+}
+
+// info[0..n) = 0 where no copy precedes the factorisation (empty matrices).
+__global__ void zero_info_kernel(int* __restrict__ info, int64_t n) {
+  for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < n; t += (int64_t)gridDim.x * blockDim.x)
+    info[t] = 0;
 }
 
 // Value of lane (lane & ~3) | O for every lane of each quad (DPP quad_perm, no LDS).
@@ -1041,65 +1049,51 @@ __global__ __launch_bounds__(256) void zero_upper_kernel(T* __restrict__ w, int6
     for (int64_t j = i + 1 + threadIdx.x; j < n; j += 256) w[i * ld + j] = T(0);
 }
 
-// rocBLAS handle of the current device for this host thread, created on first use and kept until
-// the process ends.
-rocblas_handle blas_handle() {
-  thread_local std::unordered_map<int, rocblas_handle> handles;
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return nullptr;
-  const auto it = handles.find(dev);
-  if (it != handles.end()) return it->second;
-  rocblas_handle h = nullptr;
-  if (rocblas_create_handle(&h) != rocblas_status_success) return nullptr;
-  // no atomics (rocBLAS's default, set explicitly): split-sum GEMMs with atomic accumulation would
-  // make the last bits of the result change from run to run
-  if (rocblas_set_atomics_mode(h, rocblas_atomics_not_allowed) != rocblas_status_success) {
-    rocblas_destroy_handle(h);
-    return nullptr;
-  }
-  handles.emplace(dev, h);
-  return h;
-}
-
-// Row-major, strided-batched D = alpha A B + beta D (A: M x K, B: K x N) on rocBLAS's fp32 GEMM,
-// as the column-major product D^T = B^T A^T; `ws` (ws_bytes) is the GEMM's workspace, so that
-// rocBLAS allocates nothing.
-int blas_gemm_rm(int64_t M, int64_t N, int64_t K, int64_t batch, const float* A, int64_t lda, int64_t sa,
-                 const float* B, int64_t ldb, int64_t sb, float* D, int64_t ldd, int64_t sd, float alpha, float beta,
-                 void* ws, size_t ws_bytes, hipStream_t stream) {
-  rocblas_handle h = blas_handle();
-  if (!h || rocblas_set_stream(h, stream) != rocblas_status_success ||
-      rocblas_set_workspace(h, ws, ws_bytes) != rocblas_status_success)
-    return GPTQ2D_EUNSUPPORTED;
-  const rocblas_status st = rocblas_sgemm_strided_batched(
-      h, rocblas_operation_none, rocblas_operation_none, (rocblas_int)N, (rocblas_int)M, (rocblas_int)K, &alpha, B,
-      (rocblas_int)ldb, sb, A, (rocblas_int)lda, sa, &beta, D, (rocblas_int)ldd, sd, (rocblas_int)batch);
-  return st == rocblas_status_success ? 0 : GPTQ2D_EUNSUPPORTED;
-}
-
-// A level product of the triangular inverse: the MFMA kernel that skips the zero triangle of the
-// inverted block (tri = 1: B lower, 2: A lower), or rocBLAS's dense GEMM where that kernel's layout
-// conditions do not hold (rows not on 16-byte boundaries).
+// A level product of the triangular inverse, D = alpha A B (tri = 1: B lower, 2: A lower): the MFMA
+// kernel that skips the zero triangle of the inverted block, or, where that kernel's layout
+// conditions do not hold (rows not on 16-byte boundaries, operands of 2^29 elements or more), the
+// library's general strided GEMM with the same triangular structure.
 int level_gemm(int64_t M, int64_t N, int64_t K, int64_t batch, const float* A, int64_t lda, int64_t sa,
                const float* B, int64_t ldb, int64_t sb, float* D, int64_t ldd, int64_t sd, float alpha, int tri,
-               void* ws, size_t ws_bytes, hipStream_t stream) {
+               hipStream_t stream) {
   TriGemm g{M, N, K, batch, A, lda, sa, B, ldb, sb, D, ldd, sd, alpha, tri};
   const int rc = gptq2d_tri_gemm_f32(g, stream);
   if (rc != GPTQ2D_EUNSUPPORTED) return rc;
-  return blas_gemm_rm(M, N, K, batch, A, lda, sa, B, ldb, sb, D, ldd, sd, alpha, 0.f, ws, ws_bytes, stream);
+  GemmProblem<float> h{};
+  h.M = M;
+  h.N = N;
+  h.K = K;
+  h.batch = batch;
+  h.A = A;
+  h.a_rs = lda;
+  h.a_cs = 1;
+  h.a_bs = sa;
+  h.B = B;
+  h.b_rs = ldb;
+  h.b_cs = 1;
+  h.b_bs = sb;
+  h.D = D;
+  h.d_rs = ldd;
+  h.d_cs = 1;
+  h.d_bs = sd;
+  h.alpha = alpha;
+  h.beta = 0.f;
+  h.a_tri = tri == 2 ? TRI_LOWER : TRI_NONE;
+  h.b_tri = tri == 1 ? TRI_LOWER : TRI_NONE;
+  return gptq2d_gemm<float>(h, stream);
 }
 
 // In-place inverse of the lower triangular n x n diagonal block at w (row stride ld): leaves, then
-// the levels.  tmp: >= n*n/4 + n elements for the levels' products.  blas (fp32): the levels on
-// rocBLAS with workspace ws; the block's strict upper triangle is zeroed first (the dense GEMMs
-// read it as the triangles' padding).
+// the levels.  tmp: >= n*n/4 + n elements for the levels' products.  tri (fp32): the levels on
+// level_gemm; the block's strict upper triangle is zeroed first (the MFMA kernel reads it as the
+// padding of the triangles' boundary k-tiles).
 template <typename T>
-int trtri_block(T* w, int64_t ld, int64_t n, T* tmp, bool blas, void* ws, size_t ws_bytes, hipStream_t stream) {
+int trtri_block(T* w, int64_t ld, int64_t n, T* tmp, bool tri, hipStream_t stream) {
   constexpr int NB = LdlBlock<T>::NB;
   int rc;
   hipLaunchKernelGGL((trtri_leaf_kernel<T, NB>), dim3((unsigned)cdiv(n, NB)), dim3(64), 0, stream, w, ld, n);
   if ((rc = (int)hipGetLastError())) return rc;
-  if (blas) {
+  if (tri) {
     hipLaunchKernelGGL(zero_upper_kernel<T>, dim3((unsigned)(n < 8192 ? n : 8192)), dim3(256), 0, stream, w, ld, n);
     if ((rc = (int)hipGetLastError())) return rc;
   }
@@ -1114,13 +1108,13 @@ int trtri_block(T* w, int64_t ld, int64_t n, T* tmp, bool blas, void* ws, size_t
       const int64_t s2 = part == 0 ? s : tail;
       const int64_t bs = 2 * s * ld + 2 * s;
       if constexpr (sizeof(T) == 4) {
-        if (blas) {
+        if (tri) {
           // T = B A^{-1}, then B <- -D^{-1} T
           if ((rc = level_gemm(s2, s, s, pairs, w + (r0 + s) * ld + r0, ld, bs, w + r0 * ld + r0, ld, bs, tmp, s,
-                               s2 * s, 1.f, 1, ws, ws_bytes, stream)))
+                               s2 * s, 1.f, 1, stream)))
             return rc;
           if ((rc = level_gemm(s2, s, s2, pairs, w + (r0 + s) * ld + (r0 + s), ld, bs, tmp, s, s2 * s,
-                               w + (r0 + s) * ld + r0, ld, bs, -1.f, 2, ws, ws_bytes, stream)))
+                               w + (r0 + s) * ld + r0, ld, bs, -1.f, 2, stream)))
             return rc;
           continue;
         }
@@ -1175,7 +1169,7 @@ int trtri_block(T* w, int64_t ld, int64_t n, T* tmp, bool blas, void* ws, size_t
 }
 
 // Split point of the triangular inverse of a k x k factor: s = NB 2^j, the largest below k, for
-// fp32 from k = 2048 (levels on rocBLAS); 0: no split.  With a split, the inverse of C = [A 0; B D]
+// fp32 from k = 2048 (levels on level_gemm); 0: no split.  With a split, the inverse of C = [A 0; B D]
 // (A: s x s) runs in three parts:
 //   1. A^{-1} in place and T = B A^{-1} -- these read only the Cholesky's columns < s, so they can
 //      run while the factorisation of the columns >= s goes on;
@@ -1196,13 +1190,11 @@ int64_t trtri_split(int64_t k) {
 }
 
 // Where the three parts keep their data in `out` (k x k elements, free until the normalisation; its
-// last PB x PB elements stage the Cholesky's diagonal blocks while part 1 runs): T (n2 x s, and
-// before it part 1's level products), part 2's level products, then one rocBLAS workspace for part
-// 1 and one for parts 2 and 3 -- disjoint, as parts 1 and 2 may run at the same time.
+// last 2 PB x PB elements stage the Cholesky's diagonal blocks while part 1 runs): T (n2 x s, and
+// before it part 1's level products), then part 2's level products -- disjoint, as parts 1 and 2
+// may run at the same time.  s >= k / 2 >= n2, so n2 s + n2^2 / 4 + n2 stays below k^2 - 2 PB^2.
 struct TrtriLayout {
   int64_t s, n2, t_off, tmp2_off;
-  void *ws1, *ws2;
-  size_t ws_bytes;
 };
 
 template <typename T>
@@ -1213,33 +1205,14 @@ TrtriLayout trtri_layout(T* out, int64_t k, int64_t s) {
   L.t_off = 0;
   const int64_t t_end = L.n2 * s > s * s / 4 + s ? L.n2 * s : s * s / 4 + s;
   L.tmp2_off = t_end;
-  const int64_t tmp2_end = L.tmp2_off + L.n2 * L.n2 / 4 + L.n2;
-  const uintptr_t lo = ((uintptr_t)(out + tmp2_end) + 255) & ~(uintptr_t)255;
-  const uintptr_t hi = (uintptr_t)(out + stage_offset<T>(k)) & ~(uintptr_t)255;
-  size_t half = hi > lo ? ((hi - lo) / 2) & ~(size_t)255 : 0;
-  if (half > ((size_t)64 << 20)) half = (size_t)64 << 20;
-  L.ws1 = (void*)lo;
-  L.ws2 = (void*)(lo + half);
-  L.ws_bytes = half;
   return L;
 }
 
-// In-place inverse of the lower triangular W (k x k) in one sequence; tmp: a k x k buffer (its
-// first k*k/4 + k elements hold the levels' products, for fp32 the rest serves as GEMM workspace).
+// In-place inverse of the lower triangular W (k x k) in one sequence; tmp: a buffer of >= k*k/4 + k
+// elements for the levels' products.  fp32 from k = 512: the levels on level_gemm.
 template <typename T>
 int trtri_inplace(T* w, int64_t k, T* tmp, hipStream_t stream) {
-  void* ws = nullptr;
-  size_t ws_bytes = 0;
-  bool blas = false;
-  if constexpr (sizeof(T) == 4) {
-    const uintptr_t lo = ((uintptr_t)(tmp + k * k / 4 + k) + 255) & ~(uintptr_t)255, hi = (uintptr_t)(tmp + k * k);
-    blas = k >= 512 && hi > lo;
-    if (blas) {
-      ws = (void*)lo;
-      ws_bytes = hi - lo < ((size_t)64 << 20) ? hi - lo : ((size_t)64 << 20);
-    }
-  }
-  return trtri_block<T>(w, k, k, tmp, blas, ws, ws_bytes, stream);
+  return trtri_block<T>(w, k, k, tmp, sizeof(T) == 4 && k >= 512, stream);
 }
 
 template <typename T>
@@ -1259,18 +1232,16 @@ int trtri_part(T* out, T* w, int64_t k, int64_t size, int phase, hipStream_t str
   }
   if constexpr (sizeof(T) == 4) {
     const TrtriLayout L = trtri_layout<T>(out, k, s);
-    if (L.ws_bytes == 0) return GPTQ2D_EUNSUPPORTED;
     if (phase == 1) {
-      if ((rc = trtri_block<T>(w, k, s, out + L.t_off, true, L.ws1, L.ws_bytes, stream))) return rc;
+      if ((rc = trtri_block<T>(w, k, s, out + L.t_off, true, stream))) return rc;
       // T = B A^{-1}: (n2 x s) = (n2 x s) (s x s)
-      return level_gemm(L.n2, s, s, 1, w + s * k, k, 0, w, k, 0, out + L.t_off, s, 0, 1.f, 1, L.ws1, L.ws_bytes,
-                        stream);
+      return level_gemm(L.n2, s, s, 1, w + s * k, k, 0, w, k, 0, out + L.t_off, s, 0, 1.f, 1, stream);
     }
-    if (phase == 2) return trtri_block<T>(w + s * k + s, k, L.n2, out + L.tmp2_off, true, L.ws2, L.ws_bytes, stream);
+    if (phase == 2) return trtri_block<T>(w + s * k + s, k, L.n2, out + L.tmp2_off, true, stream);
     if (phase == 3) {
       // B <- -D^{-1} T: (n2 x s) = (n2 x n2) (n2 x s)
       if ((rc = level_gemm(L.n2, s, L.n2, 1, w + s * k + s, k, 0, out + L.t_off, s, 0, w + s * k, k, 0, -1.f, 2,
-                           L.ws2, L.ws_bytes, stream)))
+                           stream)))
         return rc;
       return normalize<T>(out, w, k, size, (k - 1) * k + (k - 1), -1, -k, stream);
     }
@@ -1306,12 +1277,15 @@ int ldl_of_inverse_part(const T* m, T* out, T* work, int* info, int64_t k, int64
   if (col_begin < 0 || (col_begin % PB && col_begin != k) || (col_end >= 0 && col_end < col_begin) ||
       (col_end >= 0 && col_end % PB && col_end < k))
     return GPTQ2D_EINVAL;
-  if (k == 0) return 0;
+  if (k == 0) {
+    if (col_begin == 0) hipLaunchKernelGGL(zero_info_kernel, dim3(1), dim3(64), 0, stream, info, (int64_t)1);
+    return (int)hipGetLastError();
+  }
   int rc;
   const int64_t kk = k * k;
   if (col_begin == 0) {
     const int64_t blocks = cdiv(kk, 256) < 8192 ? cdiv(kk, 256) : 8192;
-    hipLaunchKernelGGL(copy_kernel<T>, dim3((unsigned)blocks), dim3(256), 0, stream, work, m, kk, 1);
+    hipLaunchKernelGGL(copy_kernel<T>, dim3((unsigned)blocks), dim3(256), 0, stream, work, m, kk, 1, info, 1);
     if ((rc = (int)hipGetLastError())) return rc;
   }
   if (col_begin < k &&
@@ -1366,11 +1340,15 @@ int ldl_of_inverse_pair(const T* const* m, T* const* out, T* const* work, int* c
   const bool twinned = k[0] == k[1] && k[0] > 0 && twin.twin(work[1], info[1], out[1] + stage_offset<T>(k[1]));
   for (int f = 0; f < 2; ++f) {
     split[f] = k[f] > 0 ? trtri_split<T>(k[f]) : 0;
-    if (k[f] == 0) continue;
+    if (k[f] == 0) {
+      hipLaunchKernelGGL(zero_info_kernel, dim3(1), dim3(64), 0, stream[f], info[f], (int64_t)1);
+      if ((rc = (int)hipGetLastError())) return rc;
+      continue;
+    }
     const int64_t kk = k[f] * k[f];
     const int64_t blocks = cdiv(kk, 256) < 8192 ? cdiv(kk, 256) : 8192;
     hipLaunchKernelGGL(copy_kernel<T>, dim3((unsigned)blocks), dim3(256), 0, stream[twinned ? 0 : f], work[f], m[f],
-                       kk, 1);
+                       kk, 1, info[f], 1);
     if ((rc = (int)hipGetLastError())) return rc;
   }
   if (twinned) {
@@ -1379,10 +1357,9 @@ int ldl_of_inverse_pair(const T* const* m, T* const* out, T* const* work, int* c
     // and 3 of factor f on stream[f] after the chain (an event for stream[1]), part 3 of factor 0
     // after its part 1 (an event on stream[2])
     bool lead = split[0] == 0;
-    const int64_t lead_col = getenv("GPTQ2D_LEAD") ? split[0] + atoll(getenv("GPTQ2D_LEAD")) : split[0];  // EXPERIMENT
     while (!twin.done || !lead) {
       if ((rc = twin.step())) return rc;
-      if (!lead && (twin.done || twin.j0 >= lead_col)) {
+      if (!lead && (twin.done || twin.j0 >= split[0])) {
         if (hipEventRecord(ev[0], stream[0]) != hipSuccess || hipStreamWaitEvent(stream[2], ev[0], 0) != hipSuccess ||
             hipStreamWaitEvent(stream[1], ev[0], 0) != hipSuccess)
           return GPTQ2D_EUNSUPPORTED;
@@ -1434,7 +1411,12 @@ int ldl_impl(bool inverse, const T* m, T* out, T* work, int* info, int64_t batch
              hipStream_t stream) {
   if (batch < 0 || k < 0 || size <= 0 || (k > 0 && k % size)) return GPTQ2D_EINVAL;
   if (size > 1 && size > LdlBlock<T>::NB) return GPTQ2D_EUNSUPPORTED;
-  if (batch == 0 || k == 0) return 0;
+  if (batch == 0) return 0;
+  if (k == 0) {
+    hipLaunchKernelGGL(zero_info_kernel, dim3((unsigned)(cdiv(batch, 256) < 1024 ? cdiv(batch, 256) : 1024)), dim3(256),
+                       0, stream, info, batch);
+    return (int)hipGetLastError();
+  }
   int rc;
   const int64_t kk = k * k;
   for (int64_t b = 0; b < batch; ++b) {
@@ -1443,7 +1425,8 @@ int ldl_impl(bool inverse, const T* m, T* out, T* work, int* info, int64_t batch
     T* wb = work + b * kk;
     int* ib = info + b;
     const int64_t blocks = cdiv(kk, 256) < 8192 ? cdiv(kk, 256) : 8192;
-    hipLaunchKernelGGL(copy_kernel<T>, dim3((unsigned)blocks), dim3(256), 0, stream, wb, mb, kk, inverse ? 1 : 0);
+    hipLaunchKernelGGL(copy_kernel<T>, dim3((unsigned)blocks), dim3(256), 0, stream, wb, mb, kk, inverse ? 1 : 0, ib,
+                       1);
     if ((rc = (int)hipGetLastError())) return rc;
     // ob is free until the inverse / normalisation: its last elements stage the factored diagonal
     // blocks

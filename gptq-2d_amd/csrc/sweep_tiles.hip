@@ -675,7 +675,11 @@ int sweep_fused(T* y, T* c, T* e, const T* l, const T* u, int64_t m, int64_t n, 
   if (B == 0) return 0;
   const int64_t mt = cdiv(m, TR), nt = cdiv(n, TR), stages = mt + nt - 1;
   if (stage_end < 0 || stage_end > stages) stage_end = stages;
-  if (stage_begin < 0 || stage_begin > stage_end || stage_begin % outer_tiles) return GPTQ2D_EINVAL;
+  // a call covers whole outer blocks: [stage_begin, stage_end) starts on an outer block's first stage and
+  // ends after one's last (or at the end of the sweep), so that consecutive calls resume exactly
+  if (stage_begin < 0 || stage_begin > stage_end || stage_begin % outer_tiles ||
+      (stage_end % outer_tiles && stage_end != stages))
+    return GPTQ2D_EINVAL;
   int rc;
   if (stage_begin == 0 && (rc = gptq2d_fill<T>(c, T(0), B * m * n, stream))) return rc;
   // 128-bit operand loads of the MFMA pull: rows, matrices and pointers 16-byte aligned

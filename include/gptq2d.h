@@ -38,7 +38,9 @@ extern "C" {
    * zero point qb (quantizer_int.py:63-83, 161-244); 2: prescribed values qa (teacher forcing; no     \
    * reference counterpart).  ypre (optional, [B,m,n]) receives Y of every entry just before it is    \
    * rounded.  c, e: [B,m,n] scratch.  Stages of tiles [stage_begin, stage_end) (-1: to the end),     \
-   * outer_tiles tile stages per outer block.  y is updated in place. */                               \
+   * outer_tiles tile stages per outer block; both ends on outer-block boundaries (or stage_end at   \
+   * the end of the sweep), else GPTQ2D_EINVAL; a later call resumes from the same y, c, e.  y is    \
+   * updated in place. */                                                                              \
   int gptq2d_sweep_fused_##SUF(T* y, T* c, T* e, const T* l, const T* u, int64_t m, int64_t n, int32_t bnd,         \
                                const int64_t* bshape, const int64_t* l_stride, const int64_t* u_stride,             \
                                int32_t qkind, const T* qa, const int64_t* qa_stride, const T* qb,                   \
@@ -138,7 +140,26 @@ extern "C" {
   int gptq2d_gemm_##SUF(int64_t M, int64_t N, int64_t K, int64_t batch, const T* A, int64_t a_rs, int64_t a_cs,     \
                         int64_t a_bs, const T* B, int64_t b_rs, int64_t b_cs, int64_t b_bs, T* D, int64_t d_rs,      \
                         int64_t d_cs, int64_t d_bs, double alpha, double beta, int32_t a_tri, int32_t b_tri,        \
-                        int32_t d_tri, void* stream);
+                        int32_t d_tri, void* stream);                                                               \
+                                                                                                                      \
+  /* Trellis (Viterbi) quantizer of `rows` contiguous sequences x[rows, steps*V] over the code table   \
+   * table[2^L, V] (row s = the values of state s): the state path of least squared distance whose    \
+   * consecutive states overlap in L - K*V bits (next = ((s << K*V) | h) mod 2^L), first-index ties,   \
+   * with tail_biting != 0 the path circular (the reference's two-pass search on x rolled by half).    \
+   * Replaces _viterbi_step_kernel / _viterbi_final_kernel / _viterbi_backtrack_kernel and their       \
+   * driver _trellis_quantize_triton (quantizer_trellis.py:146-341) in one launch; the same search as   \
+   * _viterbi / _trellis_quantize_torch (quantizer_trellis.py:82-143).  hist: caller-owned workspace of \
+   * gptq2d_viterbi_workspace(rows, steps, L, K, V) elements (T), overwritten.  scale (optional,       \
+   * [rows]): out = table values * scale.  out (optional, [rows, steps*V]) and states (optional,      \
+   * [rows, steps], int64) receive the result.  1 <= L <= 24, V in {1, 2}, K*V <= min(L, 8). */      \
+  int gptq2d_viterbi_##SUF(const T* x, const T* table, T* hist, const T* scale, T* out, int64_t* states,            \
+                           int64_t rows, int64_t steps, int32_t L, int32_t K, int32_t V, int32_t tail_biting,      \
+                           void* stream);
+
+/* Elements of the history workspace gptq2d_viterbi_* needs for `rows` sequences of `steps` steps (-1 if
+ * the arguments are invalid).  Part of the trellis quantizer above (quantizer_trellis.py:146-341 keeps its
+ * step minima in a torch-allocated [steps, rows, 2^L] buffer). */
+int64_t gptq2d_viterbi_workspace(int64_t rows, int64_t steps, int32_t L, int32_t K, int32_t V);
 
 GPTQ2D_DECLARE(float, f32)
 GPTQ2D_DECLARE(double, f64)

@@ -9,8 +9,12 @@ other functions only need to be exact in fp64.
 
 Pinned by: tests/test_oracle_algorithms.py (every sweep equals Algorithm 1 on
 vec(X) bitwise in fp64 on the reference's test shapes, with a
-coordinate-dependent codebook) and tests/test_oracle_golden.py (fp32 codes of
-``gptq_2d_torch`` at 512x512 against vectors written from the reference).
+coordinate-dependent codebook), tests/test_oracle_golden.py (fp32 codes of
+``gptq_2d_torch`` at 512x512 against vectors written from the reference) and
+tests/test_oracle_sweep_state.py (``TorchSweepState`` run stage by stage
+against the same golden codes and against Algorithm 1 with NaN-poisoned
+triangles; ``stage_work`` against a brute-force count of the entries the
+stage's ``addcmul_`` calls update).
 """
 
 from __future__ import annotations
@@ -82,42 +86,18 @@ def _round(y_flat, selection, *, out):
     torch.round(sel, out=out)
 
 
-@torch.no_grad()
-def gptq_2d_torch(x, l, u, *, quantizer: Callable = _round, inplace=False, quantizer_inputs=()):
-    """Algorithm 3 with three ``addcmul_`` per stage, same operation order as gptq_2d.py:1197-1236."""
-    y, m, n, batch = _output(x, l, u, inplace)
-    if y.numel() == 0:
-        return y
-    B = batch.numel()
-    c = torch.zeros_like(y)
-    yf, cf = y.flatten(-2), c.flatten(-2)
-    lf = unit_triangular(l, upper=False).flip(-1)
-    uf = unit_triangular(u, upper=True).flip(-2)
-    zbuf = y.new_empty(B * min(m, n))
-    for s in range(m + n - 1):
-        isl, jsl, asl = stage_geometry(m, n, s)
-        ysel, z = _call_quantizer(zbuf, yf, asl, quantizer, quantizer_inputs)
-        e = z - ysel
-        lcols = lf[..., isl.start:, m - isl.stop:m - isl.start]
-        erow = e.flip(-1)[..., None, :]
-        c[..., isl.start:, jsl].addcmul_(lcols, erow)
-        y[..., isl.start:, jsl].addcmul_(lcols, erow)
-        urows = uf[..., n - jsl.stop:n - jsl.start, jsl.start:]
-        y[..., isl, jsl.start:].addcmul_(cf[..., asl, None], urows)
-        yf[..., asl] = z
-    return y
-
-
 class TorchSweepState:
-    """The loop state of ``gptq_2d_torch`` for running chosen stages one at a time (CPU baseline timing).
+    """The loop of the reference's ``gptq_2d_torch`` (gptq_2d.py:1197-1236), one stage at a time.
 
-    ``run_stage(s)`` is exactly the body of the loop of gptq_2d.py:1217-1235 for stage s.  Its cost
-    depends only on the shapes, so timing a sample of stages on full-size tensors and weighting by
-    ``stage_work`` gives the time of the whole sweep.
+    ``run_stage(s)`` is the body of the loop of gptq_2d.py:1217-1235 for stage s; ``gptq_2d_torch``
+    below runs it over every stage, so this class is the only copy of that body.  The CPU baseline
+    times a sample of stages on full-size tensors and weights them by ``stage_work`` (a stage's
+    cost depends only on the shapes).
     """
 
-    def __init__(self, x, l, u, quantizer: Callable = _round, quantizer_inputs=()):
-        self.y, self.m, self.n, batch = _output(x, l, u, False)
+    def __init__(self, x, l, u, quantizer: Callable = _round, quantizer_inputs=(), inplace=False):
+        self.y, self.m, self.n, batch = _output(x, l, u, inplace)
+        self.stages = self.m + self.n - 1
         self.c = torch.zeros_like(self.y)
         self.yf, self.cf = self.y.flatten(-2), self.c.flatten(-2)
         self.lf = unit_triangular(l, upper=False).flip(-1)
@@ -138,6 +118,17 @@ class TorchSweepState:
         urows = self.uf[..., n - jsl.stop:n - jsl.start, jsl.start:]
         y[..., isl, jsl.start:].addcmul_(self.cf[..., asl, None], urows)
         self.yf[..., asl] = z
+
+
+@torch.no_grad()
+def gptq_2d_torch(x, l, u, *, quantizer: Callable = _round, inplace=False, quantizer_inputs=()):
+    """Algorithm 3 with three ``addcmul_`` per stage, same operation order as gptq_2d.py:1197-1236."""
+    st = TorchSweepState(x, l, u, quantizer=quantizer, quantizer_inputs=quantizer_inputs, inplace=inplace)
+    if st.y.numel() == 0:
+        return st.y
+    for s in range(st.stages):
+        st.run_stage(s)
+    return st.y
 
 
 def stage_work(m: int, n: int, s: int) -> int:
@@ -222,9 +213,3 @@ def direct_2d_super_entry(x, l, u, *, quantizer: Callable = None, super_entry_sh
         y[..., i0:, j0:] += lt[..., i0:, i0:isl.stop * p] @ right
         ysel.copy_(z)
     return y
-
-
-def objective(z: torch.Tensor, x: torch.Tensor, g: torch.Tensor, h: torch.Tensor) -> float:
-    """tr(R^T G R H) with R = Z - X, in fp64 (demo.ipynb cell 3, ``objective``)."""
-    r = (z - x).double()
-    return float(((g.double() @ r) * (r @ h.double())).sum())

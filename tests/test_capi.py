@@ -1,5 +1,6 @@
-"""The C ABI: include/gptq2d.h compiles as C and C++, and libgptq2d.so exports every symbol it declares
-(loaded with ctypes; no compute call, so this runs without a GPU)."""
+"""The C ABI: include/gptq2d.h compiles as C and C++, libgptq2d.so exports every symbol it declares, and
+every gptq2d_* symbol the library exports is declared (loaded with ctypes and read with nm; no compute
+call, so this runs without a GPU)."""
 
 import ctypes
 import pathlib
@@ -44,3 +45,21 @@ def test_library_exports_declared_symbols():
     lib = ctypes.CDLL(str(LIB))
     missing = [n for n in names if not hasattr(lib, n)]
     assert not missing, missing
+
+
+def exported_symbols():
+    nm = shutil.which("nm")
+    if nm is None:
+        pytest.skip("nm missing")
+    res = subprocess.run([nm, "-D", "--defined-only", str(LIB)], capture_output=True, text=True, check=True)
+    return sorted({line.split()[-1] for line in res.stdout.splitlines()
+                   if line.split() and line.split()[-1].startswith("gptq2d_")})
+
+
+def test_every_export_is_declared():
+    if not LIB.exists():
+        pytest.skip("libgptq2d.so is not built (run __graft_entry__.build())")
+    exported = exported_symbols()
+    assert len(exported) > 30
+    undeclared = sorted(set(exported) - set(declared_symbols()))
+    assert not undeclared, undeclared

@@ -1,11 +1,11 @@
 """Parity of the benchmark configurations on the GPU (the layer shapes and quantizers of C2-C5 and H).
 
-At full size the CPU oracle cannot run the whole sweep in a test, so the full-size tests use the
-oracle where it is cheap -- the first antidiagonals, which span the first outer block and the
-first outer flush (only the first rows of U and columns of L are touched there) -- and
-size-independent properties everywhere: valid codes, bitwise determinism, and an objective below
-round-to-nearest.  The reduced-size tests run the reference's whole algorithm in fp64, where the
-codes must be equal.
+Full-size layers (C2, C3, H) run in the benchmark's configuration (fp32 fused engine, 1024-antidiagonal
+outer blocks) and are checked against the CPU oracle run over the whole sweep, with the tolerances of the
+benchmark definition: free-running codes agree in >= 99.99% of entries, the objective tr(R^T A R B) within
+1e-4 relative, and, with every stage teacher-forced to the oracle's codes, the engine's own Y before
+rounding gives the oracle's code everywhere except at near-ties |frac - 0.5| < 1e-5 (code units).  The
+reduced-size tests run the reference's whole algorithm in fp64, where the codes must be equal.
 
 Factors here are Wishart-like as in the benchmark definition, F = G diag(i^-alpha) G^T / (4k) +
 1e-2 I, but G is drawn with torch's GPU generator (the numpy PCG64 draws of the benchmark's
@@ -13,6 +13,7 @@ generator take seconds at these sizes); both sides of every comparison use the s
 """
 
 import functools
+import time
 
 import pytest
 import torch
@@ -51,62 +52,84 @@ def _objective(z, x, a, b):
 
 # ------------------------------------------------------------------------------------------------ full size
 
-@pytest.mark.parametrize("name", ["C2", "C3", "H"])
+# outer block of the benchmark (bench.py OUTER_BLOCK): 32 tile stages
+BENCH_OUTER = 1024
+
+
+@pytest.mark.timeout(900)
+@pytest.mark.parametrize("name", ["C2", "H", "C3"])
 def test_full_size_layer(name):
-    """C2 (4096^2 INT4 asymmetric g128), C3 (14336 x 4096 INT3 per-row), H (8192^2 INT4 per-row), fp32 fused
-    engine.  Oracle check on the first 640 antidiagonals (first outer block, its flush into the next block,
-    and in-block pulls): with those stages teacher-forced to the oracle's codes, the engine's Y before
-    rounding agrees with the oracle's to 1e-4 code units and its own rounding reproduces the oracle's codes
-    except at near-ties |frac - 0.5| < 1e-5.  Whole layer: codes in range and on the grid, bitwise identical
-    on a second run, objective tr(R^T A R B) below round-to-nearest's."""
+    """C2 (4096^2 INT4 asymmetric g128), H (8192^2 INT4 per-row), C3 (14336 x 4096 INT3 per-row), fp32 fused
+    engine with the benchmark's outer blocks, against the CPU oracle over every stage (see the module
+    docstring for the tolerances).  Also: codes in range and on the grid, bitwise identical on a second run,
+    objective below round-to-nearest's."""
     cfg = instances.CONFIGS[name]
     m, n = cfg.m, cfg.n
-    print(f"{name}: {m}x{n} qmin={cfg.qmin} qmax={cfg.qmax}", flush=True)
+    print(f"{name}: {m}x{n} qmin={cfg.qmin} qmax={cfg.qmax} outer={BENCH_OUTER}", flush=True)
     x = instances.weights(m, n, cfg.seeds[0], cfg.outliers, cfg.bf16).float().to(DEV)
     a = _gpu_factor(m, cfg.alpha, 11)
     b = _gpu_factor(n, cfg.alpha, 12)
     lo, up = LDL.feedback_factors_of_grams(a.float(), b.float())
     scale, zp = instances.quantizer_inputs(cfg, x)
     q = functools.partial(QI.affine_quantizer_hip, qmin=cfg.qmin, qmax=cfg.qmax)
-    z = G.gptq_2d(x, lo, up, quantizer=q, quantizer_inputs=(scale, zp))
-    z2 = G.gptq_2d(x, lo, up, quantizer=q, quantizer_inputs=(scale, zp))
+    run = functools.partial(G.gptq_2d, x, lo, up, outer_block_size=BENCH_OUTER)
+    z = run(quantizer=q, quantizer_inputs=(scale, zp))
+    z2 = run(quantizer=q, quantizer_inputs=(scale, zp))
     torch.cuda.synchronize()
     assert z.equal(z2), "not deterministic"
     codes = torch.round(z / scale + zp)
     assert codes.min() >= cfg.qmin and codes.max() <= cfg.qmax
     assert torch.equal(z, (codes - zp) * scale), "values off the quantization grid"
     rtn = (torch.clamp(torch.round(x / scale + zp), cfg.qmin, cfg.qmax) - zp) * scale
-    ratio = _objective(z, x, a, b) / _objective(rtn, x, a, b)
+    obj = _objective(z, x, a, b)
+    ratio = obj / _objective(rtn, x, a, b)
     print(f"  objective / RTN = {ratio:.4f}", flush=True)
     assert ratio < 1.
 
-    # oracle on the first antidiagonals (CPU, fp32, the reference's own operation sequence)
-    stages = 640
+    # the CPU oracle over the whole sweep (fp32, the reference's own operation sequence), recording every
+    # entry's Y just before it is rounded
+    xc, sc, zc = x.cpu(), scale.cpu(), zp.cpu()
     pre_o = torch.full((m, n), float("nan"))
 
-    def spy(y_flat, sl, sc, zz, *, out):
+    def spy(y_flat, sl, s_, z_, *, out):
         pre_o.view(-1)[sl] = y_flat[sl]
-        OQ.affine_quantizer(y_flat, sl, sc, zz, out=out, qmin=cfg.qmin, qmax=cfg.qmax)
+        OQ.affine_quantizer(y_flat, sl, s_, z_, out=out, qmin=cfg.qmin, qmax=cfg.qmax)
 
-    st = S.TorchSweepState(x.cpu(), lo.cpu(), up.cpu(), quantizer=spy, quantizer_inputs=(scale.cpu(), zp.cpu()))
-    for s in range(stages):
+    st = S.TorchSweepState(xc, lo.cpu(), up.cpu(), quantizer=spy, quantizer_inputs=(sc, zc))
+    t0 = time.perf_counter()
+    for s in range(st.stages):
         st.run_stage(s)
-    early = (torch.arange(m)[:, None] + torch.arange(n)[None, :]) < stages
-    values = torch.where(early.to(DEV), st.y.to(DEV), z)
+        if s % 4096 == 4095:
+            print(f"  oracle: {s + 1} / {st.stages} stages, {time.perf_counter() - t0:.0f} s", flush=True)
+    assert not pre_o.isnan().any()
+    ref_codes = torch.round(st.y / sc + zc)
+
+    # free running
+    agree = float((codes.cpu() == ref_codes).double().mean())
+    obj_o = _objective(st.y.to(DEV), x, a, b)
+    rel = abs(obj - obj_o) / obj_o
+    zdiff = float((z.cpu() - st.y).double().norm() / st.y.double().norm())
+    print(f"  free running: code agreement {agree:.6%} ({int((codes.cpu() != ref_codes).sum())} of {m * n} differ),"
+          f" objective {obj:.8e} vs oracle {obj_o:.8e} (rel {rel:.2e}), |Z - Z_oracle| / |Z_oracle| {zdiff:.2e}",
+          flush=True)
+    assert agree >= 0.9999
+    assert rel <= 1e-4
+
+    # teacher forced: every stage takes the oracle's codes; the engine's own Y before rounding must round to
+    # the oracle's code except at near-ties
     pre_e = torch.full_like(x, float("nan"))
-    zf = G.gptq_2d(x, lo, up, quantizer=QI.teacher_forced_quantizer, quantizer_inputs=(values, pre_e))
-    assert zf.equal(values)
-    sc = scale.cpu()[early]
-    ye, yo = (pre_e.cpu()[early] / sc + zp.cpu()[early]), (pre_o[early] / sc + zp.cpu()[early])
-    assert not ye.isnan().any() and not yo.isnan().any()
-    dev = (ye - yo).abs()
+    zf = run(quantizer=QI.teacher_forced_quantizer, quantizer_inputs=(st.y.to(DEV), pre_e))
+    assert zf.equal(st.y.to(DEV))
+    ye = (pre_e / scale + zp).cpu()
+    yo = pre_o / sc + zc
+    assert not ye.isnan().any()
     own = ye.round().clamp(cfg.qmin, cfg.qmax)
-    ref = (st.y[early] / sc + zp.cpu()[early]).round()
-    mism = own != ref
+    mism = own != ref_codes
     frac = (ye - ye.floor() - .5).abs()
-    print(f"  first {stages} antidiagonals ({int(early.sum())} entries): max |dY| {dev.max():.2e} code units, "
-          f"own-rounding mismatches {int(mism.sum())}", flush=True)
-    assert dev.max() < 1e-4
+    dev = (ye - yo).abs()
+    print(f"  teacher forced: own-rounding mismatches {int(mism.sum())}, max |dY| {dev.max():.2e} code units "
+          f"(median {dev.median():.2e}), largest mismatch |frac - 0.5| "
+          f"{float(frac[mism].max()) if mism.any() else 0.:.2e}", flush=True)
     assert (frac[mism] < 1e-5).all()
 
 

@@ -275,3 +275,39 @@ def test_fused_fp32_quantizer_special_values(qmin, qmax, last_zp):
     assert torch.equal(got.isnan(), expected.isnan())
     ok = ~expected.isnan()
     assert torch.equal(got[ok], expected[ok])
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+def test_fused_resume_at_block_boundary(dtype):
+    """gptq2d_sweep_fused over [0, S) then [S, end) with S on an outer-block boundary equals one call over the
+    whole sweep bit for bit (the C scratch carries the state); an end inside an outer block is rejected."""
+    import _hip
+
+    print(f"fused resume {dtype}", flush=True)
+    m, n, outer_tiles = 200, 330, 2
+    g = torch.Generator().manual_seed(9)
+    x = (4. * torch.randn(m, n, generator=g, dtype=torch.float64)).to(DEV, dtype)
+    lo = S.unit_triangular(.3 / m ** .5 * torch.randn(m, m, generator=g, dtype=torch.float64), upper=False)
+    up = S.unit_triangular(.3 / n ** .5 * torch.randn(n, n, generator=g, dtype=torch.float64), upper=True)
+    lo, up = lo.to(DEV, dtype), up.to(DEV, dtype)
+    stages = -(-m // 32) + -(-n // 32) - 1
+    bshape, strides = _hip.i64_array([]), _hip.i64_array([])
+    st = _hip.stream(x.device)
+
+    def run(y, c, e, begin, end):
+        _hip.call("sweep_fused", dtype, _hip.ptr(y), _hip.ptr(c), _hip.ptr(e), _hip.ptr(lo), _hip.ptr(up), m, n, 0,
+                  bshape, strides, strides, 0, None, None, None, None, 0., 0., None, outer_tiles, begin, end, st)
+
+    whole = x.clone()
+    c, e = torch.empty_like(x), torch.empty_like(x)
+    run(whole, c, e, 0, -1)
+    split = x.clone()
+    c, e = torch.empty_like(x), torch.empty_like(x)
+    run(split, c, e, 0, 4)
+    run(split, c, e, 4, stages)
+    torch.cuda.synchronize()
+    assert split.equal(whole)
+    with pytest.raises(_hip.GPTQ2DError):
+        run(x.clone(), c, e, 0, 3)
+    with pytest.raises(_hip.GPTQ2DError):
+        run(x.clone(), c, e, 1, stages)

@@ -209,3 +209,35 @@ def test_headline_size_fp32():
     err = ((got.double() - ref).abs().max() / ref.abs().max()).item()
     print(f"8192 fp32 vs fp64: max rel err {err:.2e}", flush=True)
     assert err < 1e-3
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+@pytest.mark.parametrize("k", [0, 96, 640])
+def test_info_zeroed_by_library(dtype, k):
+    """The C ABI reports the pivot status in info itself: info pre-filled with garbage (a stale failure) reads 0
+    after a successful factorisation, on two calls in a row, through all three LDL entry points."""
+    print(f"info k={k} {dtype}", flush=True)
+    m = instances.wishart_factor(max(k, 1), .5, 3)[:k, :k].to(DEV, dtype).contiguous()
+    out, work = torch.empty_like(m), torch.empty_like(m)
+    st = _hip.stream(m.device)
+    for _ in range(2):
+        info = torch.full((1,), 12345, dtype=torch.int32, device=DEV)
+        _hip.call("ldl_of_inverse", dtype, _hip.ptr(m), _hip.ptr(out), _hip.ptr(work), _hip.ptr(info), 1, k, 1, st)
+        torch.cuda.synchronize()
+        assert int(info.item()) == 0
+        info.fill_(-7)
+        _hip.call("ldl_of_inverse_part", dtype, _hip.ptr(m), _hip.ptr(out), _hip.ptr(work), _hip.ptr(info), k, 1, 0,
+                  -1, 1, st)
+        torch.cuda.synchronize()
+        assert int(info.item()) == 0
+    m1 = m.clone()
+    out1, work1 = torch.empty_like(m), torch.empty_like(m)
+    infos = torch.full((2,), 99, dtype=torch.int32, device=DEV)
+    streams = [torch.cuda.Stream() for _ in range(3)]
+    for s in streams:
+        s.wait_stream(torch.cuda.current_stream())
+    _hip.call("ldl_of_inverse_pair", dtype, _hip.ptr(m), _hip.ptr(out), _hip.ptr(work), _hip.ptr(infos[0:1]), k, 1,
+              _hip.ptr(m1), _hip.ptr(out1), _hip.ptr(work1), _hip.ptr(infos[1:2]), k, 1,
+              *(ctypes.c_void_p(s.cuda_stream) for s in streams))
+    torch.cuda.synchronize()
+    assert infos.tolist() == [0, 0]
