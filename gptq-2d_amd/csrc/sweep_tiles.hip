@@ -20,6 +20,8 @@
 #include "common.h"
 #include "profile.h"
 
+#include <utility>
+
 template <typename T>
 int gptq2d_flush(T* y, T* c, const T* e, const T* l, const T* u, int64_t m, int64_t n, int64_t P, int64_t Q,
                  int64_t s0, int64_t s1, int64_t s_end, const BatchMap& lmap, const BatchMap& umap, int64_t B,
@@ -148,16 +150,6 @@ __global__ __launch_bounds__(NTHREADS) void sweep_tiles_kernel(T* __restrict__ y
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
-// Sum over the 8 lanes of each aligned group of 8 (all lanes receive it): xor 1 and xor 2 inside the
-// quad (quad_perm [1,0,3,2] and [2,3,0,1]), then the other quad of the group (row_half_mirror,
-// which maps lane i of each half-row to lane 7 - i).  VALU data movement only, no LDS.
-__device__ __forceinline__ float group8_sum(float v) {
-  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xf, 0xf, false));
-  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xf, 0xf, false));
-  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xf, 0xf, false));
-  return v;
-}
-
 // Quantizer of the fused sweeps, applied to one value.
 template <int KIND>
 __device__ __forceinline__ float quantize_entry(float yv, float sv, float zv, float qmin, float qmax) {
@@ -216,37 +208,42 @@ __device__ __forceinline__ void pull_chunks(floatx16& acc, const float* __restri
   }
 }
 
-// LDS row pitch of the tile arrays: 40 = 8 (mod 32) keeps the antidiagonal walks (32 r + t) and the
-// column walks (8 lanes x 8 rows) at most 2-way bank-conflicted; a pitch of 33 puts a whole
-// antidiagonal into one bank.
+// LDS row pitch of the tile's Y and E images: 40 = 8 (mod 32) keeps the column walks of the E reads
+// (a row step of 39 = -7 mod 32 banks between neighbouring columns) and the final row-wise stores free
+// of bank conflicts beyond 2-way.
 constexpr int SP = 40;
 
-// LDS image of one tile for the fp32 in-tile sweep.  L[I,I] and U[J,J] are stored with zero
-// padding so that the sweep reads them at any offset in [-TR, 2 TR) without masks:
+// LDS image of one tile for the fp32 in-tile sweep.  L[I,I] and U[J,J] are stored with zero padding so
+// that the sweep reads them at any offset in [-TR, 2 TR) without masks:
 // Lp[r][TR + k] = L[i0+r, i0+k] for 0 <= k < r (zero elsewhere), Up[TR + k][c] = U[j0+k, j0+c] for
-// k < c (zero elsewhere).  Ys, Cs, Ss, Zs: the tile's Y (feedback pulled in), C, quantizer inputs
-// on entry; Ys, Cs, Es the result.  Ed / Cr: errors (by column) and C (by row) of the entries
-// rounded on the current antidiagonal, double-buffered by its parity.
-constexpr int LPW = 3 * TR + 1;
-constexpr int UPW = TR + 1;
+// k < c (zero elsewhere).  Ys: the tile's Y with the pulled feedback (on entry), the result (at the end).
+// Cs[r][TR + c] and Es[TR + r][c]: the C and E images, padded by TR zero columns (C) and rows (E) on
+// each side: C holds C + pulled D on entry and each entry's final C from its rounding on; E holds
+// zeros on entry and each entry's error from its rounding on.  The sweep reads both at offsets that
+// leave the tile (times zero coefficients), so the padding must hold finite values.
+// Row pitches of the padded L, U and C images: with 103, 39 and 98 floats every per-step read of the
+// sweep (L[r, t - c], U[t - r, c], C[r, t - r] over a half-wave's 4 rows x 8 parts) falls on 32 distinct
+// banks; the natural pitches (97, 33, 97) put 4 rows on one bank in each of them.
+constexpr int LPW = 3 * TR + 7;
+constexpr int UPW = TR + 7;
+constexpr int CPW = 3 * TR + 2;
+constexpr int EROWS = 3 * TR;
 
 struct TileLds {
+  float Ys[TR][SP];  // first: the sweep's base pointers below reach up to 23 rows / columns before Lp and Up
   float Lp[TR][LPW];
   float Up[3 * TR][UPW];
-  float Ys[TR][SP];
-  float Cs[TR][SP];
-  float Es[TR][SP];
-  float Ss[TR][SP];
-  float Zs[TR][SP];
-  float Ed[2][TR];
-  float Cr[2][TR];
+  float Cs[TR][CPW];
+  float Es[EROWS][SP];
 };
 
 // Affine / round / forced quantizer of the in-tile sweep, given the precomputed correctly rounded
 // reciprocal rv = 1/sv and whether sv lies in [2^-60, 2^60] (affine only).  y / s is formed as
 // q0 = y rv, then one FMA correction with the exact remainder y - q0 s (Markstein's method): the
-// IEEE quotient whenever also |y| in [2^-60, 2^60] or y = 0 (then nothing over- or underflows);
-// `exact` says whether that holds, and otherwise quantize_entry_div (the division itself) gives the
+// IEEE quotient whenever also 2^-60 <= |y| < 2^61 (then no product or remainder over- or
+// underflows: |q0| lies in [2^-121, 2^121] and the remainder is a multiple of 2^-107).  `exact` says
+// whether that holds -- the biased exponent of y in [67, 187], one bit-field test (zero, denormal,
+// infinite and NaN y fail it) -- and otherwise quantize_entry_div (the division itself) gives the
 // value.  This keeps the division's ten dependent operations off the per-antidiagonal critical path.
 template <int KIND>
 __device__ __forceinline__ float quantize_entry_rcp(float yv, float sv, float zv, float rv, bool s_ok, float qmin,
@@ -258,11 +255,11 @@ __device__ __forceinline__ float quantize_entry_rcp(float yv, float sv, float zv
     const float q0 = yv * rv;
     const float rem = __builtin_fmaf(-q0, sv, yv);
     const float q = __builtin_fmaf(rem, rv, q0);
-    const float ay = __builtin_fabsf(yv);
     // s_ok also holds only when the zero point is not NaN and qmin <= qmax: then q is the IEEE
     // quotient, round(q + z) is not NaN, and the median of (x, qmin, qmax) is the clamp, in one
     // operation on the per-step critical path
-    exact = s_ok && ay <= 0x1p60f && (ay >= 0x1p-60f || yv == 0.f);
+    const unsigned ex = (__float_as_uint(yv) >> 23) & 0xffu;
+    exact = s_ok && ex - 67u <= 120u;
     const float code = __builtin_amdgcn_fmed3f(round_even(q + zv), qmin, qmax);
     return (code - zv) * sv;
   } else if constexpr (KIND == Q_FORCED) {
@@ -280,71 +277,137 @@ __device__ __forceinline__ float quantize_entry_div(float yv, float sv, float zv
   return (code - zv) * sv;
 }
 
-// The tile's 63 antidiagonals, in push form.  Thread (r, part) = (tid / 8, tid % 8) owns the four
-// entries (r, c) of its row with (c + r) % 8 == part; register k holds the one with
-// ((c + r) / 8) % 4 == k.  Entries of antidiagonal t have c + r = t, so the entry rounded at step t
-// is register (t / 8) % 4 of thread part t % 8 in every row: a compile-time register in the
-// unrolled loop.  A step: the rounding threads quantize (their entries' feedback is complete) and
-// publish the error (by column) and final C (by row) to LDS; one barrier; then every thread adds
-// the step's feedback to its entries' sums -- down: L[r, t-c] E[t-c, c], right: C[r, t-r] U[t-r, c].
-// An entry is rounded at y = (Y + down) + right, and its C becomes (C + down) + error.  The
-// zero-padded diagonal blocks make the terms vanish for entries already rounded and for sources
-// outside the tile.  Then Y, C and E of the tile go to global memory.  Expects the tile image
-// complete in LDS (a barrier after it was written).
+// Thread ownership of the in-tile sweep.  Thread (r, part) = (tid / 8, tid % 8) owns the four entries
+// (r, c) of its row with (c + r) % 8 == part; slot j holds the one whose antidiagonal t_e = r + c has
+// (t_e / 8) % 4 == j.  The entry rounded at step t is then slot (t / 8) % 4 of part t % 8 in every row: a
+// compile-time register in the unrolled loop over t.
+__device__ __forceinline__ void slot_columns(int r, int part, int (&cs)[4]) {
+  const int qlo = (r - part + 7) >> 3;  // smallest q with 8 q + part >= r
+#pragma unroll
+  for (int j = 0; j < 4; ++j) cs[j] = 8 * (qlo + ((j - qlo) & 3)) + part - r;  // in [0, TR)
+}
+
+// f(integral_constant<int, I>) for I = 0, 1, ..., in order: a loop whose index is a compile-time constant in
+// every iteration.
+template <typename F, int... I>
+__device__ __forceinline__ void static_for(F& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+
+// Quantizer inputs of the sweep's entries in its own layout (slot order), read from global memory at
+// the start of the kernel so that their latency overlaps the pull.
 template <int KIND>
-__device__ __forceinline__ void sweep_tile_push(TileLds& tl, float* __restrict__ y, float* __restrict__ c,
-                                                float* __restrict__ e, const QSpec<float>& qs, int64_t m, int64_t n,
-                                                int64_t i0, int64_t j0, int64_t mat) {
+struct SweepInputs {
+  float s[4], z[4];
+
+  __device__ __forceinline__ void load(const QSpec<float>& qs, int64_t b, int64_t m, int64_t n, int64_t i0,
+                                       int64_t j0) {
+    const int tid = threadIdx.x, r = tid >> 3, part = tid & 7;
+    int cs[4];
+    slot_columns(r, part, cs);
+    const int rows_in = m - i0 < TR ? (int)(m - i0) : TR, cols_in = n - j0 < TR ? (int)(n - j0) : TR;
+    const int64_t corner = i0 * n + j0;
+    const float* st = KIND != Q_ROUND ? qs.scale + qs.smap.offset(b) + corner : nullptr;
+    const float* zt = KIND == Q_AFFINE ? qs.zp + qs.zmap.offset(b) + corner : nullptr;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const bool in = r < rows_in && cs[j] < cols_in;
+      const int off = r * (int)n + cs[j];
+      s[j] = z[j] = 0.f;
+      if constexpr (KIND == Q_AFFINE) {
+        s[j] = in ? st[off] : 1.f;
+        z[j] = in ? zt[off] : 0.f;
+      } else if constexpr (KIND == Q_FORCED) {
+        s[j] = in ? st[off] : 0.f;
+      }
+    }
+  }
+};
+
+// The tile's 63 antidiagonals, in push form.  A step: the rounding lanes quantize (their entries'
+// feedback is complete) and write the error into the E image and the final C into the C image; one
+// workgroup barrier; then every lane reads the step's error in each of its columns (E[t - c, c]) and
+// the final C of its row (C[r, t - r]) and adds the step's feedback to its entries' sums -- down:
+// L[r, t-c] E[t-c, c], right: C[r, t-r] U[t-r, c].  An entry is rounded at y = (Y + down) + right,
+// and its C becomes (C + down) + error.  The zero-padded diagonal blocks make the terms vanish for
+// entries already rounded, for sources below the entry (not yet written in the images: their zeros or
+// values times zero) and for sources outside the tile.  Then Y, C and E of the tile go to global
+// memory.  Expects the tile image complete in LDS (a barrier after it was written).
+//
+// The step is bound by its chain (the quantizer's ~13 dependent operations, the LDS write, barrier
+// and read-back, ~150 clocks measured for the exchange alone) and by the LDS reads of four waves
+// (13 per lane); the image pitches keep every read free of bank conflicts.
+template <int KIND, bool YPRE>
+__device__ __forceinline__ void sweep_tile(TileLds& tl, const SweepInputs<KIND>& in, float* __restrict__ y,
+                                           float* __restrict__ c, float* __restrict__ e, const QSpec<float>& qs,
+                                           int64_t m, int64_t n, int64_t i0, int64_t j0, int64_t mat) {
   const int tid = threadIdx.x;
-  const int r = tid / PARTS, part = tid % PARTS;
+  const int r = tid >> 3, part = tid & 7;
   const int rows_in = m - i0 < TR ? (int)(m - i0) : TR;  // tile rows / columns inside the matrix
   const int cols_in = n - j0 < TR ? (int)(n - j0) : TR;
   const bool row_in = r < rows_in;
-  const int qlo = (r - part + 7) >> 3;  // smallest q with 8 q + part >= r
-  int ck[4];
+  int cs[4];
+  slot_columns(r, part, cs);
   // per entry: Y and C on entry, the in-tile down and right feedback sums D and F (kept apart from
   // Y, so that their rounding errors scale with the feedback, not with Y), the error E, the
-  // quantizer inputs S, Z and the reciprocal R of S
+  // quantizer inputs S, Z and the reciprocal R of S, and the step at which the entry is rounded (-1
+  // for entries outside the matrix)
   float Y[4], C[4], D[4], F[4], E[4], S[4], Z[4], R[4];
+  int tr[4];
   bool s_ok[4];
   const bool qmin_le_qmax = qs.qmin <= qs.qmax;
 #pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    ck[k] = 8 * (qlo + ((k - qlo) & 3)) + part - r;  // in [0, TR)
-    Y[k] = tl.Ys[r][ck[k]];
-    C[k] = tl.Cs[r][ck[k]];
-    D[k] = F[k] = E[k] = 0.f;
-    S[k] = Z[k] = R[k] = 0.f;
-    s_ok[k] = false;
+  for (int j = 0; j < 4; ++j) {
+    tr[j] = row_in && cs[j] < cols_in ? r + cs[j] : -1;
+    Y[j] = tl.Ys[r][cs[j]];
+    C[j] = tl.Cs[r][TR + cs[j]];
+    D[j] = F[j] = E[j] = 0.f;
+    S[j] = in.s[j];
+    Z[j] = in.z[j];
+    R[j] = 0.f;
+    s_ok[j] = false;
     if constexpr (KIND == Q_AFFINE) {
-      S[k] = tl.Ss[r][ck[k]];
-      Z[k] = tl.Zs[r][ck[k]];
-      R[k] = 1.f / S[k];
-      const float as = __builtin_fabsf(S[k]);
-      s_ok[k] = as >= 0x1p-60f && as <= 0x1p60f && Z[k] == Z[k] && qmin_le_qmax;
-    } else if constexpr (KIND == Q_FORCED) {
-      S[k] = tl.Ss[r][ck[k]];
+      R[j] = 1.f / S[j];
+      const float as = __builtin_fabsf(S[j]);
+      s_ok[j] = as >= 0x1p-60f && as <= 0x1p60f && Z[j] == Z[j] && qmin_le_qmax;
     }
   }
-  const bool has_ypre = qs.ypre != nullptr;
-  float* ypre_row = has_ypre ? qs.ypre + mat + (i0 + r) * n + j0 : nullptr;
+  float* ypre_row = YPRE ? qs.ypre + mat + (i0 + r) * n + j0 : nullptr;
   // clamp bounds pinned in registers (an empty asm makes them opaque): otherwise the compiler
   // re-reads them from the kernel arguments on every step
   float qmin = qs.qmin, qmax = qs.qmax;
   asm volatile("" : "+v"(qmin), "+v"(qmax));
-  // L and U coefficients of the next step, read a step ahead (they do not depend on the sweep), so
-  // that only the published errors and C are read between a barrier and the feedback update
-  float LV[4], UV[4];
+  // what a thread reads and writes at step t, as pointers plus t or t times the row pitch (immediate
+  // offsets): the C of its row's rounded entry C[r, t - r] (which the rounding lane writes), that
+  // lane's E[r, t - r], and per slot the source E[t - c, c] and the coefficients L[r, t - c], U[t - r, c]
+  float* const cp = &tl.Cs[r][TR] - r;
+  float* const ewp = &tl.Es[TR + r][0] - r;
+  const float* ep[4];
+  const float* lp[4];
+  const float* up[4];
 #pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    LV[k] = tl.Lp[r][TR - ck[k]];
-    UV[k] = tl.Up[TR - r][ck[k]];
+  for (int j = 0; j < 4; ++j) {
+    ep[j] = &tl.Es[TR][0] + (cs[j] - cs[j] * SP);
+    lp[j] = &tl.Lp[r][TR] - cs[j];
+    up[j] = &tl.Up[TR][0] + (cs[j] - r * UPW);
   }
+  constexpr int STEPS = 2 * TR - 1;
+  // L and U coefficients of step t in LV[t & 1], UV[t & 1], read a step ahead (they do not depend on
+  // the sweep), so that only the published errors and C are read between the barrier and the
+  // feedback update, and no register copies are needed in the unrolled loop
+  float LV[2][4], UV[2][4];
 #pragma unroll
-  for (int t = 0; t < 2 * TR - 1; ++t) {
-    const int ka = (t >> 3) & 3, buf = t & 1;
-    // every lane evaluates its step-t register; only the rounding lanes keep and publish it
-    const bool rnd = part == (t & 7) && row_in && t - r >= 0 && t - r < cols_in;
+  for (int j = 0; j < 4; ++j) {
+    LV[0][j] = lp[j][0];
+    UV[0][j] = up[j][0];
+  }
+  // one step at compile-time index t (the loop is unrolled by a fold over the steps: the register slot,
+  // the parity buffers and the LDS immediates are compile-time in every step)
+  auto step = [&](auto t_c) __attribute__((always_inline)) {
+    constexpr int t = decltype(t_c)::value;
+    constexpr int cur = t & 1, ka = (t >> 3) & 3;
+    // every lane evaluates its step's register; only the rounding lanes keep and publish it
+    const bool rnd = tr[ka] == t;
     const float yv = (Y[ka] + D[ka]) + F[ka];
     {
       bool exact;
@@ -355,8 +418,8 @@ __device__ __forceinline__ void sweep_tile_push(TileLds& tl, float* __restrict__
       if (rnd) {
         // published at once; a lane whose quotient needs the division writes again (same address:
         // the later write stands), behind a branch taken only when some lane of the wave needs it
-        tl.Ed[buf][t - r] = ev;
-        tl.Cr[buf][r] = cf;
+        ewp[t] = ev;
+        cp[t] = cf;
         if constexpr (KIND == Q_AFFINE) {
           if (__builtin_amdgcn_ballot_w64(!exact)) {
             asm volatile("");  // keeps the division behind the branch (no speculation into a select)
@@ -364,8 +427,8 @@ __device__ __forceinline__ void sweep_tile_push(TileLds& tl, float* __restrict__
               z = quantize_entry_div(yv, S[ka], Z[ka], qmin, qmax);
               ev = z - yv;
               cf = cd + ev;
-              tl.Ed[buf][t - r] = ev;
-              tl.Cr[buf][r] = cf;
+              ewp[t] = ev;
+              cp[t] = cf;
             }
           }
         }
@@ -374,45 +437,40 @@ __device__ __forceinline__ void sweep_tile_push(TileLds& tl, float* __restrict__
         C[ka] = cf;
       }
     }
-    __syncthreads();
-    if (t == 2 * TR - 2) {
-      if (has_ypre && rnd) ypre_row[t - r] = yv;
-      break;  // nothing left to receive feedback
+    if constexpr (t == STEPS - 1) {
+      if constexpr (YPRE) {
+        if (rnd) ypre_row[t - r] = yv;
+      }
+      return;  // nothing left to receive feedback
     }
-    const float cr = tl.Cr[buf][r];
+    __syncthreads();  // every wave's writes of this step before any wave's reads
+    const float cr = cp[t];
     float ev[4];
 #pragma unroll
-    for (int k = 0; k < 4; ++k) ev[k] = tl.Ed[buf][ck[k]];
-    float LN[4], UN[4];
-    if (t + 1 < 2 * TR - 2) {
+    for (int j = 0; j < 4; ++j) ev[j] = ep[j][t * SP];
+    if constexpr (t + 1 < STEPS - 1) {
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        LN[k] = tl.Lp[r][TR + t + 1 - ck[k]];
-        UN[k] = tl.Up[TR + t + 1 - r][ck[k]];
+      for (int j = 0; j < 4; ++j) {
+        LV[cur ^ 1][j] = lp[j][t + 1];
+        UV[cur ^ 1][j] = up[j][(t + 1) * UPW];
       }
     }
-    // the pre-quantization value out while this step's published values are read back
-    if (has_ypre && rnd) ypre_row[t - r] = yv;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      D[k] += LV[k] * ev[k];
-      F[k] += cr * UV[k];
+    for (int j = 0; j < 4; ++j) {
+      D[j] += LV[cur][j] * ev[j];
+      F[j] += cr * UV[cur][j];
     }
-    if (t + 1 < 2 * TR - 2) {
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        LV[k] = LN[k];
-        UV[k] = UN[k];
-      }
+    // the pre-quantization value out after the step's feedback is issued
+    if constexpr (YPRE) {
+      if (rnd) ypre_row[t - r] = yv;
     }
-  }
+    // no second barrier: every image entry is written once (at its entry's step), so the next step's
+    // writes never touch what this step reads
+  };
+  static_for(step, std::make_integer_sequence<int, STEPS>{});
 
 #pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    tl.Ys[r][ck[k]] = Y[k];
-    tl.Cs[r][ck[k]] = C[k];
-    tl.Es[r][ck[k]] = E[k];
-  }
+  for (int j = 0; j < 4; ++j) tl.Ys[r][cs[j]] = Y[j];
   __syncthreads();
   float* yt = y + mat + i0 * n + j0;
   float* ct = c + mat + i0 * n + j0;
@@ -422,14 +480,12 @@ __device__ __forceinline__ void sweep_tile_push(TileLds& tl, float* __restrict__
     if (rr < rows_in && cc < cols_in) {
       const int off = rr * (int)n + cc;
       yt[off] = tl.Ys[rr][cc];
-      ct[off] = tl.Cs[rr][cc];
-      et[off] = tl.Es[rr][cc];
+      ct[off] = tl.Cs[rr][TR + cc];
+      et[off] = tl.Es[TR + rr][cc];
     }
   }
 }
 
-// Own tile data of the fp32 kernels, read before the tile's feedback is complete (it does not
-// depend on it): entry q of this thread is (t / TR, t % TR) with t = threadIdx.x + NTHREADS q.
 // The pulled feedback at (r, cc) from the four waves' partial sums (wave w's in red[w / 2][w % 2]):
 // waves [0, wd) summed the down product D, the others the right product R (in wave order).
 __device__ __forceinline__ void pulled_sums(const float (*red)[2][TR][TR + 1], int wd, int r, int cc, float& dd,
@@ -439,15 +495,15 @@ __device__ __forceinline__ void pulled_sums(const float (*red)[2][TR][TR + 1], i
   rr = (wd > 0 ? 0.f : s0) + (wd > 1 ? 0.f : s1) + (wd > 2 ? 0.f : s2) + (wd > 3 ? 0.f : s3);
 }
 
-template <int KIND>
+// Own tile data of the fp32 kernels, read before the tile's feedback is complete (it does not
+// depend on it): entry q of this thread is (t / TR, t % TR) with t = threadIdx.x + NTHREADS q.
 struct TileRegs {
   static constexpr int NQ = TR * TR / NTHREADS;
-  float y[NQ], c[NQ], l[NQ], u[NQ], s[NQ], z[NQ];
+  float y[NQ], c[NQ], l[NQ], u[NQ];
 
   __device__ __forceinline__ void load(const float* __restrict__ yg, const float* __restrict__ cg,
-                                       const float* __restrict__ lb, const float* __restrict__ ub,
-                                       const QSpec<float>& qs, int64_t b, int64_t m, int64_t n, int64_t i0,
-                                       int64_t j0, int64_t mat) {
+                                       const float* __restrict__ lb, const float* __restrict__ ub, int64_t m,
+                                       int64_t n, int64_t i0, int64_t j0, int64_t mat) {
     // the tile's corner in every operand (64-bit arithmetic once, uniform), then 32-bit offsets in
     // the tile (32 rows of at most 2^26 elements)
     const int rows_in = m - i0 < TR ? (int)(m - i0) : TR, cols_in = n - j0 < TR ? (int)(n - j0) : TR;
@@ -457,8 +513,6 @@ struct TileRegs {
     const float* ct = cg + mat + corner;
     const float* lt = lb + i0 * m + i0;  // L[i0 + r, i0 + cc] at r m + cc
     const float* ut = ub + j0 * n + j0;  // U[j0 + r, j0 + cc] at r n + cc
-    const float* st = KIND != Q_ROUND ? qs.scale + qs.smap.offset(b) + corner : nullptr;
-    const float* zt = KIND == Q_AFFINE ? qs.zp + qs.zmap.offset(b) + corner : nullptr;
 #pragma unroll
     for (int q = 0; q < NQ; ++q) {
       const int t = threadIdx.x + NTHREADS * q;
@@ -470,18 +524,12 @@ struct TileRegs {
       // L[i0+r, i0+cc] strictly below the diagonal; U[j0+r, j0+cc] strictly above it
       l[q] = (cc < r && r < rows_in) ? lt[r * mi + cc] : 0.f;
       u[q] = (r < cc && cc < cols_in) ? ut[off] : 0.f;
-      if constexpr (KIND == Q_AFFINE) {
-        s[q] = in ? st[off] : 1.f;
-        z[q] = in ? zt[off] : 0.f;
-      } else if constexpr (KIND == Q_FORCED) {
-        s[q] = in ? st[off] : 0.f;
-      }
     }
   }
 
   // LDS image of the tile with the pulled feedback D (down) and R (right) added: C + D, Y + (D + R),
-  // and the zero padding of the diagonal blocks.  red holds the waves' partial sums when `pulled`
-  // (pulled_sums: the first wd waves' are D's).
+  // the zero padding of the diagonal blocks and of the C image, and the zeroed E image.  red holds
+  // the waves' partial sums when `pulled` (pulled_sums: the first wd waves' are D's).
   __device__ __forceinline__ void store(TileLds& tl, const float (*red)[2][TR][TR + 1], bool pulled, int wd) const {
 #pragma unroll
     for (int q = 0; q < NQ; ++q) {
@@ -490,35 +538,38 @@ struct TileRegs {
       float dd = 0.f, rr = 0.f;
       if (pulled) pulled_sums(red, wd, r, cc, dd, rr);
       tl.Ys[r][cc] = y[q] + (dd + rr);
-      tl.Cs[r][cc] = c[q] + dd;
+      tl.Cs[r][TR + cc] = c[q] + dd;
       tl.Lp[r][TR + cc] = l[q];
       tl.Up[TR + r][cc] = u[q];
-      if constexpr (KIND != Q_ROUND) tl.Ss[r][cc] = s[q];
-      if constexpr (KIND == Q_AFFINE) tl.Zs[r][cc] = z[q];
     }
-    // zero padding without divisions: 8 threads per row of Lp (its 65 padding columns), 4 per padding
-    // row of Up (33 columns each); a strided column walk per thread
+    // zero padding without divisions: 8 threads per row of Lp and of Cs (71 and 66 padding columns), 4 per
+    // padding row of Up (39 columns each); a strided column walk per thread
     {
-      static_assert(NTHREADS == 8 * TR && LPW - TR <= 72 && UPW <= 36, "padding walk shape");
+      static_assert(NTHREADS == 8 * TR && LPW - TR <= 72 && CPW - TR <= 72 && UPW <= 40, "padding walk shape");
       const int r = threadIdx.x >> 3, sub = threadIdx.x & 7;
 #pragma unroll
       for (int i = 0; i < 9; ++i) {
         const int k = sub + 8 * i;
         if (k < LPW - TR) tl.Lp[r][k < TR ? k : k + TR] = 0.f;
+        if (k < CPW - TR) tl.Cs[r][k < TR ? k : k + TR] = 0.f;
       }
       const int row = threadIdx.x >> 2, sub4 = threadIdx.x & 3;
       float* up_row = tl.Up[row < TR ? row : row + TR];
 #pragma unroll
-      for (int i = 0; i < 9; ++i) {
+      for (int i = 0; i < 10; ++i) {
         const int col = sub4 + 4 * i;
         if (col < UPW) up_row[col] = 0.f;
       }
     }
-    // slots of antidiagonals that miss a row or column are read (times a zero factor) before any
-    // write: they must hold finite values, never leftover LDS contents
-    if (threadIdx.x < 2 * TR) {
-      tl.Ed[threadIdx.x / TR][threadIdx.x % TR] = 0.f;
-      tl.Cr[threadIdx.x / TR][threadIdx.x % TR] = 0.f;
+    // the E image: all zeros (read times zero coefficients before the entries' errors are written)
+    {
+      float* es = &tl.Es[0][0];
+      constexpr int EN = EROWS * SP;
+#pragma unroll
+      for (int i = 0; i < (EN + NTHREADS - 1) / NTHREADS; ++i) {
+        const int k = threadIdx.x + NTHREADS * i;
+        if (k < EN) es[k] = 0.f;
+      }
     }
   }
 };
@@ -539,11 +590,11 @@ __device__ __forceinline__ void stash_partial(float (*red)[2][TR][TR + 1], const
 //    the k-tiles before the last one (t < I-1, resp. t < J-1: stages up to T-1, all final) to
 //    their Y and C in global memory -- no tile of stage T touches those;
 //  * sweep workgroups take the tiles of stage T, pull the last k-tile (the tiles (I-1, J) and
-//    (I, J-1) of stage T-1) and sweep the tile's 63 antidiagonals in LDS (sweep_tile_push).
+//    (I, J-1) of stage T-1) and sweep the tile's 63 antidiagonals in LDS (sweep_tile).
 // So only one k-tile of each product is on the stage-to-stage critical path; the rest runs beside
 // the previous stage's sweeps.  Waves 0-1 take the down product, waves 2-3 the right one, each
 // every second 8-deep k-chunk; the two halves meet in LDS.
-template <bool VEC, int KIND>
+template <bool VEC, int KIND, bool YPRE>
 __global__ __launch_bounds__(NTHREADS, 2) void tile_stage_kernel(float* __restrict__ y, float* __restrict__ c,
                                                                  float* __restrict__ e, const float* __restrict__ l,
                                                                  const float* __restrict__ u, int64_t m, int64_t n,
@@ -580,8 +631,12 @@ __global__ __launch_bounds__(NTHREADS, 2) void tile_stage_kernel(float* __restri
   if (!sweep && !pulled) return;
 
   // own tile data first: it does not depend on the pull, so its loads overlap the pull's
-  TileRegs<KIND> own;
-  if (sweep) own.load(y, c, lb, ub, qs, b, m, n, i0, j0, mat);
+  TileRegs own;
+  SweepInputs<KIND> qin;
+  if (sweep) {
+    own.load(y, c, lb, ub, m, n, i0, j0, mat);
+    qin.load(qs, b, m, n, i0, j0);
+  }
 
   // the four waves dealt to the two products in proportion to their chunk counts (a tile near its
   // outer block's edge has nearly all its history in one of them), each product's chunks
@@ -623,7 +678,19 @@ __global__ __launch_bounds__(NTHREADS, 2) void tile_stage_kernel(float* __restri
   // ---- the tile image in LDS, then the in-tile sweep
   own.store(tl, red, pulled, wd);
   __syncthreads();
-  sweep_tile_push<KIND>(tl, y, c, e, qs, m, n, i0, j0, mat);
+  sweep_tile<KIND, YPRE>(tl, qin, y, c, e, qs, m, n, i0, j0, mat);
+}
+
+template <bool VEC, int KIND>
+void launch_tile_stage_k(dim3 grid, hipStream_t stream, float* y, float* c, float* e, const float* l, const float* u,
+                         int64_t m, int64_t n, int64_t st, int64_t S0, int64_t lo, int64_t n_sweep, int64_t prep_lo,
+                         const BatchMap& lmap, const BatchMap& umap, const QSpec<float>& qs, int64_t nx, int64_t ny) {
+  if (qs.ypre)
+    hipLaunchKernelGGL((tile_stage_kernel<VEC, KIND, true>), grid, dim3(NTHREADS), 0, stream, y, c, e, l, u, m, n, st,
+                       S0, lo, n_sweep, prep_lo, lmap, umap, qs, nx, ny);
+  else
+    hipLaunchKernelGGL((tile_stage_kernel<VEC, KIND, false>), grid, dim3(NTHREADS), 0, stream, y, c, e, l, u, m, n, st,
+                       S0, lo, n_sweep, prep_lo, lmap, umap, qs, nx, ny);
 }
 
 template <bool VEC>
@@ -632,14 +699,14 @@ void launch_tile_stage(int32_t kind, dim3 grid, hipStream_t stream, float* y, fl
                        int64_t prep_lo, const BatchMap& lmap, const BatchMap& umap, const QSpec<float>& qs, int64_t nx,
                        int64_t ny) {
   if (kind == Q_AFFINE)
-    hipLaunchKernelGGL((tile_stage_kernel<VEC, Q_AFFINE>), grid, dim3(NTHREADS), 0, stream, y, c, e, l, u, m, n, st, S0,
-                       lo, n_sweep, prep_lo, lmap, umap, qs, nx, ny);
+    launch_tile_stage_k<VEC, Q_AFFINE>(grid, stream, y, c, e, l, u, m, n, st, S0, lo, n_sweep, prep_lo, lmap, umap, qs,
+                                       nx, ny);
   else if (kind == Q_FORCED)
-    hipLaunchKernelGGL((tile_stage_kernel<VEC, Q_FORCED>), grid, dim3(NTHREADS), 0, stream, y, c, e, l, u, m, n, st, S0,
-                       lo, n_sweep, prep_lo, lmap, umap, qs, nx, ny);
+    launch_tile_stage_k<VEC, Q_FORCED>(grid, stream, y, c, e, l, u, m, n, st, S0, lo, n_sweep, prep_lo, lmap, umap, qs,
+                                       nx, ny);
   else
-    hipLaunchKernelGGL((tile_stage_kernel<VEC, Q_ROUND>), grid, dim3(NTHREADS), 0, stream, y, c, e, l, u, m, n, st, S0,
-                       lo, n_sweep, prep_lo, lmap, umap, qs, nx, ny);
+    launch_tile_stage_k<VEC, Q_ROUND>(grid, stream, y, c, e, l, u, m, n, st, S0, lo, n_sweep, prep_lo, lmap, umap, qs,
+                                      nx, ny);
 }
 
 bool aligned16(const void* p) { return p == nullptr || ((uintptr_t)p & 15) == 0; }

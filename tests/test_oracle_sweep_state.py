@@ -101,3 +101,23 @@ def test_stage_work_brute_force(m, n):
             i_lo, j_lo = max(0, s - n + 1), max(0, s - m + 1)
             closed += 2 * (m - i_lo) + (n - j_lo)
     assert total == closed
+
+
+@pytest.mark.parametrize("m,n", [(13, 5), (9, 16), (24, 40)])
+def test_transposed_layer_is_the_same_rounding(m, n):
+    """The yardstick of the full-size free-running comparison: the sweep of X^T with L' = U^T and U' = L^T (rows
+    and columns exchanged) rounds exactly as the sweep of X, transposed, in fp64 with a coordinate-dependent
+    codebook; in fp32 only the summation order differs."""
+    Am, Bm, X = A.random_instance((m, n), 3 * m + n)
+    L, U = A.feedback_factors(Am, Bm)
+
+    def coord(transposed):
+        def q(y_flat, sl, *, out):
+            idx = torch.arange(sl.start, sl.stop, sl.step)
+            i, j = (idx % m, idx // m) if transposed else (idx // n, idx % n)
+            out.copy_(A.coordinate_round(y_flat[sl], i, j))
+        return q
+
+    z = S.gptq_2d_torch(X, L, U, quantizer=coord(False))
+    zt = S.gptq_2d_torch(X.t().contiguous(), U.t().contiguous(), L.t().contiguous(), quantizer=coord(True))
+    assert zt.t().equal(z)
