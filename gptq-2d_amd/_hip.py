@@ -32,6 +32,8 @@ _SIGNATURES = {
     "flush": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I32, _AP, _AP, _AP, _P],
     "sweep_fused": [_P, _P, _P, _P, _P, _I64, _I64, _I32, _AP, _AP, _AP, _I32, _P, _AP, _P, _AP, _F64, _F64, _P,
                     _I64, _I64, _I64, _P],
+    "sweep_fused_noalloc": [_P, _P, _P, _I64, _I64, _I32, _AP, _AP, _AP, _I32, _P, _AP, _P, _AP, _F64, _F64, _P, _I64,
+                            _P],
     "affine_quantize": [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I32, _AP, _AP, _AP, _F64, _F64, _P],
     "round_quantize": [_P, _P, _I64, _I64, _I64, _I64, _I32, _AP, _P],
     "affine_quantize_se": [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I32, _AP, _AP, _AP, _F64,
@@ -67,6 +69,8 @@ def lib() -> ctypes.CDLL:
                 fn = getattr(handle, f"gptq2d_{name}_{suffix}")
                 fn.argtypes = argtypes
                 fn.restype = ctypes.c_int
+        handle.gptq2d_sweep_fused_noalloc_capacity.argtypes = [_I32]
+        handle.gptq2d_sweep_fused_noalloc_capacity.restype = ctypes.c_int64
         handle.gptq2d_viterbi_workspace.argtypes = [_I64, _I64, _I32, _I32, _I32]
         handle.gptq2d_viterbi_workspace.restype = ctypes.c_int64
         handle.gptq2d_profile_start.argtypes = [_I64, ctypes.c_uint32]

@@ -19,6 +19,7 @@
 // Error codes returned by the C ABI besides hipError_t values (which are > 0).
 #define GPTQ2D_EINVAL (-1)
 #define GPTQ2D_EUNSUPPORTED (-2)
+#define GPTQ2D_ESCRATCH (-3)
 
 struct BatchMap {
   int32_t nd;

@@ -20,6 +20,7 @@
 #include "common.h"
 #include "profile.h"
 
+#include <mutex>
 #include <utility>
 
 template <typename T>
@@ -792,6 +793,55 @@ int sweep_fused(T* y, T* c, T* e, const T* l, const T* u, int64_t m, int64_t n, 
   return 0;
 }
 
+// ------------------------------------------------------------------------------------------------ no-alloc entry
+
+// Scratch of gptq2d_sweep_fused_noalloc_*: the sweep's C and E buffers, each half of this array, in a
+// fixed device array that the HIP runtime places on every GPU that loads the library (it stays there
+// until the process ends).  Host code never uses the name `scratch` as an address (it is a host-side
+// stand-in): the device address comes from hipGetSymbolAddress, once per device, on the first call
+// made with that device current.
+constexpr int64_t NOALLOC_SCRATCH_BYTES = (int64_t)128 << 20;
+static __device__ __align__(256) unsigned char scratch[NOALLOC_SCRATCH_BYTES];
+
+constexpr int NOALLOC_MAX_DEVICES = 64;
+std::mutex scratch_mutex;
+void* scratch_ptr[NOALLOC_MAX_DEVICES];
+
+// Device address of the current device's scratch array, or nullptr if it cannot be had.
+void* scratch_address() {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= NOALLOC_MAX_DEVICES) return nullptr;
+  std::lock_guard<std::mutex> lock(scratch_mutex);
+  if (!scratch_ptr[dev]) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess) return nullptr;
+    scratch_ptr[dev] = p;
+  }
+  return scratch_ptr[dev];
+}
+
+template <typename T>
+int sweep_fused_noalloc(T* y, const T* l, const T* u, int64_t m, int64_t n, int32_t bnd, const int64_t* bshape,
+                        const int64_t* lstride, const int64_t* ustride, int32_t qkind, const T* qa,
+                        const int64_t* qa_stride, const T* qb, const int64_t* qb_stride, double qmin, double qmax,
+                        T* ypre, int64_t outer_tiles, hipStream_t stream) {
+  if (m < 0 || n < 0 || bnd < 0 || bnd > GPTQ2D_MAX_BATCH_DIMS) return GPTQ2D_EINVAL;
+  // each of C and E takes half the array: B m n elements of T at most (checked before any product can
+  // overflow: every factor is below 2^31 once the first test passes)
+  const int64_t cap = NOALLOC_SCRATCH_BYTES / 2 / (int64_t)sizeof(T);
+  int64_t count = 1;
+  for (int32_t d = 0; d < bnd; ++d) {
+    if (bshape[d] < 0) return GPTQ2D_EINVAL;
+    count = bshape[d] == 0 || count == 0 ? 0 : (bshape[d] > cap / count ? cap + 1 : count * bshape[d]);
+  }
+  if (m > 0 && n > 0 && count > 0 && (m > cap || n > cap / m || count > cap / (m * n))) return GPTQ2D_ESCRATCH;
+  T* c = static_cast<T*>(scratch_address());
+  if (!c) return GPTQ2D_EUNSUPPORTED;
+  T* e = c + cap;
+  return sweep_fused<T>(y, c, e, l, u, m, n, bnd, bshape, lstride, ustride, qkind, qa, qa_stride, qb, qb_stride, qmin,
+                        qmax, ypre, outer_tiles, 0, -1, stream);
+}
+
 }  // namespace
 
 extern "C" {
@@ -805,7 +855,19 @@ extern "C" {
     return sweep_fused<T>(y, c, e, l, u, m, n, bnd, bshape, lstride, ustride, qkind, qa, qa_stride, qb, qb_stride,   \
                           qmin, qmax, ypre, outer_tiles, stage_begin, stage_end, stream);                             \
   }                                                                                                                  \
-  int64_t gptq2d_sweep_fused_tile_##SUF(void) { return TR; }
+  int64_t gptq2d_sweep_fused_tile_##SUF(void) { return TR; }                                                      \
+  int gptq2d_sweep_fused_noalloc_##SUF(T* y, const T* l, const T* u, int64_t m, int64_t n, int32_t bnd,              \
+                                       const int64_t* bshape, const int64_t* lstride, const int64_t* ustride,       \
+                                       int32_t qkind, const T* qa, const int64_t* qa_stride, const T* qb,           \
+                                       const int64_t* qb_stride, double qmin, double qmax, T* ypre,                 \
+                                       int64_t outer_tiles, hipStream_t stream) {                                    \
+    return sweep_fused_noalloc<T>(y, l, u, m, n, bnd, bshape, lstride, ustride, qkind, qa, qa_stride, qb, qb_stride, \
+                                  qmin, qmax, ypre, outer_tiles, stream);                                            \
+  }
+
+int64_t gptq2d_sweep_fused_noalloc_capacity(int32_t elem_bytes) {
+  return elem_bytes == 4 || elem_bytes == 8 ? NOALLOC_SCRATCH_BYTES / 2 / elem_bytes : -1;
+}
 
 GPTQ2D_FUSED_ABI(f32, float)
 GPTQ2D_FUSED_ABI(f64, double)

@@ -3,7 +3,8 @@
  * Every entry point takes raw device pointers and int64 sizes, launches HIP kernels on the given
  * stream (a hipStream_t, passed as void*), never allocates device memory, never synchronises
  * with the host, uses no atomics (results are deterministic) and returns 0 on success, a
- * positive hipError_t, or GPTQ2D_EINVAL / GPTQ2D_EUNSUPPORTED.  The caller owns all memory.
+ * positive hipError_t, or GPTQ2D_EINVAL / GPTQ2D_EUNSUPPORTED / GPTQ2D_ESCRATCH.  The caller owns all
+ * memory (the *_noalloc entry point aside, whose scratch is the library's own).
  * Everything except the profiler may be captured in a hipGraph.
  *
  * Layout conventions.  Y, C and E are contiguous row-major [B, m, n] with B the product of the
@@ -29,6 +30,7 @@ extern "C" {
 
 #define GPTQ2D_EINVAL (-1)
 #define GPTQ2D_EUNSUPPORTED (-2)
+#define GPTQ2D_ESCRATCH (-3) /* the problem does not fit the fixed scratch of a *_noalloc entry point */
 
 #define GPTQ2D_DECLARE(T, SUF)                                                                                        \
   /* Whole sweep with a built-in per-entry quantizer fused in: replaces the stage loop of              \
@@ -48,6 +50,19 @@ extern "C" {
                                int64_t stage_begin, int64_t stage_end, void* stream);                               \
   /* Tile edge of the fused sweep. */                                                                  \
   int64_t gptq2d_sweep_fused_tile_##SUF(void);                                                                       \
+  /* The whole fused sweep (as gptq2d_sweep_fused with stage_begin 0, stage_end -1) with no c and e:     \
+   * its scratch is a fixed device array of the library (128 MiB on every GPU that loads it, held until \
+   * the process ends), so the call allocates nothing at all -- for callers that cannot allocate device  \
+   * memory (code under stream capture, serving loops, allocation-free harnesses).  No counterpart in    \
+   * the reference, which allocates its scratch per call from torch's caching allocator                 \
+   * (gptq_2d.py:1324-1334).  B m n must not exceed gptq2d_sweep_fused_noalloc_capacity(sizeof(T)),     \
+   * else GPTQ2D_ESCRATCH and nothing runs.  All calls on one GPU share its array: calls that overlap   \
+   * on one GPU (other streams, other host threads) race and give wrong results. */                      \
+  int gptq2d_sweep_fused_noalloc_##SUF(T* y, const T* l, const T* u, int64_t m, int64_t n, int32_t bnd,              \
+                                       const int64_t* bshape, const int64_t* l_stride, const int64_t* u_stride,     \
+                                       int32_t qkind, const T* qa, const int64_t* qa_stride, const T* qb,           \
+                                       const int64_t* qb_stride, double qmin, double qmax, T* ypre,                 \
+                                       int64_t outer_tiles, void* stream);                                           \
                                                                                                                       \
   /* Plug-in path, plain entries: push of stage s inside the block ending at s1 -- error, down and     \
    * right feedback, commit of z, capture of the next stage's values (_push_kernel,                   \
@@ -155,6 +170,11 @@ extern "C" {
   int gptq2d_viterbi_##SUF(const T* x, const T* table, T* hist, const T* scale, T* out, int64_t* states,            \
                            int64_t rows, int64_t steps, int32_t L, int32_t K, int32_t V, int32_t tail_biting,      \
                            void* stream);
+
+/* Largest B m n (elements per matrix of the batch) gptq2d_sweep_fused_noalloc_* accepts for elements of
+ * elem_bytes bytes (4 or 8; -1 otherwise): 2^24 for float, 2^23 for double.  No counterpart in the
+ * reference (see gptq2d_sweep_fused_noalloc). */
+int64_t gptq2d_sweep_fused_noalloc_capacity(int32_t elem_bytes);
 
 /* Elements of the history workspace gptq2d_viterbi_* needs for `rows` sequences of `steps` steps (-1 if
  * the arguments are invalid).  Part of the trellis quantizer above (quantizer_trellis.py:146-341 keeps its
