@@ -32,6 +32,8 @@ _SIGNATURES = {
     "flush": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I32, _AP, _AP, _AP, _P],
     "sweep_fused": [_P, _P, _P, _P, _P, _I64, _I64, _I32, _AP, _AP, _AP, _I32, _P, _AP, _P, _AP, _F64, _F64, _P,
                     _I64, _I64, _I64, _P],
+    "sweep_fused_se": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I32, _AP, _AP, _AP, _I32, _P, _AP, _P, _AP, _F64,
+                       _F64, _I32, _P, _I64, _I64, _I64, _P],
     "sweep_fused_noalloc": [_P, _P, _P, _I64, _I64, _I32, _AP, _AP, _AP, _I32, _P, _AP, _P, _AP, _F64, _F64, _P, _I64,
                             _P],
     "affine_quantize": [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I32, _AP, _AP, _AP, _F64, _F64, _P],

@@ -21,6 +21,7 @@
 #include "profile.h"
 
 #include <mutex>
+#include <type_traits>
 #include <utility>
 
 template <typename T>
@@ -36,7 +37,9 @@ constexpr int TR = 32;       // tile edge
 constexpr int PARTS = 8;     // threads cooperating on one entry of an antidiagonal
 constexpr int NTHREADS = TR * PARTS;
 
-enum QKind : int32_t { Q_ROUND = 0, Q_AFFINE = 1, Q_FORCED = 2 };
+// Q_ABSMAX: the abs-max INT quantizer of a super-entry row (int_abs_max_quantizer, quantizer_int.py:120-134),
+// only with 1 x TR super-entries.
+enum QKind : int32_t { Q_ROUND = 0, Q_AFFINE = 1, Q_FORCED = 2, Q_ABSMAX = 3 };
 
 template <typename T>
 struct QSpec {
@@ -45,8 +48,165 @@ struct QSpec {
   const T* zp;     // affine: full [*, m, n] zero point
   BatchMap smap, zmap;
   T qmin, qmax;
-  T* ypre;  // optional [B, m, n]: Y of every entry just before it is rounded
+  T* ypre;          // optional [B, m, n]: Y of every entry just before it is rounded
+  int32_t dtype16;  // abs-max: the scale's 16-bit type (1 bf16, 2 fp16)
 };
+
+// f(integral_constant<int, I>) for I = 0, 1, ..., in order: a loop whose index is a compile-time constant in
+// every iteration.
+template <typename F, int... I>
+__device__ __forceinline__ void static_for(F& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+
+// ------------------------------------------------------------------------------------------------ 1 x TR super-entries
+//
+// With super-entries of one row and TR columns (gptq_2d_super_entry with super_entry_shape (1, TR), e.g. the
+// three-factor layer's 1 x 32 abs-max groups) a tile holds the TR super-entries (i0 + r, J) of one coarse
+// column, ordered by row; the tiles' coarse stages and the feedback between tiles (pulls, flushes) are
+// those of plain entries, and U's TR x TR diagonal blocks -- identity by the super-entry convention -- are
+// never read.  Inside a tile the sweep is TR steps, one per row: the row's entries are rounded jointly
+// from y = Y + down (the in-tile feedback through L[I,I]), then their errors are pushed to the rows below.
+// Thread (g, c) = (tid / 32, tid % 32) owns column c of rows 4g .. 4g + 3; a row is the 32 lanes of one
+// half-wave, so the abs-max of a super-entry row is a half-wave reduction.
+
+// Maximum over the 32 lanes of each half-wave (all of them receive it).
+template <typename T>
+__device__ __forceinline__ T halfwave_max(T v) {
+#pragma unroll
+  for (int k = 16; k >= 1; k >>= 1) {
+    const T o = __shfl_xor(v, k, 32);
+    v = o > v ? o : v;
+  }
+  return v;
+}
+
+// The rows' quantizer inputs (affine: scale and zero point; forced: the values), read from global memory
+// at the start of the kernel.
+template <typename T, int KIND>
+struct RowInputs {
+  T s[4], z[4];
+
+  __device__ __forceinline__ void load(const QSpec<T>& qs, int64_t b, int64_t m, int64_t n, int64_t i0, int64_t j0) {
+    const int cc = threadIdx.x & 31, g = threadIdx.x >> 5;
+    const int rows_in = m - i0 < TR ? (int)(m - i0) : TR;
+    const int64_t corner = i0 * n + j0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = 4 * g + i;
+      const bool in = r < rows_in;
+      const int64_t off = corner + (int64_t)r * n + cc;
+      s[i] = z[i] = T(0);
+      if constexpr (KIND == Q_AFFINE) {
+        s[i] = in ? qs.scale[qs.smap.offset(b) + off] : T(1);
+        z[i] = in ? qs.zp[qs.zmap.offset(b) + off] : T(0);
+      } else if constexpr (KIND == Q_FORCED) {
+        s[i] = in ? qs.scale[qs.smap.offset(b) + off] : T(0);
+      }
+    }
+  }
+};
+
+// The TR row steps of one tile, then its Y, C and E to global memory.  ys / cs: the tile's Y and C with
+// the pulled feedback (row pitches ysp, csp); lp[r lpp + k] = L[i0 + r, i0 + k] for k < r, zero
+// elsewhere; es: TR x esp floats for the published errors.  Expects the image complete (a barrier after
+// it was written).
+template <typename T, int KIND, bool YPRE>
+__device__ __forceinline__ void sweep_rows(const T* ys, int ysp, const T* cs, int csp, const T* lp, int lpp, T* es,
+                                           int esp, const RowInputs<T, KIND>& in, T* __restrict__ y,
+                                           T* __restrict__ c, T* __restrict__ e, const QSpec<T>& qs, int64_t m,
+                                           int64_t n, int64_t i0, int64_t j0, int64_t mat) {
+  const int cc = threadIdx.x & 31, g = threadIdx.x >> 5;
+  const int rows_in = m - i0 < TR ? (int)(m - i0) : TR;  // the super-entries span the tile's columns
+  T Y[4], C[4], D[4], E[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    Y[i] = ys[(4 * g + i) * ysp + cc];
+    C[i] = cs[(4 * g + i) * csp + cc];
+    D[i] = E[i] = T(0);
+  }
+  const T qmin = qs.qmin, qmax = qs.qmax, half = (qs.qmax - qs.qmin) / T(2);
+  auto step = [&](auto r_c) __attribute__((always_inline)) {
+    constexpr int r = decltype(r_c)::value, slot = r & 3;
+    const bool own = g == (r >> 2) && r < rows_in;
+    const T yv = Y[slot] + D[slot];
+    T z;
+    if constexpr (KIND == Q_ABSMAX) {
+      // scale from the row's current abs max (a NaN entry counts as 0, as in the plug-in's comparison
+      // loop), rounded to the 16-bit type through fp32, 0 -> 1; the reduction runs on every lane
+      const T a = own ? __builtin_fmax(__builtin_fabs(yv), T(0)) : T(0);
+      const T amax = halfwave_max(a);
+      T sc = round_scale16(amax / half, qs.dtype16);
+      sc = sc == T(0) ? T(1) : sc;
+      z = clamp_val(round_even(yv / sc), qmin, qmax) * sc;
+    } else if constexpr (KIND == Q_AFFINE) {
+      z = (clamp_val(round_even(yv / in.s[slot] + in.z[slot]), qmin, qmax) - in.z[slot]) * in.s[slot];
+    } else if constexpr (KIND == Q_FORCED) {
+      z = in.s[slot];
+    } else {
+      z = round_even(yv);
+    }
+    const T ev = z - yv;
+    const T cf = (C[slot] + D[slot]) + ev;
+    if (own) {
+      Y[slot] = z;
+      E[slot] = ev;
+      C[slot] = cf;
+      es[r * esp + cc] = ev;
+      if constexpr (YPRE) qs.ypre[mat + (i0 + r) * n + j0 + cc] = yv;
+    }
+    if constexpr (r + 1 < TR) {
+      __syncthreads();  // the row's errors before the rows below read them
+      const T er = es[r * esp + cc];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) D[i] += lp[(4 * g + i) * lpp + r] * er;
+    }
+  };
+  static_for(step, std::make_integer_sequence<int, TR>{});
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = 4 * g + i;
+    if (r < rows_in) {
+      const int64_t off = mat + (i0 + r) * n + j0 + cc;
+      y[off] = Y[i];
+      c[off] = C[i];
+      e[off] = E[i];
+    }
+  }
+}
+
+// One launch per coarse stage of the row-super-entry sweep on the generic (fp64) path: each workgroup
+// loads its tile's Y, C and L[I,I] and sweeps it (the feedback of earlier tiles was flushed in).
+template <typename T, int KIND, bool YPRE>
+__global__ __launch_bounds__(NTHREADS) void sweep_rows_kernel(T* __restrict__ y, T* __restrict__ c,
+                                                              T* __restrict__ e, const T* __restrict__ l, int64_t m,
+                                                              int64_t n, int64_t stage, int64_t tile_lo,
+                                                              BatchMap lmap, QSpec<T> qs, int64_t nx, int64_t ny) {
+  __shared__ T Ys[TR][TR + 1];
+  __shared__ T Cs[TR][TR + 1];
+  __shared__ T Ls[TR][TR + 1];
+  __shared__ T Es[TR][TR + 1];
+  const GridIds id = grid_ids(nx, ny);
+  const int64_t b = id.b;
+  const int64_t I = tile_lo + id.x, J = stage - I;
+  const int64_t i0 = I * TR, j0 = J * TR;
+  const int64_t mat = b * m * n;
+  const T* lb = l + lmap.offset(b);
+  const int rows_in = m - i0 < TR ? (int)(m - i0) : TR;
+  RowInputs<T, KIND> in;
+  in.load(qs, b, m, n, i0, j0);
+  for (int t = threadIdx.x; t < TR * TR; t += NTHREADS) {
+    const int r = t / TR, cc = t % TR;
+    const bool rin = r < rows_in;
+    const int64_t off = mat + (i0 + r) * n + j0 + cc;
+    Ys[r][cc] = rin ? y[off] : T(0);
+    Cs[r][cc] = rin ? c[off] : T(0);
+    Ls[r][cc] = (cc < r && rin) ? lb[(i0 + r) * m + i0 + cc] : T(0);  // strictly below the diagonal
+  }
+  __syncthreads();
+  sweep_rows<T, KIND, YPRE>(&Ys[0][0], TR + 1, &Cs[0][0], TR + 1, &Ls[0][0], TR + 1, &Es[0][0], TR + 1, in, y, c, e, qs,
+                            m, n, i0, j0, mat);
+}
 
 template <typename T>
 __global__ __launch_bounds__(NTHREADS) void sweep_tiles_kernel(T* __restrict__ y, T* __restrict__ c,
@@ -288,13 +448,6 @@ __device__ __forceinline__ void slot_columns(int r, int part, int (&cs)[4]) {
   for (int j = 0; j < 4; ++j) cs[j] = 8 * (qlo + ((j - qlo) & 3)) + part - r;  // in [0, TR)
 }
 
-// f(integral_constant<int, I>) for I = 0, 1, ..., in order: a loop whose index is a compile-time constant in
-// every iteration.
-template <typename F, int... I>
-__device__ __forceinline__ void static_for(F& f, std::integer_sequence<int, I...>) {
-  (f(std::integral_constant<int, I>{}), ...);
-}
-
 // Quantizer inputs of the sweep's entries in its own layout (slot order), read from global memory at
 // the start of the kernel so that their latency overlaps the pull.
 template <int KIND>
@@ -498,6 +651,9 @@ __device__ __forceinline__ void pulled_sums(const float (*red)[2][TR][TR + 1], i
 
 // Own tile data of the fp32 kernels, read before the tile's feedback is complete (it does not
 // depend on it): entry q of this thread is (t / TR, t % TR) with t = threadIdx.x + NTHREADS q.
+// ROWS: the tile image of the row-super-entry sweep (1 x TR super-entries): no U block (identity by the
+// super-entry convention, never read), no padding and no E image.
+template <bool ROWS>
 struct TileRegs {
   static constexpr int NQ = TR * TR / NTHREADS;
   float y[NQ], c[NQ], l[NQ], u[NQ];
@@ -524,7 +680,7 @@ struct TileRegs {
       c[q] = in ? ct[off] : 0.f;
       // L[i0+r, i0+cc] strictly below the diagonal; U[j0+r, j0+cc] strictly above it
       l[q] = (cc < r && r < rows_in) ? lt[r * mi + cc] : 0.f;
-      u[q] = (r < cc && cc < cols_in) ? ut[off] : 0.f;
+      u[q] = (!ROWS && r < cc && cc < cols_in) ? ut[off] : 0.f;
     }
   }
 
@@ -541,8 +697,9 @@ struct TileRegs {
       tl.Ys[r][cc] = y[q] + (dd + rr);
       tl.Cs[r][TR + cc] = c[q] + dd;
       tl.Lp[r][TR + cc] = l[q];
-      tl.Up[TR + r][cc] = u[q];
+      if constexpr (!ROWS) tl.Up[TR + r][cc] = u[q];
     }
+    if constexpr (ROWS) return;
     // zero padding without divisions: 8 threads per row of Lp and of Cs (71 and 66 padding columns), 4 per
     // padding row of Up (39 columns each); a strided column walk per thread
     {
@@ -595,7 +752,7 @@ __device__ __forceinline__ void stash_partial(float (*red)[2][TR][TR + 1], const
 // So only one k-tile of each product is on the stage-to-stage critical path; the rest runs beside
 // the previous stage's sweeps.  Waves 0-1 take the down product, waves 2-3 the right one, each
 // every second 8-deep k-chunk; the two halves meet in LDS.
-template <bool VEC, int KIND, bool YPRE>
+template <bool VEC, int KIND, bool YPRE, bool ROWS>
 __global__ __launch_bounds__(NTHREADS, 2) void tile_stage_kernel(float* __restrict__ y, float* __restrict__ c,
                                                                  float* __restrict__ e, const float* __restrict__ l,
                                                                  const float* __restrict__ u, int64_t m, int64_t n,
@@ -632,11 +789,15 @@ __global__ __launch_bounds__(NTHREADS, 2) void tile_stage_kernel(float* __restri
   if (!sweep && !pulled) return;
 
   // own tile data first: it does not depend on the pull, so its loads overlap the pull's
-  TileRegs own;
-  SweepInputs<KIND> qin;
+  TileRegs<ROWS> own;
+  SweepInputs<ROWS ? Q_ROUND : KIND> qin;
+  RowInputs<float, ROWS ? KIND : Q_ROUND> rin;
   if (sweep) {
     own.load(y, c, lb, ub, m, n, i0, j0, mat);
-    qin.load(qs, b, m, n, i0, j0);
+    if constexpr (ROWS)
+      rin.load(qs, b, m, n, i0, j0);
+    else
+      qin.load(qs, b, m, n, i0, j0);
   }
 
   // the four waves dealt to the two products in proportion to their chunk counts (a tile near its
@@ -679,35 +840,53 @@ __global__ __launch_bounds__(NTHREADS, 2) void tile_stage_kernel(float* __restri
   // ---- the tile image in LDS, then the in-tile sweep
   own.store(tl, red, pulled, wd);
   __syncthreads();
-  sweep_tile<KIND, YPRE>(tl, qin, y, c, e, qs, m, n, i0, j0, mat);
+  if constexpr (ROWS)
+    sweep_rows<float, KIND, YPRE>(&tl.Ys[0][0], SP, &tl.Cs[0][TR], CPW, &tl.Lp[0][TR], LPW, &tl.Es[TR][0], SP, rin, y, c,
+                                  e, qs, m, n, i0, j0, mat);
+  else
+    sweep_tile<KIND, YPRE>(tl, qin, y, c, e, qs, m, n, i0, j0, mat);
 }
 
-template <bool VEC, int KIND>
+template <bool VEC, int KIND, bool ROWS>
 void launch_tile_stage_k(dim3 grid, hipStream_t stream, float* y, float* c, float* e, const float* l, const float* u,
                          int64_t m, int64_t n, int64_t st, int64_t S0, int64_t lo, int64_t n_sweep, int64_t prep_lo,
                          const BatchMap& lmap, const BatchMap& umap, const QSpec<float>& qs, int64_t nx, int64_t ny) {
   if (qs.ypre)
-    hipLaunchKernelGGL((tile_stage_kernel<VEC, KIND, true>), grid, dim3(NTHREADS), 0, stream, y, c, e, l, u, m, n, st,
-                       S0, lo, n_sweep, prep_lo, lmap, umap, qs, nx, ny);
+    hipLaunchKernelGGL((tile_stage_kernel<VEC, KIND, true, ROWS>), grid, dim3(NTHREADS), 0, stream, y, c, e, l, u, m, n,
+                       st, S0, lo, n_sweep, prep_lo, lmap, umap, qs, nx, ny);
   else
-    hipLaunchKernelGGL((tile_stage_kernel<VEC, KIND, false>), grid, dim3(NTHREADS), 0, stream, y, c, e, l, u, m, n, st,
-                       S0, lo, n_sweep, prep_lo, lmap, umap, qs, nx, ny);
+    hipLaunchKernelGGL((tile_stage_kernel<VEC, KIND, false, ROWS>), grid, dim3(NTHREADS), 0, stream, y, c, e, l, u, m,
+                       n, st, S0, lo, n_sweep, prep_lo, lmap, umap, qs, nx, ny);
 }
 
-template <bool VEC>
+template <bool VEC, bool ROWS>
 void launch_tile_stage(int32_t kind, dim3 grid, hipStream_t stream, float* y, float* c, float* e, const float* l,
                        const float* u, int64_t m, int64_t n, int64_t st, int64_t S0, int64_t lo, int64_t n_sweep,
                        int64_t prep_lo, const BatchMap& lmap, const BatchMap& umap, const QSpec<float>& qs, int64_t nx,
                        int64_t ny) {
   if (kind == Q_AFFINE)
-    launch_tile_stage_k<VEC, Q_AFFINE>(grid, stream, y, c, e, l, u, m, n, st, S0, lo, n_sweep, prep_lo, lmap, umap, qs,
-                                       nx, ny);
+    launch_tile_stage_k<VEC, Q_AFFINE, ROWS>(grid, stream, y, c, e, l, u, m, n, st, S0, lo, n_sweep, prep_lo, lmap,
+                                             umap, qs, nx, ny);
   else if (kind == Q_FORCED)
-    launch_tile_stage_k<VEC, Q_FORCED>(grid, stream, y, c, e, l, u, m, n, st, S0, lo, n_sweep, prep_lo, lmap, umap, qs,
-                                       nx, ny);
+    launch_tile_stage_k<VEC, Q_FORCED, ROWS>(grid, stream, y, c, e, l, u, m, n, st, S0, lo, n_sweep, prep_lo, lmap,
+                                             umap, qs, nx, ny);
+  else if (ROWS && kind == Q_ABSMAX)
+    launch_tile_stage_k<VEC, Q_ABSMAX, true>(grid, stream, y, c, e, l, u, m, n, st, S0, lo, n_sweep, prep_lo, lmap,
+                                             umap, qs, nx, ny);
   else
-    launch_tile_stage_k<VEC, Q_ROUND>(grid, stream, y, c, e, l, u, m, n, st, S0, lo, n_sweep, prep_lo, lmap, umap, qs,
-                                      nx, ny);
+    launch_tile_stage_k<VEC, Q_ROUND, ROWS>(grid, stream, y, c, e, l, u, m, n, st, S0, lo, n_sweep, prep_lo, lmap,
+                                            umap, qs, nx, ny);
+}
+
+template <typename T, int KIND>
+void launch_rows_stage(dim3 grid, hipStream_t stream, T* y, T* c, T* e, const T* l, int64_t m, int64_t n, int64_t st,
+                       int64_t lo, const BatchMap& lmap, const QSpec<T>& qs, int64_t nx, int64_t ny) {
+  if (qs.ypre)
+    hipLaunchKernelGGL((sweep_rows_kernel<T, KIND, true>), grid, dim3(NTHREADS), 0, stream, y, c, e, l, m, n, st, lo,
+                       lmap, qs, nx, ny);
+  else
+    hipLaunchKernelGGL((sweep_rows_kernel<T, KIND, false>), grid, dim3(NTHREADS), 0, stream, y, c, e, l, m, n, st, lo,
+                       lmap, qs, nx, ny);
 }
 
 bool aligned16(const void* p) { return p == nullptr || ((uintptr_t)p & 15) == 0; }
@@ -718,18 +897,21 @@ bool strides_mult4(const BatchMap& bm) {
   return true;
 }
 
+// rows: super-entries of 1 x TR (the row sweep); dtype16: the abs-max scale's 16-bit type.
 template <typename T>
 int sweep_fused(T* y, T* c, T* e, const T* l, const T* u, int64_t m, int64_t n, int32_t bnd, const int64_t* bshape,
                 const int64_t* lstride, const int64_t* ustride, int32_t qkind, const T* qa, const int64_t* qa_stride,
                 const T* qb, const int64_t* qb_stride, double qmin, double qmax, T* ypre, int64_t outer_tiles,
-                int64_t stage_begin, int64_t stage_end, hipStream_t stream) {
+                int64_t stage_begin, int64_t stage_end, hipStream_t stream, bool rows = false, int32_t dtype16 = 0) {
   BatchMap lmap, umap;
   if (!make_batch_map(lmap, bnd, bshape, lstride) || !make_batch_map(umap, bnd, bshape, ustride)) return GPTQ2D_EINVAL;
   if (m <= 0 || n <= 0 || outer_tiles < 1) return GPTQ2D_EINVAL;
   // the fp32 tile kernels index inside a tile with 32-bit offsets (32 rows of a row length < 2^26)
   if (sizeof(T) == 4 && (m >= ((int64_t)1 << 26) || n >= ((int64_t)1 << 26))) return GPTQ2D_EUNSUPPORTED;
-  if (qkind != Q_ROUND && qkind != Q_AFFINE && qkind != Q_FORCED) return GPTQ2D_EINVAL;
+  if (qkind != Q_ROUND && qkind != Q_AFFINE && qkind != Q_FORCED && !(rows && qkind == Q_ABSMAX)) return GPTQ2D_EINVAL;
   if ((qkind == Q_AFFINE && (!qa || !qb)) || (qkind == Q_FORCED && !qa)) return GPTQ2D_EINVAL;
+  if (qkind == Q_ABSMAX && (!(qmin < qmax) || (dtype16 != 1 && dtype16 != 2))) return GPTQ2D_EINVAL;
+  if (rows && n % TR) return GPTQ2D_EINVAL;  // the super-entries tile the rows
   QSpec<T> qs;
   qs.kind = qkind;
   qs.scale = qa;
@@ -739,6 +921,7 @@ int sweep_fused(T* y, T* c, T* e, const T* l, const T* u, int64_t m, int64_t n, 
   qs.qmin = (T)qmin;
   qs.qmax = (T)qmax;
   qs.ypre = ypre;
+  qs.dtype16 = dtype16;
   const int64_t B = batch_count(bnd, bshape);
   if (B == 0) return 0;
   const int64_t mt = cdiv(m, TR), nt = cdiv(n, TR), stages = mt + nt - 1;
@@ -768,16 +951,31 @@ int sweep_fused(T* y, T* c, T* e, const T* l, const T* u, int64_t m, int64_t n, 
           pcount = (st + 1 < mt - 1 ? st + 1 : mt - 1) - plo + 1;
         }
         const Grid3 g = make_grid(hi - lo + 1 + pcount, 1, B);
+        auto launch = [&](auto vec_c, auto rows_c) {
+          launch_tile_stage<decltype(vec_c)::value, decltype(rows_c)::value>(
+              qkind, g.grid, stream, y, c, e, l, u, m, n, st, S0, lo, hi - lo + 1, plo, lmap, umap, qs, g.nx, g.ny);
+        };
+        using True = std::true_type;
+        using False = std::false_type;
         if (vec)
-          launch_tile_stage<true>(qkind, g.grid, stream, y, c, e, l, u, m, n, st, S0, lo, hi - lo + 1, plo, lmap, umap,
-                                  qs, g.nx, g.ny);
+          rows ? launch(True{}, True{}) : launch(True{}, False{});
         else
-          launch_tile_stage<false>(qkind, g.grid, stream, y, c, e, l, u, m, n, st, S0, lo, hi - lo + 1, plo, lmap, umap,
-                                   qs, g.nx, g.ny);
+          rows ? launch(False{}, True{}) : launch(False{}, False{});
       } else {
         const Grid3 g = make_grid(hi - lo + 1, 1, B);
-        hipLaunchKernelGGL(sweep_tiles_kernel<T>, g.grid, dim3(NTHREADS), 0, stream, y, c, e, l, u, m, n, st, lo,
-                           lmap, umap, qs, g.nx, g.ny);
+        if (rows) {
+          if (qkind == Q_AFFINE)
+            launch_rows_stage<T, Q_AFFINE>(g.grid, stream, y, c, e, l, m, n, st, lo, lmap, qs, g.nx, g.ny);
+          else if (qkind == Q_FORCED)
+            launch_rows_stage<T, Q_FORCED>(g.grid, stream, y, c, e, l, m, n, st, lo, lmap, qs, g.nx, g.ny);
+          else if (qkind == Q_ABSMAX)
+            launch_rows_stage<T, Q_ABSMAX>(g.grid, stream, y, c, e, l, m, n, st, lo, lmap, qs, g.nx, g.ny);
+          else
+            launch_rows_stage<T, Q_ROUND>(g.grid, stream, y, c, e, l, m, n, st, lo, lmap, qs, g.nx, g.ny);
+        } else {
+          hipLaunchKernelGGL(sweep_tiles_kernel<T>, g.grid, dim3(NTHREADS), 0, stream, y, c, e, l, u, m, n, st, lo,
+                             lmap, umap, qs, g.nx, g.ny);
+        }
       }
       // work of a tile sweep: its entries (the in-tile feedback is latency-, not throughput-bound)
       if (prof) gptq2d_prof_end(PROF_TILE_SWEEP, (double)B * (hi - lo + 1) * TR * TR, stream);
@@ -856,6 +1054,20 @@ extern "C" {
                           qmin, qmax, ypre, outer_tiles, stage_begin, stage_end, stream);                             \
   }                                                                                                                  \
   int64_t gptq2d_sweep_fused_tile_##SUF(void) { return TR; }                                                      \
+  int gptq2d_sweep_fused_se_##SUF(T* y, T* c, T* e, const T* l, const T* u, int64_t m, int64_t n, int64_t p,         \
+                                  int64_t q, int32_t bnd, const int64_t* bshape, const int64_t* lstride,             \
+                                  const int64_t* ustride, int32_t qkind, const T* qa, const int64_t* qa_stride,     \
+                                  const T* qb, const int64_t* qb_stride, double qmin, double qmax, int32_t dtype16, \
+                                  T* ypre, int64_t outer_tiles, int64_t stage_begin, int64_t stage_end,             \
+                                  hipStream_t stream) {                                                              \
+    if (p <= 0 || q <= 0 || m % p || n % q) return GPTQ2D_EINVAL;                                                  \
+    if (p == 1 && q == 1 && qkind != Q_ABSMAX)                                                                       \
+      return sweep_fused<T>(y, c, e, l, u, m, n, bnd, bshape, lstride, ustride, qkind, qa, qa_stride, qb, qb_stride, \
+                            qmin, qmax, ypre, outer_tiles, stage_begin, stage_end, stream);                          \
+    if (p != 1 || q != TR) return GPTQ2D_EUNSUPPORTED;                                                              \
+    return sweep_fused<T>(y, c, e, l, u, m, n, bnd, bshape, lstride, ustride, qkind, qa, qa_stride, qb, qb_stride,   \
+                          qmin, qmax, ypre, outer_tiles, stage_begin, stage_end, stream, true, dtype16);             \
+  }                                                                                                                  \
   int gptq2d_sweep_fused_noalloc_##SUF(T* y, const T* l, const T* u, int64_t m, int64_t n, int32_t bnd,              \
                                        const int64_t* bshape, const int64_t* lstride, const int64_t* ustride,       \
                                        int32_t qkind, const T* qa, const int64_t* qa_stride, const T* qb,           \

@@ -6,10 +6,11 @@ are antidiagonals s = i + j; each rounds its entries at once and feeds the error
 
 Two engines sit behind the same API:
 
-* the fused tile sweep (built-in per-entry quantizers: ``round_quantizer``, the affine plug-ins,
-  ``teacher_forced_quantizer``; plain entries): one C-ABI call runs the whole sweep as a stream of
-  HIP kernels -- LDS-resident tile sweeps with the rounding fused in, and masked band GEMMs for
-  the feedback between tiles (``csrc/sweep_tiles.hip``, ``csrc/flush.hip``);
+* the fused tile sweep (built-in quantizers: ``round_quantizer``, the affine plug-ins,
+  ``teacher_forced_quantizer``, and for 1 x 32 super-entries also the abs-max plug-ins; plain entries
+  or 1 x 32 super-entries): one C-ABI call runs the whole sweep as a stream of HIP kernels --
+  LDS-resident tile sweeps with the rounding fused in, and masked band GEMMs for the feedback
+  between tiles (``csrc/sweep_tiles.hip``, ``csrc/flush_mfma.hip``, ``csrc/flush.hip``);
 * the plug-in path (any Python quantizer, any super-entry shape): the host calls the quantizer
   once per antidiagonal and HIP kernels push the errors inside the current block and flush whole
   blocks, with the reference's two-level blocking (``csrc/sweep_generic.hip``).
@@ -126,11 +127,18 @@ def _matrix_input(t, y, batch_shape):
     return t.contiguous()
 
 
-def _fused_spec(quantizer, quantizer_inputs, y, batch_shape):
-    """Recognise a built-in per-entry quantizer the tile sweep can fuse; None for any other plug-in."""
+def _fused_spec(quantizer, quantizer_inputs, y, batch_shape, rows=False):
+    """Recognise a built-in quantizer the tile sweep can fuse; None for any other plug-in.  ``rows``: super-entries
+    of one tile row (1 x TILE), where the abs-max quantizer of a super-entry row is fused too."""
     fn, kw = _unwrap(quantizer)
     if fn in (round_quantizer, round_quantizer_super_entry) and not kw and not quantizer_inputs:
         return dict(kind=0, qa=None, qb=None, qmin=0.0, qmax=0.0, ypre=None)
+    if rows and fn in (_qi.int_abs_max_quantizer_hip, _qi.int_abs_max_quantizer_torch) and set(kw) == {
+            "qmin", "qmax", "dtype"} and not quantizer_inputs:
+        if kw["dtype"] not in _qi._SCALE_DTYPES or not float(kw["qmin"]) < float(kw["qmax"]):
+            return None
+        return dict(kind=3, qa=None, qb=None, qmin=float(kw["qmin"]), qmax=float(kw["qmax"]), ypre=None,
+                    dtype16=_qi._SCALE_DTYPES[kw["dtype"]])
     if fn in (_qi.affine_quantizer_hip, _qi.affine_quantizer_torch, _qi.affine_quantizer_super_entry_hip,
               _qi.affine_quantizer_super_entry_torch) and set(kw) <= {"qmin", "qmax"}:
         if len(quantizer_inputs) != 2:
@@ -156,7 +164,7 @@ def _outer_tiles(outer_block_size):
     return max(1, int(outer_block_size) // TILE) if outer_block_size and outer_block_size > 0 else 1
 
 
-def _run_fused(y, l, u, m, n, batch_shape, spec, outer_block_size):
+def _run_fused(y, l, u, m, n, batch_shape, spec, outer_block_size, p=1, q=1):
     B = batch_shape.numel()
     yb = y.reshape(B, m, n)
     c = torch.empty_like(yb)  # zeroed by the library
@@ -165,11 +173,11 @@ def _run_fused(y, l, u, m, n, batch_shape, spec, outer_block_size):
     nd = len(batch_shape)
     qa, qb = spec["qa"], spec["qb"]
     _hip.call(
-        "sweep_fused", y.dtype, _hip.ptr(yb), _hip.ptr(c), _hip.ptr(e), _hip.ptr(l), _hip.ptr(u), m, n, nd, bshape,
-        _hip.batch_strides(l, batch_shape), _hip.batch_strides(u, batch_shape), spec["kind"], _hip.ptr(qa),
+        "sweep_fused_se", y.dtype, _hip.ptr(yb), _hip.ptr(c), _hip.ptr(e), _hip.ptr(l), _hip.ptr(u), m, n, p, q, nd,
+        bshape, _hip.batch_strides(l, batch_shape), _hip.batch_strides(u, batch_shape), spec["kind"], _hip.ptr(qa),
         _hip.batch_strides(qa, batch_shape) if qa is not None else None, _hip.ptr(qb),
         _hip.batch_strides(qb, batch_shape) if qb is not None else None, spec["qmin"], spec["qmax"],
-        _hip.ptr(spec["ypre"]), _outer_tiles(outer_block_size), 0, -1, _hip.stream(y.device),
+        spec.get("dtype16", 0), _hip.ptr(spec["ypre"]), _outer_tiles(outer_block_size), 0, -1, _hip.stream(y.device),
     )
 
 
@@ -236,12 +244,13 @@ def _sweep(x, l, u, quantizer, super_entry_shape, inner_block_size, outer_block_
         return y
     l, u = l.contiguous(), u.contiguous()
     spec = None
-    if fused is not False and p == q == 1:
-        spec = _fused_spec(quantizer, quantizer_inputs, y, batch_shape)
-    assert not (fused is True and spec is None), "fused=True needs a built-in per-entry quantizer and plain entries"
+    if fused is not False and (p, q) in ((1, 1), (1, TILE)):
+        spec = _fused_spec(quantizer, quantizer_inputs, y, batch_shape, rows=(p, q) == (1, TILE))
+    assert not (fused is True and spec is None), (
+        "fused=True needs a built-in quantizer and plain entries or 1 x 32 super-entries")
     with torch.cuda.device(x.device):
         if spec is not None:
-            _run_fused(y, l, u, m, n, batch_shape, spec, outer_block_size)
+            _run_fused(y, l, u, m, n, batch_shape, spec, outer_block_size, p, q)
         else:
             _run_blocked(y, l, u, m, n, batch_shape, p, q, super_entry_shape is not None, quantizer,
                          quantizer_inputs, inner_block_size, outer_block_size)
@@ -275,7 +284,9 @@ def gptq_2d_super_entry(x, l, u, *, quantizer: Callable = round_quantizer_super_
 
     The quantizer receives a ``select`` callable viewing any [..., m*n] tensor as the [..., d, p, q]
     super-entries of the current coarse antidiagonal.  L and U have implicit identity p x p and
-    q x q diagonal blocks.  1 x 1 super-entries with a built-in per-entry quantizer run fused.
+    q x q diagonal blocks.  1 x 1 super-entries with a built-in per-entry quantizer, and 1 x 32
+    super-entries with a built-in per-entry or abs-max quantizer, run fused (``outer_block_size``
+    then counts entry antidiagonals of 32-wide tiles, as for ``gptq_2d``).
     """
     return _sweep(x, l, u, quantizer, tuple(super_entry_shape), inner_block_size, outer_block_size, inplace,
                   quantizer_inputs, fused)

@@ -48,6 +48,18 @@ extern "C" {
                                int32_t qkind, const T* qa, const int64_t* qa_stride, const T* qb,                   \
                                const int64_t* qb_stride, double qmin, double qmax, T* ypre, int64_t outer_tiles,    \
                                int64_t stage_begin, int64_t stage_end, void* stream);                               \
+  /* The fused sweep over p x q super-entries (gptq_2d_super_entry, gptq_2d.py:1421-1447, with a       \
+   * built-in quantizer): p = q = 1 is gptq2d_sweep_fused; p = 1, q = 32 (one super-entry per tile     \
+   * row, n % 32 == 0) sweeps each tile row by row, U's 32 x 32 diagonal blocks never read, with qkind \
+   * 0-2 as above per entry or 3: the abs-max INT quantizer of each super-entry row from its current     \
+   * values with the scale rounded to bf16 (dtype16 1) or fp16 (2) (int_abs_max_quantizer,              \
+   * quantizer_int.py:120-134, 408-470); other shapes GPTQ2D_EUNSUPPORTED.  Other arguments as above. */ \
+  int gptq2d_sweep_fused_se_##SUF(T* y, T* c, T* e, const T* l, const T* u, int64_t m, int64_t n, int64_t p,         \
+                                  int64_t q, int32_t bnd, const int64_t* bshape, const int64_t* l_stride,           \
+                                  const int64_t* u_stride, int32_t qkind, const T* qa, const int64_t* qa_stride,    \
+                                  const T* qb, const int64_t* qb_stride, double qmin, double qmax, int32_t dtype16, \
+                                  T* ypre, int64_t outer_tiles, int64_t stage_begin, int64_t stage_end,             \
+                                  void* stream);                                                                     \
   /* Tile edge of the fused sweep. */                                                                  \
   int64_t gptq2d_sweep_fused_tile_##SUF(void);                                                                       \
   /* The whole fused sweep (as gptq2d_sweep_fused with stage_begin 0, stage_end -1) with no c and e:     \
