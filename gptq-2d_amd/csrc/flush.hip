@@ -236,10 +236,10 @@ int gptq2d_flush(T* y, T* c, const T* e, const T* l, const T* u, int64_t m, int6
   if (m <= 0 || n <= 0 || P <= 0 || Q <= 0 || s0 < 0 || s1 <= s0 || s_end < s1) return GPTQ2D_EINVAL;
   if (B == 0 || s_end == s1) return 0;
   if constexpr (sizeof(T) == 4) {
-    // 32 x 32 coarse cells (the fused engine's tiles, or 32 x 32 super-entries): fp32 MFMA
-    // (staging uses 32-bit byte offsets: every operand matrix under 2^31 bytes)
-    const int64_t big = m > n ? m : n;
-    if (P == 32 && Q == 32 && big * big < ((int64_t)1 << 29) - 16) {
+    // 32 x 32 coarse cells (the fused engine's tiles, or 32 x 32 super-entries): fp32 MFMA (its buffer
+    // resources are based at each panel, so 32-bit offsets hold for rows and k-tiles of up to 2^20
+    // elements, i.e. any m, n < 2^20)
+    if (P == 32 && Q == 32 && m < ((int64_t)1 << 20) && n < ((int64_t)1 << 20)) {
       const bool prof = gptq2d_prof_on(PROF_FLUSH);
       if (prof) gptq2d_prof_begin(PROF_FLUSH, stream);
       const int rc = gptq2d_flush_tiles_mfma(y, c, e, l, u, m, n, s0, s1, s_end, lmap, umap, B, stream);

@@ -109,10 +109,22 @@ struct FlushLds {
   float b[2][BSZ];
 };
 
-// One product phase (0: D = L E, 1: R = C U) of a workgroup, accumulated into acc.
+// Buffer resource over the elements [first, total) of a matrix stored from `base`: offsets count from
+// element `first`, so that they stay small whatever the matrix size (extents capped below OOB).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rebased_rsrc(const float* base, int64_t first, int64_t total) {
+  int64_t elems = total - first;
+  const int64_t cap = (OOB >> 2) - 64;
+  elems = elems < 0 ? 0 : (elems > cap ? cap : elems);
+  return matrix_rsrc(base + first, elems);
+}
+
+// One product phase (0: D = L E, 1: R = C U) of a workgroup, accumulated into acc.  a_mat / b_mat: the
+// operand matrices (a_elems / b_elems elements): A is staged through a buffer resource based at the
+// workgroup's first row, B through one based at each k-tile's first row and the workgroup's first
+// column, so that every offset stays below 2^31 bytes for any matrix a tile row or a k-tile of which does.
 template <int WT, bool VEC, int PHASE>
-__device__ __forceinline__ void flush_phase(floatx16 (&acc)[WT / 2][WT / 2], FlushLds<WT>& sm,
-                                            __amdgpu_buffer_rsrc_t ra_src, __amdgpu_buffer_rsrc_t rb_src,
+__device__ __forceinline__ void flush_phase(floatx16 (&acc)[WT / 2][WT / 2], FlushLds<WT>& sm, const float* a_mat,
+                                            int64_t a_elems, const float* b_mat, int64_t b_elems,
                                             const TileFlush& g, int64_t I0, int64_t J0, int wi, int wj,
                                             int64_t t_lo, int64_t t_hi, const int (&tlo)[WT / 2][WT / 2],
                                             const int (&thi)[WT / 2][WT / 2]) {
@@ -126,7 +138,8 @@ __device__ __forceinline__ void flush_phase(floatx16 (&acc)[WT / 2][WT / 2], Flu
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: LDS bases in scalar registers
   const int kmax = (int)(PHASE == 0 ? g.m : g.n);  // k extent of both operands
   const int alda = (int)(PHASE == 0 ? g.m : g.n);  // row stride of A (L or C)
-  const int gm = (int)g.m, gn = (int)g.n, s0 = (int)g.S0, s1 = (int)g.S1;  // < 2^15: 32-bit index math
+  const int gm = (int)g.m, gn = (int)g.n, s0 = (int)g.S0, s1 = (int)g.S1;  // < 2^20: 32-bit index math
+  const __amdgpu_buffer_rsrc_t ra_src = rebased_rsrc(a_mat, I0 * TS * (int64_t)alda, a_elems);
 
   // per-lane staging geometry of load x: A row i (tile at, k offset akk), B column j (tile bt, k row
   // kb); loop-invariant, so kept in registers for the 128-bit path (NI = 4) and recomputed for the
@@ -143,12 +156,12 @@ __device__ __forceinline__ void flush_phase(floatx16 (&acc)[WT / 2][WT / 2], Flu
     const int i = (int)I0 * TS + row;
     o.a_in = i < gm;
     o.a_t = i >> 5;
-    o.a_off = ((o.a_in ? i * alda : 0) + o.a_kk) * 4;
+    o.a_off = ((o.a_in ? row * alda : 0) + o.a_kk) * 4;  // from the workgroup's first row
     o.b_kb = f / ROWS;
     const int j = (int)J0 * TS + f % ROWS;
     o.b_in = j < gn;
     o.b_t = j >> 5;
-    o.b_off = (o.b_kb * gn + (o.b_in ? j : 0)) * 4;
+    o.b_off = (o.b_kb * gn + (o.b_in ? f % ROWS : 0)) * 4;  // from the k-tile's first row, the first column
     return o;
   };
   Geo pre[VEC ? NI : 1];
@@ -161,6 +174,7 @@ __device__ __forceinline__ void flush_phase(floatx16 (&acc)[WT / 2][WT / 2], Flu
   // diagonal tiles, C and E on the band, U strictly above its diagonal tiles, nothing outside)
   auto issue = [&](int64_t t, int buf) {
     const int ts = (int)t, k0 = ts * TS;
+    const __amdgpu_buffer_rsrc_t rb_src = rebased_rsrc(b_mat, (int64_t)k0 * gn + J0 * TS, b_elems);
 #pragma unroll
     for (int x = 0; x < NI; ++x) {
       const Geo o = VEC ? pre[x] : geo(x);
@@ -170,7 +184,7 @@ __device__ __forceinline__ void flush_phase(floatx16 (&acc)[WT / 2][WT / 2], Flu
       dma_load<W>(ra_src, &sm.a[buf][f0], aok ? o.a_off + k0 * 4 : OOB);
       const bool bband = PHASE == 0 ? (ts + o.b_t >= s0 && ts + o.b_t < s1) : ts < o.b_t;
       const bool bok = o.b_in && bband && k0 + o.b_kb < kmax;
-      dma_load<W>(rb_src, &sm.b[buf][f0 + f0 / 256 * L::BPAD], bok ? o.b_off + k0 * gn * 4 : OOB);
+      dma_load<W>(rb_src, &sm.b[buf][f0 + f0 / 256 * L::BPAD], bok ? o.b_off : OOB);
     }
   };
 
@@ -323,14 +337,13 @@ __global__ __launch_bounds__(256, 2) void flush_tiles_mfma_kernel(float* __restr
       for (int r = 0; r < 16; ++r) acc[a][d][r] = 0.f;
 
   // phase 0: D = L E, then C += D; phase 1: R = C U on top of D, then Y += D + R
-  const __amdgpu_buffer_rsrc_t rl = matrix_rsrc(l + lmap.offset(b), g.m * g.m);
-  const __amdgpu_buffer_rsrc_t re = matrix_rsrc(e + mat, g.m * g.n);
-  const __amdgpu_buffer_rsrc_t rc = matrix_rsrc(c + mat, g.m * g.n);
-  const __amdgpu_buffer_rsrc_t ru = matrix_rsrc(u + umap.offset(b), g.n * g.n);
-  flush_phase<WT, VEC, 0>(acc, sm, rl, re, g, I0, J0, wi, wj, lo0, hi0, tlo[0], thi[0]);
+  const float* lm = l + lmap.offset(b);
+  const float* um = u + umap.offset(b);
+  flush_phase<WT, VEC, 0>(acc, sm, lm, g.m * g.m, e + mat, g.m * g.n, g, I0, J0, wi, wj, lo0, hi0, tlo[0], thi[0]);
 #pragma unroll
   for (int ph = 0; ph < 2; ++ph) {
-    if (ph == 1) flush_phase<WT, VEC, 1>(acc, sm, rc, ru, g, I0, J0, wi, wj, lo1, hi1, tlo[1], thi[1]);
+    if (ph == 1)
+      flush_phase<WT, VEC, 1>(acc, sm, c + mat, g.m * g.n, um, g.n * g.n, g, I0, J0, wi, wj, lo1, hi1, tlo[1], thi[1]);
     // epilogue of the phase: C += D after the down products, Y += D + R after the right ones
 #pragma unroll
     for (int a = 0; a < H; ++a)
@@ -340,14 +353,16 @@ __global__ __launch_bounds__(256, 2) void flush_tiles_mfma_kernel(float* __restr
                                  : (tlo[0][a][d] < thi[0][a][d] || tlo[1][a][d] < thi[1][a][d]);
         if (!has) continue;
         const int64_t I = I0 + wi + a, J = J0 + wj + d;
-        const __amdgpu_buffer_rsrc_t rd = ph == 0 ? rc : matrix_rsrc(y + mat, g.m * g.n);
+        // the target tile's rows from a resource based at its first row (offsets below 2^31 bytes)
+        const __amdgpu_buffer_rsrc_t rd = rebased_rsrc(ph == 0 ? c + mat : y + mat, I * TS * g.n, g.m * g.n);
         // all 16 reads in flight before the first write; masked lanes address past the matrix
         int off[16];
         float cur[16];
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const int64_t i = I * TS + 8 * (r >> 2) + 4 * hh + (r & 3), j = J * TS + li;
-          off[r] = (i < g.m && j < g.n) ? (int)(i * g.n + j) * 4 : OOB;
+          const int ri = 8 * (r >> 2) + 4 * hh + (r & 3);
+          const int64_t i = I * TS + ri, j = J * TS + li;
+          off[r] = (i < g.m && j < g.n) ? (ri * (int)g.n + (int)j) * 4 : OOB;
           cur[r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rd, off[r], 0, 0));
         }
 #pragma unroll

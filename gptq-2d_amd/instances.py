@@ -112,3 +112,33 @@ def layer(cfg: Config, device="cpu", factor_device=None):
     a = wishart_factor(cfg.m, cfg.alpha, sa, fd).to(device)
     b = wishart_factor(cfg.n, cfg.alpha, sb, fd).to(device)
     return w, a, b
+
+
+@dataclasses.dataclass
+class ThreeFactorConfig:
+    """W [m, n1 n2] (columns c = b1 n2 + b2) under the Hessian A (m) (x) B1 (n1) (x) B2 (n2), quantized in
+    1 x ``group`` super-entries with the abs-max INT quantizer (qmin..qmax, bf16 scales)."""
+    name: str
+    m: int
+    n1: int
+    n2: int
+    alpha: float
+    qmin: int
+    qmax: int
+    group: int
+    seeds: tuple  # W, A, B1, B2
+
+
+THREE_FACTOR = {
+    "C5a": ThreeFactorConfig("C5a", 8192, 112, 256, 0.5, -8, 7, 32, (0, 1, 3, 4)),
+}
+
+
+def three_factor_layer(cfg: ThreeFactorConfig, device="cpu"):
+    """(W, A, B1, B2) in fp64 on ``device``: W with 0.5% outliers, Wishart-like factors (s_i = i^-alpha)."""
+    sw, sa, sb1, sb2 = cfg.seeds
+    w = weights(cfg.m, cfg.n1 * cfg.n2, sw, True, False).to(device)
+    a = wishart_factor(cfg.m, cfg.alpha, sa, device)
+    b1 = wishart_factor(cfg.n1, cfg.alpha, sb1, device)
+    b2 = wishart_factor(cfg.n2, cfg.alpha, sb2, device)
+    return w, a, b1, b2

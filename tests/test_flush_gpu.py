@@ -70,3 +70,39 @@ def test_flush(m, n, P, Q, s0, s1, s_end, dtype):
     for got, exp in ((gy, ey), (gc, ec)):
         err = ((got[tgt] - exp[tgt]).abs() / (1 + exp[tgt].abs())).max().item() if tgt.any() else 0.
         assert err < tol * max(1., (m + n) ** .5), err
+
+
+def test_flush_mfma_large_operand():
+    """The MFMA flush on a layer whose U has more than 2^29 entries (n = 24576): the staging resources are
+    based at each panel, so the 32-bit offsets hold and the result matches the dense statement (computed on
+    the GPU in fp64), with NaN everywhere the flush must not read."""
+    m, n, P, Q, s0, s1, s_end = 96, 24576, 32, 32, 100, 110, 400
+    print(f"flush {m}x{n} [{s0},{s1})->[{s1},{s_end}) fp32, U with {n * n} entries", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(5)
+    y, c, e = (torch.randn(m, n, generator=g, device=DEV, dtype=torch.float64) for _ in range(3))
+    l = torch.randn(m, m, generator=g, device=DEV, dtype=torch.float64) / m ** .5
+    i = torch.arange(m, device=DEV)[:, None]
+    j = torch.arange(n, device=DEV)[None, :]
+    st = i // P + j // Q
+    band = (st >= s0) & (st < s1)
+    tgt = (st >= s1) & (st < s_end)
+    lm = torch.where(i.t() // P < i // P, l, 0.)
+    d = lm @ torch.where(band, e, 0.)
+    u = torch.randn(n, n, generator=g, device=DEV, dtype=torch.float32) / n ** .5
+    ar = torch.arange(n, device=DEV)
+    upper = (ar[:, None] // Q) < (ar[None, :] // Q)
+    r = torch.where(band, c.float().double(), 0.) @ torch.where(upper, u, 0.).double()
+    ey = torch.where(tgt, (y.float().double() + d) + r, y)
+    u.masked_fill_(~upper, torch.nan)
+    del upper
+    yd, cd = y.float().contiguous(), c.float().masked_fill(~band & ~tgt, torch.nan).contiguous()
+    ed = e.float().masked_fill(~band, torch.nan).contiguous()
+    ld = l.float().masked_fill(i.t() // P >= i // P, torch.nan).contiguous()
+    one = _hip.i64_array([])
+    _hip.call("flush", torch.float32, _hip.ptr(yd), _hip.ptr(cd), _hip.ptr(ed), _hip.ptr(ld), _hip.ptr(u), m, n, P, Q,
+              s0, s1, s_end, 0, one, one, one, _hip.stream(yd.device))
+    torch.cuda.synchronize()
+    assert torch.equal(yd[~tgt], y.float()[~tgt])
+    err = ((yd.double()[tgt] - ey[tgt]).abs() / (1 + ey[tgt].abs())).max().item()
+    print(f"  max rel err {err:.2e}", flush=True)
+    assert err < 2e-5 * (m + n) ** .5
