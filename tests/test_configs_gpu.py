@@ -239,6 +239,81 @@ def test_c5a_full_size():
     assert agree >= 0.999
 
 
+def _trellis_rows(v, table, scale, K, rows_per_call=512):
+    """Trellis quantization of every 16 x 16 block of v (read row by row) on its own, in calls of
+    ``rows_per_call`` sequences (the search's history workspace is 2 MB per sequence at L = 16)."""
+    m, n = v.shape
+    seqs = (v.view(m // 16, 16, n // 16, 16).permute(0, 2, 1, 3).reshape(-1, 256) / scale).contiguous()
+    out = torch.empty_like(seqs)
+    sc = torch.full((seqs.size(0),), float(scale), device=v.device, dtype=v.dtype)
+    for r0 in range(0, seqs.size(0), rows_per_call):
+        QT.trellis_quantize_hip(seqs[r0:r0 + rows_per_call], table, K, True, out=out[r0:r0 + rows_per_call],
+                                scale=sc[r0:r0 + rows_per_call])
+    return out.view(m // 16, n // 16, 16, 16).permute(0, 2, 1, 3).reshape(m, n)
+
+
+@pytest.mark.timeout(900)
+def test_c4_full_size():
+    """C4: 8192^2 weights (the headline layer's distribution) in 16 x 16 super-entries under the HYB trellis code,
+    L = 16, K = 2, V = 2, tail-biting, scale RMS(W) / (0.9 RMS(table)) (demo.ipynb:541-545), fp32 plug-in engine
+    with the one-launch HIP search per stage.  Checks: bitwise determinism; every output pair is a row of the
+    code table times the scale; the objective is below quantizing each super-entry of W on its own; and on the
+    first 4 coarse antidiagonals the values agree with the CPU oracle (super-entry Algorithm 3 with the PyTorch
+    search on the cropped layer, which holds every entry they depend on) in >= 99% of the entries."""
+    m = n = 8192
+    print(f"C4: {m}x{n}, 16x16 super-entries, HYB L=16 K=2 V=2", flush=True)
+    x = instances.weights(m, n, 0, True, False).float().to(DEV)
+    a = _gpu_factor(m, .5, 31)
+    b = _gpu_factor(n, .5, 32)
+    lo = LDL.ldl_of_inverse(a.float(), size=16)
+    up = LDL.ldl_of_inverse(b.float(), size=16).t().contiguous()
+    table_cpu = OT.hyb(L=16)  # the pinned CPU table (golden fixture), on both sides
+    table = table_cpu.to(DEV)
+    scale = x.pow(2).mean().sqrt() / (0.9 * table.pow(2).mean().sqrt())
+    q = functools.partial(QT.trellis_quantizer_super_entry_hip, table=table, K=2)
+    run = functools.partial(G.gptq_2d_super_entry, x, lo, up, super_entry_shape=(16, 16), quantizer=q,
+                            quantizer_inputs=(scale,))
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    z = run()
+    torch.cuda.synchronize()
+    print(f"  layer sweep {time.perf_counter() - t0:.2f} s", flush=True)
+    assert run().equal(z), "not deterministic"
+
+    def keys(pairs):
+        bits = pairs.contiguous().view(torch.int32).to(torch.int64) & 0xFFFFFFFF
+        return (bits[..., 0] << 32) | bits[..., 1]
+
+    grid = keys(table * scale)
+    assert torch.isin(keys(z.view(m, n // 2, 2)), grid).all(), "values off the code grid"
+
+    def objective(zz):
+        r = (zz - x).double()
+        return float(((a @ r) * (r @ b)).sum())
+
+    ratio = objective(z) / objective(_trellis_rows(x, table, scale, 2))
+    print(f"  objective / no-feedback trellis = {ratio:.4f}", flush=True)
+    assert ratio < 1.
+
+    K = 4
+    W = 16 * K
+    xc, lc, uc = x[:W, :W].cpu(), lo[:W, :W].cpu(), up[:W, :W].cpu()
+    sc = scale.cpu()
+
+    def oq(y, i, j):
+        out = torch.empty_like(y)
+        OT.trellis_quantizer_super_entry(y, lambda t: t, sc, out=out, table=table_cpu, K=2)
+        return out
+
+    zo = A.alg3_super_entry(xc, S.unit_triangular(lc, False, 16), S.unit_triangular(uc, True, 16), Q=oq,
+                            super_entry_shape=(16, 16))
+    win = (torch.arange(W)[:, None] // 16 + torch.arange(W)[None, :] // 16) < K
+    agree = float((z[:W, :W].cpu()[win] == zo[win]).double().mean())
+    print(f"  first {K} coarse antidiagonals ({int(win.sum())} entries): agreement with the oracle {agree:.4%}",
+          flush=True)
+    assert agree >= 0.99
+
+
 def test_c5b_batch_capture():
     """C5b: a batch of 8 independent 2048 x 2048 INT4 layers in one hipGraph-captured call: every replay equals
     the eager batched call, which equals the eight layers quantized one at a time (bitwise)."""
