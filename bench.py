@@ -68,7 +68,31 @@ def _parse():
     ap.add_argument("--config", default="H", help="workload from instances.CONFIGS (default: the headline layer)")
     ap.add_argument("--cpu-stages", type=int, default=4096, help="sweep stages in the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--configs", default="C2,C3,C4,C5a,C5b",
+                    help="comma-separated other configurations to time after the headline layer ('' for none)")
     return ap.parse_args()
+
+
+def _physical_cores():
+    """(physical cores, logical CPUs) among the CPUs this process may run on (from /proc/cpuinfo)."""
+    allowed = os.sched_getaffinity(0) if hasattr(os, "sched_getaffinity") else set(range(os.cpu_count() or 1))
+    cores, proc, phys, core = set(), None, None, None
+    try:
+        for line in open("/proc/cpuinfo"):
+            key, _, val = line.partition(":")
+            key, val = key.strip(), val.strip()
+            if key == "processor":
+                proc, phys, core = int(val), None, None
+            elif key == "physical id":
+                phys = val
+            elif key == "core id":
+                core = val
+            if proc is not None and phys is not None and core is not None and proc in allowed:
+                cores.add((phys, core))
+                proc = None
+    except OSError:
+        pass
+    return (len(cores) or len(allowed)), len(allowed)
 
 
 def _cpu_model() -> str:
@@ -90,7 +114,9 @@ def _cpu_baseline(cfg, x, a, b, scale, zp, l_dev, u_dev, stages_in_sample):
     from oracle import quantize as OQ
     from oracle import sweep as OS
 
-    threads = torch.get_num_threads()
+    cores, logical = _physical_cores()
+    threads = cores
+    torch.set_num_threads(threads)
     ac, bc = a.cpu(), b.cpu()
     t0 = time.perf_counter()
     OA.ldl_of_inverse(ac)
@@ -119,7 +145,8 @@ def _cpu_baseline(cfg, x, a, b, scale, zp, l_dev, u_dev, stages_in_sample):
         "unit": "s/layer",
         "cores": threads,
         "kind": "port",
-        "sample": (f"restated reference PyTorch path on {threads} threads of {_cpu_model()}: ldl_of_inverse(A) "
+        "sample": (f"restated reference PyTorch path on {threads} threads ({cores} physical cores of the {logical} "
+                   f"logical CPUs this process may use) of {_cpu_model()}: ldl_of_inverse(A) "
                    f"{t_ldl_a:.2f} s and ldl_of_inverse(B) {t_ldl_b:.2f} s in full; gptq_2d_torch {len(sample)} of "
                    f"{stages} stages on the full {m}x{n} tensors ({t_sample:.1f} s), extrapolated by exact "
                    f"per-stage work to {t_sweep:.1f} s"),
@@ -156,6 +183,132 @@ def _viterbi_bench(torch, dev, steps_timed=3):
         "roofline": {"bound": "valu", "achieved": ops / sec / 1e12, "peak": VALU_FP32_OPS_PEAK / 1e12,
                      "unit": "Tops/s (fp32, 7 per state evaluation)", "frac": ops / sec / VALU_FP32_OPS_PEAK},
     }
+
+
+def _timed(torch, fn, steps, warmup=1):
+    """Seconds per call of fn (synchronised around the timed calls), after warmup calls."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        fn()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / steps
+
+
+def _config_lines(torch, dev, h_layer, names, steps=2):
+    """Layer time (feedback factors + sweep, each timed on its own) of the other benchmark configurations on
+    one GPU: C2 and C3 (fused sweep, affine INT quantizers), C4 (the headline layer's weights and factors in
+    16 x 16 super-entries, HYB trellis search per stage), C5a (three-factor layer, 1 x 32 abs-max super-entries,
+    fused), C5b (eight 2048^2 layers in one captured graph replay)."""
+    import gptq_2d as G
+    import gptq_2d_ldl as LDL
+    import instances
+    import quantizer_int as QI
+
+    lines = {}
+
+    def line(workload, t_ldl, t_sweep, **extra):
+        return {"workload": workload, "layer_s": round(t_ldl + t_sweep, 5), "factors_ms": round(1e3 * t_ldl, 3),
+                "sweep_ms": round(1e3 * t_sweep, 3), **extra}
+
+    for name in [nm for nm in ("C2", "C3") if nm in names]:
+        cfg = instances.CONFIGS[name]
+        x = instances.weights(cfg.m, cfg.n, cfg.seeds[0], cfg.outliers, cfg.bf16).float().to(dev)
+        a = instances.wishart_factor(cfg.m, cfg.alpha, cfg.seeds[1], device=dev).float()
+        b = instances.wishart_factor(cfg.n, cfg.alpha, cfg.seeds[2], device=dev).float()
+        scale, zp = instances.quantizer_inputs(cfg, x)
+        q = functools.partial(QI.affine_quantizer_hip, qmin=cfg.qmin, qmax=cfg.qmax)
+        factors = lambda: LDL.feedback_factors_of_grams(a, b, check=False)
+        lo, up = factors()
+        t_ldl = _timed(torch, factors, steps)
+        t_sw = _timed(torch, lambda: G.gptq_2d(x, lo, up, quantizer=q, quantizer_inputs=(scale, zp),
+                                               outer_block_size=OUTER_BLOCK), steps)
+        kind = "INT4 asymmetric per (row, 128 columns)" if cfg.quantizer == "int_g128" else (
+            f"INT{(cfg.qmax - cfg.qmin + 1).bit_length() - 1} symmetric per row")
+        lines[name] = line(f"{cfg.m}x{cfg.n} {kind}, fused sweep", t_ldl, t_sw)
+        del x, a, b, scale, zp, lo, up
+
+    x, a, b = h_layer
+    m, n = x.shape
+    if "C4" in names:
+        _c4_line(torch, dev, x, a, b, steps, lines, line)
+    if "C5a" in names:
+        _c5a_line(torch, dev, a, m, steps, lines, line)
+    if "C5b" in names:
+        _c5b_line(torch, dev, steps, lines, line)
+    return lines
+
+
+def _c4_line(torch, dev, x, a, b, steps, lines, line):
+    import gptq_2d as G
+    import gptq_2d_ldl as LDL
+    import quantizer_trellis as QT
+
+    m, n = x.shape
+    table = QT.hyb(L=16).to(dev)  # the tlut's k-means on the CPU (the pinned table), then moved
+    scale = x.pow(2).mean().sqrt() / (0.9 * table.pow(2).mean().sqrt())
+    q = functools.partial(QT.trellis_quantizer_super_entry_hip, table=table, K=2)
+    factors = lambda: LDL.feedback_factors_of_grams(a, b, super_entry_shape=(16, 16), check=False)
+    lo, up = factors()
+    t_ldl = _timed(torch, factors, steps)
+    t_sw = _timed(torch, lambda: G.gptq_2d_super_entry(x, lo, up, super_entry_shape=(16, 16), quantizer=q,
+                                                       quantizer_inputs=(scale,)), 1)
+    lines["C4"] = line(f"{m}x{n} HYB trellis L=16 K=2 V=2 tail-biting, 16x16 super-entries, per-stage HIP "
+                       "search", t_ldl, t_sw)
+
+
+def _c5a_line(torch, dev, a, m, steps, lines, line):
+    import gptq_2d as G
+    import gptq_2d_ldl as LDL
+    import instances
+    import quantizer_int as QI
+
+    cfg = instances.THREE_FACTOR["C5a"]
+    n = cfg.n1 * cfg.n2
+    w = instances.weights(cfg.m, n, cfg.seeds[0], True, False).float().to(dev)
+    a5 = a if cfg.seeds[1] == instances.CONFIGS["H"].seeds[1] and cfg.m == m else (
+        instances.wishart_factor(cfg.m, cfg.alpha, cfg.seeds[1], device=dev).float())
+    b1 = instances.wishart_factor(cfg.n1, cfg.alpha, cfg.seeds[2], device=dev).float()
+    b2 = instances.wishart_factor(cfg.n2, cfg.alpha, cfg.seeds[3], device=dev).float()
+    q = functools.partial(QI.int_abs_max_quantizer_hip, qmin=cfg.qmin, qmax=cfg.qmax, dtype=torch.bfloat16)
+
+    def factors5():
+        lo5 = LDL.ldl_of_inverse(a5, check=False)
+        up5 = torch.kron(LDL.ldl_of_inverse(b1, check=False).t().contiguous(),
+                         LDL.ldl_of_inverse(b2, size=cfg.group, check=False).t().contiguous())
+        return lo5, up5
+
+    lo, up = factors5()
+    t_ldl = _timed(torch, factors5, steps)
+    t_sw = _timed(torch, lambda: G.gptq_2d_super_entry(w, lo, up, super_entry_shape=(1, cfg.group), quantizer=q,
+                                                       outer_block_size=OUTER_BLOCK), steps)
+    lines["C5a"] = line(f"{cfg.m}x{n} = {cfg.m}x({cfg.n1}x{cfg.n2}), A (x) B1 (x) B2, INT4 abs-max per 1x{cfg.group} "
+                        "super-entry (bf16 scales), fused sweep; U = U_B1 (x) U_B2", t_ldl, t_sw)
+
+
+def _c5b_line(torch, dev, steps, lines, line):
+    import gptq_2d as G
+    import gptq_2d_ldl as LDL
+    import instances
+    import quantizer_int as QI
+
+    B, k = 8, 2048
+    xb = torch.stack([instances.weights(k, k, 100 + i, True, False) for i in range(B)]).float().to(dev)
+    ga = torch.stack([instances.wishart_factor(k, .5, 200 + i, device=dev) for i in range(B)]).float()
+    gb = torch.stack([instances.wishart_factor(k, .5, 300 + i, device=dev) for i in range(B)]).float()
+    sb = instances.abs_max_row_scale(xb, -8, 7).expand_as(xb).contiguous()
+    zb = torch.zeros_like(xb)
+    q = functools.partial(QI.affine_quantizer_hip, qmin=-8, qmax=7)
+    factors_b = lambda: (LDL.ldl_of_inverse(ga, check=False), LDL.ldl_of_inverse(gb, check=False).transpose(-1, -2))
+    lo, up = factors_b()
+    up = up.contiguous()
+    t_ldl = _timed(torch, factors_b, steps)
+    replay = G.capture_gptq_2d(xb, lo, up, quantizer=q, quantizer_inputs=(sb, zb), outer_block_size=OUTER_BLOCK)
+    t_sw = _timed(torch, lambda: replay(xb, lo, up, sb, zb), steps)
+    lines["C5b"] = line(f"{B} x {k}x{k} INT4 per row, batched factors + one hipGraph replay of the fused sweep "
+                        "(input copies included)", t_ldl, t_sw)
 
 
 def main() -> int:
@@ -278,6 +431,9 @@ def main() -> int:
         "viterbi": None,
         "cpu_baseline": None,
     }
+    names = [nm for nm in args.configs.split(",") if nm]
+    if names:
+        result["configs"] = _config_lines(torch, dev, (x, a, b), names)
     vit = _viterbi_bench(torch, dev)
     result["viterbi"] = vit
     result["viterbi_weights_per_s"] = vit["weights_per_s"]
