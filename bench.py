@@ -68,7 +68,7 @@ def _parse():
     ap.add_argument("--config", default="H", help="workload from instances.CONFIGS (default: the headline layer)")
     ap.add_argument("--cpu-stages", type=int, default=4096, help="sweep stages in the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--configs", default="C2,C3,C4,C5a,C5b",
+    ap.add_argument("--configs", default="C2,C3,C4,C5a,C5a3,C5b",
                     help="comma-separated other configurations to time after the headline layer ('' for none)")
     return ap.parse_args()
 
@@ -201,7 +201,8 @@ def _config_lines(torch, dev, h_layer, names, steps=2):
     """Layer time (feedback factors + sweep, each timed on its own) of the other benchmark configurations on
     one GPU: C2 and C3 (fused sweep, affine INT quantizers), C4 (the headline layer's weights and factors in
     16 x 16 super-entries, HYB trellis search per stage), C5a (three-factor layer, 1 x 32 abs-max super-entries,
-    fused), C5b (eight 2048^2 layers in one captured graph replay)."""
+    fused), C5a3 (the same layer three-sided, D-sided sweep), C5b (eight 2048^2 layers in one captured graph
+    replay)."""
     import gptq_2d as G
     import gptq_2d_ldl as LDL
     import instances
@@ -236,6 +237,8 @@ def _config_lines(torch, dev, h_layer, names, steps=2):
         _c4_line(torch, dev, x, a, b, steps, lines, line)
     if "C5a" in names:
         _c5a_line(torch, dev, a, m, steps, lines, line)
+    if "C5a3" in names:
+        _c5a3_line(torch, dev, steps, lines, line)
     if "C5b" in names:
         _c5b_line(torch, dev, steps, lines, line)
     return lines
@@ -286,6 +289,32 @@ def _c5a_line(torch, dev, a, m, steps, lines, line):
                                                        outer_block_size=OUTER_BLOCK), steps)
     lines["C5a"] = line(f"{cfg.m}x{n} = {cfg.m}x({cfg.n1}x{cfg.n2}), A (x) B1 (x) B2, INT4 abs-max per 1x{cfg.group} "
                         "super-entry (bf16 scales), fused sweep; U = U_B1 (x) U_B2", t_ldl, t_sw)
+
+
+def _c5a3_line(torch, dev, steps, lines, line):
+    """C5a's layer as the three-sided tensor X[i, b1, b2] (D-sided sweep), static abs-max INT4 scales per 32
+    consecutive b2; factors are the three mode LDLs (A, B1, B2)."""
+    import gptq_2d_ldl as LDL
+    import gptq_d_sided as DS
+    import instances
+    import quantizer_int as QI
+
+    cfg = instances.THREE_FACTOR["C5a"]
+    x = instances.weights(cfg.m, cfg.n1 * cfg.n2, cfg.seeds[0], True, False).float().view(
+        cfg.m, cfg.n1, cfg.n2).to(dev)
+    grams = [instances.wishart_factor(k, cfg.alpha, s, device=dev).float()
+             for k, s in zip((cfg.m, cfg.n1, cfg.n2), cfg.seeds[1:])]
+    scale = instances.abs_max_group_scale(x, cfg.group, cfg.qmin, cfg.qmax)
+    zero = torch.zeros_like(x)
+    q = functools.partial(QI.affine_quantizer_hip, qmin=cfg.qmin, qmax=cfg.qmax)
+    factors = lambda: [LDL.ldl_of_inverse(g, check=False) for g in grams]
+    ls = factors()
+    t_ldl = _timed(torch, factors, steps)
+    t_sw = _timed(torch, lambda: DS.gptq_d_sided(x, ls, quantizer=q, quantizer_inputs=(scale, zero),
+                                                 outer_block_size=OUTER_BLOCK), steps)
+    lines["C5a3"] = line(f"{cfg.m}x{cfg.n1}x{cfg.n2} three-sided (D-sided sweep on the two-sided engine, U = "
+                         f"(L_B2 (x) L_B1)^T formed per call), static INT4 abs-max scale per {cfg.group} b2 (bf16)",
+                         t_ldl, t_sw)
 
 
 def _c5b_line(torch, dev, steps, lines, line):

@@ -59,6 +59,13 @@ def abs_max_row_scale(w: torch.Tensor, qmin: int, qmax: int, dtype=torch.bfloat1
     return s.masked_fill_(s == 0, 1.)
 
 
+def abs_max_group_scale(w: torch.Tensor, group: int, qmin: int, qmax: int, dtype=torch.bfloat16) -> torch.Tensor:
+    """Static symmetric scale of each run of ``group`` consecutive entries along w's last mode (the abs-max
+    scale of ``abs_max_row_scale`` per run), as a full tensor shaped like w."""
+    runs = w.reshape(*w.shape[:-1], w.size(-1) // group, group)
+    return abs_max_row_scale(runs, qmin, qmax, dtype).expand_as(runs).reshape(w.shape).contiguous()
+
+
 def group_affine(w: torch.Tensor, group: int, qmax: int = 15):
     """Asymmetric scale (max-min)/qmax and zero point round(-min/s) per (row, group of columns), as full
     [m, n] tensors; min/max include 0 so the grid holds zero."""

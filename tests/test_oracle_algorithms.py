@@ -11,6 +11,7 @@ import functools
 import pytest
 import torch
 
+import gptq_d_sided as DS
 from oracle import algorithms as A
 from oracle import sweep as S
 
@@ -153,3 +154,42 @@ def test_ldl_invariants():
     M2 = a2 @ a2.t() + torch.eye(k2, dtype=torch.float64)
     assert torch.allclose(A.ldl_of_inverse(torch.kron(M1, M2)),
                           torch.kron(A.ldl_of_inverse(M1), A.ldl_of_inverse(M2)), atol=1e-10)
+
+
+@pytest.mark.parametrize("shape", [(3, 4, 5), (6, 2, 3), (1, 5, 4), (4, 1, 1), (2, 3, 2, 3), (5, 7)])
+def test_d_sided_is_a_2d_sweep(shape):
+    """The map the GPU D-sided entry point (gptq_d_sided) uses: for X [n_1, ..., n_D] and unit lower L_1..L_D, Algorithm 4
+    equals the two-sided sweep (Algorithm 3) of the [n_1, n_2 ... n_D] matrix whose column index is
+    i_2 + n_2 (i_3 + n_3 (...)) -- mode 2 fastest, i.e. X permuted to (1, D, ..., 2) -- under L = L_1 and
+    U = (L_D (x) ... (x) L_2)^T; bitwise in fp64 with a codebook that depends on every coordinate."""
+    D = len(shape)
+    for seed in range(2):
+        *bases, X = A.random_instance(shape, 50 + seed)
+        Ls = [A.ldl_of_inverse(b.t() @ b) for b in bases]
+
+        def Qd(x, *idx):
+            return A.coordinate_round(x, idx[0], sum(int(k) * i for k, i in enumerate(idx[1:], 1)))
+
+        expected = A.alg4(X, Ls, Q=Qd)
+        n1, rest = shape[0], shape[1:]
+        perm = DS.mode_permutation(D)
+        assert perm == (0, *range(D - 1, 0, -1))
+        W = X.permute(*perm).reshape(n1, -1)
+        U = Ls[-1]
+        for f in reversed(Ls[1:-1]):
+            U = torch.kron(U, f)
+        U = U.t()
+        # the product's factor reads each L_d strictly below its diagonal only
+        poisoned = [f.masked_fill(torch.ones_like(f, dtype=torch.bool).triu(), torch.nan) for f in Ls]
+        assert DS.column_factor(poisoned).equal(U)
+        strides = [1]
+        for k in rest[:-1]:
+            strides.append(strides[-1] * k)
+
+        def Q2(x, i, c):
+            coords = [(c // s_) % k for s_, k in zip(strides, rest)]
+            return Qd(x, i, *coords)
+
+        got = A.alg3(W, Ls[0], U, Q=Q2)
+        got = got.reshape(n1, *reversed(rest)).permute(*[perm.index(d) for d in range(D)])
+        assert got.equal(expected), seed
