@@ -33,7 +33,7 @@ _SIGNATURES = {
     "sweep_fused": [_P, _P, _P, _P, _P, _I64, _I64, _I32, _AP, _AP, _AP, _I32, _P, _AP, _P, _AP, _F64, _F64, _P,
                     _I64, _I64, _I64, _P],
     "sweep_fused_se": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I32, _AP, _AP, _AP, _I32, _P, _AP, _P, _AP, _F64,
-                       _F64, _I32, _P, _I64, _I64, _I64, _P],
+                       _F64, _I32, _P, _P, _I64, _I64, _I64, _P],
     "sweep_fused_noalloc": [_P, _P, _P, _I64, _I64, _I32, _AP, _AP, _AP, _I32, _P, _AP, _P, _AP, _F64, _F64, _P, _I64,
                             _P],
     "affine_quantize": [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I32, _AP, _AP, _AP, _F64, _F64, _P],
@@ -42,7 +42,7 @@ _SIGNATURES = {
                            _F64, _P],
     "round_quantize_se": [_P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I32, _AP, _P],
     "absmax_scale": [_P, _P, _I64, _I64, _I64, _I64, _F64, _F64, _I32, _P],
-    "absmax_quantize_se": [_P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _F64, _F64, _I32, _P],
+    "absmax_quantize_se": [_P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _F64, _F64, _I32, _P, _P],
     "ldl_of_inverse": [_P, _P, _P, _P, _I64, _I64, _I64, _P],
     "ldl": [_P, _P, _P, _P, _I64, _I64, _I64, _P],
     "ldl_of_inverse_part": [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I32, _P],
@@ -50,6 +50,9 @@ _SIGNATURES = {
     "gemm": [_I64, _I64, _I64, _I64, _P, _I64, _I64, _I64, _P, _I64, _I64, _I64, _P, _I64, _I64, _I64, _F64, _F64,
              _I32, _I32, _I32, _P],
     "viterbi": [_P, _P, _P, _P, _P, _P, _I64, _I64, _I32, _I32, _I32, _I32, _P],
+    "pack_int": [_P, _I64, _I64, _I64, _P, _AP, _P, _AP, _F64, _F64, _I32, _P, _I64, _P, _P],
+    "unpack_int": [_P, _I64, _I64, _I64, _I64, _P, _AP, _P, _AP, _F64, _I32, _P, _P],
+    "trellis_unpack": [_P, _I64, _I64, _I64, _I64, _I64, _I64, _I32, _I32, _I32, _I32, _P, _P, _I64, _P, _P, _P],
 }
 
 _lib = None
@@ -75,6 +78,13 @@ def lib() -> ctypes.CDLL:
         handle.gptq2d_sweep_fused_noalloc_capacity.restype = ctypes.c_int64
         handle.gptq2d_viterbi_workspace.argtypes = [_I64, _I64, _I32, _I32, _I32]
         handle.gptq2d_viterbi_workspace.restype = ctypes.c_int64
+        handle.gptq2d_int_code_bits.argtypes = [_F64, _F64]
+        handle.gptq2d_int_code_bits.restype = ctypes.c_int32
+        handle.gptq2d_trellis_stream_words.argtypes = [_I64, _I32, _I32, _I32, _I32]
+        handle.gptq2d_trellis_stream_words.restype = ctypes.c_int64
+        handle.gptq2d_trellis_pack.argtypes = [_P, _I64, _I64, _I64, _I64, _I64, _I32, _I32, _I32, _I32, _I32, _P,
+                                               _I64, _P, _P]
+        handle.gptq2d_trellis_pack.restype = ctypes.c_int
         handle.gptq2d_profile_start.argtypes = [_I64, ctypes.c_uint32]
         handle.gptq2d_profile_start.restype = ctypes.c_int
         handle.gptq2d_profile_read.argtypes = [_I32, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double),
@@ -84,6 +94,13 @@ def lib() -> ctypes.CDLL:
         handle.gptq2d_profile_stop.restype = ctypes.c_int
         _lib = handle
     return _lib
+
+
+def call_untyped(name: str, *args) -> None:
+    """Call ``gptq2d_<name>`` (an entry point with no element type) and raise on a non-zero return code."""
+    rc = getattr(lib(), f"gptq2d_{name}")(*args)
+    if rc != 0:
+        raise GPTQ2DError(f"gptq2d_{name} failed with code {rc}")
 
 
 def call(name: str, dtype: torch.dtype, *args) -> None:

@@ -55,7 +55,7 @@ static inline int64_t batch_count(int32_t nd, const int64_t* shape) {
   return b;
 }
 
-static inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+__host__ __device__ static inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 // Launch grid helper: (x, y, batch) as a 3-D grid while y and batch fit the
 // 65535 limit of those axes, else every block linearised on axis x.  Kernels

@@ -87,12 +87,13 @@ __global__ __launch_bounds__(256) void absmax_scale_kernel(T* __restrict__ out, 
 }
 
 // One thread per row of one super-entry: scale from the row's current abs max, then
-// clamp(rint(y / s), qmin, qmax) * s.
+// clamp(rint(y / s), qmin, qmax) * s.  scale_out (optional): a per-entry map laid out like y (the same view
+// strides), where every entry of the row receives the row's scale.
 template <typename T>
 __global__ __launch_bounds__(256) void absmax_se_kernel(T* __restrict__ out, const T* __restrict__ y, int64_t msize,
                                                         int64_t d, int64_t p, int64_t q, int64_t sd, int64_t sp,
-                                                        int64_t sq, T qmin, T qmax, int dtype16, int64_t nx,
-                                                        int64_t ny) {
+                                                        int64_t sq, T qmin, T qmax, int dtype16,
+                                                        T* __restrict__ scale_out, int64_t nx, int64_t ny) {
   const GridIds id = grid_ids(nx, ny);
   const int64_t rr = id.x * 256 + threadIdx.x;
   if (rr >= d * p) return;
@@ -107,6 +108,10 @@ __global__ __launch_bounds__(256) void absmax_se_kernel(T* __restrict__ out, con
   const T s = absmax_scale(amax, (qmax - qmin) / T(2), dtype16);
   T* o = out + (b * d * p + rr) * q;
   for (int64_t cc = 0; cc < q; ++cc) o[cc] = clamp_val(round_even(yr[cc * sq] / s), qmin, qmax) * s;
+  if (scale_out) {
+    T* so = scale_out + b * msize + kk * sd + r * sp;
+    for (int64_t cc = 0; cc < q; ++cc) so[cc * sq] = s;
+  }
 }
 
 template <typename T>
@@ -187,13 +192,13 @@ extern "C" {
   }                                                                                                                   \
   int gptq2d_absmax_quantize_se_##SUF(T* out, const T* y, int64_t msize, int64_t B, int64_t d, int64_t p, int64_t q, \
                                       int64_t sd, int64_t sp, int64_t sq, double qmin, double qmax, int32_t dtype16, \
-                                      hipStream_t stream) {                                                          \
+                                      T* scale_out, hipStream_t stream) {                                            \
     if (B < 0 || d < 0 || p <= 0 || q <= 0 || !(qmin < qmax) || (dtype16 != 1 && dtype16 != 2))                     \
       return GPTQ2D_EINVAL;                                                                                           \
     if (B == 0 || d == 0) return 0;                                                                                   \
     Grid3 g = make_grid(cdiv(d * p, 256), 1, B);                                                                     \
     hipLaunchKernelGGL(absmax_se_kernel<T>, g.grid, dim3(256), 0, stream, out, y, msize, d, p, q, sd, sp, sq,        \
-                       (T)qmin, (T)qmax, dtype16, g.nx, g.ny);                                                       \
+                       (T)qmin, (T)qmax, dtype16, scale_out, g.nx, g.ny);                                            \
     return (int)hipGetLastError();                                                                                    \
   }
 

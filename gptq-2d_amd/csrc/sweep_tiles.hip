@@ -49,6 +49,7 @@ struct QSpec {
   BatchMap smap, zmap;
   T qmin, qmax;
   T* ypre;          // optional [B, m, n]: Y of every entry just before it is rounded
+  T* sout;          // abs-max, optional [B, m, n]: the scale each entry's row was rounded with
   int32_t dtype16;  // abs-max: the scale's 16-bit type (1 bf16, 2 fp16)
 };
 
@@ -130,13 +131,13 @@ __device__ __forceinline__ void sweep_rows(const T* ys, int ysp, const T* cs, in
     constexpr int r = decltype(r_c)::value, slot = r & 3;
     const bool own = g == (r >> 2) && r < rows_in;
     const T yv = Y[slot] + D[slot];
-    T z;
+    T z, sc = T(1);
     if constexpr (KIND == Q_ABSMAX) {
       // scale from the row's current abs max (a NaN entry counts as 0, as in the plug-in's comparison
       // loop), rounded to the 16-bit type through fp32, 0 -> 1; the reduction runs on every lane
       const T a = own ? __builtin_fmax(__builtin_fabs(yv), T(0)) : T(0);
       const T amax = halfwave_max(a);
-      T sc = round_scale16(amax / half, qs.dtype16);
+      sc = round_scale16(amax / half, qs.dtype16);
       sc = sc == T(0) ? T(1) : sc;
       z = clamp_val(round_even(yv / sc), qmin, qmax) * sc;
     } else if constexpr (KIND == Q_AFFINE) {
@@ -154,6 +155,9 @@ __device__ __forceinline__ void sweep_rows(const T* ys, int ysp, const T* cs, in
       C[slot] = cf;
       es[r * esp + cc] = ev;
       if constexpr (YPRE) qs.ypre[mat + (i0 + r) * n + j0 + cc] = yv;
+      if constexpr (KIND == Q_ABSMAX) {
+        if (qs.sout) qs.sout[mat + (i0 + r) * n + j0 + cc] = sc;
+      }
     }
     if constexpr (r + 1 < TR) {
       __syncthreads();  // the row's errors before the rows below read them
@@ -902,7 +906,8 @@ template <typename T>
 int sweep_fused(T* y, T* c, T* e, const T* l, const T* u, int64_t m, int64_t n, int32_t bnd, const int64_t* bshape,
                 const int64_t* lstride, const int64_t* ustride, int32_t qkind, const T* qa, const int64_t* qa_stride,
                 const T* qb, const int64_t* qb_stride, double qmin, double qmax, T* ypre, int64_t outer_tiles,
-                int64_t stage_begin, int64_t stage_end, hipStream_t stream, bool rows = false, int32_t dtype16 = 0) {
+                int64_t stage_begin, int64_t stage_end, hipStream_t stream, bool rows = false, int32_t dtype16 = 0,
+                T* scale_out = nullptr) {
   BatchMap lmap, umap;
   if (!make_batch_map(lmap, bnd, bshape, lstride) || !make_batch_map(umap, bnd, bshape, ustride)) return GPTQ2D_EINVAL;
   if (m <= 0 || n <= 0 || outer_tiles < 1) return GPTQ2D_EINVAL;
@@ -921,6 +926,7 @@ int sweep_fused(T* y, T* c, T* e, const T* l, const T* u, int64_t m, int64_t n, 
   qs.qmin = (T)qmin;
   qs.qmax = (T)qmax;
   qs.ypre = ypre;
+  qs.sout = qkind == Q_ABSMAX ? scale_out : nullptr;
   qs.dtype16 = dtype16;
   const int64_t B = batch_count(bnd, bshape);
   if (B == 0) return 0;
@@ -1058,15 +1064,15 @@ extern "C" {
                                   int64_t q, int32_t bnd, const int64_t* bshape, const int64_t* lstride,             \
                                   const int64_t* ustride, int32_t qkind, const T* qa, const int64_t* qa_stride,     \
                                   const T* qb, const int64_t* qb_stride, double qmin, double qmax, int32_t dtype16, \
-                                  T* ypre, int64_t outer_tiles, int64_t stage_begin, int64_t stage_end,             \
-                                  hipStream_t stream) {                                                              \
+                                  T* ypre, T* scale_out, int64_t outer_tiles, int64_t stage_begin,                  \
+                                  int64_t stage_end, hipStream_t stream) {                                           \
     if (p <= 0 || q <= 0 || m % p || n % q) return GPTQ2D_EINVAL;                                                  \
     if (p == 1 && q == 1 && qkind != Q_ABSMAX)                                                                       \
       return sweep_fused<T>(y, c, e, l, u, m, n, bnd, bshape, lstride, ustride, qkind, qa, qa_stride, qb, qb_stride, \
                             qmin, qmax, ypre, outer_tiles, stage_begin, stage_end, stream);                          \
     if (p != 1 || q != TR) return GPTQ2D_EUNSUPPORTED;                                                              \
     return sweep_fused<T>(y, c, e, l, u, m, n, bnd, bshape, lstride, ustride, qkind, qa, qa_stride, qb, qb_stride,   \
-                          qmin, qmax, ypre, outer_tiles, stage_begin, stage_end, stream, true, dtype16);             \
+                          qmin, qmax, ypre, outer_tiles, stage_begin, stage_end, stream, true, dtype16, scale_out);  \
   }                                                                                                                  \
   int gptq2d_sweep_fused_noalloc_##SUF(T* y, const T* l, const T* u, int64_t m, int64_t n, int32_t bnd,              \
                                        const int64_t* bshape, const int64_t* lstride, const int64_t* ustride,       \

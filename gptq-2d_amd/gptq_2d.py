@@ -134,11 +134,15 @@ def _fused_spec(quantizer, quantizer_inputs, y, batch_shape, rows=False):
     if fn in (round_quantizer, round_quantizer_super_entry) and not kw and not quantizer_inputs:
         return dict(kind=0, qa=None, qb=None, qmin=0.0, qmax=0.0, ypre=None)
     if rows and fn in (_qi.int_abs_max_quantizer_hip, _qi.int_abs_max_quantizer_torch) and set(kw) == {
-            "qmin", "qmax", "dtype"} and not quantizer_inputs:
+            "qmin", "qmax", "dtype"} and len(quantizer_inputs) <= 1:
         if kw["dtype"] not in _qi._SCALE_DTYPES or not float(kw["qmin"]) < float(kw["qmax"]):
             return None
+        sout = quantizer_inputs[0] if quantizer_inputs else None
+        if sout is not None and (not isinstance(sout, torch.Tensor) or sout.shape != y.shape or
+                                 not sout.is_contiguous() or sout.dtype != y.dtype or sout.device != y.device):
+            return None
         return dict(kind=3, qa=None, qb=None, qmin=float(kw["qmin"]), qmax=float(kw["qmax"]), ypre=None,
-                    dtype16=_qi._SCALE_DTYPES[kw["dtype"]])
+                    dtype16=_qi._SCALE_DTYPES[kw["dtype"]], sout=sout)
     if fn in (_qi.affine_quantizer_hip, _qi.affine_quantizer_torch, _qi.affine_quantizer_super_entry_hip,
               _qi.affine_quantizer_super_entry_torch) and set(kw) <= {"qmin", "qmax"}:
         if len(quantizer_inputs) != 2:
@@ -177,7 +181,8 @@ def _run_fused(y, l, u, m, n, batch_shape, spec, outer_block_size, p=1, q=1):
         bshape, _hip.batch_strides(l, batch_shape), _hip.batch_strides(u, batch_shape), spec["kind"], _hip.ptr(qa),
         _hip.batch_strides(qa, batch_shape) if qa is not None else None, _hip.ptr(qb),
         _hip.batch_strides(qb, batch_shape) if qb is not None else None, spec["qmin"], spec["qmax"],
-        spec.get("dtype16", 0), _hip.ptr(spec["ypre"]), _outer_tiles(outer_block_size), 0, -1, _hip.stream(y.device),
+        spec.get("dtype16", 0), _hip.ptr(spec["ypre"]), _hip.ptr(spec.get("sout")), _outer_tiles(outer_block_size), 0,
+        -1, _hip.stream(y.device),
     )
 
 

@@ -166,17 +166,29 @@ def int_abs_max_scale_hip(x: torch.Tensor, *, qmin: float, qmax: float, dtype: t
     return out
 
 
-def int_abs_max_quantizer_torch(y_flat, select, *, out, qmin, qmax, dtype) -> None:
+def _scale_map(scales, y_flat):
+    """The optional per-entry scale map of the abs-max quantizers: [*batch, m, n] like Y, flattened."""
+    flat = scales.flatten(start_dim=-2)
+    assert flat.shape == y_flat.shape and flat.dtype == y_flat.dtype and flat.device == y_flat.device, (
+        "scales must be a [*batch, m, n] tensor of Y's batch shape, dtype and device"
+    )
+    return flat
+
+
+def int_abs_max_quantizer_torch(y_flat, select, scales=None, *, out, qmin, qmax, dtype) -> None:
     """Round each row of the selected super-entries to qmin..qmax times its current abs-max scale, with PyTorch
-    (quantizer_int.py:120-134)."""
+    (quantizer_int.py:120-134).  ``scales`` (optional, [*batch, m, n], no reference counterpart): every entry
+    receives the scale its row was rounded with -- the scales of the packed layer."""
     x = select(y_flat)
     scale = int_abs_max_scale_torch(x, qmin=qmin, qmax=qmax, dtype=dtype)
     torch.div(x, scale, out=out).round_().clamp_(qmin, qmax).mul_(scale)
+    if scales is not None:
+        select(_scale_map(scales, y_flat)).copy_(scale.expand_as(x))
 
 
-def int_abs_max_quantizer_hip(y_flat, select, *, out, qmin, qmax, dtype) -> None:
+def int_abs_max_quantizer_hip(y_flat, select, scales=None, *, out, qmin, qmax, dtype) -> None:
     """``int_abs_max_quantizer_torch`` in one HIP kernel that reads each row through the view's strides
-    (quantizer_int.py:442-470)."""
+    (quantizer_int.py:442-470); ``scales`` as there, written by the same kernel."""
     x = select(y_flat)
     _hip.require_device(y_flat)
     assert y_flat.is_contiguous() and out.is_contiguous(), "the HIP quantizer requires contiguous Y and out"
@@ -186,8 +198,14 @@ def int_abs_max_quantizer_hip(y_flat, select, *, out, qmin, qmax, dtype) -> None
     d, p, q = x.shape[-3:]
     sd, sp, sq = x.stride()[-3:]
     B = y_flat.shape[:-1].numel()
+    sv = None
+    if scales is not None:
+        flat = _scale_map(scales, y_flat)
+        assert flat.is_contiguous(), "the HIP quantizer writes a contiguous scale map"
+        sv = select(flat)
+        assert sv.stride() == x.stride(), "select must view the scale map as it views Y"
     _hip.call("absmax_quantize_se", y_flat.dtype, _hip.ptr(out), _hip.ptr(x), y_flat.size(-1), B, d, p, q, sd, sp, sq,
-              float(qmin), float(qmax), _SCALE_DTYPES[dtype], _hip.stream(y_flat.device))
+              float(qmin), float(qmax), _SCALE_DTYPES[dtype], _hip.ptr(sv), _hip.stream(y_flat.device))
 
 
 # ------------------------------------------------------------------------------------------------ teacher forcing

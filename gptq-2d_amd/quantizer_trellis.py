@@ -171,26 +171,41 @@ def trellis_quantize_torch(x: torch.Tensor, table: torch.Tensor, K: int, tail_bi
 
 # ------------------------------------------------------------------------------------------------ plug-ins
 
-def trellis_quantizer_super_entry_torch(y_flat: torch.Tensor, select: Callable, scale: torch.Tensor, *,
-                                        out: torch.Tensor, table: torch.Tensor, K: int,
-                                        tail_biting: bool = True) -> None:
+def _record_states(states, y_flat, select, st, V):
+    """Write each super-entry's states into the per-entry state map ``states`` [*batch, m, n] (int64): the
+    entries t*V .. t*V + V - 1 of a super-entry, read row by row, hold its state t (the state that emitted
+    them) -- the input of packing.pack_trellis."""
+    flat = states.flatten(start_dim=-2)
+    assert flat.shape == y_flat.shape and flat.dtype == torch.int64 and flat.device == y_flat.device, (
+        "states must be an int64 [*batch, m, n] tensor of Y's batch shape on Y's device"
+    )
+    view = select(flat)
+    view.copy_(st.repeat_interleave(V, dim=-1).view(view.shape))
+
+
+def trellis_quantizer_super_entry_torch(y_flat: torch.Tensor, select: Callable, scale: torch.Tensor,
+                                        states: torch.Tensor | None = None, *, out: torch.Tensor,
+                                        table: torch.Tensor, K: int, tail_biting: bool = True) -> None:
     """Each super-entry of ``select(y_flat) / scale``, read row by row, is one sequence; ``out`` gets
     ``scale`` times its trellis values (quantizer_trellis.py:344-369).  Rows are padded with zero
-    sequences to a power of two, as the reference does, so that graph memory pools stay small."""
+    sequences to a power of two, as the reference does, so that graph memory pools stay small.
+    ``states`` (optional, no reference counterpart): the per-entry state map of ``_record_states``."""
     x = select(y_flat) / scale
     seqs = x.reshape(-1, x.size(-2) * x.size(-1))
     rows, T = seqs.shape
     padded = torch.cat((seqs, seqs.new_zeros((1 << (rows - 1).bit_length()) - rows, T)))
-    values, _ = trellis_quantize_torch(padded, table, K, tail_biting)
+    values, st = trellis_quantize_torch(padded, table, K, tail_biting)
     torch.mul(values[:rows, :].view_as(x), scale, out=out)
+    if states is not None:
+        _record_states(states, y_flat, select, st[:rows], table.size(1))
 
 
-def trellis_quantizer_super_entry_hip(y_flat: torch.Tensor, select: Callable, scale: torch.Tensor, *,
-                                      out: torch.Tensor, table: torch.Tensor, K: int,
-                                      tail_biting: bool = True) -> None:
+def trellis_quantizer_super_entry_hip(y_flat: torch.Tensor, select: Callable, scale: torch.Tensor,
+                                      states: torch.Tensor | None = None, *, out: torch.Tensor,
+                                      table: torch.Tensor, K: int, tail_biting: bool = True) -> None:
     """``trellis_quantizer_super_entry_torch`` with the search in one HIP launch per call
     (quantizer_trellis.py:372-391).  ``y_flat``, ``scale`` and ``table`` must be on one GPU; ``scale``
-    broadcasts against the super-entries and is constant within each."""
+    broadcasts against the super-entries and is constant within each.  ``states`` as there."""
     _hip.require_device(y_flat)
     assert table.device == y_flat.device and (not isinstance(scale, torch.Tensor) or scale.device == y_flat.device), (
         "the HIP trellis quantizer requires Y, scale, and table on one GPU"
@@ -198,7 +213,11 @@ def trellis_quantizer_super_entry_hip(y_flat: torch.Tensor, select: Callable, sc
     x = select(y_flat) / scale
     seqs = x.flatten(start_dim=-2)
     sc = torch.as_tensor(scale, dtype=x.dtype, device=x.device).broadcast_to(x.shape)[..., 0, 0]
-    trellis_quantize_hip(seqs, table, K, tail_biting, out=out.view(seqs.shape), scale=sc)
+    st = None if states is None else torch.empty(seqs.shape[:-1].numel(), seqs.size(-1) // table.size(1),
+                                                 dtype=torch.int64, device=x.device)
+    trellis_quantize_hip(seqs, table, K, tail_biting, out=out.view(seqs.shape), scale=sc, states=st)
+    if states is not None:
+        _record_states(states, y_flat, select, st.view(*seqs.shape[:-1], -1), table.size(1))
 
 
 # The reference's Triton name, kept for drop-in use: one implementation, not two.

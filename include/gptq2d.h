@@ -53,13 +53,15 @@ extern "C" {
    * row, n % 32 == 0) sweeps each tile row by row, U's 32 x 32 diagonal blocks never read, with qkind \
    * 0-2 as above per entry or 3: the abs-max INT quantizer of each super-entry row from its current     \
    * values with the scale rounded to bf16 (dtype16 1) or fp16 (2) (int_abs_max_quantizer,              \
-   * quantizer_int.py:120-134, 408-470); other shapes GPTQ2D_EUNSUPPORTED.  Other arguments as above. */ \
+   * quantizer_int.py:120-134, 408-470); other shapes GPTQ2D_EUNSUPPORTED.  scale_out (optional,         \
+   * [B,m,n], qkind 3 only): every entry receives the scale its row was rounded with (no reference       \
+   * counterpart: the scales of a packed layer).  Other arguments as above. */                          \
   int gptq2d_sweep_fused_se_##SUF(T* y, T* c, T* e, const T* l, const T* u, int64_t m, int64_t n, int64_t p,         \
                                   int64_t q, int32_t bnd, const int64_t* bshape, const int64_t* l_stride,           \
                                   const int64_t* u_stride, int32_t qkind, const T* qa, const int64_t* qa_stride,    \
                                   const T* qb, const int64_t* qb_stride, double qmin, double qmax, int32_t dtype16, \
-                                  T* ypre, int64_t outer_tiles, int64_t stage_begin, int64_t stage_end,             \
-                                  void* stream);                                                                     \
+                                  T* ypre, T* scale_out, int64_t outer_tiles, int64_t stage_begin,                  \
+                                  int64_t stage_end, void* stream);                                                  \
   /* Tile edge of the fused sweep. */                                                                  \
   int64_t gptq2d_sweep_fused_tile_##SUF(void);                                                                       \
   /* The whole fused sweep (as gptq2d_sweep_fused with stage_begin 0, stage_end -1) with no c and e:     \
@@ -128,10 +130,11 @@ extern "C" {
   int gptq2d_absmax_scale_##SUF(T* out, const T* x, int64_t rows, int64_t size, int64_t row_stride,                 \
                                 int64_t col_stride, double qmin, double qmax, int32_t dtype16, void* stream);       \
   /* Abs-max INT quantizer per row of each super-entry from its current values                        \
-   * (_int_abs_max_quantize_kernel, quantizer_int.py:408-470). */                                      \
+   * (_int_abs_max_quantize_kernel, quantizer_int.py:408-470).  scale_out (optional): a map laid out     \
+   * like y (same view strides, matrices msize apart) whose entries receive their row's scale. */      \
   int gptq2d_absmax_quantize_se_##SUF(T* out, const T* y, int64_t msize, int64_t B, int64_t d, int64_t p, int64_t q, \
                                       int64_t sd, int64_t sp, int64_t sq, double qmin, double qmax, int32_t dtype16, \
-                                      void* stream);                                                                \
+                                      T* scale_out, void* stream);                                                  \
                                                                                                                       \
   /* Unit lower (block) triangular L with M^{-1} = L Lambda L^T for `batch` contiguous k x k SPD      \
    * matrices m; work: [batch, k, k] scratch; info[batch]: first non-positive pivot (1-based) or 0     \
@@ -181,7 +184,33 @@ extern "C" {
    * [rows, steps], int64) receive the result.  1 <= L <= 24, V in {1, 2}, K*V <= min(L, 8). */      \
   int gptq2d_viterbi_##SUF(const T* x, const T* table, T* hist, const T* scale, T* out, int64_t* states,            \
                            int64_t rows, int64_t steps, int32_t L, int32_t K, int32_t V, int32_t tail_biting,      \
-                           void* stream);
+                           void* stream);                                                                           \
+                                                                                                                      \
+  /* Packed INT codes (no reference counterpart: the reference returns dequantized values only).  z     \
+   * [B,m,n] holds affine-quantizer outputs (q - zp) * s, q integer in [qmin, qmax]; scale / zp are     \
+   * read at b*stride[0] + i*stride[1] + j*stride[2] (zp optional: 0).  Code u = q - qmin in `bits` bits  \
+   * (gptq2d_int_code_bits), little-endian bit fields per row: code j at bits [j*bits, (j+1)*bits) of   \
+   * the row, bit k in bit k%32 of word k/32; row_words >= ceil(n*bits/32) words per row, tail zero.    \
+   * bad (optional, [B*m]): per row, the entries not equal to (q - zp) * s for q = rint(z/s + zp) in    \
+   * range (packed as 0). */                                                                            \
+  int gptq2d_pack_int_##SUF(const T* z, int64_t B, int64_t m, int64_t n, const T* scale,                            \
+                            const int64_t* scale_stride, const T* zp, const int64_t* zp_stride, double qmin,       \
+                            double qmax, int32_t bits, uint32_t* words, int64_t row_words, int32_t* bad,           \
+                            void* stream);                                                                          \
+  /* z = (u + qmin - zp) * scale from packed codes: the inverse of gptq2d_pack_int (exact for a row   \
+   * with no bad entries; a zero's sign is not kept). */                                                \
+  int gptq2d_unpack_int_##SUF(const uint32_t* words, int64_t B, int64_t m, int64_t n, int64_t row_words,             \
+                              const T* scale, const int64_t* scale_stride, const T* zp,                             \
+                              const int64_t* zp_stride, double qmin, int32_t bits, T* z, void* stream);             \
+  /* Decode trellis streams (see gptq2d_trellis_pack): sequence r = the p x q block (b, I, J) of a      \
+   * [B,m,n] layout read row by row (a plain [R, T] array: B 1, m R, n T, p 1, q T), state t = the     \
+   * L-bit window at stream bit t*K*V.  values (optional, the [B,m,n] layout): entries t*V .. t*V+V-1   \
+   * of each block = table[s_t, v] * scale[r * scale_stride] (scale optional: 1), the trellis           \
+   * quantizer's values (quantizer_trellis.py:143, 344-391); states (optional, [seqs, p*q/V] int64). */ \
+  int gptq2d_trellis_unpack_##SUF(const uint32_t* words, int64_t B, int64_t m, int64_t n, int64_t p, int64_t q,       \
+                                  int64_t row_words, int32_t L, int32_t K, int32_t V, int32_t tail_biting,           \
+                                  const T* table, const T* scale, int64_t scale_stride, T* values, int64_t* states,  \
+                                  void* stream);
 
 /* Largest B m n (elements per matrix of the batch) gptq2d_sweep_fused_noalloc_* accepts for elements of
  * elem_bytes bytes (4 or 8; -1 otherwise): 2^24 for float, 2^23 for double.  No counterpart in the
@@ -192,6 +221,26 @@ int64_t gptq2d_sweep_fused_noalloc_capacity(int32_t elem_bytes);
  * the arguments are invalid).  Part of the trellis quantizer above (quantizer_trellis.py:146-341 keeps its
  * step minima in a torch-allocated [steps, rows, 2^L] buffer). */
 int64_t gptq2d_viterbi_workspace(int64_t rows, int64_t steps, int32_t L, int32_t K, int32_t V);
+
+/* Bits of a packed INT code for integer qmin <= qmax: ceil(log2(qmax - qmin + 1)), -1 beyond 16 or for
+ * non-integer bounds.  Part of the packed format (no reference counterpart). */
+int32_t gptq2d_int_code_bits(double qmin, double qmax);
+
+/* Words of one trellis stream of `steps` states: ceil(steps*K*V / 32) with tail_biting, else
+ * ceil((steps*K*V + L - K*V) / 32); -1 for invalid arguments. */
+int64_t gptq2d_trellis_stream_words(int64_t steps, int32_t L, int32_t K, int32_t V, int32_t tail_biting);
+
+/* Pack bitshift-trellis paths (quantizer_trellis.py:82-143, which returns the states; the reference's
+ * docstring, quantizer_trellis.py:11-16, counts T*K bits per tail-biting sequence but keeps no stream) into
+ * one MSB-first stream per sequence: the top K*V bits of every state in order (stream bit k = bit 31-k%32
+ * of word k/32), plus the low L - K*V bits of the last state without tail-biting.  Sequences as in
+ * gptq2d_trellis_unpack_*; state t of a sequence is its entry t*copies (copies = V: a per-entry state map
+ * in which each state repeats over the V entries it emitted, every copy checked; 1: one entry per state).
+ * bad (optional, [seqs]): states out of [0, 2^L), breaks of s_{t+1} >> KV == s_t mod 2^(L-KV) (and, with
+ * tail_biting, between the last state and the first) and disagreeing copies.  L <= 30. */
+int gptq2d_trellis_pack(const int64_t* states, int64_t B, int64_t m, int64_t n, int64_t p, int64_t q, int32_t copies,
+                        int32_t L, int32_t K, int32_t V, int32_t tail_biting, uint32_t* words, int64_t row_words,
+                        int32_t* bad, void* stream);
 
 GPTQ2D_DECLARE(float, f32)
 GPTQ2D_DECLARE(double, f64)
