@@ -11,6 +11,9 @@
 //
 // The right product reads C only on the band, which the down product never writes (it writes
 // targets only), so both run in one pass per output tile with a single read-modify-write of Y and C.
+// Both products run on MFMA: fp32 32 x 32 cells (the fused engine's tiles) on the tuned kernel of
+// flush_mfma.hip, every other cell shape and fp64 on flush_mfma_kernel here (16 x 16 x 4 MFMA, entries
+// masked one by one at staging, so any P and Q).
 // L is read only strictly below its P x P diagonal blocks and U strictly above its Q x Q ones;
 // masked loads never touch other entries (they may hold NaN).
 //
@@ -22,7 +25,7 @@
 
 namespace {
 
-constexpr int FB_M = 64, FB_N = 64, FB_K = 16;
+constexpr int FB_M = 64, FB_N = 64, FB_K = 32;
 
 struct FlushGeom {
   int64_t m, n, P, Q, s0, s1, s_end;
@@ -45,16 +48,54 @@ __host__ __device__ inline void target_cols(const FlushGeom& g, int64_t i0, int6
   jt_hi = (j_hi + FB_N - 1) / FB_N;
 }
 
+// MFMA operand and accumulator types of the 16 x 16 x 4 products.  In both v_mfma_f32_16x16x4f32 and
+// v_mfma_f64_16x16x4f64 lane l supplies A(l % 16, l / 16) and B(l / 16, l % 16); accumulator element r of
+// lane l holds D(row(l / 16, r), l % 16) with row = 4 (l / 16) + r for fp32 and l / 16 + 4 r for fp64
+// (measured with a one-wave probe of each instruction).
 template <typename T>
-__global__ __launch_bounds__(256) void flush_valu_kernel(T* __restrict__ y, T* __restrict__ c,
+struct Mfma16;
+template <>
+struct Mfma16<float> {
+  typedef float acc_t __attribute__((ext_vector_type(4)));
+  static __device__ __forceinline__ acc_t mma(float a, float b, acc_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ int row(int kq, int r) { return 4 * kq + r; }
+};
+template <>
+struct Mfma16<double> {
+  typedef double acc_t __attribute__((ext_vector_type(4)));
+  static __device__ __forceinline__ acc_t mma(double a, double b, acc_t c) {
+    return __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ int row(int kq, int r) { return kq + 4 * r; }
+};
+
+// LDS pitch of the staged panels (elements per k-row of FB_M or FB_N entries): a half-wave's MFMA operand
+// read spans two k-rows of 16 entries, which the pad of 16 puts on disjoint banks.
+constexpr int FB_P = FB_M + 16;
+
+// The flush of one FB_M x FB_N output tile on MFMA: the two masked band products of FB_K-deep k-blocks
+// staged in LDS, wave w computing the 32 x 32 quadrant (w / 2, w % 2) as 2 x 2 blocks of 16 x 16 x 4
+// products, D and R in their own accumulators; then C += D and Y = (Y + D) + R on the targets.  Every
+// staged operand entry is masked to what its product may read -- L strictly below its P x P diagonal
+// blocks, U strictly above its Q x Q ones, E and C on the band, nothing outside the matrix -- through k
+// limits that a staging thread computes once for each of its rows or columns (a row i of L is read for k
+// below P floor(i / P); a column j of E for k in [P (s0 - floor(j / Q)), P (s1 - floor(j / Q))); and the
+// same with the roles of P and Q exchanged for C and U), so that no division runs in the k loop.
+template <typename T>
+__global__ __launch_bounds__(256) void flush_mfma_kernel(T* __restrict__ y, T* __restrict__ c,
                                                          const T* __restrict__ e, const T* __restrict__ l,
                                                          const T* __restrict__ u, FlushGeom g, BatchMap lmap,
                                                          BatchMap umap, int64_t nx, int64_t ny) {
-  __shared__ T As[FB_K][FB_M + 1];
-  __shared__ T Bs[FB_K][FB_N + 1];
+  using M = Mfma16<T>;
+  using acc_t = typename M::acc_t;
+  constexpr int AL = FB_M * FB_K / 256;  // staged entries per thread and operand
+  __shared__ T As[FB_K][FB_P];
+  __shared__ T Bs[FB_K][FB_P];
   const GridIds id = grid_ids(nx, ny);
   const int64_t b = id.b;
-  const int64_t m = g.m, n = g.n, P = g.P, Q = g.Q;
+  const int64_t m = g.m, n = g.n;
   const int64_t i0 = id.y * FB_M;
   const int64_t i1 = i0 + FB_M < m ? i0 + FB_M : m;
   int64_t jt_lo, jt_hi;
@@ -64,129 +105,145 @@ __global__ __launch_bounds__(256) void flush_valu_kernel(T* __restrict__ y, T* _
   const int64_t j0 = jt * FB_N;
   const int64_t j1 = j0 + FB_N < n ? j0 + FB_N : n;
   // whole tile outside the targets?
-  if ((i1 - 1) / P + (j1 - 1) / Q < g.s1 || i0 / P + j0 / Q >= g.s_end) return;
+  if ((i1 - 1) / g.P + (j1 - 1) / g.Q < g.s1 || i0 / g.P + j0 / g.Q >= g.s_end) return;
 
-  const int tid = threadIdx.x;
-  const int tx = tid & 15, ty = tid >> 4;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int li = lane & 15, kq = lane >> 4;                 // operand row / column in a block, k in a 4-step
+  const int wi = 32 * (wave >> 1), wj = 32 * (wave & 1);    // the wave's quadrant
+  // staging roles: A entry x of this thread is (row ar + (256 / FB_K) x, k-offset ak); B entry x is
+  // (k-offset bk + (256 / FB_N) x, column bj)
+  constexpr int ASTEP = 256 / FB_K, BSTEP = 256 / FB_N;
+  const int ak = tid % FB_K, ar = tid / FB_K;
+  const int bj = tid % FB_N, bk = tid / FB_N;
+  const int64_t P = g.P, Q = g.Q, s0 = g.s0, s1 = g.s1;
+  // a k limit clamped into [0, k_hi] (so that it fits 32 bits like every k)
+  auto clampk = [](int64_t v, int64_t k_hi) { return (int)(v < 0 ? 0 : (v < k_hi ? v : k_hi)); };
   const int64_t mat = b * m * n;
   const T* lb = l + lmap.offset(b);
   const T* ub = u + umap.offset(b);
 
-  T accd[4][4], accr[4][4];
+  acc_t accd[2][2], accr[2][2];
 #pragma unroll
-  for (int a = 0; a < 4; ++a)
+  for (int a = 0; a < 2; ++a)
 #pragma unroll
-    for (int q2 = 0; q2 < 4; ++q2) accd[a][q2] = accr[a][q2] = T(0);
+    for (int d = 0; d < 2; ++d)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) accd[a][d][r] = accr[a][d][r] = T(0);
 
-  // ---------------- down: D = L E over the band (only columns j < s1*Q have band rows)
-  if (j0 / Q < g.s1) {
-    int64_t k_lo = (g.s0 - (j1 - 1) / Q) * P;
-    if (k_lo < 0) k_lo = 0;
-    int64_t k_hi = (g.s1 - j0 / Q) * P;
-    const int64_t k_cap = ((i1 - 1) / P) * P;  // L strictly below diagonal blocks
-    if (k_hi > k_cap) k_hi = k_cap;
-    if (k_hi > m) k_hi = m;
-    for (int64_t kb = k_lo; kb < k_hi; kb += FB_K) {
-      // A = L[i, k]: thread t loads k = kb + t%16, i = i0 + t/16 + 16*ld
+  // the staged k-block's products into acc: FB_K / 4 steps of 4 k, 2 x 2 blocks
+  auto mma_block = [&](acc_t (&acc)[2][2]) {
 #pragma unroll
-      for (int ld = 0; ld < 4; ++ld) {
-        const int kl = tid & 15, il = (tid >> 4) + 16 * ld;
-        const int64_t i = i0 + il, k = kb + kl;
-        T v = T(0);
-        if (i < i1 && k < k_hi && k / P < i / P) v = lb[i * m + k];
-        As[kl][il] = v;
+    for (int k4 = 0; k4 < FB_K; k4 += 4) {
+      T av[2], bv[2];
+#pragma unroll
+      for (int a = 0; a < 2; ++a) av[a] = As[k4 + kq][wi + 16 * a + li];
+#pragma unroll
+      for (int d = 0; d < 2; ++d) bv[d] = Bs[k4 + kq][wj + 16 * d + li];
+#pragma unroll
+      for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int d = 0; d < 2; ++d) acc[a][d] = M::mma(av[a], bv[d], acc[a][d]);
+    }
+  };
+
+  // one band product: A rows from arow[x] (k limits [alo[x], ahi[x])), B columns from bcol (k limits
+  // [blo, bhi)), k-blocks from k_lo up to k_hi; operand entries outside their limits are staged as zero
+  // (the next k-block's entries are loaded into registers while the current one's MFMAs run)
+  auto product = [&](acc_t (&acc)[2][2], const T* const (&arow)[AL], const int (&alo)[AL], const int (&ahi)[AL],
+                     const T* bcol, int64_t bld, int blo, int bhi, int64_t k_lo, int64_t k_hi) {
+    T ra[AL], rb[AL];
+    auto load = [&](int64_t kb) {
+      const int ka = (int)kb + ak;
+#pragma unroll
+      for (int x = 0; x < AL; ++x) ra[x] = (ka >= alo[x] && ka < ahi[x]) ? arow[x][ka] : T(0);
+#pragma unroll
+      for (int x = 0; x < AL; ++x) {
+        const int kr = (int)kb + bk + BSTEP * x;
+        rb[x] = (kr >= blo && kr < bhi) ? bcol[(int64_t)kr * bld] : T(0);
       }
-      // B = E[k, j] on the band: thread t loads j = j0 + t%64, k = kb + t/64 + 4*ld
+    };
+    if (k_lo < k_hi) load(k_lo);
+    for (int64_t kb = k_lo; kb < k_hi; kb += FB_K) {
 #pragma unroll
-      for (int ld = 0; ld < 4; ++ld) {
-        const int jl = tid & 63, kl = (tid >> 6) + 4 * ld;
-        const int64_t j = j0 + jl, k = kb + kl;
-        T v = T(0);
-        if (j < j1 && k < k_hi) {
-          const int64_t st = k / P + j / Q;
-          if (st >= g.s0 && st < g.s1) v = e[mat + k * n + j];
-        }
-        Bs[kl][jl] = v;
+      for (int x = 0; x < AL; ++x) {
+        As[ak][ar + ASTEP * x] = ra[x];
+        Bs[bk + BSTEP * x][bj] = rb[x];
       }
       __syncthreads();
-#pragma unroll
-      for (int kk = 0; kk < FB_K; ++kk) {
-        T av[4], bv[4];
-#pragma unroll
-        for (int a = 0; a < 4; ++a) av[a] = As[kk][ty + 16 * a];
-#pragma unroll
-        for (int q2 = 0; q2 < 4; ++q2) bv[q2] = Bs[kk][tx + 16 * q2];
-#pragma unroll
-        for (int a = 0; a < 4; ++a)
-#pragma unroll
-          for (int q2 = 0; q2 < 4; ++q2) accd[a][q2] += av[a] * bv[q2];
-      }
+      if (kb + FB_K < k_hi) load(kb + FB_K);
+      mma_block(acc);
       __syncthreads();
     }
+  };
+
+  // ---------------- down: D = L E over the band (only columns j < s1*Q have band rows)
+  if (j0 / g.Q < g.s1) {
+    int64_t k_lo = (g.s0 - (j1 - 1) / g.Q) * g.P;
+    if (k_lo < 0) k_lo = 0;
+    int64_t k_hi = (g.s1 - j0 / g.Q) * g.P;
+    const int64_t k_cap = ((i1 - 1) / g.P) * g.P;  // L strictly below diagonal blocks
+    if (k_hi > k_cap) k_hi = k_cap;
+    if (k_hi > m) k_hi = m;
+    const T* arow[AL];
+    int alo[AL], ahi[AL];
+#pragma unroll
+    for (int x = 0; x < AL; ++x) {
+      const int64_t i = i0 + ar + ASTEP * x;
+      const bool in = i < i1;
+      arow[x] = lb + (in ? i : 0) * m;
+      alo[x] = 0;
+      ahi[x] = in ? clampk(i / P * P, k_hi) : 0;  // k / P < i / P
+    }
+    const int64_t j = j0 + bj;
+    int blo = 0, bhi = 0;
+    if (j < j1) {  // s0 <= k / P + j / Q < s1
+      blo = clampk((s0 - j / Q) * P, k_hi);
+      bhi = clampk((s1 - j / Q) * P, k_hi);
+    }
+    product(accd, arow, alo, ahi, e + mat + (j < j1 ? j : 0), n, blo, bhi, k_lo, k_hi);
   }
 
   // ---------------- right: R = C U over the band (only rows i < s1*P have band columns)
-  if (i0 / P < g.s1) {
-    int64_t k_lo = (g.s0 - (i1 - 1) / P) * Q;
+  if (i0 / g.P < g.s1) {
+    int64_t k_lo = (g.s0 - (i1 - 1) / g.P) * g.Q;
     if (k_lo < 0) k_lo = 0;
-    int64_t k_hi = (g.s1 - i0 / P) * Q;
-    const int64_t k_cap = ((j1 - 1) / Q) * Q;  // U strictly above diagonal blocks
+    int64_t k_hi = (g.s1 - i0 / g.P) * g.Q;
+    const int64_t k_cap = ((j1 - 1) / g.Q) * g.Q;  // U strictly above diagonal blocks
     if (k_hi > k_cap) k_hi = k_cap;
     if (k_hi > n) k_hi = n;
-    for (int64_t kb = k_lo; kb < k_hi; kb += FB_K) {
-      // A = C[i, k] on the band
+    const T* arow[AL];
+    int alo[AL], ahi[AL];
 #pragma unroll
-      for (int ld = 0; ld < 4; ++ld) {
-        const int kl = tid & 15, il = (tid >> 4) + 16 * ld;
-        const int64_t i = i0 + il, k = kb + kl;
-        T v = T(0);
-        if (i < i1 && k < k_hi) {
-          const int64_t st = i / P + k / Q;
-          if (st >= g.s0 && st < g.s1) v = c[mat + i * n + k];
-        }
-        As[kl][il] = v;
-      }
-      // B = U[k, j] strictly above diagonal blocks
-#pragma unroll
-      for (int ld = 0; ld < 4; ++ld) {
-        const int jl = tid & 63, kl = (tid >> 6) + 4 * ld;
-        const int64_t j = j0 + jl, k = kb + kl;
-        T v = T(0);
-        if (j < j1 && k < k_hi && k / Q < j / Q) v = ub[k * n + j];
-        Bs[kl][jl] = v;
-      }
-      __syncthreads();
-#pragma unroll
-      for (int kk = 0; kk < FB_K; ++kk) {
-        T av[4], bv[4];
-#pragma unroll
-        for (int a = 0; a < 4; ++a) av[a] = As[kk][ty + 16 * a];
-#pragma unroll
-        for (int q2 = 0; q2 < 4; ++q2) bv[q2] = Bs[kk][tx + 16 * q2];
-#pragma unroll
-        for (int a = 0; a < 4; ++a)
-#pragma unroll
-          for (int q2 = 0; q2 < 4; ++q2) accr[a][q2] += av[a] * bv[q2];
-      }
-      __syncthreads();
+    for (int x = 0; x < AL; ++x) {
+      const int64_t i = i0 + ar + ASTEP * x;
+      const bool in = i < i1;
+      arow[x] = c + mat + (in ? i : 0) * n;
+      alo[x] = clampk((s0 - i / P) * Q, k_hi);  // s0 <= i / P + k / Q < s1
+      ahi[x] = in ? clampk((s1 - i / P) * Q, k_hi) : 0;
     }
+    const int64_t j = j0 + bj;
+    const int bhi = j < j1 ? clampk(j / Q * Q, k_hi) : 0;  // k / Q < j / Q
+    product(accr, arow, alo, ahi, ub + (j < j1 ? j : 0), n, 0, bhi, k_lo, k_hi);
   }
 
   // ---------------- epilogue: only the targets receive the feedback
 #pragma unroll
-  for (int a = 0; a < 4; ++a) {
-    const int64_t i = i0 + ty + 16 * a;
-    if (i >= i1) continue;
+  for (int d = 0; d < 2; ++d) {
+    const int64_t j = j0 + wj + 16 * d + li;
+    if (j >= j1) continue;
+    const int64_t jc = j / g.Q;
 #pragma unroll
-    for (int q2 = 0; q2 < 4; ++q2) {
-      const int64_t j = j0 + tx + 16 * q2;
-      if (j >= j1) continue;
-      const int64_t st = i / P + j / Q;
-      if (st < g.s1 || st >= g.s_end) continue;
-      const int64_t off = mat + i * n + j;
-      c[off] = c[off] + accd[a][q2];
-      y[off] = (y[off] + accd[a][q2]) + accr[a][q2];
-    }
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int64_t i = i0 + wi + 16 * a + M::row(kq, r);
+        if (i >= i1) continue;
+        const int64_t st = i / g.P + jc;
+        if (st < g.s1 || st >= g.s_end) continue;
+        const int64_t off = mat + i * n + j;
+        c[off] = c[off] + accd[a][d][r];
+        y[off] = (y[off] + accd[a][d][r]) + accr[a][d][r];
+      }
   }
 }
 
@@ -236,9 +293,9 @@ int gptq2d_flush(T* y, T* c, const T* e, const T* l, const T* u, int64_t m, int6
   if (m <= 0 || n <= 0 || P <= 0 || Q <= 0 || s0 < 0 || s1 <= s0 || s_end < s1) return GPTQ2D_EINVAL;
   if (B == 0 || s_end == s1) return 0;
   if constexpr (sizeof(T) == 4) {
-    // 32 x 32 coarse cells (the fused engine's tiles, or 32 x 32 super-entries): fp32 MFMA (its buffer
-    // resources are based at each panel, so 32-bit offsets hold for rows and k-tiles of up to 2^20
-    // elements, i.e. any m, n < 2^20)
+    // 32 x 32 coarse cells (the fused engine's tiles, or 32 x 32 super-entries): the tuned fp32 kernel (its
+    // buffer resources are based at each panel, so 32-bit offsets hold for rows and k-tiles of up to 2^20
+    // elements, i.e. any m, n < 2^20); everything else on the cell-masked MFMA kernel below
     if (P == 32 && Q == 32 && m < ((int64_t)1 << 20) && n < ((int64_t)1 << 20)) {
       const bool prof = gptq2d_prof_on(PROF_FLUSH);
       if (prof) gptq2d_prof_begin(PROF_FLUSH, stream);
@@ -254,7 +311,7 @@ int gptq2d_flush(T* y, T* c, const T* e, const T* l, const T* u, int64_t m, int6
   Grid3 gr = make_grid(nx, nrow_tiles, B);
   const bool prof = gptq2d_prof_on(PROF_FLUSH);
   if (prof) gptq2d_prof_begin(PROF_FLUSH, stream);
-  hipLaunchKernelGGL(flush_valu_kernel<T>, gr.grid, dim3(256), 0, stream, y, c, e, l, u, g, lmap, umap, gr.nx, gr.ny);
+  hipLaunchKernelGGL(flush_mfma_kernel<T>, gr.grid, dim3(256), 0, stream, y, c, e, l, u, g, lmap, umap, gr.nx, gr.ny);
   if (prof) gptq2d_prof_end(PROF_FLUSH, (double)B * gptq2d_flush_flops(m, n, P, Q, s0, s1, s_end), stream);
   return (int)hipGetLastError();
 }

@@ -1,5 +1,6 @@
-"""GPU tests of the block flush (gptq2d_flush_*), both the generic kernel and the tile-aligned MFMA one
-(fp32 with 32 x 32 coarse cells), against a dense CPU statement of the flush:
+"""GPU tests of the block flush (gptq2d_flush_*), both the cell-masked MFMA kernel (any cell shape, fp32 and
+fp64) and the tuned tile-aligned one (fp32 with 32 x 32 coarse cells), against a dense CPU statement of the
+flush:
 
   stage(i, j) = i // P + j // Q;  band = [s0, s1);  targets = [s1, s_end)
   D = (L masked to k//P < i//P) @ (E masked to the band);  R = (C masked to the band) @ (U masked to k//Q < j//Q)
@@ -39,6 +40,9 @@ CASES = [  # m, n, P, Q, s0, s1, s_end
     (300, 200, 32, 32, 2, 3, 9), (300, 200, 32, 32, 4, 8, 20), (1000, 1000, 32, 32, 0, 16, 63),
     (1000, 1000, 32, 32, 16, 32, 63), (1000, 1000, 32, 32, 40, 41, 48), (520, 1030, 32, 32, 10, 14, 50),
     (64, 96, 1, 1, 10, 20, 150), (48, 40, 4, 8, 2, 5, 17), (90, 75, 3, 5, 3, 9, 34),
+    # 16 x 16 cells (the trellis configuration's super-entries), 1 x 32 rows, cells taller than an output tile
+    (256, 320, 16, 16, 3, 9, 40), (520, 130, 16, 16, 0, 4, 30), (1000, 600, 16, 16, 20, 30, 90),
+    (96, 256, 1, 32, 4, 12, 30), (300, 200, 100, 40, 0, 1, 5),
 ]
 
 
