@@ -68,7 +68,7 @@ def _parse():
     ap.add_argument("--config", default="H", help="workload from instances.CONFIGS (default: the headline layer)")
     ap.add_argument("--cpu-stages", type=int, default=4096, help="sweep stages in the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--configs", default="C2,C3,C4,C5a,C5a3,C5b",
+    ap.add_argument("--configs", default="C2,C3,H64,C4,C5a,C5a3,C5b",
                     help="comma-separated other configurations to time after the headline layer ('' for none)")
     return ap.parse_args()
 
@@ -202,7 +202,7 @@ def _config_lines(torch, dev, h_layer, names, steps=2):
     one GPU: C2 and C3 (fused sweep, affine INT quantizers), C4 (the headline layer's weights and factors in
     16 x 16 super-entries, HYB trellis search per stage), C5a (three-factor layer, 1 x 32 abs-max super-entries,
     fused), C5a3 (the same layer three-sided, D-sided sweep), C5b (eight 2048^2 layers in one captured graph
-    replay)."""
+    replay), H64 (the headline layer in fp64)."""
     import gptq_2d as G
     import gptq_2d_ldl as LDL
     import instances
@@ -233,6 +233,8 @@ def _config_lines(torch, dev, h_layer, names, steps=2):
 
     x, a, b = h_layer
     m, n = x.shape
+    if "H64" in names:
+        _h64_line(torch, x, a, b, steps, lines, line)
     if "C4" in names:
         _c4_line(torch, dev, x, a, b, steps, lines, line)
     if "C5a" in names:
@@ -242,6 +244,26 @@ def _config_lines(torch, dev, h_layer, names, steps=2):
     if "C5b" in names:
         _c5b_line(torch, dev, steps, lines, line)
     return lines
+
+
+def _h64_line(torch, x, a, b, steps, lines, line):
+    """The headline layer in fp64 end to end: fp64 LDLs (VALU GEMMs) and the fused fp64 sweep (tile sweep on
+    VALU, flushes on fp64 MFMA)."""
+    import gptq_2d as G
+    import gptq_2d_ldl as LDL
+    import instances
+    import quantizer_int as QI
+
+    cfg = instances.CONFIGS["H"]
+    x64, a64, b64 = x.double(), a.double(), b.double()
+    scale, zp = instances.quantizer_inputs(cfg, x64)
+    q = functools.partial(QI.affine_quantizer_hip, qmin=cfg.qmin, qmax=cfg.qmax)
+    factors = lambda: LDL.feedback_factors_of_grams(a64, b64, check=False)
+    lo, up = factors()
+    t_ldl = _timed(torch, factors, steps)
+    t_sw = _timed(torch, lambda: G.gptq_2d(x64, lo, up, quantizer=q, quantizer_inputs=(scale, zp),
+                                           outer_block_size=OUTER_BLOCK), steps)
+    lines["H64"] = line(f"{x.size(0)}x{x.size(1)} INT4 symmetric per row in fp64 (factors and sweep)", t_ldl, t_sw)
 
 
 def _c4_line(torch, dev, x, a, b, steps, lines, line):

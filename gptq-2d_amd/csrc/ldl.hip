@@ -58,11 +58,13 @@ template <>
 struct LdlBlock<float> {
   static constexpr int NB = 64;
   static constexpr int PB = 64;
+  static constexpr int SB = 128;  // largest diagonal block of the block normalisation (LDS solve above NB)
 };
 template <>
 struct LdlBlock<double> {
   static constexpr int NB = 32;
   static constexpr int PB = 32;
+  static constexpr int SB = 64;
 };
 
 __device__ __forceinline__ float bcast(float v, int lane) {
@@ -629,6 +631,59 @@ __global__ __launch_bounds__(256) void normalize_block_kernel(T* __restrict__ ou
       v = T(0);
       for (int tt = lc; tt < p; ++tt) v += rows[li][tt] * dinv[tt][lc];
     }
+    out[i * k + j] = v;
+  }
+}
+
+// Block normalisation for NB < p <= PM: as normalize_block_kernel, but the rows below the block solve
+// X D_b = R_b (forward substitution from the last column, one thread per row) against the diagonal block
+// D_b staged in LDS, instead of multiplying by an inverse held in one wave's registers.
+template <typename T, int PM>
+__global__ __launch_bounds__(256) void normalize_block_solve_kernel(T* __restrict__ out, const T* __restrict__ w,
+                                                                    int64_t k, int p, int64_t base, int64_t rs,
+                                                                    int64_t cs) {
+  __shared__ T dblk[PM][PM + 1];
+  __shared__ T rows[64][PM + 1];
+  const int64_t b = blockIdx.x, c0 = b * p;
+  const int64_t i0 = (int64_t)blockIdx.y * 64;
+  const int tid = threadIdx.x;
+  const bool below = i0 + 63 >= c0 + p;  // this chunk has rows strictly below the block
+  const bool row_fast = rs == 1 || rs == -1;
+  if (below) {
+    for (int t = tid; t < p * p; t += 256) {
+      const int r = row_fast ? t % p : t / p, cc = row_fast ? t / p : t % p;
+      dblk[r][cc] = cc <= r ? w[base + (c0 + r) * rs + (c0 + cc) * cs] : T(0);
+    }
+    for (int t = tid; t < 64 * p; t += 256) {
+      const int li = row_fast ? t % 64 : t / p, lc = row_fast ? t / 64 : t % p;
+      const int64_t i = i0 + li;
+      rows[li][lc] = (i < k && i >= c0 + p) ? w[base + i * rs + (c0 + lc) * cs] : T(0);
+    }
+  }
+  __syncthreads();
+  if (below && tid < 64) {
+    const int64_t i = i0 + tid;
+    if (i < k && i >= c0 + p) {
+      T* x = rows[tid];
+      for (int cc = p - 1; cc >= 0; --cc) {
+        T acc = x[cc];
+        for (int t = cc + 1; t < p; ++t) acc -= x[t] * dblk[t][cc];
+        x[cc] = acc / dblk[cc][cc];
+      }
+    }
+  }
+  __syncthreads();
+  for (int t = tid; t < 64 * p; t += 256) {
+    const int li = t / p, lc = t % p;
+    const int64_t i = i0 + li, j = c0 + lc;
+    if (i >= k) continue;
+    T v;
+    if (i < c0)
+      v = T(0);
+    else if (i < c0 + p)
+      v = (i - c0 == lc) ? T(1) : T(0);
+    else
+      v = rows[li][lc];
     out[i * k + j] = v;
   }
 }
@@ -1256,10 +1311,15 @@ int normalize(T* out, const T* w, int64_t k, int64_t size, int64_t base, int64_t
     const dim3 grid((unsigned)cdiv(k, 32), (unsigned)cdiv(k, 32));
     hipLaunchKernelGGL(normalize_unit_kernel<T>, grid, dim3(256), 0, stream, out, w, k, base, rs, cs);
   } else {
-    if (size > NB) return GPTQ2D_EUNSUPPORTED;
+    constexpr int SB = LdlBlock<T>::SB;
+    if (size > SB) return GPTQ2D_EUNSUPPORTED;
     const dim3 grid((unsigned)(k / size), (unsigned)cdiv(k, 64));
-    hipLaunchKernelGGL((normalize_block_kernel<T, NB>), grid, dim3(256), 0, stream, out, w, k, (int)size, base, rs,
-                       cs);
+    if (size <= NB)
+      hipLaunchKernelGGL((normalize_block_kernel<T, NB>), grid, dim3(256), 0, stream, out, w, k, (int)size, base, rs,
+                         cs);
+    else
+      hipLaunchKernelGGL((normalize_block_solve_kernel<T, SB>), grid, dim3(256), 0, stream, out, w, k, (int)size,
+                         base, rs, cs);
   }
   return (int)hipGetLastError();
 }
@@ -1272,7 +1332,7 @@ int ldl_of_inverse_part(const T* m, T* out, T* work, int* info, int64_t k, int64
                         int64_t col_end, bool finish, hipStream_t stream) {
   constexpr int PB = LdlBlock<T>::PB;
   if (k < 0 || size <= 0 || (k > 0 && k % size)) return GPTQ2D_EINVAL;
-  if (size > 1 && size > LdlBlock<T>::NB) return GPTQ2D_EUNSUPPORTED;
+  if (size > 1 && size > LdlBlock<T>::SB) return GPTQ2D_EUNSUPPORTED;
   // range ends on panel boundaries, or at k (col_begin = k: nothing left to factor)
   if (col_begin < 0 || (col_begin % PB && col_begin != k) || (col_end >= 0 && col_end < col_begin) ||
       (col_end >= 0 && col_end % PB && col_end < k))
@@ -1410,7 +1470,7 @@ template <typename T>
 int ldl_impl(bool inverse, const T* m, T* out, T* work, int* info, int64_t batch, int64_t k, int64_t size,
              hipStream_t stream) {
   if (batch < 0 || k < 0 || size <= 0 || (k > 0 && k % size)) return GPTQ2D_EINVAL;
-  if (size > 1 && size > LdlBlock<T>::NB) return GPTQ2D_EUNSUPPORTED;
+  if (size > 1 && size > LdlBlock<T>::SB) return GPTQ2D_EUNSUPPORTED;
   if (batch == 0) return 0;
   if (k == 0) {
     hipLaunchKernelGGL(zero_info_kernel, dim3((unsigned)(cdiv(batch, 256) < 1024 ? cdiv(batch, 256) : 1024)), dim3(256),

@@ -19,8 +19,9 @@ import torch
 
 import _hip
 
-# p x p diagonal blocks up to this size are normalised on the GPU (fp32; fp64: 32).
-MAX_BLOCK = {torch.float32: 64, torch.float64: 32}
+# p x p diagonal blocks up to this size are normalised on the GPU (one wave's register inverse up to 64 /
+# 32, a triangular solve against the block in LDS above that).
+MAX_BLOCK = {torch.float32: 128, torch.float64: 64}
 
 # Three side streams per device for feedback_factors_of_grams (created once: a new stream per call
 # would cost a stream creation and defeat the caching allocator's reuse of its blocks).

@@ -97,18 +97,23 @@ def _check_factor(got, m, size, inverse, tol):
 def test_ldl_of_inverse(k, dtype):
     """fp32 from k = 512 on: the inverse's level products on the triangular MFMA kernel (600, 1000:
     short last pairs and ragged 128-blocks; 1536: three full levels and a short one; 2052: the inverse
-    split at its top level), or on rocBLAS where rows are not 16-byte aligned (777)."""
+    split at its top level), or on the library's strided GEMM where rows are not 16-byte aligned (777)."""
     print(f"ldl_of_inverse k={k} {dtype}", flush=True)
     m = instances.wishart_factor(k, .5, 10 + k).to(dtype).to(DEV)
     got = LDL.ldl_of_inverse(m)
     _check_factor(got, m, 1, True, 1e-9 if dtype == torch.float64 else 2e-4)
 
 
-@pytest.mark.parametrize("k,size", [(64, 2), (96, 4), (256, 16), (128, 32), (192, 64)])
+@pytest.mark.parametrize("k,size", [(64, 2), (96, 4), (256, 16), (128, 32), (192, 64), (240, 48), (384, 96),
+                                    (256, 128)])
 @pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
 def test_ldl_of_inverse_blocks(k, size, dtype):
+    """Diagonal blocks up to the one-wave register inverse (64 fp32, 32 fp64) and, above it, the LDS solve
+    (up to 128 fp32, 64 fp64; larger blocks are refused)."""
     if size > LDL.MAX_BLOCK[dtype]:
-        pytest.skip("block larger than the GPU normalisation supports for this dtype")
+        with pytest.raises(AssertionError):
+            LDL.ldl_of_inverse(torch.eye(k, dtype=dtype, device=DEV), size=size)
+        return
     print(f"ldl_of_inverse k={k} size={size} {dtype}", flush=True)
     m = instances.wishart_factor(k, 1., 20 + k).to(dtype).to(DEV)
     got = LDL.ldl_of_inverse(m, size=size)
