@@ -4,8 +4,9 @@
 // reversals (negative strides) and sub-blocks without copies.  Structurally zero parts of
 // triangular operands are skipped in the K loop and masked at load time, so they are never
 // read.  fp32 runs on the MFMA path (v_mfma_f32_32x32x2_f32: 128 x 128 output tile per
-// workgroup, four waves of 64 x 64, K staged through LDS 16 deep); fp64 and tiles that
-// are mostly empty use the VALU path (64 x 64 tile, 4 x 4 outputs per thread).
+// workgroup, four waves of 64 x 64, K staged through LDS 16 deep), fp32 products of fewer than 64
+// rows or columns on the VALU path (64 x 64 tile, 4 x 4 outputs per thread); fp64 on MFMA
+// (v_mfma_f64_16x16x4_f64, 64 x 64 tile).
 #include "linalg.h"
 
 namespace {
@@ -361,6 +362,80 @@ __global__ __launch_bounds__(256, 2) void gemm_mfma_vec_kernel(GemmProblem<float
       }
 }
 
+// ------------------------------------------------------------------------------------------------ MFMA path (fp64)
+
+constexpr int DT = 64, DK = 32;
+
+// 256 threads = 4 waves; wave w owns the 32 x 32 quadrant (w / 2, w % 2) of the 64 x 64 tile as 2 x 2 blocks
+// of v_mfma_f64_16x16x4_f64, whose lane l supplies A(l % 16, l / 16) and B(l / 16, l % 16) and whose
+// accumulator element r of lane l holds D(l / 16 + 4 r, l % 16).  K is staged through LDS 32 deep, with the
+// next k-block loaded into registers while the current one's MFMAs run; the loads apply the operands'
+// triangle masks.
+__global__ __launch_bounds__(256) void gemm_mfma64_kernel(GemmProblem<double> p) {
+  typedef double double4_t __attribute__((ext_vector_type(4)));
+  constexpr int AL = DT * DK / 256;  // staged entries per thread and operand
+  __shared__ double As[DK][DT + 1];
+  __shared__ double Bs[DK][DT + 1];
+  const int64_t bi = blockIdx.z;
+  const int64_t i0 = (int64_t)blockIdx.y * DT, j0 = (int64_t)blockIdx.x * DT;
+  const int64_t i1 = i0 + DT < p.M ? i0 + DT : p.M, j1 = j0 + DT < p.N ? j0 + DT : p.N;
+  const TileRange kr = tile_k_range(p, i0, i1, j0, j1);
+  if (kr.empty) return;
+  const double* a = p.A + bi * p.a_bs;
+  const double* b = p.B + bi * p.b_bs;
+  double* d = p.D + bi * p.d_bs;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int li = lane & 15, kq = lane >> 4;
+  const int wi = 32 * (wave >> 1), wj = 32 * (wave & 1);
+  const int ak = tid % DK, ar = tid / DK;  // A entry x: (ar + (256 / DK) x, ak)
+  const int bj = tid % DT, bk = tid / DT;  // B entry x: (bk + (256 / DT) x, bj)
+  double4_t acc[2][2];
+#pragma unroll
+  for (int r = 0; r < 2; ++r)
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[r][c][e] = 0.;
+  double ra[AL], rb[AL];
+  auto load = [&](int64_t kb) {
+#pragma unroll
+    for (int x = 0; x < AL; ++x) {
+      ra[x] = load_a(p, a, i0 + ar + (256 / DK) * x, kb + ak, kr.k_hi);
+      rb[x] = load_b(p, b, kb + bk + (256 / DT) * x, j0 + bj, kr.k_hi);
+    }
+  };
+  if (kr.k_lo < kr.k_hi) load(kr.k_lo);
+  for (int64_t kb = kr.k_lo; kb < kr.k_hi; kb += DK) {
+#pragma unroll
+    for (int x = 0; x < AL; ++x) {
+      As[ak][ar + (256 / DK) * x] = ra[x];
+      Bs[bk + (256 / DT) * x][bj] = rb[x];
+    }
+    __syncthreads();
+    if (kb + DK < kr.k_hi) load(kb + DK);
+#pragma unroll
+    for (int k4 = 0; k4 < DK; k4 += 4) {
+      double av[2], bv[2];
+#pragma unroll
+      for (int r = 0; r < 2; ++r) av[r] = As[k4 + kq][wi + 16 * r + li];
+#pragma unroll
+      for (int c = 0; c < 2; ++c) bv[c] = Bs[k4 + kq][wj + 16 * c + li];
+#pragma unroll
+      for (int r = 0; r < 2; ++r)
+#pragma unroll
+        for (int c = 0; c < 2; ++c) acc[r][c] = __builtin_amdgcn_mfma_f64_16x16x4f64(av[r], bv[c], acc[r][c], 0, 0, 0);
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int r = 0; r < 2; ++r)
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        store_d(p, d, i0 + wi + 16 * r + kq + 4 * e, j0 + wj + 16 * c + li, acc[r][c][e]);
+}
+
 bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15) == 0; }
 
 // The vectorised path applies: strides, offsets and the K extent in float4 granules.
@@ -380,7 +455,11 @@ int gptq2d_gemm(const GemmProblem<T>& p, hipStream_t stream) {
   if (p.M < 0 || p.N < 0 || p.K < 0 || p.batch < 0) return GPTQ2D_EINVAL;
   if (p.M == 0 || p.N == 0 || p.batch == 0) return 0;
   if (p.batch > 65535) return GPTQ2D_EUNSUPPORTED;
-  if constexpr (sizeof(T) == 4) {
+  if constexpr (sizeof(T) == 8) {
+    const dim3 grid((unsigned)cdiv(p.N, DT), (unsigned)cdiv(p.M, DT), (unsigned)p.batch);
+    hipLaunchKernelGGL(gemm_mfma64_kernel, grid, dim3(256), 0, stream, p);
+    return (int)hipGetLastError();
+  } else {
     bool bk = false;
     if (vec_ok(p, bk)) {
       const dim3 grid((unsigned)cdiv(p.N, MT), (unsigned)cdiv(p.M, MT), (unsigned)p.batch);

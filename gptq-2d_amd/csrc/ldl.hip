@@ -1025,11 +1025,40 @@ struct CholeskyRun {
     return 0;
   }
 
-  // fp64 (and fp32 with k % 4 != 0): panel, staged block into W, trailing update on gemm.hip.
+  // fp64 (and fp32 with k % 4 != 0): strips of NS columns, left-looking inside a strip, right-looking
+  // between strips.  Step j0: the panel's columns first receive the updates of the strip's earlier panels
+  // (W[j0:, j0:j0+n] -= W[j0:, s0:j0] W[j0:j0+n, s0:j0]^T), then the panel is factored and its diagonal
+  // block staged into W; at a strip's end the whole trailing triangle receives the strip in one rank-NS
+  // update.  Against a rank-PB update of the trailing triangle per panel this reads and writes it once per
+  // strip instead of once per panel (the update is bound by that traffic, not by its flops).
+  static constexpr int64_t NS = 256;
+  static_assert(NS % PB == 0, "strips hold whole panels");
+
   int step_plain() {
     int rc;
     const int n = k - j0 < PB ? (int)(k - j0) : PB;
     const int64_t rest = k - j0 - PB;
+    const int64_t s0 = j0 / NS * NS;  // this panel's strip
+    if (j0 > s0) {
+      GemmProblem<T> g{};
+      g.M = k - j0;
+      g.N = n;
+      g.K = j0 - s0;
+      g.batch = 1;
+      g.A = w + j0 * k + s0;  // W[j0:, s0:j0]
+      g.a_rs = k;
+      g.a_cs = 1;
+      g.B = g.A;  // B(kk, jj) = W[j0 + jj, s0 + kk]
+      g.b_rs = 1;
+      g.b_cs = k;
+      g.D = w + j0 * k + j0;
+      g.d_rs = k;
+      g.d_cs = 1;
+      g.alpha = T(-1);
+      g.beta = T(1);
+      g.d_tri = TRI_LOWER;
+      if ((rc = gptq2d_gemm<T>(g, stream))) return rc;
+    }
     const unsigned blocks = rest > 0 ? (unsigned)(cdiv(rest, 64) < 256 ? cdiv(rest, 64) : 256) : 1u;
     hipLaunchKernelGGL((potrf_panel_kernel<T, PB>), dim3(blocks), dim3(256), 0, stream, w, k, j0, n, k, info, stage);
     if ((rc = (int)hipGetLastError())) return rc;
@@ -1039,18 +1068,20 @@ struct CholeskyRun {
       done = true;
       return 0;
     }
-    // trailing lower triangle: W22 -= P P^T with P = W[j0+PB:, j0:j0+PB]
+    const int64_t s1 = j0 + PB;
+    if (s1 % NS) return 0;  // the strip goes on
+    // trailing lower triangle: W22 -= P P^T with P = W[s1:, s0:s1]
     GemmProblem<T> g{};
     g.M = g.N = rest;
-    g.K = PB;
+    g.K = s1 - s0;
     g.batch = 1;
-    g.A = w + (j0 + PB) * k + j0;
+    g.A = w + s1 * k + s0;
     g.a_rs = k;
     g.a_cs = 1;
     g.B = g.A;
     g.b_rs = 1;
     g.b_cs = k;
-    g.D = w + (j0 + PB) * k + j0 + PB;
+    g.D = w + s1 * k + s1;
     g.d_rs = k;
     g.d_cs = 1;
     g.alpha = T(-1);
