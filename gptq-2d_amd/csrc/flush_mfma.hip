@@ -94,9 +94,9 @@ __host__ __device__ inline void row_block_span(const G& g, Int by, Int& first, I
 }
 
 // Panels in LDS, per k-tile (ROWS = 32 WT), both double-buffered:
-//   A (ROWS x 32 k; k contiguous in memory): float f holds row f / 32 and k = 4 (q ^ (row % 8)) + f % 4
-//     with q = (f % 32) / 4 -- the 16-byte k-quads XOR-swizzled by row, so that the 8 rows that 8
-//     lanes read at one k-quad lie in 8 different bank groups;
+//   A (ROWS x 32 k; k contiguous in memory): float f holds row f / 32 and k = 4 (q ^ quad_swizzle(row)) +
+//     f % 4 with q = (f % 32) / 4 -- the 16-byte k-quads XOR-swizzled by row (lds_dma.h), so that the
+//     rows that lanes read together at one k-quad lie in different bank groups;
 //   B (32 k x ROWS columns; columns contiguous in memory): k-row k at k ROWS, plus BPAD floats per
 //     256-float group of rows, so that the lane halves (rows k and k + 16) fall 32 banks apart.
 template <int WT>
@@ -152,7 +152,7 @@ __device__ __forceinline__ void flush_phase(floatx16 (&acc)[WT / 2][WT / 2], Flu
     Geo o;
     const int f = (wave + 4 * x) * PER + lane * W;
     const int row = f / TS;
-    o.a_kk = 4 * (((f % TS) / 4) ^ (row & 7)) + f % 4;
+    o.a_kk = 4 * (((f % TS) / 4) ^ quad_swizzle(row)) + f % 4;
     const int i = (int)I0 * TS + row;
     o.a_in = i < gm;
     o.a_t = i >> 5;
@@ -191,7 +191,7 @@ __device__ __forceinline__ void flush_phase(floatx16 (&acc)[WT / 2][WT / 2], Flu
   // fragments: A tile a, k-quad 4 hh + v of row (wi + a) 32 + li; B tile d, k = 16 hh + s, column
   // (wj + d) 32 + li -- the k of MFMA s is 16 hh + s for both operands
   const int a_base = (wi * TS + li) * TS;
-  const int sw = li & 7;
+  const int sw = quad_swizzle(li);
   const int b_base = 16 * hh * ROWS + wj * TS + li + 16 * hh * ROWS / 256 * L::BPAD;
 
   auto step = [&](int64_t t, auto cur_c) {

@@ -695,9 +695,9 @@ __global__ __launch_bounds__(256) void normalize_block_solve_kernel(T* __restric
 // of P, and the 128 rows that are its columns) are loaded one k-tile ahead straight into LDS
 // (buffer loads with the LDS destination bit), double-buffered, one barrier per k-tile; rows past R
 // (A) or past min(R, C) (B) load as zeros.  Both panels use the same layout -- P's k runs along a row
-// for both operands of D = P P^T: float f of a panel holds row f / 32 and k = 4 (q ^ (row % 8)) +
-// f % 4, q = (f % 32) / 4 (16-byte k-quads XOR-swizzled by row, so that 8 lanes reading one quad of
-// 8 rows hit 8 bank groups), and every fragment read is 128 bits.  Lane l (i = l % 32, h = l / 32)
+// for both operands of D = P P^T: float f of a panel holds row f / 32 and k = 4 (q ^ quad_swizzle(row))
+// + f % 4, q = (f % 32) / 4 (16-byte k-quads XOR-swizzled by row, lds_dma.h, so that the lanes reading one
+// quad of different rows hit different bank groups), and every fragment read is 128 bits.  Lane l (i = l % 32, h = l / 32)
 // feeds A(i, 16 h + s) and B(16 h + s, i) to MFMA s; the accumulators hold
 // D(8 (r / 4) + 4 h + r % 4, i).  The epilogue subtracts the products from D in place (read all
 // 16 entries of a block, then write), masked to the lower triangle, to i < R and to j < C.
@@ -729,7 +729,7 @@ __device__ __forceinline__ void syrk_wide_block(WideLds& sm, float* __restrict__
 #pragma unroll
   for (int x = 0; x < 4; ++x) {
     const int f = (wave + 4 * x) * 256 + 4 * lane;
-    const int row = f >> 5, kq = ((f >> 2) & 7) ^ (row & 7);
+    const int row = f >> 5, kq = ((f >> 2) & 7) ^ quad_swizzle(row);
     const int ia = I0 + row, ib = J0 + row;
     aoff[x] = ia < R ? (ia * ild + 4 * kq) * 4 : OOB;
     boff[x] = ib < CR ? (ib * ild + 4 * kq) * 4 : OOB;
@@ -753,7 +753,7 @@ __device__ __forceinline__ void syrk_wide_block(WideLds& sm, float* __restrict__
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[a][d][r] = 0.f;
 
-  const int sw = li & 7;
+  const int sw = quad_swizzle(li);
   const int a_base = (64 * wy + li) * WK, b_base = (64 * wx + li) * WK;
   auto step = [&](int t, auto cur_c) {
     constexpr int cur = decltype(cur_c)::value;

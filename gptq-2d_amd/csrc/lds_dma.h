@@ -14,6 +14,18 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t matrix_rsrc(const float* base,
 }
 constexpr int OOB = 0x7ffffff0;  // a byte offset past every extent these kernels accept
 
+// Swizzle of the 16-byte k-quads of a staged 32-float panel row: quad q of row `row` is stored at quad
+// position q ^ quad_swizzle(row).  A 128-bit operand read has the lanes of 32 consecutive rows read one
+// quad each; over row % 32, (r ^ (r >> 3)) % 8 gives distinct positions to any 8 consecutive rows (an LDS
+// of 32 banks serves 8 such lanes a cycle) and to any 8 rows of one parity among 16 consecutive ones (an
+// LDS of 64 banks serves 16 lanes a cycle, rows r and r + 1 lying 32 banks apart), so neither stalls on
+// bank conflicts.  (The plain row % 8 puts rows r and r + 8 on one bank group of a 64-bank LDS: counters
+// showed a conflict cycle for every MFMA of the flush.)
+__device__ __forceinline__ int quad_swizzle(int row) {
+  const int r = row & 31;
+  return (r ^ (r >> 3)) & 7;
+}
+
 typedef __attribute__((address_space(3))) float lds_float;
 
 // LDS-direct load of W floats per lane (W = 4: 128 bits, W = 1: 32 bits) from byte offset `off` of

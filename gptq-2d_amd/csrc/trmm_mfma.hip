@@ -14,7 +14,8 @@
 // walks k-tiles of 32; both panels are loaded one k-tile ahead straight into LDS (buffer loads with
 // the LDS destination bit), double-buffered, one barrier per k-tile -- the scheme of the sweep's
 // outer flush (flush_mfma.hip), with the same LDS layouts: A (128 rows x 32 k) with its 16-byte
-// k-quads XOR-swizzled by row, B (32 k-rows x 128 columns) padded by 4 floats per two k-rows.
+// k-quads XOR-swizzled by row (quad_swizzle, lds_dma.h), B (32 k-rows x 128 columns) padded by 4 floats per
+// two k-rows.
 // Loads past the matrices return zeros (buffer range checks), so ragged edges need no branches.
 #include "common.h"
 #include "lds_dma.h"
@@ -74,7 +75,7 @@ __global__ __launch_bounds__(256, 2) void tri_gemm_kernel(TriGemm g, int64_t nbn
 #pragma unroll
   for (int x = 0; x < 4; ++x) {
     const int f = (wave + 4 * x) * 256 + 4 * lane;
-    const int row = f >> 5, kq = ((f >> 2) & 7) ^ (row & 7);
+    const int row = f >> 5, kq = ((f >> 2) & 7) ^ quad_swizzle(row);
     akk[x] = 4 * kq;
     aoff[x] = I0 + row < M ? ((I0 + row) * lda + akk[x]) * 4 : OOB;
     bk[x] = f >> 7;
@@ -104,7 +105,7 @@ __global__ __launch_bounds__(256, 2) void tri_gemm_kernel(TriGemm g, int64_t nbn
   // fragments: A tile a, k-quad 4 hh + v of row 64 wy + 32 a + li; B tile d, k = 16 hh + s, column
   // 64 wx + 32 d + li -- the k of MFMA s is 16 hh + s for both operands
   const int wy = wave >> 1, wx = wave & 1;
-  const int a_base = (64 * wy + li) * KT, sw = li & 7;
+  const int a_base = (64 * wy + li) * KT, sw = quad_swizzle(li);
   const int b_base = 16 * hh * TB + 64 * wx + li + 16 * hh * TB / 256 * BPAD;
   auto step = [&](int t, auto cur_c) {
     constexpr int cur = decltype(cur_c)::value;
