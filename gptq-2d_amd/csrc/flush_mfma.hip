@@ -93,6 +93,94 @@ __host__ __device__ inline void row_block_span(const G& g, Int by, Int& first, I
   count = (I0 < (Int)g.mt && jt_hi >= jt_lo) ? jt_hi / WT - first + 1 : 0;
 }
 
+// Order of the work items.  Row blocks are grouped in bands of SR, and a band's items are numbered column
+// block by column block (inside a column by row block), so that a run of 16 consecutive items -- which go
+// to one XCD, see the kernel -- is about 4 row blocks x 4 column blocks: every L / C row panel and E / U
+// column panel the run streams through its L2 serves four of its workgroups (a run along one row block
+// shares its row panel 16 ways and no column panel).
+constexpr int SR = 4;
+
+// Inclusive prefix sum over the 64 lanes of a wave.
+__device__ __forceinline__ int wave_scan(int v) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int o = __shfl_up(v, d, 64);
+    v += lane >= d ? o : 0;
+  }
+  return v;
+}
+
+// The entry of the sequence of counts f(0), f(1), ..., f(n - 1) that holds position k, with k reduced by the
+// counts before it; -1 when k lies past the end.  Each lane evaluates one count per pass of 64 (wave-uniform
+// result).
+template <typename F>
+__device__ __forceinline__ int wave_locate(const F& f, int n, int& k) {
+  const int lane = threadIdx.x & 63;
+  for (int base = 0; base < n; base += 64) {
+    const int cnt = base + lane < n ? f(base + lane) : 0;
+    const int s = wave_scan(cnt);
+    const int tot = __builtin_amdgcn_readfirstlane(__shfl(s, 63, 64));
+    if (k < tot) {
+      const unsigned long long hit = __ballot(s > k);  // lane 63 at least
+      const int j = __builtin_amdgcn_readfirstlane(__builtin_ctzll(hit));
+      k -= __builtin_amdgcn_readfirstlane(__shfl(s - cnt, j, 64));
+      return base + j;
+    }
+    k -= tot;
+  }
+  return -1;
+}
+
+// Row block `by` and column block `bx` of work item `item` (false past the last item).  Wave-parallel: a few
+// hundred cycles, where a serial walk over the row blocks cost 10-36 thousand per workgroup at 8192^2.
+template <int WT>
+__device__ __forceinline__ bool item_block(const TileGeo32& q, int item, int& by, int& bx) {
+  const int nby = (q.mt + WT - 1) / WT, nbands = (nby + SR - 1) / SR;
+  auto band_items = [&](int band) {
+    int tot = 0;
+#pragma unroll
+    for (int i = 0; i < SR; ++i) {
+      int first = 0, count = 0;
+      if (band * SR + i < nby) row_block_span<WT>(q, band * SR + i, first, count);
+      tot += count;
+    }
+    return tot;
+  };
+  int k = item;
+  const int band = wave_locate(band_items, nbands, k);
+  if (band < 0) return false;
+  int f[SR], c[SR], lo = INT32_MAX, hi = 0;  // the band's spans [f, f + c); columns [lo, hi)
+#pragma unroll
+  for (int i = 0; i < SR; ++i) {
+    f[i] = c[i] = 0;
+    if (band * SR + i < nby) row_block_span<WT>(q, band * SR + i, f[i], c[i]);
+    if (c[i] > 0) {
+      lo = f[i] < lo ? f[i] : lo;
+      hi = f[i] + c[i] > hi ? f[i] + c[i] : hi;
+    }
+  }
+  auto column_items = [&](int x) {
+    int cnt = 0;
+#pragma unroll
+    for (int i = 0; i < SR; ++i) cnt += lo + x >= f[i] && lo + x < f[i] + c[i] ? 1 : 0;
+    return cnt;
+  };
+  const int x = wave_locate(column_items, hi - lo, k);
+  if (x < 0) return false;
+  bx = lo + x;
+#pragma unroll
+  for (int i = 0; i < SR; ++i)
+    if (bx >= f[i] && bx < f[i] + c[i]) {
+      if (k == 0) {
+        by = band * SR + i;
+        return true;
+      }
+      --k;
+    }
+  return false;
+}
+
 // Panels in LDS, per k-tile (ROWS = 32 WT), both double-buffered:
 //   A (ROWS x 32 k; k contiguous in memory): float f holds row f / 32 and k = 4 (q ^ quad_swizzle(row)) +
 //     f % 4 with q = (f % 32) / 4 -- the 16-byte k-quads XOR-swizzled by row (lds_dma.h), so that the
@@ -262,8 +350,8 @@ __global__ __launch_bounds__(256, 2) void flush_tiles_mfma_kernel(float* __restr
   __shared__ __align__(16) FlushLds<WT> sm;
 
   // XCD-aware order: the hardware deals workgroup w to XCD w % 8; runs of XG consecutive work items
-  // (neighbouring column blocks of a row block, which share L / C rows) go to one XCD and its L2,
-  // and the XCDs take turns run by run, so that all of them see the same mix of item sizes
+  // (about SR x SR neighbouring blocks, item_block) go to one XCD and its L2, and the XCDs take turns
+  // run by run, so that all of them see the same mix of item sizes
   constexpr int XG = 16;
   const int nwg = (int)gridDim.x, w = (int)blockIdx.x;
   const int full = nwg / (8 * XG) * (8 * XG);
@@ -274,15 +362,10 @@ __global__ __launch_bounds__(256, 2) void flush_tiles_mfma_kernel(float* __restr
   }
   const int64_t b = b0 + blockIdx.y;
   const TileGeo32 q{(int)g.mt, (int)g.nt, (int)g.S0, (int)g.S1, (int)g.S_end};
-  int by = 0, first = 0, count = 0;
-  for (; by * WT < q.mt; ++by) {
-    row_block_span<WT>(q, by, first, count);
-    if (item < count) break;
-    item -= count;
-  }
-  if (by * WT >= q.mt) return;
+  int by = 0, bx = 0;
+  if (!item_block<WT>(q, item, by, bx)) return;
   const int I0 = by * WT;
-  const int J0 = (first + item) * WT;
+  const int J0 = bx * WT;
   if (J0 >= q.nt || I0 + J0 >= q.S_end || I0 + J0 + 2 * WT - 2 < q.S1) return;
 
   // workgroup-wide k ranges; nothing to do -> no memory touched
