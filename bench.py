@@ -53,7 +53,7 @@ OUTER_BLOCK = 1024
 # (x1.9997 and x1.0000).  Counters cannot be read inside the timed run, so the figure is the
 # measured one, with the command and per-kernel values in profiles/flush_traffic_H_int4.md; the
 # algorithmic minimum (every operand once) is FLUSH_ALGORITHMIC_BYTES.
-FLUSH_TRAFFIC_BYTES = 2.735e9
+FLUSH_TRAFFIC_BYTES = 2.045e9
 FLUSH_ALGORITHMIC_BYTES = 0.525e9
 # fp32 VALU operations per trellis state evaluation: 2 sub, 2 mul, 1 add (the squared distance),
 # 1 add (the predecessor group's minimum), 1 min.
