@@ -200,9 +200,14 @@ struct FlushLds {
 // Buffer resource over the elements [first, total) of a matrix stored from `base`: offsets count from
 // element `first`, so that they stay small whatever the matrix size (extents capped below OOB).
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rebased_rsrc(const float* base, int64_t first, int64_t total) {
-  int64_t elems = total - first;
-  const int64_t cap = (OOB >> 2) - 64;
-  elems = elems < 0 ? 0 : (elems > cap ? cap : elems);
+  // clamped with shifts and 32-bit compares (the scalar unit has no 64-bit ordered compare, and these are
+  // evaluated once per k-tile in the MFMA loops): a negative extent -> 0, one of 2^29 or more -> cap
+  const uint64_t rem = (uint64_t)(total - first);
+  constexpr unsigned cap = (OOB >> 2) - 64;  // < 2^29
+  unsigned hi = (unsigned)(rem >> 32);
+  const unsigned lo = (unsigned)rem;
+  asm("" : "+s"(hi));  // opaque: otherwise the tests below are folded back into 64-bit compares
+  const unsigned elems = (hi >> 31) ? 0u : (hi != 0 || lo > cap ? cap : lo);
   return matrix_rsrc(base + first, elems);
 }
 
@@ -214,7 +219,7 @@ template <int WT, bool VEC, int PHASE>
 __device__ __forceinline__ void flush_phase(floatx16 (&acc)[WT / 2][WT / 2], FlushLds<WT>& sm, const float* a_mat,
                                             int64_t a_elems, const float* b_mat, int64_t b_elems,
                                             const TileFlush& g, int64_t I0, int64_t J0, int wi, int wj,
-                                            int64_t t_lo, int64_t t_hi, const int (&tlo)[WT / 2][WT / 2],
+                                            int t_lo, int t_hi, const int (&tlo)[WT / 2][WT / 2],
                                             const int (&thi)[WT / 2][WT / 2]) {
   using L = FlushLds<WT>;
   constexpr int H = WT / 2;
@@ -258,11 +263,34 @@ __device__ __forceinline__ void flush_phase(floatx16 (&acc)[WT / 2][WT / 2], Flu
     for (int x = 0; x < NI; ++x) pre[x] = geo(x);
   }
 
+  // whether the workgroup's A rows and B columns are whole tiles inside the matrix (uniform)
+  const int i0t = (int)I0, j0t = (int)J0;
+  const bool full = (i0t + WT) * TS <= gm && (j0t + WT) * TS <= gn;
+
   // loads of k-tile t into buffer buf, each masked to what a product may read (L strictly below its
   // diagonal tiles, C and E on the band, U strictly above its diagonal tiles, nothing outside)
-  auto issue = [&](int64_t t, int buf) {
+  auto issue = [&](int t, int buf) {
     const int ts = (int)t, k0 = ts * TS;
     const __amdgpu_buffer_rsrc_t rb_src = rebased_rsrc(b_mat, (int64_t)k0 * gn + J0 * TS, b_elems);
+    // an interior k-tile, where no lane of the workgroup is masked (every row and column inside the matrix and
+    // every A row / B column tile inside its band or triangle -- all k-tiles of a product but its first and
+    // last few): the loads take their loop-invariant lane offsets with the k-tile's offset added in the
+    // scalar field, no vector instruction.  Vector work between the MFMA bursts is what the k-step waits
+    // for (every vector instruction waits for an issue slot beside the other waves' MFMAs): the masked
+    // form's 20-odd per k-tile had cost more cycles than the 16 MFMAs.
+    if constexpr (VEC) {
+      const bool inner = PHASE == 0 ? ts < i0t && ts + j0t >= s0 && ts + j0t + WT - 1 < s1
+                                    : ts < j0t && ts + i0t >= s0 && ts + i0t + WT - 1 < s1;
+      if (full && inner && k0 + TS <= kmax) {
+#pragma unroll
+        for (int x = 0; x < NI; ++x) {
+          const int f0 = (wave + 4 * x) * PER;
+          dma_load_so<W>(ra_src, &sm.a[buf][f0], pre[x].a_off, k0 * 4);
+          dma_load<W>(rb_src, &sm.b[buf][f0 + f0 / 256 * L::BPAD], pre[x].b_off);
+        }
+        return;
+      }
+    }
 #pragma unroll
     for (int x = 0; x < NI; ++x) {
       const Geo o = VEC ? pre[x] : geo(x);
@@ -282,20 +310,20 @@ __device__ __forceinline__ void flush_phase(floatx16 (&acc)[WT / 2][WT / 2], Flu
   const int sw = quad_swizzle(li);
   const int b_base = 16 * hh * ROWS + wj * TS + li + 16 * hh * ROWS / 256 * L::BPAD;
 
-  auto step = [&](int64_t t, auto cur_c) {
+  auto step = [&](int t, auto cur_c) {
     constexpr int cur = decltype(cur_c)::value;
     __syncthreads();  // buffer cur is complete; buffer 1 - cur is no longer read
     if (t + 1 < t_hi) issue(t + 1, 1 - cur);
     // a wave skips a k-tile on which none of its tiles is active; otherwise it runs the full MFMA
     // block -- the staging masks have zeroed the operands of any tile outside its own range, so
     // the inactive tiles of a partial step accumulate exact zeros
-    const int ts = (int)t;
-    bool any = false;
+    const int ts = t;
+    int any = 0;  // wave-uniform; an int so that it stays in scalar registers
 #pragma unroll
     for (int a = 0; a < H; ++a)
 #pragma unroll
-      for (int d = 0; d < H; ++d) any |= ts >= tlo[a][d] && ts < thi[a][d];
-    if (__builtin_amdgcn_readfirstlane((int)any)) {
+      for (int d = 0; d < H; ++d) any |= ts >= tlo[a][d] && ts < thi[a][d] ? 1 : 0;
+    if (any) {
       const float* as = &sm.a[cur][a_base];
       const float* bs = &sm.b[cur][b_base];
       float4 fa[2][H];
@@ -333,7 +361,7 @@ __device__ __forceinline__ void flush_phase(floatx16 (&acc)[WT / 2][WT / 2], Flu
   __syncthreads();  // the previous phase's last reads of both buffers are done
   issue(t_lo, 0);
   wait_dma();
-  for (int64_t t = t_lo; t < t_hi; t += 2) {
+  for (int t = t_lo; t < t_hi; t += 2) {
     step(t, std::integral_constant<int, 0>{});
     if (t + 1 < t_hi) step(t + 1, std::integral_constant<int, 1>{});
   }

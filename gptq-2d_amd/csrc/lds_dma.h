@@ -52,6 +52,28 @@ __device__ __forceinline__ void dma_load(__amdgpu_buffer_rsrc_t r, float* dst, i
         : "v"(off), "s"(r), "s"(lds)
         : "memory");
 }
+// dma_load with a wave-uniform byte offset `soff` added in the instruction's scalar offset field, so that
+// a loop can step through a matrix with a loop-invariant per-lane offset and no vector instruction.  Only
+// for loads whose every lane is in range (the scalar offset is not part of the buffer's range check).
+template <int W>
+__device__ __forceinline__ void dma_load_so(__amdgpu_buffer_rsrc_t r, float* dst, int off, int soff) {
+  const unsigned lds = __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)(lds_float*)dst);
+  unsigned saved;
+  if constexpr (W == 4)
+    asm volatile(
+        "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %4 offen lds\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "v"(off), "s"(r), "s"(lds), "s"(soff)
+        : "memory");
+  else
+    asm volatile(
+        "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\tbuffer_load_dword %1, %2, %4 offen lds\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "v"(off), "s"(r), "s"(lds), "s"(soff)
+        : "memory");
+}
 // All of this wave's LDS-direct loads have landed.
 __device__ __forceinline__ void wait_dma() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
