@@ -734,7 +734,19 @@ __device__ __forceinline__ void syrk_wide_block(WideLds& sm, float* __restrict__
     aoff[x] = ia < R ? (ia * ild + 4 * kq) * 4 : OOB;
     boff[x] = ib < CR ? (ib * ild + 4 * kq) * 4 : OOB;
   }
+  // a block whose rows and columns all lie inside the update takes the k offset in the loads' scalar field:
+  // no vector instruction beside the MFMA bursts
+  const bool full = I0 + WB <= R && J0 + WB <= CR;
   auto issue = [&](int t, int buf) {
+    if (full) {
+#pragma unroll
+      for (int x = 0; x < 4; ++x) {
+        const int f0 = (wave + 4 * x) * 256;
+        dma_load_so<4>(rp, &sm.a[buf][f0], aoff[x], t * WK * 4);
+        dma_load_so<4>(rp, &sm.b[buf][f0], boff[x], t * WK * 4);
+      }
+      return;
+    }
 #pragma unroll
     for (int x = 0; x < 4; ++x) {
       const int f0 = (wave + 4 * x) * 256;

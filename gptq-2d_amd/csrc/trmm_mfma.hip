@@ -82,8 +82,20 @@ __global__ __launch_bounds__(256, 2) void tri_gemm_kernel(TriGemm g, int64_t nbn
     const int col = J0 + (f & (TB - 1));
     boff[x] = col < N ? (bk[x] * ldb + col) * 4 : OOB;
   }
+  // a block whose rows and columns all lie inside D takes its interior k-tiles (every lane in range) with
+  // the k offset in the loads' scalar field: no vector instruction beside the MFMA bursts
+  const bool full = I0 + TB <= M && J0 + TB <= N;
   auto issue = [&](int t, int buf) {
     const int k0 = t * KT;
+    if (full && k0 + KT <= K) {
+#pragma unroll
+      for (int x = 0; x < 4; ++x) {
+        const int f0 = (wave + 4 * x) * 256;
+        dma_load_so<4>(ra, &sm.a[buf][f0], aoff[x], k0 * 4);
+        dma_load_so<4>(rb, &sm.b[buf][f0 + f0 / 256 * BPAD], boff[x], k0 * ldb * 4);
+      }
+      return;
+    }
 #pragma unroll
     for (int x = 0; x < 4; ++x) {
       const int f0 = (wave + 4 * x) * 256;
