@@ -57,6 +57,20 @@ static inline int64_t batch_count(int32_t nd, const int64_t* shape) {
 
 __host__ __device__ static inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// Compute units of the current device (queried once per device and host thread).
+static inline int device_cus() {
+  thread_local int cached_dev = -1, cached_cus = 256;
+  int dev = 0;
+  if (hipGetDevice(&dev) == hipSuccess && dev != cached_dev) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && cus > 0) {
+      cached_cus = cus;
+      cached_dev = dev;
+    }
+  }
+  return cached_cus;
+}
+
 // Launch grid helper: (x, y, batch) as a 3-D grid while y and batch fit the
 // 65535 limit of those axes, else every block linearised on axis x.  Kernels
 // decode with GridIds.

@@ -485,19 +485,6 @@ __global__ __launch_bounds__(256, 2) void flush_tiles_mfma_kernel(float* __restr
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
-// Compute units of the current device (queried once per device and host thread).
-int device_cus() {
-  thread_local int cached_dev = -1, cached_cus = 256;
-  int dev = 0;
-  if (hipGetDevice(&dev) == hipSuccess && dev != cached_dev) {
-    int cus = 0;
-    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && cus > 0) {
-      cached_cus = cus;
-      cached_dev = dev;
-    }
-  }
-  return cached_cus;
-}
 
 bool strides_mult4(const BatchMap& bm) {
   for (int d = 0; d < bm.nd; ++d)

@@ -383,10 +383,12 @@ int viterbi(const T* x, const T* table, T* hist, const T* scale, T* out, int64_t
   if (rows == 0) return 0;
   if (rows > 0x7fffffff || steps > 0x7fffffff) return GPTQ2D_EUNSUPPORTED;
   const int64_t G = (int64_t)1 << (L - KV);
-  // two sequences per workgroup (each table load serves both) when their minima fit in LDS and
-  // there are enough rows to fill the chip, else one
+  // two sequences per workgroup (each table load serves both) when their minima fit in LDS and one per
+  // workgroup would put more workgroups than compute units on the chip: a CU then runs two of them at half
+  // speed each (C4's calls of 257 to 511 sequences: 2.8-2.9 ms with one sequence per workgroup, 1.8-1.9 ms
+  // with two), else one
   const size_t lds1 = 2 * G * sizeof(T), lds2 = 2 * lds1;
-  const bool two = lds2 <= 96 * 1024 && rows >= 512;
+  const bool two = lds2 <= 96 * 1024 && rows > device_cus();
   const size_t lds = two ? lds2 : lds1;
   const bool in_lds = lds <= 96 * 1024;
   if (two) {

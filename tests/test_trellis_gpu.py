@@ -76,15 +76,16 @@ def test_against_torch_and_oracle(dtype):
     assert st.cpu().equal(OT.trellis_quantize(x, table, 2, True)[1])
 
 
+@pytest.mark.parametrize("rows", [257, 301, 517])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
-def test_many_rows(dtype):
-    """Calls with 512 rows or more search two sequences per workgroup (one table load per state for both):
-    517 rows (the last workgroup holds one), L = 12, V = 1 and 2, with and without tail-biting -- equal to
-    the PyTorch formulation, values and states."""
+def test_many_rows(dtype, rows):
+    """Calls with more rows than the device has compute units search two sequences per workgroup (one table
+    load per state for both): 257, 301 and 517 rows (the last workgroup of the odd counts holds one), L = 12,
+    V = 1 and 2, with and without tail-biting -- equal to the PyTorch formulation, values and states."""
     g = torch.Generator().manual_seed(13)
     for (L, K, V, T), tb in itertools.product(((12, 2, 2, 32), (12, 3, 1, 24)), (False, True)):
         table = torch.randn(1 << L, V, generator=g, dtype=dtype).to(DEV)
-        x = torch.randn(517, T, generator=g, dtype=dtype).to(DEV)
+        x = torch.randn(rows, T, generator=g, dtype=dtype).to(DEV)
         vals, st = QT.trellis_quantize_hip(x, table, K, tb)
         tv, ts = QT.trellis_quantize_torch(x, table, K, tb)
         assert st.equal(ts) and vals.equal(tv), (L, K, V, T, tb)
