@@ -136,30 +136,57 @@ __device__ void forward_pass(const Sequence<T, V> (&seq)[NS], const bool (&live)
         // KV >= 2 they share the predecessor group s >> KV, whose minimum is read once per sequence;
         // the operations of each state evaluation are those of the loop below
         // the first step and the others as separate loops (no per-evaluation select on t == 0)
-        auto groups = [&](auto first_c) {
-        constexpr bool first = decltype(first_c)::value;
+        // PL: the previous minima are in LDS (prev_lds), read and written through LDS-typed pointers --
+        // through the generic ones the compiler emits flat accesses, whose waits also wait for the table's
+        // loads in flight
+        auto groups = [&](auto first_c, auto pl_c) {
+        constexpr bool first = decltype(first_c)::value, PL = decltype(pl_c)::value;
+        using lds_ct = const __attribute__((address_space(3))) T*;
+        typedef float f4v __attribute__((ext_vector_type(4)));
+        using lds_t4 = __attribute__((address_space(3))) f4v*;
+        const T* prev_g[NS];
+        lds_ct prev_l[NS];
+#pragma unroll
+        for (int k = 0; k < NS; ++k) {
+          prev_g[k] = prev[k];
+          prev_l[k] = PL ? (lds_ct)prev[k] : nullptr;
+        }
         for (int j = 4 * tid; j < G32; j += 4 * VT_THREADS) {
           T best[NS][4];
 #pragma unroll
           for (int k = 0; k < NS; ++k)
 #pragma unroll
             for (int e = 0; e < 4; ++e) best[k][e] = inf;
+          // the next h's table entries are loaded before this h's states are evaluated, so that each
+          // load has a whole iteration to arrive (loaded and used in one iteration, every iteration
+          // waited out the L2 latency)
+          const float4* tq = reinterpret_cast<const float4*>(table) + (int64_t)j * V / 4;
+          const int64_t tstep = (int64_t)G32 * V / 4;  // float4s per h
+          float4 nxt[V];
+#pragma unroll
+          for (int q = 0; q < V; ++q) nxt[q] = tq[q];
 #pragma unroll 4
           for (int h = 0; h < H32; ++h) {
             const int s = h * G32 + j;
             T tv[4 * V];
 #pragma unroll
             for (int q = 0; q < V; ++q) {
-              const float4 f = *reinterpret_cast<const float4*>(table + (int64_t)s * V + 4 * q);
+              const float4 f = nxt[q];
               tv[4 * q] = f.x;
               tv[4 * q + 1] = f.y;
               tv[4 * q + 2] = f.z;
               tv[4 * q + 3] = f.w;
             }
+            const int hn = h + 1 < H32 ? h + 1 : h;  // no branch: the last iteration reloads its own
+#pragma unroll
+            for (int q = 0; q < V; ++q) nxt[q] = tq[(int64_t)hn * tstep + q];
+            // issued here, not sunk to their use by the scheduler: one sequence per workgroup only (with two,
+            // each h has twice the evaluations to cover the latency, and pinning the loads slowed it down)
+            if constexpr (NS == 1) __builtin_amdgcn_sched_barrier(0);
             const int ps = s >> kv;
 #pragma unroll
             for (int k = 0; k < NS; ++k) {
-              const T pv = first ? T(0) : prev[k][ps];
+              const T pv = first ? T(0) : (PL ? prev_l[k][ps] : prev_g[k][ps]);
               const bool masked_out = first && masked && ps != overlap[k];
 #pragma unroll
               for (int e = 0; e < 4; ++e) {
@@ -181,14 +208,22 @@ __device__ void forward_pass(const Sequence<T, V> (&seq)[NS], const bool (&live)
           for (int k = 0; k < NS; ++k) {
             const float4 b4 = make_float4(best[k][0], best[k][1], best[k][2], best[k][3]);
             if (live[k]) *reinterpret_cast<float4*>(hist[k] + (int64_t)t * G + j) = b4;
-            if (cur_lds[k]) *reinterpret_cast<float4*>(cur_lds[k] + j) = b4;
+            if constexpr (PL)
+              *(lds_t4)(cur_lds[k] + j) = f4v{b4.x, b4.y, b4.z, b4.w};
           }
         }
         };
-        if (t == 0)
-          groups(std::true_type{});
-        else
-          groups(std::false_type{});
+        if (prev_lds) {
+          if (t == 0)
+            groups(std::true_type{}, std::true_type{});
+          else
+            groups(std::false_type{}, std::true_type{});
+        } else {
+          if (t == 0)
+            groups(std::true_type{}, std::false_type{});
+          else
+            groups(std::false_type{}, std::false_type{});
+        }
         __syncthreads();
         continue;
       }
