@@ -41,20 +41,21 @@ HBM_PEAK_GBS = 8000.0
 # fp32 VALU without packed instructions (which this build does not use): half the published 157.3
 # TFLOP/s vector figure, i.e. 78.6 TFLOP/s of FMA = 39.3e12 single fp32 operations per second.
 VALU_FP32_OPS_PEAK = 39.3e12
-# Outer block of the fused sweep, in antidiagonals (32 tile stages).  A longer outer block moves
+# Outer block of the fused sweep, in antidiagonals (24 tile stages).  A longer outer block moves
 # more of the cross-tile feedback into the few large outer flushes, which run closest to the MFMA
-# peak, at the price of more in-block prep work per tile stage; at 8192^2 on one MI355X: 512 ->
-# sweep 27.7 ms (flush 72.9 TFLOP/s), 1024 -> 26.1 ms (81.0), 2048 -> 28.0 ms (83.1).  It changes
-# the order of the fp32 additions only, not the algorithm.
-OUTER_BLOCK = 1024
-# HBM bytes per outer-flush launch at OUTER_BLOCK on the headline layer, mean over a step's 15
+# peak, at the price of more in-block prep work per tile stage (whose MFMA pulls slow the in-tile
+# sweeps beside them); sweep of the 8192^2 layer on one MI355X, best of four: 512 -> 19.7 ms,
+# 640 -> 19.1, 704 -> 19.0, 768 -> 19.1, 832 -> 19.1, 1024 -> 19.6, 1536 -> 21.4, 2048 -> 23.9 ms.
+# It changes the order of the fp32 additions only, not the algorithm.
+OUTER_BLOCK = 768
+# HBM bytes per outer-flush launch at OUTER_BLOCK on the headline layer, mean over a step's 21
 # launches: rocprofv3 FETCH_SIZE and WRITE_SIZE passes (one counter per run) over this benchmark,
 # each scaled by what the same counter reads for a plain 256 MiB copy kernel in the same run
 # (x1.9997 and x1.0000).  Counters cannot be read inside the timed run, so the figure is the
 # measured one, with the command and per-kernel values in profiles/flush_traffic_H_int4.md; the
 # algorithmic minimum (every operand once) is FLUSH_ALGORITHMIC_BYTES.
-FLUSH_TRAFFIC_BYTES = 2.045e9
-FLUSH_ALGORITHMIC_BYTES = 0.525e9
+FLUSH_TRAFFIC_BYTES = 1.718e9
+FLUSH_ALGORITHMIC_BYTES = 0.489e9
 # fp32 VALU operations per trellis state evaluation: 2 sub, 2 mul, 1 add (the squared distance),
 # 1 add (the predecessor group's minimum), 1 min.
 OPS_PER_STATE_EVAL = 7
@@ -443,9 +444,9 @@ def main() -> int:
         "peak": FP32_MFMA_PEAK_TFLOPS,
         "unit": "TFLOP/s",
         "frac": achieved / FP32_MFMA_PEAK_TFLOPS if achieved else None,
-        "traffic": FLUSH_TRAFFIC_BYTES if (m, n) == (8192, 8192) and OUTER_BLOCK == 1024 else None,
+        "traffic": FLUSH_TRAFFIC_BYTES if (m, n) == (8192, 8192) and OUTER_BLOCK == 768 else None,
         "traffic_unit": "B per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-calibrated)",
-        "traffic_algorithmic": FLUSH_ALGORITHMIC_BYTES if (m, n) == (8192, 8192) and OUTER_BLOCK == 1024 else None,
+        "traffic_algorithmic": FLUSH_ALGORITHMIC_BYTES if (m, n) == (8192, 8192) and OUTER_BLOCK == 768 else None,
         "kernel": "cross-tile feedback panels (flush), fp32",
         "launches": flush_n // max(1, args.steps),
         "avg_launch_us": avg_us,
