@@ -56,6 +56,13 @@ OUTER_BLOCK = 768
 # algorithmic minimum (every operand once) is FLUSH_ALGORITHMIC_BYTES.
 FLUSH_TRAFFIC_BYTES = 1.718e9
 FLUSH_ALGORITHMIC_BYTES = 0.489e9
+# The same two counter passes give the other kernels' HBM bytes, from which the line reports their achieved
+# HBM rates against the live timings: a tile-stage launch at OUTER_BLOCK on the headline layer (FETCH_SIZE
+# 13703.9 KiB x 1.9997 + WRITE_SIZE 2479.6 KiB, mean over a step's 511 launches) and one Viterbi call of the
+# benchmark's search (FETCH_SIZE 103382.2 KiB x 2.0 + WRITE_SIZE 2081280.0 KiB: its step-minimum history);
+# profiles/flush_traffic_H_int4.md and profiles/counters_H_int4.md.
+TILE_STAGE_TRAFFIC_BYTES = 30.60e6
+VITERBI_TRAFFIC_BYTES = 2.343e9
 # fp32 VALU operations per trellis state evaluation: 2 sub, 2 mul, 1 add (the squared distance),
 # 1 add (the predecessor group's minimum), 1 min.
 OPS_PER_STATE_EVAL = 7
@@ -175,6 +182,8 @@ def _viterbi_bench(torch, dev, steps_timed=3):
     torch.cuda.synchronize()
     sec = e0.elapsed_time(e1) / steps_timed / 1e3
     evals = rows * 2 * (T // V) * (1 << L)  # two passes, every state at every step
+    hbm = {"traffic": VITERBI_TRAFFIC_BYTES, "traffic_unit": "B per call (rocprofv3, copy-calibrated)",
+           "achieved_gbs": VITERBI_TRAFFIC_BYTES / sec / 1e9, "peak_gbs": HBM_PEAK_GBS}
     ops = evals * OPS_PER_STATE_EVAL
     return {
         "workload": "C4 longest antidiagonal: 512 sequences of 256 (16x16 super-entries), HYB L=16 K=2 V=2, "
@@ -183,6 +192,22 @@ def _viterbi_bench(torch, dev, steps_timed=3):
         "ms_per_call": sec * 1e3,
         "roofline": {"bound": "valu", "achieved": ops / sec / 1e12, "peak": VALU_FP32_OPS_PEAK / 1e12,
                      "unit": "Tops/s (fp32, 7 per state evaluation)", "frac": ops / sec / VALU_FP32_OPS_PEAK},
+        "hbm": hbm,
+    }
+
+
+def _tile_stage_line(sweep_ms, flush_ms, m, n):
+    launches = (m + 31) // 32 + (n + 31) // 32 - 1
+    us = 1e3 * (sweep_ms - flush_ms) / launches
+    known = (m, n) == (8192, 8192) and OUTER_BLOCK == 768
+    return {
+        "launches": launches,
+        "us_per_launch": round(us, 2),
+        "traffic": TILE_STAGE_TRAFFIC_BYTES if known else None,
+        "traffic_unit": "B per launch (rocprofv3, copy-calibrated)",
+        "achieved_gbs": round(TILE_STAGE_TRAFFIC_BYTES / (us * 1e-6) / 1e9, 1) if known else None,
+        "peak_gbs": HBM_PEAK_GBS,
+        "bound": "latency (63 dependent in-tile steps per launch, one barrier each)",
     }
 
 
@@ -478,6 +503,9 @@ def main() -> int:
             "flush_ms_per_step": round(flush_ms / args.steps, 3),
             "objective_vs_rtn": round(obj_ratio, 5),
         },
+        # the tile stages: the sweep less its outer flushes, per launch (launch gaps included), and the HBM
+        # rate of their measured bytes per launch
+        "tile_stage": _tile_stage_line(parts["sweep_ms"], flush_ms / args.steps, m, n),
         "roofline": roofline,
         "viterbi_weights_per_s": None,
         "viterbi": None,
