@@ -48,6 +48,10 @@ VALU_FP32_OPS_PEAK = 39.3e12
 # 640 -> 19.1, 704 -> 19.0, 768 -> 19.1, 832 -> 19.1, 1024 -> 19.6, 1536 -> 21.4, 2048 -> 23.9 ms.
 # It changes the order of the fp32 additions only, not the algorithm.
 OUTER_BLOCK = 768
+# The 8192 x 28672 layers of C5a (1 x 32 super-entry rows, and the three-sided D-sided form) sweep fastest with
+# longer blocks: C5a 768 -> 101.1 ms, 1024 -> 99.0, 1280 -> 97.6, 1536 -> 98.8; C5a three-sided 768 -> 109.7,
+# 1024 -> 107.7, 1280 -> 106.9 ms.
+OUTER_BLOCK_WIDE = 1280
 # HBM bytes per outer-flush launch at OUTER_BLOCK on the headline layer, mean over a step's 21
 # launches: rocprofv3 FETCH_SIZE and WRITE_SIZE passes (one counter per run) over this benchmark,
 # each scaled by what the same counter reads for a plain 256 MiB copy kernel in the same run
@@ -334,7 +338,7 @@ def _c5a_line(torch, dev, a, m, steps, lines, line):
     lo, up = factors5()
     t_ldl = _timed(torch, factors5, steps)
     t_sw = _timed(torch, lambda: G.gptq_2d_super_entry(w, lo, up, super_entry_shape=(1, cfg.group), quantizer=q,
-                                                       outer_block_size=OUTER_BLOCK), steps)
+                                                       outer_block_size=OUTER_BLOCK_WIDE), steps)
     lines["C5a"] = line(f"{cfg.m}x{n} = {cfg.m}x({cfg.n1}x{cfg.n2}), A (x) B1 (x) B2, INT4 abs-max per 1x{cfg.group} "
                         "super-entry (bf16 scales), fused sweep; U = U_B1 (x) U_B2", t_ldl, t_sw)
 
@@ -359,7 +363,7 @@ def _c5a3_line(torch, dev, steps, lines, line):
     ls = factors()
     t_ldl = _timed(torch, factors, steps)
     t_sw = _timed(torch, lambda: DS.gptq_d_sided(x, ls, quantizer=q, quantizer_inputs=(scale, zero),
-                                                 outer_block_size=OUTER_BLOCK), steps)
+                                                 outer_block_size=OUTER_BLOCK_WIDE), steps)
     lines["C5a3"] = line(f"{cfg.m}x{cfg.n1}x{cfg.n2} three-sided (D-sided sweep on the two-sided engine, U = "
                          f"(L_B2 (x) L_B1)^T formed per call), static INT4 abs-max scale per {cfg.group} b2 (bf16)",
                          t_ldl, t_sw)
