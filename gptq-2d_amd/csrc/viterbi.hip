@@ -165,7 +165,7 @@ __device__ void forward_pass(const Sequence<T, V> (&seq)[NS], const bool (&live)
           float4 nxt[V];
 #pragma unroll
           for (int q = 0; q < V; ++q) nxt[q] = tq[q];
-#pragma unroll 4
+#pragma unroll 2  // 4 or 8: 1.98-2.00 ms for a 512-sequence call, 2: 1.92 ms
           for (int h = 0; h < H32; ++h) {
             const int s = h * G32 + j;
             T tv[4 * V];
