@@ -216,6 +216,28 @@ def test_headline_size_fp32():
     assert err < 1e-3
 
 
+@pytest.mark.parametrize("k", [3584, 7168])
+def test_split_inverse_fp32(k):
+    """fp32 factors whose triangular inverse splits at 2048 / 4096 with a trailing block that is not a power of
+    two (1536, 3072: short pairs at the top of its recursive doubling): against the fp64 path (not split), and
+    the factor pair (part 1 of each inverse on a side stream beside the shared Cholesky chain) against single
+    calls bitwise."""
+    print(f"split inverse k={k}", flush=True)
+    m64 = instances.wishart_factor(k, .5, 70 + k, device=DEV)
+    m = m64.float()
+    got = LDL.ldl_of_inverse(m)
+    torch.cuda.synchronize()
+    assert torch.isfinite(got).all()
+    assert (got.diagonal() == 1).all() and (got.triu(1) == 0).all()
+    ref = LDL.ldl_of_inverse(m64)
+    err = ((got.double() - ref).abs().max() / ref.abs().max()).item()
+    print(f"  fp32 vs fp64: max rel err {err:.2e}", flush=True)
+    assert err < 1e-3
+    b = instances.wishart_factor(k, .5, 80 + k, device=DEV).float()
+    lo, up = LDL.feedback_factors_of_grams(m, b, check=False)
+    assert lo.equal(got) and up.equal(LDL.ldl_of_inverse(b, check=False).t())
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
 @pytest.mark.parametrize("k", [0, 96, 640])
 def test_info_zeroed_by_library(dtype, k):
