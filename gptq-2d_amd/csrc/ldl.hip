@@ -855,7 +855,7 @@ __host__ __device__ inline int64_t trapezoid_blocks(int64_t R, int64_t C) {
 
 // A panel's update of the next panel's columns (D's first PB columns, every row: blocks (x, 0));
 // the last workgroup copies the staged diagonal block of panel `sc` (PB rows) into W.
-// The matrix of a launch of the fp32 Cholesky (blockIdx.y selects one of two, see CholeskyRun):
+// The matrix of a launch of the fp32 Cholesky (blockIdx.y selects one of a group, see CholeskyRun):
 // W, its info word, the staging block of the launch's panel and the staged block to copy into W
 // (nullptr: none).
 struct PanelPtrs {
@@ -865,11 +865,17 @@ struct PanelPtrs {
   const float* copy;
 };
 
+// Matrices of one size factored by the same launches (entries [0, gridDim.y) used), passed by value.
+constexpr int GROUP_MAX = 16;
+struct PanelGroup {
+  PanelPtrs p[GROUP_MAX];
+};
+
 template <int PB>
-__global__ __launch_bounds__(256, 2) void syrk_strip_kernel(PanelPtrs p0, PanelPtrs p1, int64_t ld, int64_t r0,
-                                                            int R, int64_t pc, int K, int64_t sc) {
+__global__ __launch_bounds__(256, 2) void syrk_strip_kernel(PanelGroup grp, int64_t ld, int64_t r0, int R,
+                                                            int64_t pc, int K, int64_t sc) {
   __shared__ __align__(16) WideLds sm;
-  const PanelPtrs& p = blockIdx.y ? p1 : p0;
+  const PanelPtrs& p = grp.p[blockIdx.y];
   if (blockIdx.x == gridDim.x - 1) {
     stage_to_w<float, PB>(p.w, ld, sc, PB, p.stage);
     return;
@@ -883,16 +889,16 @@ __global__ __launch_bounds__(256, 2) void syrk_strip_kernel(PanelPtrs p0, PanelP
 // factorisation runs beside the throughput-bound update.
 // upc >= 0: the panel first takes the rank-PB update of the panel at columns [upc, upc + PB) itself.
 // copy != nullptr: the last workgroup moves that earlier panel's staged diagonal block (at column
-// copy_j0, PB rows) into W.  The matrix: p0 or p1 by blockIdx.y (the copy set in both or neither).
+// copy_j0, PB rows) into W.  The matrix: entry blockIdx.y of the group (the copy set in all or none).
 template <int PB>
-__global__ __launch_bounds__(256, 2) void panel_step_kernel(PanelPtrs p0, PanelPtrs p1, int64_t ld, int64_t j0,
-                                                            int n, int64_t k, int64_t n_potrf, int64_t r0, int R,
-                                                            int C, int64_t pc, int K, int64_t upc, int64_t copy_j0) {
+__global__ __launch_bounds__(256, 2) void panel_step_kernel(PanelGroup grp, int64_t ld, int64_t j0, int n, int64_t k,
+                                                            int64_t n_potrf, int64_t r0, int R, int C, int64_t pc,
+                                                            int K, int64_t upc, int64_t copy_j0) {
   __shared__ __align__(16) union {
     PotrfLds<float, PB> p;
     WideLds s;
   } sm;
-  const PanelPtrs& p = blockIdx.y ? p1 : p0;
+  const PanelPtrs& p = grp.p[blockIdx.y];
   const int64_t n_upd = gridDim.x - n_potrf - (p.copy ? 1 : 0);
   if (p.copy && (int64_t)blockIdx.x == gridDim.x - 1) {
     stage_to_w<float, PB>(p.w, ld, copy_j0, PB, p.copy);
@@ -912,9 +918,10 @@ __global__ __launch_bounds__(256, 2) void panel_step_kernel(PanelPtrs p0, PanelP
 // interleave two factorisations on two streams.  Between runs (and after finish()), every earlier
 // panel's update has been applied to the whole trailing matrix and every factored diagonal block
 // is in W.  stage: PB x PB elements of scratch (a panel's factored diagonal block between its
-// launch and the next).  twin() (two-level path only): a second k x k matrix factored by the same
-// launches, as blockIdx.y = 1 of each -- one chain of latency-bound panel launches for both, and
-// twice the work in each throughput-bound update; each matrix sees the launches it would see alone.
+// launch and the next).  twin() (two-level path only): up to GROUP_MAX - 1 more k x k matrices factored
+// by the same launches, as blockIdx.y = 1, 2, ... of each -- one chain of latency-bound panel launches for
+// all, and the work of all in each throughput-bound update; each matrix sees the launches it would see
+// alone.
 template <typename T>
 struct CholeskyRun {
   static constexpr int PB = LdlBlock<T>::PB;
@@ -928,9 +935,10 @@ struct CholeskyRun {
   bool two_level, fuse, done = false;
   int64_t pr0 = 0, pC = 0, ppc = 0;  // pending trapezoid update (columns < pC of W[pr0.., pr0..])
   int pK = 0;
-  T* w1 = nullptr;  // the twin, if any
-  int* info1 = nullptr;
-  T* stage1 = nullptr;
+  int ng = 1;  // matrices of the group; entry 0 is (w, info, stage)
+  T* wg[GROUP_MAX] = {};
+  int* infog[GROUP_MAX] = {};
+  T* stageg[GROUP_MAX] = {};
 
   CholeskyRun(T* w_, int64_t k_, int* info_, T* stage_, hipStream_t s, int64_t cb = 0, int64_t ce = -1)
       : w(w_), k(k_), info(info_), stage(stage_), stream(s), col_begin(cb), col_end(ce < 0 || ce > k_ ? k_ : ce),
@@ -938,22 +946,26 @@ struct CholeskyRun {
     two_level = sizeof(T) == 4 && k % 4 == 0 && k * k < (int64_t)1 << 29;
     fuse = two_level && k * k >= 2 * (int64_t)PB * PB;
     done = j0 >= col_end;
+    wg[0] = w_;
+    infog[0] = info_;
+    stageg[0] = stage_;
   }
 
-  // Factor a second matrix (same k, its own info word and staging blocks) in the same launches; false
-  // (nothing changed) off the two-level path or once a step was taken.
+  // Factor one more matrix (same k, its own info word and staging blocks) in the same launches; false
+  // (nothing changed) off the two-level path, with a full group or once a step was taken.
   bool twin(T* w_, int* info_, T* stage_) {
-    if (!two_level || j0 != col_begin || done) return false;
-    w1 = w_;
-    info1 = info_;
-    stage1 = stage_;
+    if (!two_level || j0 != col_begin || done || ng == GROUP_MAX) return false;
+    wg[ng] = w_;
+    infog[ng] = info_;
+    stageg[ng] = stage_;
+    ++ng;
     return true;
   }
 
   // Staging block of panel j of matrix f (two alternating ones when fused: a panel's launch copies
   // the previous panel's block into W while its own workgroups stage the new one).
   T* slot(int64_t j, int f = 0) const {
-    T* st = f ? stage1 : stage;
+    T* st = stageg[f];
     return fuse && ((j / PB) & 1) ? st + (int64_t)PB * PB : st;
   }
 
@@ -995,22 +1007,20 @@ struct CholeskyRun {
     // fused: a panel after the first of its strip takes the previous panel's rank-PB update itself
     // (no launch of its own for it), and its launch moves the previous panel's staged block into W
     const bool in_strip = fuse && j0 > s_lo;
-    const unsigned ny = w1 ? 2u : 1u;
-    PanelPtrs pp[2];
-    for (int f = 0; f < 2; ++f) {
-      const int g = f < (int)ny ? f : 0;
-      pp[f] = PanelPtrs{(float*)(g ? w1 : w), g ? info1 : info, (float*)slot(j0, g),
-                        in_strip ? (const float*)slot(j0 - PB, g) : nullptr};
-    }
+    const unsigned ny = (unsigned)ng;
+    PanelGroup pp{};
+    for (int f = 0; f < ng; ++f)
+      pp.p[f] = PanelPtrs{(float*)wg[f], infog[f], (float*)slot(j0, f),
+                          in_strip ? (const float*)slot(j0 - PB, f) : nullptr};
     hipLaunchKernelGGL((panel_step_kernel<PB>), dim3((unsigned)(blocks + upd + (in_strip ? 1 : 0)), ny), dim3(256), 0,
-                       stream, pp[0], pp[1], k, j0, n, k, blocks, pr0, (int)pR, (int)pC, ppc, pK,
+                       stream, pp, k, j0, n, k, blocks, pr0, (int)pR, (int)pC, ppc, pK,
                        in_strip ? j0 - PB : (int64_t)-1, j0 - PB);
     if ((rc = (int)hipGetLastError())) return rc;
     pC = 0;
     if (rest <= 0) {  // the last panel: its staged block into W on its own
       for (unsigned f = 0; f < ny; ++f) {
-        hipLaunchKernelGGL((stage_to_w_kernel<float, PB>), dim3(1), dim3(256), 0, stream, pp[f].w, k, j0, n,
-                           (const float*)pp[f].stage);
+        hipLaunchKernelGGL((stage_to_w_kernel<float, PB>), dim3(1), dim3(256), 0, stream, pp.p[f].w, k, j0, n,
+                           (const float*)pp.p[f].stage);
         if ((rc = (int)hipGetLastError())) return rc;
       }
       done = true;
@@ -1021,8 +1031,8 @@ struct CholeskyRun {
     const int64_t pc = strip_end ? s_lo : j0;
     const int K = (int)(j0 + PB - pc);
     if (strip_end || !fuse) {
-      hipLaunchKernelGGL((syrk_strip_kernel<PB>), dim3((unsigned)cdiv(rest, WB) + 1, ny), dim3(256), 0, stream, pp[0],
-                         pp[1], k, j0 + PB, (int)rest, pc, K, j0);
+      hipLaunchKernelGGL((syrk_strip_kernel<PB>), dim3((unsigned)cdiv(rest, WB) + 1, ny), dim3(256), 0, stream, pp, k,
+                         j0 + PB, (int)rest, pc, K, j0);
       if ((rc = (int)hipGetLastError())) return rc;
     }
     // the rest: the strip's later columns, or everything to the right at a strip's end
@@ -1107,11 +1117,11 @@ struct CholeskyRun {
     if constexpr (sizeof(T) == 4) {
       if (pC <= 0) return 0;
       const int64_t pR = k - pr0;
-      const PanelPtrs p0{(float*)w, info, (float*)stage, nullptr};
-      const PanelPtrs p1 = w1 ? PanelPtrs{(float*)w1, info1, (float*)stage1, nullptr} : p0;
-      hipLaunchKernelGGL((panel_step_kernel<PB>), dim3((unsigned)trapezoid_blocks(pR, pC), w1 ? 2u : 1u), dim3(256),
-                         0, stream, p0, p1, k, (int64_t)0, 0, k, (int64_t)0, pr0, (int)pR, (int)pC, ppc, pK,
-                         (int64_t)-1, (int64_t)0);
+      PanelGroup pp{};
+      for (int f = 0; f < ng; ++f) pp.p[f] = PanelPtrs{(float*)wg[f], infog[f], (float*)stageg[f], nullptr};
+      hipLaunchKernelGGL((panel_step_kernel<PB>), dim3((unsigned)trapezoid_blocks(pR, pC), (unsigned)ng), dim3(256),
+                         0, stream, pp, k, (int64_t)0, 0, k, (int64_t)0, pr0, (int)pR, (int)pC, ppc, pK, (int64_t)-1,
+                         (int64_t)0);
       pC = 0;
       return (int)hipGetLastError();
     }
@@ -1522,24 +1532,34 @@ int ldl_impl(bool inverse, const T* m, T* out, T* work, int* info, int64_t batch
   }
   int rc;
   const int64_t kk = k * k;
-  for (int64_t b = 0; b < batch; ++b) {
-    const T* mb = m + b * kk;
-    T* ob = out + b * kk;
-    T* wb = work + b * kk;
-    int* ib = info + b;
-    const int64_t blocks = cdiv(kk, 256) < 8192 ? cdiv(kk, 256) : 8192;
-    hipLaunchKernelGGL(copy_kernel<T>, dim3((unsigned)blocks), dim3(256), 0, stream, wb, mb, kk, inverse ? 1 : 0, ib,
-                       1);
-    if ((rc = (int)hipGetLastError())) return rc;
-    // ob is free until the inverse / normalisation: its last elements stage the factored diagonal
-    // blocks
-    if ((rc = cholesky_inplace<T>(wb, k, ib, ob + stage_offset<T>(k), stream))) return rc;
-    if (inverse) {
-      for (int phase = 1; phase <= 3; ++phase)
-        if ((rc = trtri_part<T>(ob, wb, k, size, phase, stream))) return rc;
-    } else {
-      if ((rc = normalize<T>(ob, wb, k, size, 0, k, 1, stream))) return rc;
+  const int64_t blocks = cdiv(kk, 256) < 8192 ? cdiv(kk, 256) : 8192;
+  // matrices taken in groups that share every Cholesky launch (CholeskyRun::twin; one at a time off the
+  // fp32 two-level path): one chain of latency-bound panel launches per group instead of per matrix.
+  // out[b] is free until the inverse / normalisation: its last elements stage the factored diagonal blocks.
+  for (int64_t b0 = 0; b0 < batch;) {
+    CholeskyRun<T> run(work + b0 * kk, k, info + b0, out + b0 * kk + stage_offset<T>(k), stream);
+    int64_t nb = 1;
+    while (b0 + nb < batch &&
+           run.twin(work + (b0 + nb) * kk, info + b0 + nb, out + (b0 + nb) * kk + stage_offset<T>(k)))
+      ++nb;
+    for (int64_t b = b0; b < b0 + nb; ++b) {
+      hipLaunchKernelGGL(copy_kernel<T>, dim3((unsigned)blocks), dim3(256), 0, stream, work + b * kk, m + b * kk, kk,
+                         inverse ? 1 : 0, info + b, 1);
+      if ((rc = (int)hipGetLastError())) return rc;
     }
+    while (!run.done)
+      if ((rc = run.step())) return rc;
+    for (int64_t b = b0; b < b0 + nb; ++b) {
+      T* ob = out + b * kk;
+      T* wb = work + b * kk;
+      if (inverse) {
+        for (int phase = 1; phase <= 3; ++phase)
+          if ((rc = trtri_part<T>(ob, wb, k, size, phase, stream))) return rc;
+      } else {
+        if ((rc = normalize<T>(ob, wb, k, size, 0, k, 1, stream))) return rc;
+      }
+    }
+    b0 += nb;
   }
   return 0;
 }

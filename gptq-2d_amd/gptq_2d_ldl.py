@@ -83,8 +83,9 @@ def feedback_factors_of_grams(G: torch.Tensor, H: torch.Tensor, super_entry_shap
     three side streams of the current device (gptq2d_ldl_of_inverse_pair): the two Cholesky
     factorisations -- chains of latency-bound panel launches -- share every launch when the factors are
     fp32 of one size (else they run together on two streams), and the first part of each triangular
-    inverse runs beside the rest of the factorisations.  Bitwise equal to the two
-    ldl_of_inverse calls.  No counterpart in the reference, whose callers compute the two factors one
+    inverse runs beside the rest of the factorisations.  Batched Grams: each factor's batch in one call on
+    its own stream, its matrices sharing the Cholesky launches in groups of up to 16.  Bitwise equal to the
+    two ldl_of_inverse calls.  No counterpart in the reference, whose callers compute the two factors one
     after the other (demo.ipynb cell 5)."""
     p, q = super_entry_shape
     main = torch.cuda.current_stream(G.device)
@@ -111,13 +112,20 @@ def feedback_factors_of_grams(G: torch.Tensor, H: torch.Tensor, super_entry_shap
                              torch.zeros(src.size(0), dtype=torch.int32, device=m.device)))
         (sa, oa, wa, ia), (sb, ob, wb, ib) = bufs
         (_, pa, ka), (_, pb, kb) = jobs
-        if sa.dtype == sb.dtype and sa.size(0) == sb.size(0):
+        if max(sa.size(0), sb.size(0)) > 1:
+            # batches: each factor's matrices in one batched call on its own stream, whose matrices of the
+            # fp32 two-level path share every Cholesky launch (up to 16 at a time)
+            for s, (m, size, k), (src, o, w, info) in zip(streams, jobs, bufs):
+                with torch.cuda.stream(s):
+                    _hip.call("ldl_of_inverse", src.dtype, _hip.ptr(src), _hip.ptr(o), _hip.ptr(w), _hip.ptr(info),
+                              src.size(0), k, size, _hip.stream(m.device))
+        elif sa.dtype == sb.dtype and sa.size(0) == sb.size(0):
             sp = [ctypes.c_void_p(s.cuda_stream) for s in streams]
             for b in range(sa.size(0)):
                 _hip.call("ldl_of_inverse_pair", sa.dtype, _hip.ptr(sa[b]), _hip.ptr(oa[b]), _hip.ptr(wa[b]),
                           _hip.ptr(ia[b:b + 1]), ka, pa, _hip.ptr(sb[b]), _hip.ptr(ob[b]), _hip.ptr(wb[b]),
                           _hip.ptr(ib[b:b + 1]), kb, pb, *sp)
-        else:  # different dtypes or batch counts: each factor on its own stream, in one sequence
+        else:  # one matrix each, of different dtypes: each factor on its own stream
             for s, (m, size, k), (src, o, w, info) in zip(streams, jobs, bufs):
                 with torch.cuda.stream(s):
                     for b in range(src.size(0)):

@@ -138,7 +138,9 @@ extern "C" {
                                                                                                                       \
   /* Unit lower (block) triangular L with M^{-1} = L Lambda L^T for `batch` contiguous k x k SPD      \
    * matrices m; work: [batch, k, k] scratch; info[batch]: first non-positive pivot (1-based) or 0     \
-   * (ldl_of_inverse, gptq_2d_reference.py:29-49).  size <= 128 (f32) or 64 (f64). */                 \
+   * (ldl_of_inverse, gptq_2d_reference.py:29-49).  size <= 128 (f32) or 64 (f64).  fp32 matrices with \
+   * k % 4 == 0 are factored in groups of up to 16 that share every Cholesky launch; results equal    \
+   * one call per matrix bit for bit. */                                                               \
   int gptq2d_ldl_of_inverse_##SUF(const T* m, T* out, T* work, int* info, int64_t batch, int64_t k, int64_t size,  \
                                   void* stream);                                                                    \
   /* ldl_of_inverse of one k x k matrix in parts, so that the Cholesky and the inverse of two          \

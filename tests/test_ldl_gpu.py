@@ -141,6 +141,28 @@ def test_batch_and_feedback_factors():
     assert (lo.cpu() - elo).abs().max() < 1e-9 and (up.cpu() - eup).abs().max() < 1e-9
 
 
+@pytest.mark.parametrize("k", [256, 2048])
+def test_grouped_batch_fp32(k):
+    """fp32 batches factored in groups that share every Cholesky launch (16 at a time, here 16 + 2 or 3 + 0):
+    each matrix equals its own call bitwise, for ldl_of_inverse and ldl, and so do batched factor pairs;
+    a matrix that is not positive definite inside a group is reported as that batch entry."""
+    nb = 18 if k == 256 else 3
+    print(f"grouped batch k={k} nb={nb}", flush=True)
+    ms = torch.stack([instances.wishart_factor(k, .5, 90 + s) for s in range(nb)]).float().to(DEV)
+    for fn in (LDL.ldl_of_inverse, LDL.ldl):
+        got = fn(ms)
+        for b in range(nb):
+            assert got[b].equal(fn(ms[b])), (fn.__name__, b)
+    hs = torch.stack([instances.wishart_factor(k // 2, .5, 120 + s) for s in range(nb)]).float().to(DEV)
+    lo, up = LDL.feedback_factors_of_grams(ms, hs, check=False)
+    for b in range(nb):
+        assert lo[b].equal(LDL.ldl_of_inverse(ms[b])) and up[b].equal(LDL.ldl_of_inverse(hs[b]).t()), b
+    bad = ms.clone()
+    bad[nb - 2, k // 2, k // 2] = -1.
+    with pytest.raises(torch.linalg.LinAlgError, match=f"batch {nb - 2}"):
+        LDL.ldl_of_inverse(bad)
+
+
 def test_not_positive_definite():
     m = instances.wishart_factor(80, .5, 1).to(DEV)
     m[70, 70] = -1.
