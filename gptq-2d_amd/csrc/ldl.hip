@@ -536,7 +536,8 @@ __global__ __launch_bounds__(256) void stage_to_w_kernel(T* __restrict__ w, int6
 
 // One wave per diagonal NB block of the lower triangular W: replace it by its inverse.
 template <typename T, int NB>
-__global__ __launch_bounds__(64) void trtri_leaf_kernel(T* __restrict__ w, int64_t ld, int64_t k) {
+__global__ __launch_bounds__(64) void trtri_leaf_kernel(T* __restrict__ w, int64_t ld, int64_t k, int64_t mstride) {
+  w += (int64_t)blockIdx.y * mstride;  // matrix blockIdx.y of a group
   const int lane = threadIdx.x;
   const int64_t b0 = (int64_t)blockIdx.x * NB;
   const int n = k - b0 < NB ? (int)(k - b0) : NB;
@@ -556,7 +557,9 @@ __global__ __launch_bounds__(64) void trtri_leaf_kernel(T* __restrict__ w, int64
 // 1 on it, 0 above.  32 x 32 tiles through LDS so that both the read and the write coalesce.
 template <typename T>
 __global__ __launch_bounds__(256) void normalize_unit_kernel(T* __restrict__ out, const T* __restrict__ w,
-                                                             int64_t k, int64_t base, int64_t rs, int64_t cs) {
+                                                             int64_t k, int64_t base, int64_t rs, int64_t cs, int64_t mstride) {
+  out += (int64_t)blockIdx.z * mstride;  // matrix blockIdx.z of a group
+  w += (int64_t)blockIdx.z * mstride;
   __shared__ T tile[32][33];
   __shared__ T diag[32];
   const int64_t i0 = (int64_t)blockIdx.y * 32, j0 = (int64_t)blockIdx.x * 32;
@@ -589,7 +592,9 @@ __global__ __launch_bounds__(256) void normalize_unit_kernel(T* __restrict__ out
 template <typename T, int NB>
 __global__ __launch_bounds__(256) void normalize_block_kernel(T* __restrict__ out, const T* __restrict__ w,
                                                               int64_t k, int p, int64_t base, int64_t rs,
-                                                              int64_t cs) {
+                                                              int64_t cs, int64_t mstride) {
+  out += (int64_t)blockIdx.z * mstride;  // matrix blockIdx.z of a group
+  w += (int64_t)blockIdx.z * mstride;
   __shared__ T dinv[NB][NB + 1];
   __shared__ T rows[64][NB + 1];
   const int64_t b = blockIdx.x, c0 = b * p;
@@ -641,7 +646,9 @@ __global__ __launch_bounds__(256) void normalize_block_kernel(T* __restrict__ ou
 template <typename T, int PM>
 __global__ __launch_bounds__(256) void normalize_block_solve_kernel(T* __restrict__ out, const T* __restrict__ w,
                                                                     int64_t k, int p, int64_t base, int64_t rs,
-                                                                    int64_t cs) {
+                                                                    int64_t cs, int64_t mstride) {
+  out += (int64_t)blockIdx.z * mstride;  // matrix blockIdx.z of a group
+  w += (int64_t)blockIdx.z * mstride;
   __shared__ T dblk[PM][PM + 1];
   __shared__ T rows[64][PM + 1];
   const int64_t b = blockIdx.x, c0 = b * p;
@@ -1152,7 +1159,8 @@ int64_t stage_offset(int64_t k) {
 // Zero the strict upper triangle of the n x n diagonal block at w (row stride ld), one row per
 // workgroup.
 template <typename T>
-__global__ __launch_bounds__(256) void zero_upper_kernel(T* __restrict__ w, int64_t ld, int64_t n) {
+__global__ __launch_bounds__(256) void zero_upper_kernel(T* __restrict__ w, int64_t ld, int64_t n, int64_t mstride) {
+  w += (int64_t)blockIdx.y * mstride;  // matrix blockIdx.y of a group
   for (int64_t i = blockIdx.x; i < n; i += gridDim.x)
     for (int64_t j = i + 1 + threadIdx.x; j < n; j += 256) w[i * ld + j] = T(0);
 }
@@ -1163,10 +1171,19 @@ __global__ __launch_bounds__(256) void zero_upper_kernel(T* __restrict__ w, int6
 // library's general strided GEMM with the same triangular structure.
 int level_gemm(int64_t M, int64_t N, int64_t K, int64_t batch, const float* A, int64_t lda, int64_t sa,
                const float* B, int64_t ldb, int64_t sb, float* D, int64_t ldd, int64_t sd, float alpha, int tri,
-               hipStream_t stream) {
-  TriGemm g{M, N, K, batch, A, lda, sa, B, ldb, sb, D, ldd, sd, alpha, tri};
+               hipStream_t stream, int64_t ng = 1, int64_t mst = 0) {
+  // ng problems of a group of matrices mst elements apart (A, B and D alike)
+  TriGemm g{M, N, K, batch, A, lda, sa, B, ldb, sb, D, ldd, sd, alpha, tri, ng, mst, mst, mst};
   const int rc = gptq2d_tri_gemm_f32(g, stream);
   if (rc != GPTQ2D_EUNSUPPORTED) return rc;
+  if (ng > 1) {
+    for (int64_t z = 0; z < ng; ++z) {
+      const int r = level_gemm(M, N, K, batch, A + z * mst, lda, sa, B + z * mst, ldb, sb, D + z * mst, ldd, sd, alpha,
+                               tri, stream);
+      if (r) return r;
+    }
+    return 0;
+  }
   GemmProblem<float> h{};
   h.M = M;
   h.N = N;
@@ -1196,13 +1213,22 @@ int level_gemm(int64_t M, int64_t N, int64_t K, int64_t batch, const float* A, i
 // level_gemm; the block's strict upper triangle is zeroed first (the MFMA kernel reads it as the
 // padding of the triangles' boundary k-tiles).
 template <typename T>
-int trtri_block(T* w, int64_t ld, int64_t n, T* tmp, bool tri, hipStream_t stream) {
+int trtri_block(T* w, int64_t ld, int64_t n, T* tmp, bool tri, hipStream_t stream, int64_t ng = 1, int64_t mst = 0) {
   constexpr int NB = LdlBlock<T>::NB;
   int rc;
-  hipLaunchKernelGGL((trtri_leaf_kernel<T, NB>), dim3((unsigned)cdiv(n, NB)), dim3(64), 0, stream, w, ld, n);
+  // a group of ng matrices mst elements apart (w and tmp alike): one launch per step on the fp32 MFMA
+  // levels, one matrix after the other on the general GEMM
+  if (ng > 1 && !(sizeof(T) == 4 && tri)) {
+    for (int64_t z = 0; z < ng; ++z)
+      if ((rc = trtri_block<T>(w + z * mst, ld, n, tmp + z * mst, tri, stream))) return rc;
+    return 0;
+  }
+  hipLaunchKernelGGL((trtri_leaf_kernel<T, NB>), dim3((unsigned)cdiv(n, NB), (unsigned)ng), dim3(64), 0, stream, w, ld,
+                     n, mst);
   if ((rc = (int)hipGetLastError())) return rc;
   if (tri) {
-    hipLaunchKernelGGL(zero_upper_kernel<T>, dim3((unsigned)(n < 8192 ? n : 8192)), dim3(256), 0, stream, w, ld, n);
+    hipLaunchKernelGGL(zero_upper_kernel<T>, dim3((unsigned)(n < 8192 ? n : 8192), (unsigned)ng), dim3(256), 0, stream,
+                       w, ld, n, mst);
     if ((rc = (int)hipGetLastError())) return rc;
   }
   for (int64_t s = NB; s < n; s *= 2) {
@@ -1219,10 +1245,10 @@ int trtri_block(T* w, int64_t ld, int64_t n, T* tmp, bool tri, hipStream_t strea
         if (tri) {
           // T = B A^{-1}, then B <- -D^{-1} T
           if ((rc = level_gemm(s2, s, s, pairs, w + (r0 + s) * ld + r0, ld, bs, w + r0 * ld + r0, ld, bs, tmp, s,
-                               s2 * s, 1.f, 1, stream)))
+                               s2 * s, 1.f, 1, stream, ng, mst)))
             return rc;
           if ((rc = level_gemm(s2, s, s2, pairs, w + (r0 + s) * ld + (r0 + s), ld, bs, tmp, s, s2 * s,
-                               w + (r0 + s) * ld + r0, ld, bs, -1.f, 2, stream)))
+                               w + (r0 + s) * ld + r0, ld, bs, -1.f, 2, stream, ng, mst)))
             return rc;
           continue;
         }
@@ -1319,60 +1345,64 @@ TrtriLayout trtri_layout(T* out, int64_t k, int64_t s) {
 // In-place inverse of the lower triangular W (k x k) in one sequence; tmp: a buffer of >= k*k/4 + k
 // elements for the levels' products.  fp32 from k = 512: the levels on level_gemm.
 template <typename T>
-int trtri_inplace(T* w, int64_t k, T* tmp, hipStream_t stream) {
-  return trtri_block<T>(w, k, k, tmp, sizeof(T) == 4 && k >= 512, stream);
+int trtri_inplace(T* w, int64_t k, T* tmp, hipStream_t stream, int64_t ng = 1, int64_t mst = 0) {
+  return trtri_block<T>(w, k, k, tmp, sizeof(T) == 4 && k >= 512, stream, ng, mst);
 }
 
 template <typename T>
-int normalize(T* out, const T* w, int64_t k, int64_t size, int64_t base, int64_t rs, int64_t cs, hipStream_t stream);
+int normalize(T* out, const T* w, int64_t k, int64_t size, int64_t base, int64_t rs, int64_t cs, hipStream_t stream,
+              int64_t ng = 1, int64_t mst = 0);
 
 // Part `phase` (1, 2, 3 as at trtri_split) of the inverse of the Cholesky factor in work and the
 // normalisation into out (L_raw(i, j) = C^{-1}(k-1-j, k-1-i) = work[(k-1-j) k + (k-1-i)]).  Without
-// a split, part 1 does nothing, part 2 is the whole inverse and part 3 the normalisation.
+// a split, part 1 does nothing, part 2 is the whole inverse and part 3 the normalisation.  ng > 1: the
+// same part of a group of ng matrices k^2 elements apart (out and w alike), in one launch per step.
 template <typename T>
-int trtri_part(T* out, T* w, int64_t k, int64_t size, int phase, hipStream_t stream) {
-  const int64_t s = trtri_split<T>(k);
+int trtri_part(T* out, T* w, int64_t k, int64_t size, int phase, hipStream_t stream, int64_t ng = 1) {
+  const int64_t s = trtri_split<T>(k), mst = k * k;
   int rc = 0;
   if (s == 0) {
-    if (phase == 2) return trtri_inplace<T>(w, k, out, stream);
-    if (phase == 3) return normalize<T>(out, w, k, size, (k - 1) * k + (k - 1), -1, -k, stream);
+    if (phase == 2) return trtri_inplace<T>(w, k, out, stream, ng, mst);
+    if (phase == 3) return normalize<T>(out, w, k, size, (k - 1) * k + (k - 1), -1, -k, stream, ng, mst);
     return 0;
   }
   if constexpr (sizeof(T) == 4) {
     const TrtriLayout L = trtri_layout<T>(out, k, s);
     if (phase == 1) {
-      if ((rc = trtri_block<T>(w, k, s, out + L.t_off, true, stream))) return rc;
+      if ((rc = trtri_block<T>(w, k, s, out + L.t_off, true, stream, ng, mst))) return rc;
       // T = B A^{-1}: (n2 x s) = (n2 x s) (s x s)
-      return level_gemm(L.n2, s, s, 1, w + s * k, k, 0, w, k, 0, out + L.t_off, s, 0, 1.f, 1, stream);
+      return level_gemm(L.n2, s, s, 1, w + s * k, k, 0, w, k, 0, out + L.t_off, s, 0, 1.f, 1, stream, ng, mst);
     }
-    if (phase == 2) return trtri_block<T>(w + s * k + s, k, L.n2, out + L.tmp2_off, true, stream);
+    if (phase == 2) return trtri_block<T>(w + s * k + s, k, L.n2, out + L.tmp2_off, true, stream, ng, mst);
     if (phase == 3) {
       // B <- -D^{-1} T: (n2 x s) = (n2 x n2) (n2 x s)
       if ((rc = level_gemm(L.n2, s, L.n2, 1, w + s * k + s, k, 0, out + L.t_off, s, 0, w + s * k, k, 0, -1.f, 2,
-                           stream)))
+                           stream, ng, mst)))
         return rc;
-      return normalize<T>(out, w, k, size, (k - 1) * k + (k - 1), -1, -k, stream);
+      return normalize<T>(out, w, k, size, (k - 1) * k + (k - 1), -1, -k, stream, ng, mst);
     }
   }
   return rc;
 }
 
 template <typename T>
-int normalize(T* out, const T* w, int64_t k, int64_t size, int64_t base, int64_t rs, int64_t cs, hipStream_t stream) {
+int normalize(T* out, const T* w, int64_t k, int64_t size, int64_t base, int64_t rs, int64_t cs, hipStream_t stream,
+              int64_t ng, int64_t mst) {
   constexpr int NB = LdlBlock<T>::NB;
+  // ng matrices mst elements apart (out and w alike) as blockIdx.z
   if (size == 1) {
-    const dim3 grid((unsigned)cdiv(k, 32), (unsigned)cdiv(k, 32));
-    hipLaunchKernelGGL(normalize_unit_kernel<T>, grid, dim3(256), 0, stream, out, w, k, base, rs, cs);
+    const dim3 grid((unsigned)cdiv(k, 32), (unsigned)cdiv(k, 32), (unsigned)ng);
+    hipLaunchKernelGGL(normalize_unit_kernel<T>, grid, dim3(256), 0, stream, out, w, k, base, rs, cs, mst);
   } else {
     constexpr int SB = LdlBlock<T>::SB;
     if (size > SB) return GPTQ2D_EUNSUPPORTED;
-    const dim3 grid((unsigned)(k / size), (unsigned)cdiv(k, 64));
+    const dim3 grid((unsigned)(k / size), (unsigned)cdiv(k, 64), (unsigned)ng);
     if (size <= NB)
       hipLaunchKernelGGL((normalize_block_kernel<T, NB>), grid, dim3(256), 0, stream, out, w, k, (int)size, base, rs,
-                         cs);
+                         cs, mst);
     else
       hipLaunchKernelGGL((normalize_block_solve_kernel<T, SB>), grid, dim3(256), 0, stream, out, w, k, (int)size,
-                         base, rs, cs);
+                         base, rs, cs, mst);
   }
   return (int)hipGetLastError();
 }
@@ -1549,15 +1579,12 @@ int ldl_impl(bool inverse, const T* m, T* out, T* work, int* info, int64_t batch
     }
     while (!run.done)
       if ((rc = run.step())) return rc;
-    for (int64_t b = b0; b < b0 + nb; ++b) {
-      T* ob = out + b * kk;
-      T* wb = work + b * kk;
-      if (inverse) {
-        for (int phase = 1; phase <= 3; ++phase)
-          if ((rc = trtri_part<T>(ob, wb, k, size, phase, stream))) return rc;
-      } else {
-        if ((rc = normalize<T>(ob, wb, k, size, 0, k, 1, stream))) return rc;
-      }
+    // the group's inverses and normalisations, each step one launch for the group
+    if (inverse) {
+      for (int phase = 1; phase <= 3; ++phase)
+        if ((rc = trtri_part<T>(out + b0 * kk, work + b0 * kk, k, size, phase, stream, nb))) return rc;
+    } else {
+      if ((rc = normalize<T>(out + b0 * kk, work + b0 * kk, k, size, 0, k, 1, stream, nb, kk))) return rc;
     }
     b0 += nb;
   }

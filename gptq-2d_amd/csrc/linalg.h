@@ -48,6 +48,8 @@ struct TriGemm {
   int64_t ldd, sd;
   float alpha;
   int32_t tri;
+  // a second batch dimension (0 or 1: none): problem (y, z) at A + y sa + z sa2, and so on
+  int64_t batch2, sa2, sb2, sd2;
 };
 
 int gptq2d_tri_gemm_f32(const TriGemm& g, hipStream_t stream);

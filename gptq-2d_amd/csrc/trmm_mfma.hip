@@ -55,9 +55,9 @@ __global__ __launch_bounds__(256, 2) void tri_gemm_kernel(TriGemm g, int64_t nbn
   const int I0 = bi * TB, J0 = bj * TB;
   const int M = (int)g.M, N = (int)g.N, K = (int)g.K;
   const int lda = (int)g.lda, ldb = (int)g.ldb, ldd = (int)g.ldd;
-  const float* A = g.A + (int64_t)blockIdx.y * g.sa;
-  const float* B = g.B + (int64_t)blockIdx.y * g.sb;
-  float* D = g.D + (int64_t)blockIdx.y * g.sd;
+  const float* A = g.A + (int64_t)blockIdx.y * g.sa + (int64_t)blockIdx.z * g.sa2;
+  const float* B = g.B + (int64_t)blockIdx.y * g.sb + (int64_t)blockIdx.z * g.sb2;
+  float* D = g.D + (int64_t)blockIdx.y * g.sd + (int64_t)blockIdx.z * g.sd2;
 
   const int nkt = (K + KT - 1) / KT;
   int t_lo = 0, t_hi = nkt;
@@ -182,8 +182,11 @@ bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 }  // namespace
 
 int gptq2d_tri_gemm_f32(const TriGemm& g, hipStream_t stream) {
-  if (g.M < 0 || g.N < 0 || g.K < 0 || g.batch < 0 || g.tri < 0 || g.tri > 2) return GPTQ2D_EINVAL;
+  if (g.M < 0 || g.N < 0 || g.K < 0 || g.batch < 0 || g.tri < 0 || g.tri > 2 || g.batch2 < 0 || g.batch2 > 65535)
+    return GPTQ2D_EINVAL;
+  const unsigned nz = g.batch2 > 1 ? (unsigned)g.batch2 : 1u;
   if (g.M == 0 || g.N == 0 || g.batch == 0) return 0;
+  if ((g.sa2 % 4 || g.sb2 % 4) && nz > 1) return GPTQ2D_EUNSUPPORTED;
   // 128-bit staging: rows and the block offsets of every operand on 16-byte boundaries
   if (g.K % 4 || g.N % 4 || g.lda % 4 || g.ldb % 4 || g.sa % 4 || g.sb % 4 || !aligned16(g.A) || !aligned16(g.B))
     return GPTQ2D_EUNSUPPORTED;
@@ -199,7 +202,7 @@ int gptq2d_tri_gemm_f32(const TriGemm& g, hipStream_t stream) {
     h.B += b0 * g.sb;
     h.D += b0 * g.sd;
     const unsigned nb = (unsigned)(g.batch - b0 < 65535 ? g.batch - b0 : 65535);
-    hipLaunchKernelGGL(tri_gemm_kernel, dim3((unsigned)(nbm * nbn), nb), dim3(256), 0, stream, h, nbn);
+    hipLaunchKernelGGL(tri_gemm_kernel, dim3((unsigned)(nbm * nbn), nb, nz), dim3(256), 0, stream, h, nbn);
     const int rc = (int)hipGetLastError();
     if (rc) return rc;
   }
