@@ -46,6 +46,13 @@ __device__ __forceinline__ T local_cost(const T* __restrict__ table, int64_t s, 
   return c;
 }
 
+// 16 bytes of a buffer at byte offset voff + soff (soff wave-uniform, in the scalar field).
+__device__ __forceinline__ float4 table_quad(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
+  typedef float f4e __attribute__((ext_vector_type(4)));
+  const f4e v = __builtin_bit_cast(f4e, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+  return make_float4(v.x, v.y, v.z, v.w);
+}
+
 template <typename T>
 __device__ __forceinline__ T inf_value() {
   return __builtin_huge_val();
@@ -139,6 +146,8 @@ __device__ void forward_pass(const Sequence<T, V> (&seq)[NS], const bool (&live)
         // PL: the previous minima are in LDS (prev_lds), read and written through LDS-typed pointers --
         // through the generic ones the compiler emits flat accesses, whose waits also wait for the table's
         // loads in flight
+        const __amdgpu_buffer_rsrc_t trs =
+            __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(table), (short)0, (int)((int64_t)(G << kv) * V * 4), 0x00020000);
         auto groups = [&](auto first_c, auto pl_c) {
         constexpr bool first = decltype(first_c)::value, PL = decltype(pl_c)::value;
         using lds_ct = const __attribute__((address_space(3))) T*;
@@ -160,11 +169,12 @@ __device__ void forward_pass(const Sequence<T, V> (&seq)[NS], const bool (&live)
           // the next h's table entries are loaded before this h's states are evaluated, so that each
           // load has a whole iteration to arrive (loaded and used in one iteration, every iteration
           // waited out the L2 latency)
-          const float4* tq = reinterpret_cast<const float4*>(table) + (int64_t)j * V / 4;
-          const int64_t tstep = (int64_t)G32 * V / 4;  // float4s per h
+          // through a buffer resource: this lane's byte offset fixed, step h's in the scalar field (no
+          // 64-bit vector address arithmetic per load)
+          const int tvo = j * V * 4, tstep = G32 * V * 4;
           float4 nxt[V];
 #pragma unroll
-          for (int q = 0; q < V; ++q) nxt[q] = tq[q];
+          for (int q = 0; q < V; ++q) nxt[q] = table_quad(trs, tvo + 16 * q, 0);
 #pragma unroll 2  // 4 or 8: 1.98-2.00 ms for a 512-sequence call, 2: 1.92 ms
           for (int h = 0; h < H32; ++h) {
             const int s = h * G32 + j;
@@ -179,7 +189,7 @@ __device__ void forward_pass(const Sequence<T, V> (&seq)[NS], const bool (&live)
             }
             const int hn = h + 1 < H32 ? h + 1 : h;  // no branch: the last iteration reloads its own
 #pragma unroll
-            for (int q = 0; q < V; ++q) nxt[q] = tq[(int64_t)hn * tstep + q];
+            for (int q = 0; q < V; ++q) nxt[q] = table_quad(trs, tvo + 16 * q, hn * tstep);
             // issued here, not sunk to their use by the scheduler: one sequence per workgroup only (with two,
             // each h has twice the evaluations to cover the latency, and pinning the loads slowed it down)
             if constexpr (NS == 1) __builtin_amdgcn_sched_barrier(0);
