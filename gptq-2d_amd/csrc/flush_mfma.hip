@@ -527,17 +527,13 @@ int gptq2d_flush_tiles_mfma(float* y, float* c, const float* e, const float* l, 
                             int64_t B, hipStream_t stream) {
   TileFlush g{m, n, cdiv(m, TS), cdiv(n, TS), S0, S1, S_end};
   // 2 x 2 tiles per workgroup (four resident per CU), whose fine grain evens out the launch's last
-  // round over the chip, unless the 4 x 4 items (two resident per CU; each k-tile's panels serve
-  // four times the MFMAs) would fill six rounds or more, where the last round weighs little.  At
-  // 8192^2 every outer flush takes 2 x 2: 99 TFLOP/s over a layer's 15 flushes against 96-98 when
-  // the 4 x 4 grain was kept from two rounds on (with the work-item lookup in 32 bits, a small
-  // workgroup's prologue costs little).  Rows whose length is not a multiple of 4 (or matrices not
-  // 16-byte aligned) are staged 32 bits at a time, in 2 x 2 blocks only.
+  // round over the chip.  4 x 4 items (two resident per CU; each k-tile's panels serve four times the
+  // MFMAs) lose wherever measured, also in launches of many rounds: at 8192^2 99 against 96-98 TFLOP/s
+  // over a layer's flushes, at 8192 x 28672 (C5a, 6+ rounds) a sweep of 94.5 against 97.6 ms, the same
+  // bits.  Rows whose length is not a multiple of 4 (or matrices not 16-byte aligned) are staged 32
+  // bits at a time.
   const bool vec = m % 4 == 0 && n % 4 == 0 && aligned16(y) && aligned16(c) && aligned16(e) && aligned16(l) &&
                    aligned16(u) && strides_mult4(lmap) && strides_mult4(umap);
   if (!vec) return launch<2, false>(y, c, e, l, u, g, lmap, umap, B, stream);
-  const double rounds = (double)(count_items<4>(g) * B) / (2.0 * device_cus());
-  if (S1 - S0 >= 4 && rounds >= 6)
-    return launch<4, true>(y, c, e, l, u, g, lmap, umap, B, stream);
   return launch<2, true>(y, c, e, l, u, g, lmap, umap, B, stream);
 }
