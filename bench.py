@@ -49,9 +49,9 @@ VALU_FP32_OPS_PEAK = 39.3e12
 # It changes the order of the fp32 additions only, not the algorithm.
 OUTER_BLOCK = 768
 # The 8192 x 28672 layers of C5a (1 x 32 super-entry rows, and the three-sided D-sided form) sweep fastest with
-# longer blocks: C5a 768 -> 101.1 ms, 1024 -> 99.0, 1280 -> 97.6, 1536 -> 98.8; C5a three-sided 768 -> 109.7,
-# 1024 -> 107.7, 1280 -> 106.9 ms.
-OUTER_BLOCK_WIDE = 1280
+# longer blocks: C5a 768 -> 94.4 ms, 1024 -> 94.0, 1280 -> 95.2-95.9, 1536 -> 97.6, 2048 -> 104.3 (2 x 2-tile
+# outer flushes; with 4 x 4 ones 1280 had been best at 97.6).
+OUTER_BLOCK_WIDE = 1024
 # HBM bytes per outer-flush launch at OUTER_BLOCK on the headline layer, mean over a step's 21
 # launches: rocprofv3 FETCH_SIZE and WRITE_SIZE passes (one counter per run) over this benchmark,
 # each scaled by what the same counter reads for a plain 256 MiB copy kernel in the same run
