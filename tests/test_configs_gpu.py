@@ -55,8 +55,10 @@ def _objective(z, x, a, b):
 
 # ------------------------------------------------------------------------------------------------ full size
 
-# outer block of the benchmark (bench.py OUTER_BLOCK): 24 tile stages
+# outer blocks of the benchmark: bench.py OUTER_BLOCK (24 tile stages) and, for the 8192 x 28672 C5a layers,
+# OUTER_BLOCK_WIDE (32 tile stages)
 BENCH_OUTER = 768
+BENCH_OUTER_WIDE = 1024
 
 
 @pytest.mark.timeout(900)
@@ -190,7 +192,7 @@ def test_c5a_full_size():
                     LDL.ldl_of_inverse(b2.float(), size=cfg.group).t().contiguous())
     q = functools.partial(QI.int_abs_max_quantizer_hip, qmin=cfg.qmin, qmax=cfg.qmax, dtype=torch.bfloat16)
     run = functools.partial(G.gptq_2d_super_entry, x, lo, up, super_entry_shape=(1, cfg.group),
-                            outer_block_size=BENCH_OUTER, fused=True)
+                            outer_block_size=BENCH_OUTER_WIDE, fused=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     z = run(quantizer=q)
