@@ -11,8 +11,8 @@
 //
 // The right product reads C only on the band, which the down product never writes (it writes
 // targets only), so both run in one pass per output tile with a single read-modify-write of Y and C.
-// Both products run on MFMA: fp32 32 x 32 cells (the fused engine's tiles) on the tuned kernel of
-// flush_mfma.hip, every other cell shape and fp64 on flush_mfma_kernel here (16 x 16 x 4 MFMA, entries
+// Both products run on MFMA: 32 x 32 cells (the fused engine's tiles) on the tuned kernel of flush_mfma.hip
+// (fp32; fp64 with even m and n), every other cell shape on flush_mfma_kernel here (16 x 16 x 4 MFMA, entries
 // masked one by one at staging, so any P and Q).
 // L is read only strictly below its P x P diagonal blocks and U strictly above its Q x Q ones;
 // masked loads never touch other entries (they may hold NaN).
@@ -282,9 +282,13 @@ double gptq2d_flush_flops(int64_t m, int64_t n, int64_t P, int64_t Q, int64_t s0
   return total;
 }
 
-int gptq2d_flush_tiles_mfma(float* y, float* c, const float* e, const float* l, const float* u, int64_t m, int64_t n,
-                            int64_t S0, int64_t S1, int64_t S_end, const BatchMap& lmap, const BatchMap& umap,
-                            int64_t B, hipStream_t stream);
+template <typename T>
+bool gptq2d_flush_tiles_mfma_fits(const T* y, const T* c, const T* e, const T* l, const T* u, int64_t m, int64_t n,
+                                  const BatchMap& lmap, const BatchMap& umap);
+template <typename T>
+int gptq2d_flush_tiles_mfma(T* y, T* c, const T* e, const T* l, const T* u, int64_t m, int64_t n, int64_t S0,
+                            int64_t S1, int64_t S_end, const BatchMap& lmap, const BatchMap& umap, int64_t B,
+                            hipStream_t stream);
 
 template <typename T>
 int gptq2d_flush(T* y, T* c, const T* e, const T* l, const T* u, int64_t m, int64_t n, int64_t P, int64_t Q,
@@ -292,17 +296,15 @@ int gptq2d_flush(T* y, T* c, const T* e, const T* l, const T* u, int64_t m, int6
                  hipStream_t stream) {
   if (m <= 0 || n <= 0 || P <= 0 || Q <= 0 || s0 < 0 || s1 <= s0 || s_end < s1) return GPTQ2D_EINVAL;
   if (B == 0 || s_end == s1) return 0;
-  if constexpr (sizeof(T) == 4) {
-    // 32 x 32 coarse cells (the fused engine's tiles, or 32 x 32 super-entries): the tuned fp32 kernel (its
-    // buffer resources are based at each panel, so 32-bit offsets hold for rows and k-tiles of up to 2^20
-    // elements, i.e. any m, n < 2^20); everything else on the cell-masked MFMA kernel below
-    if (P == 32 && Q == 32 && m < ((int64_t)1 << 20) && n < ((int64_t)1 << 20)) {
-      const bool prof = gptq2d_prof_on(PROF_FLUSH);
-      if (prof) gptq2d_prof_begin(PROF_FLUSH, stream);
-      const int rc = gptq2d_flush_tiles_mfma(y, c, e, l, u, m, n, s0, s1, s_end, lmap, umap, B, stream);
-      if (prof) gptq2d_prof_end(PROF_FLUSH, (double)B * gptq2d_flush_flops(m, n, P, Q, s0, s1, s_end), stream);
-      return rc;
-    }
+  // 32 x 32 coarse cells (the fused engine's tiles, or 32 x 32 super-entries): the tuned kernel of
+  // flush_mfma.hip where its size and alignment limits allow (fp32: m, n < 2^20; fp64 also m, n even and
+  // 16-byte aligned matrices); everything else on the cell-masked MFMA kernel below
+  if (P == 32 && Q == 32 && gptq2d_flush_tiles_mfma_fits<T>(y, c, e, l, u, m, n, lmap, umap)) {
+    const bool prof = gptq2d_prof_on(PROF_FLUSH);
+    if (prof) gptq2d_prof_begin(PROF_FLUSH, stream);
+    const int rc = gptq2d_flush_tiles_mfma<T>(y, c, e, l, u, m, n, s0, s1, s_end, lmap, umap, B, stream);
+    if (prof) gptq2d_prof_end(PROF_FLUSH, (double)B * gptq2d_flush_flops(m, n, P, Q, s0, s1, s_end), stream);
+    return rc;
   }
   FlushGeom g{m, n, P, Q, s0, s1, s_end};
   int64_t nrow_tiles;

@@ -1,4 +1,5 @@
-// Cross-tile flush of the fused sweep on fp32 MFMA (v_mfma_f32_32x32x2_f32).
+// Cross-tile flush of the fused sweep on MFMA: fp32 (v_mfma_f32_32x32x2_f32) and fp64
+// (v_mfma_f64_16x16x4_f64, the same design with 2 x 2 such blocks per 32 x 32 tile).
 //
 // In the fused engine the stages are the coarse antidiagonals I + J of 32 x 32 tiles (P = Q = 32
 // in flush.hip's terms), so every band boundary is a tile boundary and each 32 x 32 MFMA output
@@ -20,9 +21,11 @@
 // its tiles is active (the union adds WT - 1 k-tiles per phase to a tile's range).  Tiles that
 // receive nothing are not read or written.
 //
-// Operand layout (lane l, i = l % 32, h = l / 32): A(i, kslot = h), B(kslot = h, j = i); the 16
+// Operand layout, fp32 (lane l, i = l % 32, h = l / 32): A(i, kslot = h), B(kslot = h, j = i); the 16
 // accumulators hold D(8 (r / 4) + 4 h + r % 4, i).  The k carried by slot h in MFMA s is 16 h + s
-// for both operands, so 16 MFMAs cover the 32-deep k-tile.
+// for both operands, so 16 MFMAs cover the 32-deep k-tile.  fp64 (lane l, q = l % 16, h = l / 16), per
+// 16 x 16 block: A(q, kslot = h), B(kslot = h, q); accumulator element r holds D(h + 4 r, q); the k of
+// slot h in MFMA s is 8 h + s, so 8 MFMAs per block cover the k-tile.
 //
 // Reference counterparts (IST-DASLab/GPTQ-2D, gptq_2d.py): _flush_down_kernel :766-932 and
 // _flush_right_kernel :936-1087 (fp32 `tl.dot` with input_precision="ieee"); one kernel here, with
@@ -39,8 +42,20 @@
 namespace {
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef double doublex4 __attribute__((ext_vector_type(4)));
+typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
 
-constexpr int TS = 32;      // tile edge = MFMA block edge
+constexpr int TS = 32;      // tile edge (fp32: one MFMA block; fp64: 2 x 2 blocks)
+
+// Accumulators of a wave's H x H tiles: one 32 x 32 fp32 block each, or 2 x 2 16 x 16 fp64 blocks.
+template <typename T, int H>
+struct AccOf {
+  using type = floatx16[H][H];
+};
+template <int H>
+struct AccOf<double, H> {
+  using type = doublex4[H][H][2][2];
+};
 
 struct TileFlush {
   int64_t m, n, mt, nt, S0, S1, S_end;
@@ -182,52 +197,78 @@ __device__ __forceinline__ bool item_block(const TileGeo32& q, int item, int& by
 }
 
 // Panels in LDS, per k-tile (ROWS = 32 WT), both double-buffered:
-//   A (ROWS x 32 k; k contiguous in memory): float f holds row f / 32 and k = 4 (q ^ quad_swizzle(row)) +
-//     f % 4 with q = (f % 32) / 4 -- the 16-byte k-quads XOR-swizzled by row (lds_dma.h), so that the
-//     rows that lanes read together at one k-quad lie in different bank groups;
-//   B (32 k x ROWS columns; columns contiguous in memory): k-row k at k ROWS, plus BPAD floats per
-//     256-float group of rows, so that the lane halves (rows k and k + 16) fall 32 banks apart.
-template <int WT>
+//   A (ROWS x 32 k; k contiguous in memory): element f holds row f / 32 and k = QE (q ^ swizzle(row)) +
+//     f % QE with q = (f % 32) / QE -- the 16-byte k-quads of QE elements XOR-swizzled by row, so that the
+//     rows that lanes read together at one k-quad lie in different bank groups (fp32: quad_swizzle of
+//     lds_dma.h over a row's 8 quads; fp64: row % 16 over its 16 quads, distinct for the 16 consecutive rows
+//     that the 16 lanes of a 128-bit read's cycle take, which then cover all 64 banks);
+//   B (32 k x ROWS columns; columns contiguous in memory): k-row k at k ROWS, plus BPAD elements per group
+//     of BGRP, so that the k-rows that one half-wave reads together fall 32 banks apart (fp32: rows k and
+//     k + 16; fp64: rows k and k + 8).
+template <typename T, int WT>
 struct FlushLds {
+  static_assert(sizeof(T) == 4 || WT == 2, "the fp64 layout is for 2 x 2-tile workgroups");
+  static constexpr int QE = 16 / (int)sizeof(T);  // elements per 16-byte quad
   static constexpr int ROWS = WT * TS;
   static constexpr int PANEL = ROWS * TS;
-  static constexpr int BPAD = 512 / ROWS;
-  static constexpr int BSZ = PANEL + PANEL / 256 * BPAD;
-  float a[2][PANEL];
-  float b[2][BSZ];
+  static constexpr int BGRP = sizeof(T) == 4 ? 256 : 512;
+  static constexpr int BPAD = sizeof(T) == 4 ? 512 / ROWS : 16;
+  static constexpr int BSZ = PANEL + PANEL / BGRP * BPAD;
+  T a[2][PANEL];
+  T b[2][BSZ];
 };
+
+template <typename T>
+__device__ __forceinline__ int panel_swizzle(int row) {
+  if constexpr (sizeof(T) == 4)
+    return quad_swizzle(row);
+  else
+    return row & 15;
+}
+
+// An LDS panel address as the float pointer that the LDS-direct loads take (they move dwords).
+template <typename T>
+__device__ __forceinline__ float* lds_dst(T* p) {
+  return reinterpret_cast<float*>(p);
+}
 
 // Buffer resource over the elements [first, total) of a matrix stored from `base`: offsets count from
 // element `first`, so that they stay small whatever the matrix size (extents capped below OOB).
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t rebased_rsrc(const float* base, int64_t first, int64_t total) {
+template <typename T>
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rebased_rsrc(const T* base, int64_t first, int64_t total) {
   // clamped with shifts and 32-bit compares (the scalar unit has no 64-bit ordered compare, and these are
-  // evaluated once per k-tile in the MFMA loops): a negative extent -> 0, one of 2^29 or more -> cap
+  // evaluated once per k-tile in the MFMA loops): a negative extent -> 0, a longer one than cap -> cap
   const uint64_t rem = (uint64_t)(total - first);
-  constexpr unsigned cap = (OOB >> 2) - 64;  // < 2^29
+  constexpr unsigned cap = OOB / (int)sizeof(T) - 64;  // < 2^29 floats / 2^28 doubles
   unsigned hi = (unsigned)(rem >> 32);
   const unsigned lo = (unsigned)rem;
   asm("" : "+s"(hi));  // opaque: otherwise the tests below are folded back into 64-bit compares
   const unsigned elems = (hi >> 31) ? 0u : (hi != 0 || lo > cap ? cap : lo);
-  return matrix_rsrc(base + first, elems);
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(base + first), (short)0, (int)(elems * sizeof(T)),
+                                           0x00020000);
 }
 
 // One product phase (0: D = L E, 1: R = C U) of a workgroup, accumulated into acc.  a_mat / b_mat: the
 // operand matrices (a_elems / b_elems elements): A is staged through a buffer resource based at the
 // workgroup's first row, B through one based at each k-tile's first row and the workgroup's first
 // column, so that every offset stays below 2^31 bytes for any matrix a tile row or a k-tile of which does.
-template <int WT, bool VEC, int PHASE>
-__device__ __forceinline__ void flush_phase(floatx16 (&acc)[WT / 2][WT / 2], FlushLds<WT>& sm, const float* a_mat,
-                                            int64_t a_elems, const float* b_mat, int64_t b_elems,
+template <typename T, int WT, bool VEC, int PHASE>
+__device__ __forceinline__ void flush_phase(typename AccOf<T, WT / 2>::type& acc, FlushLds<T, WT>& sm,
+                                            const T* a_mat, int64_t a_elems, const T* b_mat, int64_t b_elems,
                                             const TileFlush& g, int64_t I0, int64_t J0, int wi, int wj,
                                             int t_lo, int t_hi, const int (&tlo)[WT / 2][WT / 2],
                                             const int (&thi)[WT / 2][WT / 2]) {
-  using L = FlushLds<WT>;
+  using L = FlushLds<T, WT>;
+  static_assert(sizeof(T) == 4 || VEC, "fp64 panels are staged 128 bits at a time");
   constexpr int H = WT / 2;
   constexpr int ROWS = L::ROWS;
-  constexpr int W = VEC ? 4 : 1;          // floats per lane per load (rows of 4 k-multiples: 128 bits)
-  constexpr int PER = 64 * W;             // floats per wave load
+  constexpr int QE = L::QE;
+  constexpr int ES = (int)sizeof(T);
+  constexpr int W = VEC ? QE : 1;         // elements per lane per load (a 16-byte quad, or one float)
+  constexpr int DW = W * ES / 4;          // dwords per lane per load
+  constexpr int PER = 64 * W;             // elements per wave load
   constexpr int NI = L::PANEL / PER / 4;  // loads per wave per panel and k-tile
-  const int tid = threadIdx.x, lane = tid & 63, li = lane & 31, hh = lane >> 5;
+  const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: LDS bases in scalar registers
   const int kmax = (int)(PHASE == 0 ? g.m : g.n);  // k extent of both operands
   const int alda = (int)(PHASE == 0 ? g.m : g.n);  // row stride of A (L or C)
@@ -245,16 +286,16 @@ __device__ __forceinline__ void flush_phase(floatx16 (&acc)[WT / 2][WT / 2], Flu
     Geo o;
     const int f = (wave + 4 * x) * PER + lane * W;
     const int row = f / TS;
-    o.a_kk = 4 * (((f % TS) / 4) ^ quad_swizzle(row)) + f % 4;
+    o.a_kk = QE * (((f % TS) / QE) ^ panel_swizzle<T>(row)) + f % QE;
     const int i = (int)I0 * TS + row;
     o.a_in = i < gm;
     o.a_t = i >> 5;
-    o.a_off = ((o.a_in ? row * alda : 0) + o.a_kk) * 4;  // from the workgroup's first row
+    o.a_off = ((o.a_in ? row * alda : 0) + o.a_kk) * ES;  // from the workgroup's first row
     o.b_kb = f / ROWS;
     const int j = (int)J0 * TS + f % ROWS;
     o.b_in = j < gn;
     o.b_t = j >> 5;
-    o.b_off = (o.b_kb * gn + (o.b_in ? f % ROWS : 0)) * 4;  // from the k-tile's first row, the first column
+    o.b_off = (o.b_kb * gn + (o.b_in ? f % ROWS : 0)) * ES;  // from the k-tile's first row, the first column
     return o;
   };
   Geo pre[VEC ? NI : 1];
@@ -285,8 +326,8 @@ __device__ __forceinline__ void flush_phase(floatx16 (&acc)[WT / 2][WT / 2], Flu
 #pragma unroll
         for (int x = 0; x < NI; ++x) {
           const int f0 = (wave + 4 * x) * PER;
-          dma_load_so<W>(ra_src, &sm.a[buf][f0], pre[x].a_off, k0 * 4);
-          dma_load<W>(rb_src, &sm.b[buf][f0 + f0 / 256 * L::BPAD], pre[x].b_off);
+          dma_load_so<DW>(ra_src, lds_dst(&sm.a[buf][f0]), pre[x].a_off, k0 * ES);
+          dma_load<DW>(rb_src, lds_dst(&sm.b[buf][f0 + f0 / L::BGRP * L::BPAD]), pre[x].b_off);
         }
         return;
       }
@@ -297,18 +338,23 @@ __device__ __forceinline__ void flush_phase(floatx16 (&acc)[WT / 2][WT / 2], Flu
       const int f0 = (wave + 4 * x) * PER;
       const bool aband = PHASE == 0 ? ts < o.a_t : (o.a_t + ts >= s0 && o.a_t + ts < s1);
       const bool aok = o.a_in && aband && k0 + o.a_kk < kmax;
-      dma_load<W>(ra_src, &sm.a[buf][f0], aok ? o.a_off + k0 * 4 : OOB);
+      dma_load<DW>(ra_src, lds_dst(&sm.a[buf][f0]), aok ? o.a_off + k0 * ES : OOB);
       const bool bband = PHASE == 0 ? (ts + o.b_t >= s0 && ts + o.b_t < s1) : ts < o.b_t;
       const bool bok = o.b_in && bband && k0 + o.b_kb < kmax;
-      dma_load<W>(rb_src, &sm.b[buf][f0 + f0 / 256 * L::BPAD], bok ? o.b_off : OOB);
+      dma_load<DW>(rb_src, lds_dst(&sm.b[buf][f0 + f0 / L::BGRP * L::BPAD]), bok ? o.b_off : OOB);
     }
   };
 
-  // fragments: A tile a, k-quad 4 hh + v of row (wi + a) 32 + li; B tile d, k = 16 hh + s, column
-  // (wj + d) 32 + li -- the k of MFMA s is 16 hh + s for both operands
+  // fragments.  fp32: A tile a, k-quad 4 hh + v of row (wi + a) 32 + li; B tile d, k = 16 hh + s, column
+  // (wj + d) 32 + li -- the k of MFMA s is 16 hh + s for both operands.  fp64 (one tile per wave): A block a2,
+  // k-quad 4 hh + v of row 32 wi + 16 a2 + li; B block d2, k = 8 hh + s, column 32 wj + 16 d2 + li -- the k of
+  // MFMA s is 8 hh + s for both operands
+  constexpr int LQ = sizeof(T) == 4 ? 32 : 16;  // lanes of one k slot
+  const int li = lane % LQ, hh = lane / LQ;
+  const int kh = (sizeof(T) == 4 ? 16 : 8) * hh;  // first k of the lane's slot
   const int a_base = (wi * TS + li) * TS;
-  const int sw = quad_swizzle(li);
-  const int b_base = 16 * hh * ROWS + wj * TS + li + 16 * hh * ROWS / 256 * L::BPAD;
+  const int sw = panel_swizzle<T>(li);
+  const int b_base = kh * ROWS + wj * TS + li + kh * ROWS / L::BGRP * L::BPAD;
 
   auto step = [&](int t, auto cur_c) {
     constexpr int cur = decltype(cur_c)::value;
@@ -323,7 +369,37 @@ __device__ __forceinline__ void flush_phase(floatx16 (&acc)[WT / 2][WT / 2], Flu
     for (int a = 0; a < H; ++a)
 #pragma unroll
       for (int d = 0; d < H; ++d) any |= ts >= tlo[a][d] && ts < thi[a][d] ? 1 : 0;
-    if (any) {
+    if constexpr (sizeof(T) == 8) {
+      if (any) {
+        const double* as = &sm.a[cur][a_base];
+        const double* bs = &sm.b[cur][b_base];
+        double2 fa[2][2];     // [slot][a2]: k-quad v, i.e. k = 8 hh + 2 v + (0, 1)
+        double fb[2][2][2];   // [slot][d2][s2]: k = 8 hh + 2 v + s2
+        auto frag = [&](int v, int slot) {
+#pragma unroll
+          for (int a2 = 0; a2 < 2; ++a2)
+            fa[slot][a2] = *reinterpret_cast<const double2*>(as + a2 * 16 * TS + 2 * ((4 * hh + v) ^ sw));
+#pragma unroll
+          for (int d2 = 0; d2 < 2; ++d2)
+#pragma unroll
+            for (int s2 = 0; s2 < 2; ++s2) fb[slot][d2][s2] = bs[16 * d2 + (2 * v + s2) * ROWS];
+        };
+        frag(0, 0);
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          if (v < 3) frag(v + 1, (v + 1) & 1);
+#pragma unroll
+          for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+            for (int a2 = 0; a2 < 2; ++a2)
+#pragma unroll
+              for (int d2 = 0; d2 < 2; ++d2)
+                acc[0][0][a2][d2] = __builtin_amdgcn_mfma_f64_16x16x4f64(fa[v & 1][a2][s2], fb[v & 1][d2][s2],
+                                                                          acc[0][0][a2][d2], 0, 0, 0);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+    } else if (any) {
       const float* as = &sm.a[cur][a_base];
       const float* bs = &sm.b[cur][b_base];
       float4 fa[2][H];
@@ -337,7 +413,7 @@ __device__ __forceinline__ void flush_phase(floatx16 (&acc)[WT / 2][WT / 2], Flu
 #pragma unroll
           for (int s2 = 0; s2 < 4; ++s2) {
             const int s = 4 * v + s2;
-            fb[slot][d][s2] = bs[d * TS + s * ROWS + s * ROWS / 256 * L::BPAD];
+            fb[slot][d][s2] = bs[d * TS + s * ROWS + s * ROWS / L::BGRP * L::BPAD];
           }
       };
       frag(0, 0);
@@ -367,15 +443,13 @@ __device__ __forceinline__ void flush_phase(floatx16 (&acc)[WT / 2][WT / 2], Flu
   }
 }
 
-template <int WT, bool VEC>
-__global__ __launch_bounds__(256, 2) void flush_tiles_mfma_kernel(float* __restrict__ y, float* __restrict__ c,
-                                                                  const float* __restrict__ e,
-                                                                  const float* __restrict__ l,
-                                                                  const float* __restrict__ u, TileFlush g,
+template <typename T, int WT, bool VEC>
+__global__ __launch_bounds__(256, 2) void flush_tiles_mfma_kernel(T* __restrict__ y, T* __restrict__ c,
+                                                                  const T* __restrict__ e, const T* __restrict__ l,
+                                                                  const T* __restrict__ u, TileFlush g,
                                                                   BatchMap lmap, BatchMap umap, int64_t b0) {
   constexpr int H = WT / 2;        // tiles per wave per direction
-  constexpr int ROWS = WT * TS;    // panel rows (A) / columns (B)
-  __shared__ __align__(16) FlushLds<WT> sm;
+  __shared__ __align__(16) FlushLds<T, WT> sm;
 
   // XCD-aware order: the hardware deals workgroup w to XCD w % 8; runs of XG consecutive work items
   // (about SR x SR neighbouring blocks, item_block) go to one XCD and its L2, and the XCDs take turns
@@ -418,7 +492,8 @@ __global__ __launch_bounds__(256, 2) void flush_tiles_mfma_kernel(float* __restr
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: keeps the tile masks scalar
-  const int li = lane & 31, hh = lane >> 5;
+  constexpr int LQ = sizeof(T) == 4 ? 32 : 16;  // lanes of one accumulator row group
+  const int li = lane % LQ, hh = lane / LQ;
   const int wi = (wave >> 1) * H, wj = (wave & 1) * H;  // wave's first tile, relative to (I0, J0)
   const int64_t mat = b * g.m * g.n;
 
@@ -439,22 +514,28 @@ __global__ __launch_bounds__(256, 2) void flush_tiles_mfma_kernel(float* __restr
       }
     }
 
-  floatx16 acc[H][H];
+  typename AccOf<T, H>::type acc;
 #pragma unroll
   for (int a = 0; a < H; ++a)
 #pragma unroll
-    for (int d = 0; d < H; ++d)
+    for (int d = 0; d < H; ++d) {
+      if constexpr (sizeof(T) == 8) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) acc[a][d][r] = 0.f;
+        for (int x = 0; x < 16; ++x) acc[a][d][x >> 3][(x >> 2) & 1][x & 3] = 0.;
+      } else {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[a][d][r] = 0.f;
+      }
+    }
 
   // phase 0: D = L E, then C += D; phase 1: R = C U on top of D, then Y += D + R
-  const float* lm = l + lmap.offset(b);
-  const float* um = u + umap.offset(b);
-  flush_phase<WT, VEC, 0>(acc, sm, lm, g.m * g.m, e + mat, g.m * g.n, g, I0, J0, wi, wj, lo0, hi0, tlo[0], thi[0]);
+  const T* lm = l + lmap.offset(b);
+  const T* um = u + umap.offset(b);
+  flush_phase<T, WT, VEC, 0>(acc, sm, lm, g.m * g.m, e + mat, g.m * g.n, g, I0, J0, wi, wj, lo0, hi0, tlo[0], thi[0]);
 #pragma unroll
   for (int ph = 0; ph < 2; ++ph) {
     if (ph == 1)
-      flush_phase<WT, VEC, 1>(acc, sm, c + mat, g.m * g.n, um, g.n * g.n, g, I0, J0, wi, wj, lo1, hi1, tlo[1], thi[1]);
+      flush_phase<T, WT, VEC, 1>(acc, sm, c + mat, g.m * g.n, um, g.n * g.n, g, I0, J0, wi, wj, lo1, hi1, tlo[1], thi[1]);
     // epilogue of the phase: C += D after the down products, Y += D + R after the right ones
 #pragma unroll
     for (int a = 0; a < H; ++a)
@@ -468,27 +549,42 @@ __global__ __launch_bounds__(256, 2) void flush_tiles_mfma_kernel(float* __restr
         const __amdgpu_buffer_rsrc_t rd = rebased_rsrc(ph == 0 ? c + mat : y + mat, I * TS * g.n, g.m * g.n);
         // all 16 reads in flight before the first write; masked lanes address past the matrix
         int off[16];
-        float cur[16];
+        T cur[16];
+        if constexpr (sizeof(T) == 8) {
+          // element r of block (a2, d2) (x = 8 a2 + 4 d2 + r): row 16 a2 + hh + 4 r, column 16 d2 + li
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int ri = 8 * (r >> 2) + 4 * hh + (r & 3);
-          const int64_t i = I * TS + ri, j = J * TS + li;
-          off[r] = (i < g.m && j < g.n) ? (ri * (int)g.n + (int)j) * 4 : OOB;
-          cur[r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rd, off[r], 0, 0));
+          for (int x = 0; x < 16; ++x) {
+            const int ri = 16 * (x >> 3) + hh + 4 * (x & 3), cj = 16 * ((x >> 2) & 1) + li;
+            const int64_t i = I * TS + ri, j = J * TS + cj;
+            off[x] = (i < g.m && j < g.n) ? (ri * (int)g.n + (int)j) * 8 : OOB;
+            cur[x] = __builtin_bit_cast(double, __builtin_amdgcn_raw_buffer_load_b64(rd, off[x], 0, 0));
+          }
+#pragma unroll
+          for (int x = 0; x < 16; ++x)
+            __builtin_amdgcn_raw_buffer_store_b64(
+                __builtin_bit_cast(u32x2, cur[x] + acc[a][d][x >> 3][(x >> 2) & 1][x & 3]), rd, off[x], 0, 0);
+        } else {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int ri = 8 * (r >> 2) + 4 * hh + (r & 3);
+            const int64_t i = I * TS + ri, j = J * TS + li;
+            off[r] = (i < g.m && j < g.n) ? (ri * (int)g.n + (int)j) * 4 : OOB;
+            cur[r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rd, off[r], 0, 0));
+          }
+#pragma unroll
+          for (int r = 0; r < 16; ++r)
+            __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, cur[r] + acc[a][d][r]), rd, off[r], 0,
+                                                  0);
         }
-#pragma unroll
-        for (int r = 0; r < 16; ++r)
-          __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, cur[r] + acc[a][d][r]), rd, off[r], 0, 0);
       }
   }
 }
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
-
-bool strides_mult4(const BatchMap& bm) {
+bool strides_mult(const BatchMap& bm, int q) {
   for (int d = 0; d < bm.nd; ++d)
-    if (bm.stride[d] % 4) return false;
+    if (bm.stride[d] % q) return false;
   return true;
 }
 
@@ -505,35 +601,65 @@ int64_t count_items(const TileFlush& g) {
   return items;
 }
 
-template <int WT, bool VEC>
-int launch(float* y, float* c, const float* e, const float* l, const float* u, const TileFlush& g,
-           const BatchMap& lmap, const BatchMap& umap, int64_t B, hipStream_t stream) {
+template <typename T, int WT, bool VEC>
+int launch(T* y, T* c, const T* e, const T* l, const T* u, const TileFlush& g, const BatchMap& lmap,
+           const BatchMap& umap, int64_t B, hipStream_t stream) {
   const int64_t items = count_items<WT>(g);
   if (items == 0 || B == 0) return 0;
   if (items > 0x7fffffff) return GPTQ2D_EUNSUPPORTED;
   for (int64_t b0 = 0; b0 < B; b0 += 65535) {
     const dim3 grid((unsigned)items, (unsigned)(B - b0 < 65535 ? B - b0 : 65535));
-    hipLaunchKernelGGL((flush_tiles_mfma_kernel<WT, VEC>), grid, dim3(256), 0, stream, y, c, e, l, u, g, lmap, umap,
-                       b0);
+    hipLaunchKernelGGL((flush_tiles_mfma_kernel<T, WT, VEC>), grid, dim3(256), 0, stream, y, c, e, l, u, g, lmap,
+                       umap, b0);
   }
   return (int)hipGetLastError();
 }
 
+// Matrices whose rows, batch strides and base addresses allow 128-bit staging (q elements per 16 bytes).
+template <typename T>
+bool quad_aligned(const T* y, const T* c, const T* e, const T* l, const T* u, int64_t m, int64_t n,
+                  const BatchMap& lmap, const BatchMap& umap) {
+  constexpr int q = 16 / (int)sizeof(T);
+  return m % q == 0 && n % q == 0 && aligned16(y) && aligned16(c) && aligned16(e) && aligned16(l) && aligned16(u) &&
+         strides_mult(lmap, q) && strides_mult(umap, q);
+}
+
 }  // namespace
 
-// Flush of tile stages [S0, S1) into [S1, S_end) on MFMA.
-int gptq2d_flush_tiles_mfma(float* y, float* c, const float* e, const float* l, const float* u, int64_t m, int64_t n,
-                            int64_t S0, int64_t S1, int64_t S_end, const BatchMap& lmap, const BatchMap& umap,
-                            int64_t B, hipStream_t stream) {
-  TileFlush g{m, n, cdiv(m, TS), cdiv(n, TS), S0, S1, S_end};
-  // 2 x 2 tiles per workgroup (four resident per CU), whose fine grain evens out the launch's last
-  // round over the chip.  4 x 4 items (two resident per CU; each k-tile's panels serve four times the
-  // MFMAs) lose wherever measured, also in launches of many rounds: at 8192^2 99 against 96-98 TFLOP/s
-  // over a layer's flushes, at 8192 x 28672 (C5a, 6+ rounds) a sweep of 94.5 against 97.6 ms, the same
-  // bits.  Rows whose length is not a multiple of 4 (or matrices not 16-byte aligned) are staged 32
-  // bits at a time.
-  const bool vec = m % 4 == 0 && n % 4 == 0 && aligned16(y) && aligned16(c) && aligned16(e) && aligned16(l) &&
-                   aligned16(u) && strides_mult4(lmap) && strides_mult4(umap);
-  if (!vec) return launch<2, false>(y, c, e, l, u, g, lmap, umap, B, stream);
-  return launch<2, true>(y, c, e, l, u, g, lmap, umap, B, stream);
+// Whether gptq2d_flush_tiles_mfma takes a flush of 32 x 32 coarse cells: its buffer resources are based at
+// each panel, so 32-bit offsets hold for rows and k-tiles of up to 2^20 elements (m, n < 2^20); fp64 panels
+// are staged 128 bits at a time only, so fp64 also needs m and n even and 16-byte aligned matrices.
+template <typename T>
+bool gptq2d_flush_tiles_mfma_fits(const T* y, const T* c, const T* e, const T* l, const T* u, int64_t m, int64_t n,
+                                  const BatchMap& lmap, const BatchMap& umap) {
+  if (m >= ((int64_t)1 << 20) || n >= ((int64_t)1 << 20)) return false;
+  return sizeof(T) == 4 || quad_aligned(y, c, e, l, u, m, n, lmap, umap);
 }
+
+// Flush of tile stages [S0, S1) into [S1, S_end) on MFMA.
+template <typename T>
+int gptq2d_flush_tiles_mfma(T* y, T* c, const T* e, const T* l, const T* u, int64_t m, int64_t n, int64_t S0,
+                            int64_t S1, int64_t S_end, const BatchMap& lmap, const BatchMap& umap, int64_t B,
+                            hipStream_t stream) {
+  if (!gptq2d_flush_tiles_mfma_fits(y, c, e, l, u, m, n, lmap, umap)) return GPTQ2D_EUNSUPPORTED;
+  TileFlush g{m, n, cdiv(m, TS), cdiv(n, TS), S0, S1, S_end};
+  // 2 x 2 tiles per workgroup (four resident per CU in fp32, two in fp64), whose fine grain evens out the
+  // launch's last round over the chip.  4 x 4 fp32 items (two resident per CU; each k-tile's panels serve four
+  // times the MFMAs) lose wherever measured, also in launches of many rounds: at 8192^2 99 against 96-98
+  // TFLOP/s over a layer's flushes, at 8192 x 28672 (C5a, 6+ rounds) a sweep of 94.5 against 97.6 ms, the same
+  // bits.  fp32 rows whose length is not a multiple of 4 (or matrices not 16-byte aligned) are staged 32 bits
+  // at a time.
+  const bool vec = quad_aligned(y, c, e, l, u, m, n, lmap, umap);
+  if constexpr (sizeof(T) == 4) {
+    if (!vec) return launch<T, 2, false>(y, c, e, l, u, g, lmap, umap, B, stream);
+  }
+  return launch<T, 2, true>(y, c, e, l, u, g, lmap, umap, B, stream);
+}
+
+#define GPTQ2D_FLUSH_TILES_INST(T)                                                                                  \
+  template bool gptq2d_flush_tiles_mfma_fits<T>(const T*, const T*, const T*, const T*, const T*, int64_t, int64_t, \
+                                                const BatchMap&, const BatchMap&);                                  \
+  template int gptq2d_flush_tiles_mfma<T>(T*, T*, const T*, const T*, const T*, int64_t, int64_t, int64_t, int64_t, \
+                                          int64_t, const BatchMap&, const BatchMap&, int64_t, hipStream_t);
+GPTQ2D_FLUSH_TILES_INST(float)
+GPTQ2D_FLUSH_TILES_INST(double)

@@ -1,6 +1,6 @@
 """GPU tests of the block flush (gptq2d_flush_*), both the cell-masked MFMA kernel (any cell shape, fp32 and
-fp64) and the tuned tile-aligned one (fp32 with 32 x 32 coarse cells), against a dense CPU statement of the
-flush:
+fp64) and the tuned tile-aligned one (32 x 32 coarse cells: fp32, and fp64 with even m and n), against a dense
+CPU statement of the flush:
 
   stage(i, j) = i // P + j // Q;  band = [s0, s1);  targets = [s1, s_end)
   D = (L masked to k//P < i//P) @ (E masked to the band);  R = (C masked to the band) @ (U masked to k//Q < j//Q)
@@ -43,6 +43,8 @@ CASES = [  # m, n, P, Q, s0, s1, s_end
     # 16 x 16 cells (the trellis configuration's super-entries), 1 x 32 rows, cells taller than an output tile
     (256, 320, 16, 16, 3, 9, 40), (520, 130, 16, 16, 0, 4, 30), (1000, 600, 16, 16, 20, 30, 90),
     (96, 256, 1, 32, 4, 12, 30), (300, 200, 100, 40, 0, 1, 5),
+    # a 24-stage band over many 2 x 2-tile workgroups (interior k-tiles, the XCD order's full runs)
+    (2048, 1536, 32, 32, 20, 44, 110),
 ]
 
 
