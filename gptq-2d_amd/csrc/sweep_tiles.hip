@@ -212,17 +212,43 @@ __global__ __launch_bounds__(NTHREADS) void sweep_rows_kernel(T* __restrict__ y,
                             m, n, i0, j0, mat);
 }
 
+// Sum over the PARTS = 8 lanes of a lane group with DPP moves inside each 8-lane half-row (quad_perm xor 1,
+// quad_perm xor 2, row_half_mirror): every lane of the group ends with the same bits (each step adds a
+// lane's value to its partner's, and the partners' sums are equal, fp addition being commutative).  A
+// ds_bpermute shuffle goes through the LDS unit and back, three dependent round trips per sum.
+template <int CTRL>
+__device__ __forceinline__ double dpp_move(double v) {
+  const unsigned long long b = __builtin_bit_cast(unsigned long long, v);
+  const int lo = __builtin_amdgcn_mov_dpp((int)(unsigned)b, CTRL, 0xf, 0xf, false);
+  const int hi = __builtin_amdgcn_mov_dpp((int)(unsigned)(b >> 32), CTRL, 0xf, 0xf, false);
+  return __builtin_bit_cast(double, ((unsigned long long)(unsigned)hi << 32) | (unsigned)lo);
+}
+template <typename T>
+__device__ __forceinline__ T sum_parts(T v) {
+  static_assert(PARTS == 8, "one 8-lane half-row per entry");
+  v += dpp_move<0xB1>(v);   // quad_perm [1, 0, 3, 2]
+  v += dpp_move<0x4E>(v);   // quad_perm [2, 3, 0, 1]
+  v += dpp_move<0x141>(v);  // row_half_mirror: lane i <- lane 7 - i of the half-row (the other quad)
+  return v;
+}
+
+// LDS pitch of the step operands of sweep_tiles_kernel: 40 elements (80 dwords for fp64, = 16 mod 64 banks),
+// so that the 4 rows x 8 parts of a half-wave read 32 distinct bank pairs.
+constexpr int SWP = TR + 8;
+
 template <typename T>
 __global__ __launch_bounds__(NTHREADS) void sweep_tiles_kernel(T* __restrict__ y, T* __restrict__ c,
                                                                T* __restrict__ e, const T* __restrict__ l,
                                                                const T* __restrict__ u, int64_t m, int64_t n,
                                                                int64_t stage, int64_t tile_lo, BatchMap lmap,
                                                                BatchMap umap, QSpec<T> qs, int64_t nx, int64_t ny) {
+  // the operands that a step reads along k, each with k contiguous: Ls[r][k] = L[i0+r, i0+k], Cs[r][k],
+  // EsT[c][k] = E[i0+k, j0+c], UsT[c][k] = U[j0+k, j0+c]
   __shared__ T Ys[TR][TR + 1];
-  __shared__ T Cs[TR][TR + 1];
-  __shared__ T Es[TR][TR + 1];
-  __shared__ T Ls[TR][TR + 1];
-  __shared__ T Us[TR][TR + 1];
+  __shared__ T Cs[TR][SWP];
+  __shared__ T EsT[TR][SWP];
+  __shared__ T Ls[TR][SWP];
+  __shared__ T UsT[TR][SWP];
   __shared__ T Ss[TR][TR + 1];
   __shared__ T Zs[TR][TR + 1];
 
@@ -242,10 +268,10 @@ __global__ __launch_bounds__(NTHREADS) void sweep_tiles_kernel(T* __restrict__ y
     const int64_t off = mat + gi * n + gj;
     Ys[r][cc] = in ? y[off] : T(0);
     Cs[r][cc] = in ? c[off] : T(0);
-    Es[r][cc] = T(0);
+    EsT[cc][r] = T(0);
     // L[i0+r, i0+cc] strictly below the diagonal; U[j0+r, j0+cc] strictly above it
     Ls[r][cc] = (cc < r && gi < m) ? lb[gi * m + (i0 + cc)] : T(0);
-    Us[r][cc] = (r < cc && j0 + cc < n) ? ub[(j0 + r) * n + (j0 + cc)] : T(0);
+    UsT[cc][r] = (r < cc && j0 + cc < n) ? ub[(j0 + r) * n + (j0 + cc)] : T(0);
     if (qs.kind == Q_AFFINE) {
       Ss[r][cc] = in ? qs.scale[qs.smap.offset(b) + gi * n + gj] : T(1);
       Zs[r][cc] = in ? qs.zp[qs.zmap.offset(b) + gi * n + gj] : T(0);
@@ -265,19 +291,17 @@ __global__ __launch_bounds__(NTHREADS) void sweep_tiles_kernel(T* __restrict__ y
 #pragma unroll
       for (int k = 0; k < TR / PARTS; ++k) {
         const int rr = part + PARTS * k;
-        if (rr < r) down += Ls[r][rr] * Es[rr][cc];
+        if (rr < r) down += Ls[r][rr] * EsT[cc][rr];
       }
 #pragma unroll
       for (int k = 0; k < TR / PARTS; ++k) {
         const int c2 = part + PARTS * k;
-        if (c2 < cc) right += Cs[r][c2] * Us[c2][cc];
+        if (c2 < cc) right += Cs[r][c2] * UsT[cc][c2];
       }
     }
-#pragma unroll
-    for (int w = PARTS / 2; w >= 1; w >>= 1) {
-      down += __shfl_xor(down, w, PARTS);
-      right += __shfl_xor(right, w, PARTS);
-    }
+    // every lane of the group takes part (inactive ones with zeros): DPP reads the other lanes' registers
+    down = sum_parts(down);
+    right = sum_parts(right);
     if (active && part == 0) {
       const T yv = (Ys[r][cc] + down) + right;
       T z;
@@ -292,7 +316,7 @@ __global__ __launch_bounds__(NTHREADS) void sweep_tiles_kernel(T* __restrict__ y
       }
       const T ev = z - yv;
       Ys[r][cc] = z;
-      Es[r][cc] = ev;
+      EsT[cc][r] = ev;
       Cs[r][cc] = (Cs[r][cc] + down) + ev;
       if (qs.ypre) qs.ypre[mat + gi * n + j0 + cc] = yv;
     }
@@ -306,7 +330,7 @@ __global__ __launch_bounds__(NTHREADS) void sweep_tiles_kernel(T* __restrict__ y
       const int64_t off = mat + gi2 * n + gj;
       y[off] = Ys[rr][cc];
       c[off] = Cs[rr][cc];
-      e[off] = Es[rr][cc];
+      e[off] = EsT[cc][rr];
     }
   }
 }
