@@ -413,13 +413,17 @@ __global__ __launch_bounds__(256) void gemm_mfma64_kernel(GemmProblem<double> p)
     }
     __syncthreads();
     if (kb + DK < kr.k_hi) load(kb + DK);
+    // k slot kq of MFMA s carries k = 16 (kq & 1) + 8 (kq >> 1) + s: the two k-rows that a half-wave's
+    // 64-bit reads take together (slots 0 and 1, or 2 and 3) lie 16 rows = 32 banks apart at the odd pitch
+    // that keeps the transposing stores above free of conflicts (with k = 4 s + kq they lay 2 banks apart)
+    const int kof = 16 * (kq & 1) + 8 * (kq >> 1);
 #pragma unroll
-    for (int k4 = 0; k4 < DK; k4 += 4) {
+    for (int s = 0; s < DK / 4; ++s) {
       double av[2], bv[2];
 #pragma unroll
-      for (int r = 0; r < 2; ++r) av[r] = As[k4 + kq][wi + 16 * r + li];
+      for (int r = 0; r < 2; ++r) av[r] = As[kof + s][wi + 16 * r + li];
 #pragma unroll
-      for (int c = 0; c < 2; ++c) bv[c] = Bs[k4 + kq][wj + 16 * c + li];
+      for (int c = 0; c < 2; ++c) bv[c] = Bs[kof + s][wj + 16 * c + li];
 #pragma unroll
       for (int r = 0; r < 2; ++r)
 #pragma unroll
