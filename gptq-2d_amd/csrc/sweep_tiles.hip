@@ -6,15 +6,16 @@
 // is swept by one workgroup entirely in LDS -- its 2*TR-1 antidiagonals one after another, every
 // entry of an antidiagonal at once, the in-tile error feedback through the diagonal blocks
 // L[I,I] and U[J,J], the quantizer applied in place.  Feedback between tiles: after each outer
-// block of `outer_tiles` coarse stages, the block flush of flush.hip with P = Q = TR (on MFMA for
-// fp32) into all later stages; inside an outer block, fp32 tiles pull the feedback of the block's
-// earlier tiles on MFMA (tile_stage_kernel), fp64 stages are flushed into the rest of the block
-// after each coarse stage.  The host loop below issues every launch of the sweep from C++ in one
-// call, so a whole layer is one C-ABI call and one capturable stream of kernels.
+// block of `outer_tiles` coarse stages, the block flush of flush.hip with P = Q = TR (on MFMA) into
+// all later stages; inside an outer block, fp32 tiles pull the feedback of the block's earlier tiles
+// on MFMA (tile_stage_kernel), fp64 stages are flushed into the rest of the block after each coarse
+// stage (sweep_tile64_kernel then sweeps).  Both run the same push-form in-tile sweep (sweep_tile).
+// The host loop below issues every launch of the sweep from C++ in one call, so a whole layer is one
+// C-ABI call and one capturable stream of kernels.
 //
 // In exact arithmetic the result equals the reference's blocked sweep (gptq_2d.py:1295-1375) and
 // Algorithm 1 on vec(X) (GPTQ-2D paper, Theorem 1); in floating point the sums are accumulated in
-// a different order.  In-tile feedback of entry (r, c) is gathered ("pulled") as
+// a different order.  The in-tile value of entry (r, c) when it is rounded is
 //   y = (Y[r,c] + sum_{r'<r} L[r,r'] E[r',c]) + sum_{c'<c} C[r,c'] U[c',c]
 // where C[r,c'] is already complete (all rows above in the tile were rounded earlier).
 #include "common.h"
@@ -212,128 +213,6 @@ __global__ __launch_bounds__(NTHREADS) void sweep_rows_kernel(T* __restrict__ y,
                             m, n, i0, j0, mat);
 }
 
-// Sum over the PARTS = 8 lanes of a lane group with DPP moves inside each 8-lane half-row (quad_perm xor 1,
-// quad_perm xor 2, row_half_mirror): every lane of the group ends with the same bits (each step adds a
-// lane's value to its partner's, and the partners' sums are equal, fp addition being commutative).  A
-// ds_bpermute shuffle goes through the LDS unit and back, three dependent round trips per sum.
-template <int CTRL>
-__device__ __forceinline__ double dpp_move(double v) {
-  const unsigned long long b = __builtin_bit_cast(unsigned long long, v);
-  const int lo = __builtin_amdgcn_mov_dpp((int)(unsigned)b, CTRL, 0xf, 0xf, false);
-  const int hi = __builtin_amdgcn_mov_dpp((int)(unsigned)(b >> 32), CTRL, 0xf, 0xf, false);
-  return __builtin_bit_cast(double, ((unsigned long long)(unsigned)hi << 32) | (unsigned)lo);
-}
-template <typename T>
-__device__ __forceinline__ T sum_parts(T v) {
-  static_assert(PARTS == 8, "one 8-lane half-row per entry");
-  v += dpp_move<0xB1>(v);   // quad_perm [1, 0, 3, 2]
-  v += dpp_move<0x4E>(v);   // quad_perm [2, 3, 0, 1]
-  v += dpp_move<0x141>(v);  // row_half_mirror: lane i <- lane 7 - i of the half-row (the other quad)
-  return v;
-}
-
-// LDS pitch of the step operands of sweep_tiles_kernel: 40 elements (80 dwords for fp64, = 16 mod 64 banks),
-// so that the 4 rows x 8 parts of a half-wave read 32 distinct bank pairs.
-constexpr int SWP = TR + 8;
-
-template <typename T>
-__global__ __launch_bounds__(NTHREADS) void sweep_tiles_kernel(T* __restrict__ y, T* __restrict__ c,
-                                                               T* __restrict__ e, const T* __restrict__ l,
-                                                               const T* __restrict__ u, int64_t m, int64_t n,
-                                                               int64_t stage, int64_t tile_lo, BatchMap lmap,
-                                                               BatchMap umap, QSpec<T> qs, int64_t nx, int64_t ny) {
-  // the operands that a step reads along k, each with k contiguous: Ls[r][k] = L[i0+r, i0+k], Cs[r][k],
-  // EsT[c][k] = E[i0+k, j0+c], UsT[c][k] = U[j0+k, j0+c]
-  __shared__ T Ys[TR][TR + 1];
-  __shared__ T Cs[TR][SWP];
-  __shared__ T EsT[TR][SWP];
-  __shared__ T Ls[TR][SWP];
-  __shared__ T UsT[TR][SWP];
-  __shared__ T Ss[TR][TR + 1];
-  __shared__ T Zs[TR][TR + 1];
-
-  const GridIds id = grid_ids(nx, ny);
-  const int64_t b = id.b;
-  const int64_t I = tile_lo + id.x, J = stage - I;
-  const int64_t i0 = I * TR, j0 = J * TR;
-  const int64_t mat = b * m * n;
-  const T* lb = l + lmap.offset(b);
-  const T* ub = u + umap.offset(b);
-  const int tid = threadIdx.x;
-
-  for (int t = tid; t < TR * TR; t += NTHREADS) {
-    const int r = t / TR, cc = t % TR;
-    const int64_t gi = i0 + r, gj = j0 + cc;
-    const bool in = gi < m && gj < n;
-    const int64_t off = mat + gi * n + gj;
-    Ys[r][cc] = in ? y[off] : T(0);
-    Cs[r][cc] = in ? c[off] : T(0);
-    EsT[cc][r] = T(0);
-    // L[i0+r, i0+cc] strictly below the diagonal; U[j0+r, j0+cc] strictly above it
-    Ls[r][cc] = (cc < r && gi < m) ? lb[gi * m + (i0 + cc)] : T(0);
-    UsT[cc][r] = (r < cc && j0 + cc < n) ? ub[(j0 + r) * n + (j0 + cc)] : T(0);
-    if (qs.kind == Q_AFFINE) {
-      Ss[r][cc] = in ? qs.scale[qs.smap.offset(b) + gi * n + gj] : T(1);
-      Zs[r][cc] = in ? qs.zp[qs.zmap.offset(b) + gi * n + gj] : T(0);
-    } else if (qs.kind == Q_FORCED) {
-      Ss[r][cc] = in ? qs.scale[qs.smap.offset(b) + gi * n + gj] : T(0);
-    }
-  }
-  __syncthreads();
-
-  const int r = tid / PARTS, part = tid % PARTS;
-  const int64_t gi = i0 + r;
-  for (int t = 0; t < 2 * TR - 1; ++t) {
-    const int cc = t - r;
-    const bool active = cc >= 0 && cc < TR && gi < m && j0 + cc < n;
-    T down = T(0), right = T(0);
-    if (active) {
-#pragma unroll
-      for (int k = 0; k < TR / PARTS; ++k) {
-        const int rr = part + PARTS * k;
-        if (rr < r) down += Ls[r][rr] * EsT[cc][rr];
-      }
-#pragma unroll
-      for (int k = 0; k < TR / PARTS; ++k) {
-        const int c2 = part + PARTS * k;
-        if (c2 < cc) right += Cs[r][c2] * UsT[cc][c2];
-      }
-    }
-    // every lane of the group takes part (inactive ones with zeros): DPP reads the other lanes' registers
-    down = sum_parts(down);
-    right = sum_parts(right);
-    if (active && part == 0) {
-      const T yv = (Ys[r][cc] + down) + right;
-      T z;
-      if (qs.kind == Q_AFFINE) {
-        const T sv = Ss[r][cc], zv = Zs[r][cc];
-        const T code = clamp_val(round_even(yv / sv + zv), qs.qmin, qs.qmax);
-        z = (code - zv) * sv;
-      } else if (qs.kind == Q_FORCED) {
-        z = Ss[r][cc];
-      } else {
-        z = round_even(yv);
-      }
-      const T ev = z - yv;
-      Ys[r][cc] = z;
-      EsT[cc][r] = ev;
-      Cs[r][cc] = (Cs[r][cc] + down) + ev;
-      if (qs.ypre) qs.ypre[mat + gi * n + j0 + cc] = yv;
-    }
-    __syncthreads();
-  }
-
-  for (int t = tid; t < TR * TR; t += NTHREADS) {
-    const int rr = t / TR, cc = t % TR;
-    const int64_t gi2 = i0 + rr, gj = j0 + cc;
-    if (gi2 < m && gj < n) {
-      const int64_t off = mat + gi2 * n + gj;
-      y[off] = Ys[rr][cc];
-      c[off] = Cs[rr][cc];
-      e[off] = EsT[cc][rr];
-    }
-  }
-}
 
 // ------------------------------------------------------------------------------------------------ fp32: pull + sweep
 
@@ -418,13 +297,17 @@ constexpr int UPW = TR + 7;
 constexpr int CPW = 3 * TR + 2;
 constexpr int EROWS = 3 * TR;
 
-struct TileLds {
-  float Ys[TR][SP];  // first: the sweep's base pointers below reach up to 23 rows / columns before Lp and Up
-  float Lp[TR][LPW];
-  float Up[3 * TR][UPW];
-  float Cs[TR][CPW];
-  float Es[EROWS][SP];
+// (T = double: the same image in fp64; every pitch gives the 32 lanes of a half-wave 32 distinct positions
+// mod 32, so their 64-bit reads cover the 64 banks once)
+template <typename T>
+struct TileLdsT {
+  T Ys[TR][SP];  // first: the sweep's base pointers below reach up to 23 rows / columns before Lp and Up
+  T Lp[TR][LPW];
+  T Up[3 * TR][UPW];
+  T Cs[TR][CPW];
+  T Es[EROWS][SP];
 };
+using TileLds = TileLdsT<float>;
 
 // Affine / round / forced quantizer of the in-tile sweep, given the precomputed correctly rounded
 // reciprocal rv = 1/sv and whether sv lies in [2^-60, 2^60] (affine only).  y / s is formed as
@@ -434,23 +317,35 @@ struct TileLds {
 // whether that holds -- the biased exponent of y in [67, 187], one bit-field test (zero, denormal,
 // infinite and NaN y fail it) -- and otherwise quantize_entry_div (the division itself) gives the
 // value.  This keeps the division's ten dependent operations off the per-antidiagonal critical path.
-template <int KIND>
-__device__ __forceinline__ float quantize_entry_rcp(float yv, float sv, float zv, float rv, bool s_ok, float qmin,
-                                                    float qmax, bool& exact) {
+//
+__device__ __forceinline__ float fma_of(float a, float b, float c) { return __builtin_fmaf(a, b, c); }
+__device__ __forceinline__ double fma_of(double a, double b, double c) { return __builtin_fma(a, b, c); }
+
+// fp64: the same with 2^-500 <= |s| <= 2^500 and 2^-500 <= |y| < 2^501 (biased exponent of y in [523, 1523]):
+// |q0| lies in [2^-1001, 2^1001] and the remainder is a multiple of 2^-605, all normal.
+template <int KIND, typename T>
+__device__ __forceinline__ T quantize_entry_rcp(T yv, T sv, T zv, T rv, bool s_ok, T qmin, T qmax, bool& exact) {
   // the dequantized value is rounded on its own (as the reference's plug-in writes it), so that the
   // caller's error z - y is exactly that difference: no contraction into the caller's subtraction
 #pragma clang fp contract(off)
   if constexpr (KIND == Q_AFFINE) {
-    const float q0 = yv * rv;
-    const float rem = __builtin_fmaf(-q0, sv, yv);
-    const float q = __builtin_fmaf(rem, rv, q0);
+    const T q0 = yv * rv;
+    const T rem = fma_of(-q0, sv, yv);
+    const T q = fma_of(rem, rv, q0);
     // s_ok also holds only when the zero point is not NaN and qmin <= qmax: then q is the IEEE
     // quotient, round(q + z) is not NaN, and the median of (x, qmin, qmax) is the clamp, in one
     // operation on the per-step critical path
-    const unsigned ex = (__float_as_uint(yv) >> 23) & 0xffu;
-    exact = s_ok && ex - 67u <= 120u;
-    const float code = __builtin_amdgcn_fmed3f(round_even(q + zv), qmin, qmax);
-    return (code - zv) * sv;
+    if constexpr (sizeof(T) == 4) {
+      const unsigned ex = (__float_as_uint(yv) >> 23) & 0xffu;
+      exact = s_ok && ex - 67u <= 120u;
+      const T code = __builtin_amdgcn_fmed3f(round_even(q + zv), qmin, qmax);
+      return (code - zv) * sv;
+    } else {
+      const unsigned ex = (unsigned)(__builtin_bit_cast(unsigned long long, yv) >> 52) & 0x7ffu;
+      exact = s_ok && ex - 523u <= 1000u;
+      const T code = clamp_val(round_even(q + zv), qmin, qmax);
+      return (code - zv) * sv;
+    }
   } else if constexpr (KIND == Q_FORCED) {
     exact = true;
     return sv;
@@ -460,9 +355,10 @@ __device__ __forceinline__ float quantize_entry_rcp(float yv, float sv, float zv
   }
 }
 
-__device__ __forceinline__ float quantize_entry_div(float yv, float sv, float zv, float qmin, float qmax) {
+template <typename T>
+__device__ __forceinline__ T quantize_entry_div(T yv, T sv, T zv, T qmin, T qmax) {
 #pragma clang fp contract(off)
-  const float code = clamp_val(round_even(yv / sv + zv), qmin, qmax);
+  const T code = clamp_val(round_even(yv / sv + zv), qmin, qmax);
   return (code - zv) * sv;
 }
 
@@ -478,29 +374,29 @@ __device__ __forceinline__ void slot_columns(int r, int part, int (&cs)[4]) {
 
 // Quantizer inputs of the sweep's entries in its own layout (slot order), read from global memory at
 // the start of the kernel so that their latency overlaps the pull.
-template <int KIND>
+template <int KIND, typename T = float>
 struct SweepInputs {
-  float s[4], z[4];
+  T s[4], z[4];
 
-  __device__ __forceinline__ void load(const QSpec<float>& qs, int64_t b, int64_t m, int64_t n, int64_t i0,
+  __device__ __forceinline__ void load(const QSpec<T>& qs, int64_t b, int64_t m, int64_t n, int64_t i0,
                                        int64_t j0) {
     const int tid = threadIdx.x, r = tid >> 3, part = tid & 7;
     int cs[4];
     slot_columns(r, part, cs);
     const int rows_in = m - i0 < TR ? (int)(m - i0) : TR, cols_in = n - j0 < TR ? (int)(n - j0) : TR;
     const int64_t corner = i0 * n + j0;
-    const float* st = KIND != Q_ROUND ? qs.scale + qs.smap.offset(b) + corner : nullptr;
-    const float* zt = KIND == Q_AFFINE ? qs.zp + qs.zmap.offset(b) + corner : nullptr;
+    const T* st = KIND != Q_ROUND ? qs.scale + qs.smap.offset(b) + corner : nullptr;
+    const T* zt = KIND == Q_AFFINE ? qs.zp + qs.zmap.offset(b) + corner : nullptr;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const bool in = r < rows_in && cs[j] < cols_in;
       const int off = r * (int)n + cs[j];
-      s[j] = z[j] = 0.f;
+      s[j] = z[j] = T(0);
       if constexpr (KIND == Q_AFFINE) {
-        s[j] = in ? st[off] : 1.f;
-        z[j] = in ? zt[off] : 0.f;
+        s[j] = in ? st[off] : T(1);
+        z[j] = in ? zt[off] : T(0);
       } else if constexpr (KIND == Q_FORCED) {
-        s[j] = in ? st[off] : 0.f;
+        s[j] = in ? st[off] : T(0);
       }
     }
   }
@@ -519,10 +415,10 @@ struct SweepInputs {
 // The step is bound by its chain (the quantizer's ~13 dependent operations, the LDS write, barrier
 // and read-back, ~150 clocks measured for the exchange alone) and by the LDS reads of four waves
 // (13 per lane); the image pitches keep every read free of bank conflicts.
-template <int KIND, bool YPRE>
-__device__ __forceinline__ void sweep_tile(TileLds& tl, const SweepInputs<KIND>& in, float* __restrict__ y,
-                                           float* __restrict__ c, float* __restrict__ e, const QSpec<float>& qs,
-                                           int64_t m, int64_t n, int64_t i0, int64_t j0, int64_t mat) {
+template <int KIND, bool YPRE, typename T>
+__device__ __forceinline__ void sweep_tile(TileLdsT<T>& tl, const SweepInputs<KIND, T>& in, T* __restrict__ y,
+                                           T* __restrict__ c, T* __restrict__ e, const QSpec<T>& qs, int64_t m,
+                                           int64_t n, int64_t i0, int64_t j0, int64_t mat) {
   const int tid = threadIdx.x;
   const int r = tid >> 3, part = tid & 7;
   const int rows_in = m - i0 < TR ? (int)(m - i0) : TR;  // tile rows / columns inside the matrix
@@ -534,7 +430,7 @@ __device__ __forceinline__ void sweep_tile(TileLds& tl, const SweepInputs<KIND>&
   // Y, so that their rounding errors scale with the feedback, not with Y), the error E, the
   // quantizer inputs S, Z and the reciprocal R of S, and the step at which the entry is rounded (-1
   // for entries outside the matrix)
-  float Y[4], C[4], D[4], F[4], E[4], S[4], Z[4], R[4];
+  T Y[4], C[4], D[4], F[4], E[4], S[4], Z[4], R[4];
   int tr[4];
   bool s_ok[4];
   const bool qmin_le_qmax = qs.qmin <= qs.qmax;
@@ -543,30 +439,36 @@ __device__ __forceinline__ void sweep_tile(TileLds& tl, const SweepInputs<KIND>&
     tr[j] = row_in && cs[j] < cols_in ? r + cs[j] : -1;
     Y[j] = tl.Ys[r][cs[j]];
     C[j] = tl.Cs[r][TR + cs[j]];
-    D[j] = F[j] = E[j] = 0.f;
+    D[j] = F[j] = E[j] = T(0);
     S[j] = in.s[j];
     Z[j] = in.z[j];
-    R[j] = 0.f;
+    R[j] = T(0);
     s_ok[j] = false;
     if constexpr (KIND == Q_AFFINE) {
-      R[j] = 1.f / S[j];
-      const float as = __builtin_fabsf(S[j]);
-      s_ok[j] = as >= 0x1p-60f && as <= 0x1p60f && Z[j] == Z[j] && qmin_le_qmax;
+      R[j] = T(1) / S[j];
+      T as;
+      if constexpr (sizeof(T) == 4)
+        as = __builtin_fabsf(S[j]);
+      else
+        as = __builtin_fabs(S[j]);
+      // the range in which the quotient from the reciprocal is the IEEE one (quantize_entry_rcp)
+      constexpr T s_lo = sizeof(T) == 4 ? T(0x1p-60) : T(0x1p-500), s_hi = sizeof(T) == 4 ? T(0x1p60) : T(0x1p500);
+      s_ok[j] = as >= s_lo && as <= s_hi && Z[j] == Z[j] && qmin_le_qmax;
     }
   }
-  float* ypre_row = YPRE ? qs.ypre + mat + (i0 + r) * n + j0 : nullptr;
+  T* ypre_row = YPRE ? qs.ypre + mat + (i0 + r) * n + j0 : nullptr;
   // clamp bounds pinned in registers (an empty asm makes them opaque): otherwise the compiler
   // re-reads them from the kernel arguments on every step
-  float qmin = qs.qmin, qmax = qs.qmax;
+  T qmin = qs.qmin, qmax = qs.qmax;
   asm volatile("" : "+v"(qmin), "+v"(qmax));
   // what a thread reads and writes at step t, as pointers plus t or t times the row pitch (immediate
   // offsets): the C of its row's rounded entry C[r, t - r] (which the rounding lane writes), that
   // lane's E[r, t - r], and per slot the source E[t - c, c] and the coefficients L[r, t - c], U[t - r, c]
-  float* const cp = &tl.Cs[r][TR] - r;
-  float* const ewp = &tl.Es[TR + r][0] - r;
-  const float* ep[4];
-  const float* lp[4];
-  const float* up[4];
+  T* const cp = &tl.Cs[r][TR] - r;
+  T* const ewp = &tl.Es[TR + r][0] - r;
+  const T* ep[4];
+  const T* lp[4];
+  const T* up[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     ep[j] = &tl.Es[TR][0] + (cs[j] - cs[j] * SP);
@@ -577,7 +479,7 @@ __device__ __forceinline__ void sweep_tile(TileLds& tl, const SweepInputs<KIND>&
   // L and U coefficients of step t in LV[t & 1], UV[t & 1], read a step ahead (they do not depend on
   // the sweep), so that only the published errors and C are read between the barrier and the
   // feedback update, and no register copies are needed in the unrolled loop
-  float LV[2][4], UV[2][4];
+  T LV[2][4], UV[2][4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     LV[0][j] = lp[j][0];
@@ -590,13 +492,13 @@ __device__ __forceinline__ void sweep_tile(TileLds& tl, const SweepInputs<KIND>&
     constexpr int cur = t & 1, ka = (t >> 3) & 3;
     // every lane evaluates its step's register; only the rounding lanes keep and publish it
     const bool rnd = tr[ka] == t;
-    const float yv = (Y[ka] + D[ka]) + F[ka];
+    const T yv = (Y[ka] + D[ka]) + F[ka];
     {
       bool exact;
-      float z = quantize_entry_rcp<KIND>(yv, S[ka], Z[ka], R[ka], s_ok[ka], qmin, qmax, exact);
-      float ev = z - yv;
-      const float cd = C[ka] + D[ka];
-      float cf = cd + ev;
+      T z = quantize_entry_rcp<KIND>(yv, S[ka], Z[ka], R[ka], s_ok[ka], qmin, qmax, exact);
+      T ev = z - yv;
+      const T cd = C[ka] + D[ka];
+      T cf = cd + ev;
       if (rnd) {
         // published at once; a lane whose quotient needs the division writes again (same address:
         // the later write stands), behind a branch taken only when some lane of the wave needs it
@@ -626,8 +528,8 @@ __device__ __forceinline__ void sweep_tile(TileLds& tl, const SweepInputs<KIND>&
       return;  // nothing left to receive feedback
     }
     __syncthreads();  // every wave's writes of this step before any wave's reads
-    const float cr = cp[t];
-    float ev[4];
+    const T cr = cp[t];
+    T ev[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) ev[j] = ep[j][t * SP];
     if constexpr (t + 1 < STEPS - 1) {
@@ -654,9 +556,9 @@ __device__ __forceinline__ void sweep_tile(TileLds& tl, const SweepInputs<KIND>&
 #pragma unroll
   for (int j = 0; j < 4; ++j) tl.Ys[r][cs[j]] = Y[j];
   __syncthreads();
-  float* yt = y + mat + i0 * n + j0;
-  float* ct = c + mat + i0 * n + j0;
-  float* et = e + mat + i0 * n + j0;
+  T* yt = y + mat + i0 * n + j0;
+  T* ct = c + mat + i0 * n + j0;
+  T* et = e + mat + i0 * n + j0;
   for (int t = tid; t < TR * TR; t += NTHREADS) {
     const int rr = t / TR, cc = t % TR;
     if (rr < rows_in && cc < cols_in) {
@@ -681,47 +583,50 @@ __device__ __forceinline__ void pulled_sums(const float (*red)[2][TR][TR + 1], i
 // depend on it): entry q of this thread is (t / TR, t % TR) with t = threadIdx.x + NTHREADS q.
 // ROWS: the tile image of the row-super-entry sweep (1 x TR super-entries): no U block (identity by the
 // super-entry convention, never read), no padding and no E image.
-template <bool ROWS>
+template <bool ROWS, typename T = float>
 struct TileRegs {
   static constexpr int NQ = TR * TR / NTHREADS;
-  float y[NQ], c[NQ], l[NQ], u[NQ];
+  T y[NQ], c[NQ], l[NQ], u[NQ];
 
-  __device__ __forceinline__ void load(const float* __restrict__ yg, const float* __restrict__ cg,
-                                       const float* __restrict__ lb, const float* __restrict__ ub, int64_t m,
+  __device__ __forceinline__ void load(const T* __restrict__ yg, const T* __restrict__ cg,
+                                       const T* __restrict__ lb, const T* __restrict__ ub, int64_t m,
                                        int64_t n, int64_t i0, int64_t j0, int64_t mat) {
     // the tile's corner in every operand (64-bit arithmetic once, uniform), then 32-bit offsets in
     // the tile (32 rows of at most 2^26 elements)
     const int rows_in = m - i0 < TR ? (int)(m - i0) : TR, cols_in = n - j0 < TR ? (int)(n - j0) : TR;
     const int ni = (int)n, mi = (int)m;
     const int64_t corner = i0 * n + j0;
-    const float* yt = yg + mat + corner;
-    const float* ct = cg + mat + corner;
-    const float* lt = lb + i0 * m + i0;  // L[i0 + r, i0 + cc] at r m + cc
-    const float* ut = ub + j0 * n + j0;  // U[j0 + r, j0 + cc] at r n + cc
+    const T* yt = yg + mat + corner;
+    const T* ct = cg + mat + corner;
+    const T* lt = lb + i0 * m + i0;  // L[i0 + r, i0 + cc] at r m + cc
+    const T* ut = ub + j0 * n + j0;  // U[j0 + r, j0 + cc] at r n + cc
 #pragma unroll
     for (int q = 0; q < NQ; ++q) {
       const int t = threadIdx.x + NTHREADS * q;
       const int r = t / TR, cc = t % TR;
       const bool in = r < rows_in && cc < cols_in;
       const int off = r * ni + cc;
-      y[q] = in ? yt[off] : 0.f;
-      c[q] = in ? ct[off] : 0.f;
+      y[q] = in ? yt[off] : T(0);
+      c[q] = in ? ct[off] : T(0);
       // L[i0+r, i0+cc] strictly below the diagonal; U[j0+r, j0+cc] strictly above it
-      l[q] = (cc < r && r < rows_in) ? lt[r * mi + cc] : 0.f;
-      u[q] = (!ROWS && r < cc && cc < cols_in) ? ut[off] : 0.f;
+      l[q] = (cc < r && r < rows_in) ? lt[r * mi + cc] : T(0);
+      u[q] = (!ROWS && r < cc && cc < cols_in) ? ut[off] : T(0);
     }
   }
 
   // LDS image of the tile with the pulled feedback D (down) and R (right) added: C + D, Y + (D + R),
   // the zero padding of the diagonal blocks and of the C image, and the zeroed E image.  red holds
-  // the waves' partial sums when `pulled` (pulled_sums: the first wd waves' are D's).
-  __device__ __forceinline__ void store(TileLds& tl, const float (*red)[2][TR][TR + 1], bool pulled, int wd) const {
+  // the waves' partial sums when `pulled` (pulled_sums: the first wd waves' are D's; fp32 only).
+  __device__ __forceinline__ void store(TileLdsT<T>& tl, const float (*red)[2][TR][TR + 1], bool pulled,
+                                        int wd) const {
 #pragma unroll
     for (int q = 0; q < NQ; ++q) {
       const int t = threadIdx.x + NTHREADS * q;
       const int r = t / TR, cc = t % TR;
-      float dd = 0.f, rr = 0.f;
-      if (pulled) pulled_sums(red, wd, r, cc, dd, rr);
+      T dd = T(0), rr = T(0);
+      if constexpr (sizeof(T) == 4) {
+        if (pulled) pulled_sums(red, wd, r, cc, dd, rr);
+      }
       tl.Ys[r][cc] = y[q] + (dd + rr);
       tl.Cs[r][TR + cc] = c[q] + dd;
       tl.Lp[r][TR + cc] = l[q];
@@ -736,25 +641,25 @@ struct TileRegs {
 #pragma unroll
       for (int i = 0; i < 9; ++i) {
         const int k = sub + 8 * i;
-        if (k < LPW - TR) tl.Lp[r][k < TR ? k : k + TR] = 0.f;
-        if (k < CPW - TR) tl.Cs[r][k < TR ? k : k + TR] = 0.f;
+        if (k < LPW - TR) tl.Lp[r][k < TR ? k : k + TR] = T(0);
+        if (k < CPW - TR) tl.Cs[r][k < TR ? k : k + TR] = T(0);
       }
       const int row = threadIdx.x >> 2, sub4 = threadIdx.x & 3;
-      float* up_row = tl.Up[row < TR ? row : row + TR];
+      T* up_row = tl.Up[row < TR ? row : row + TR];
 #pragma unroll
       for (int i = 0; i < 10; ++i) {
         const int col = sub4 + 4 * i;
-        if (col < UPW) up_row[col] = 0.f;
+        if (col < UPW) up_row[col] = T(0);
       }
     }
     // the E image: all zeros (read times zero coefficients before the entries' errors are written)
     {
-      float* es = &tl.Es[0][0];
+      T* es = &tl.Es[0][0];
       constexpr int EN = EROWS * SP;
 #pragma unroll
       for (int i = 0; i < (EN + NTHREADS - 1) / NTHREADS; ++i) {
         const int k = threadIdx.x + NTHREADS * i;
-        if (k < EN) es[k] = 0.f;
+        if (k < EN) es[k] = T(0);
       }
     }
   }
@@ -875,6 +780,45 @@ __global__ __launch_bounds__(NTHREADS, 2) void tile_stage_kernel(float* __restri
     sweep_tile<KIND, YPRE>(tl, qin, y, c, e, qs, m, n, i0, j0, mat);
 }
 
+// One launch per coarse stage of the fused fp64 sweep: each workgroup takes one tile of the stage, whose
+// feedback from all earlier tiles has been flushed into its Y and C (outer flushes, then the per-stage band
+// flushes inside an outer block), builds the fp32 sweep's LDS image of it in fp64 and runs the same push-form
+// sweep of its 63 antidiagonals (sweep_tile).  The image takes 122 KB of LDS: one workgroup per CU, at most
+// one per tile of the stage.
+template <int KIND, bool YPRE>
+__global__ __launch_bounds__(NTHREADS) void sweep_tile64_kernel(double* __restrict__ y, double* __restrict__ c,
+                                                                double* __restrict__ e, const double* __restrict__ l,
+                                                                const double* __restrict__ u, int64_t m, int64_t n,
+                                                                int64_t stage, int64_t tile_lo, BatchMap lmap,
+                                                                BatchMap umap, QSpec<double> qs, int64_t nx,
+                                                                int64_t ny) {
+  __shared__ TileLdsT<double> tl;
+  const GridIds id = grid_ids(nx, ny);
+  const int64_t b = id.b;
+  const int64_t I = tile_lo + id.x, J = stage - I;
+  const int64_t i0 = I * TR, j0 = J * TR;
+  const int64_t mat = b * m * n;
+  SweepInputs<KIND, double> in;
+  in.load(qs, b, m, n, i0, j0);
+  TileRegs<false, double> regs;
+  regs.load(y, c, l + lmap.offset(b), u + umap.offset(b), m, n, i0, j0, mat);
+  regs.store(tl, nullptr, false, 0);
+  __syncthreads();
+  sweep_tile<KIND, YPRE>(tl, in, y, c, e, qs, m, n, i0, j0, mat);
+}
+
+template <int KIND>
+void launch_tile64_k(dim3 grid, hipStream_t stream, double* y, double* c, double* e, const double* l, const double* u,
+                     int64_t m, int64_t n, int64_t st, int64_t lo, const BatchMap& lmap, const BatchMap& umap,
+                     const QSpec<double>& qs, int64_t nx, int64_t ny) {
+  if (qs.ypre)
+    hipLaunchKernelGGL((sweep_tile64_kernel<KIND, true>), grid, dim3(NTHREADS), 0, stream, y, c, e, l, u, m, n, st, lo,
+                       lmap, umap, qs, nx, ny);
+  else
+    hipLaunchKernelGGL((sweep_tile64_kernel<KIND, false>), grid, dim3(NTHREADS), 0, stream, y, c, e, l, u, m, n, st,
+                       lo, lmap, umap, qs, nx, ny);
+}
+
 template <bool VEC, int KIND, bool ROWS>
 void launch_tile_stage_k(dim3 grid, hipStream_t stream, float* y, float* c, float* e, const float* l, const float* u,
                          int64_t m, int64_t n, int64_t st, int64_t S0, int64_t lo, int64_t n_sweep, int64_t prep_lo,
@@ -935,8 +879,8 @@ int sweep_fused(T* y, T* c, T* e, const T* l, const T* u, int64_t m, int64_t n, 
   BatchMap lmap, umap;
   if (!make_batch_map(lmap, bnd, bshape, lstride) || !make_batch_map(umap, bnd, bshape, ustride)) return GPTQ2D_EINVAL;
   if (m <= 0 || n <= 0 || outer_tiles < 1) return GPTQ2D_EINVAL;
-  // the fp32 tile kernels index inside a tile with 32-bit offsets (32 rows of a row length < 2^26)
-  if (sizeof(T) == 4 && (m >= ((int64_t)1 << 26) || n >= ((int64_t)1 << 26))) return GPTQ2D_EUNSUPPORTED;
+  // the tile kernels index inside a tile with 32-bit offsets (32 rows of a row length < 2^26)
+  if (m >= ((int64_t)1 << 26) || n >= ((int64_t)1 << 26)) return GPTQ2D_EUNSUPPORTED;
   if (qkind != Q_ROUND && qkind != Q_AFFINE && qkind != Q_FORCED && !(rows && qkind == Q_ABSMAX)) return GPTQ2D_EINVAL;
   if ((qkind == Q_AFFINE && (!qa || !qb)) || (qkind == Q_FORCED && !qa)) return GPTQ2D_EINVAL;
   if (qkind == Q_ABSMAX && (!(qmin < qmax) || (dtype16 != 1 && dtype16 != 2))) return GPTQ2D_EINVAL;
@@ -1003,8 +947,13 @@ int sweep_fused(T* y, T* c, T* e, const T* l, const T* u, int64_t m, int64_t n, 
           else
             launch_rows_stage<T, Q_ROUND>(g.grid, stream, y, c, e, l, m, n, st, lo, lmap, qs, g.nx, g.ny);
         } else {
-          hipLaunchKernelGGL(sweep_tiles_kernel<T>, g.grid, dim3(NTHREADS), 0, stream, y, c, e, l, u, m, n, st, lo,
-                             lmap, umap, qs, g.nx, g.ny);
+          // the push-form sweep of the fp32 engine, in fp64
+          if (qkind == Q_AFFINE)
+            launch_tile64_k<Q_AFFINE>(g.grid, stream, y, c, e, l, u, m, n, st, lo, lmap, umap, qs, g.nx, g.ny);
+          else if (qkind == Q_FORCED)
+            launch_tile64_k<Q_FORCED>(g.grid, stream, y, c, e, l, u, m, n, st, lo, lmap, umap, qs, g.nx, g.ny);
+          else
+            launch_tile64_k<Q_ROUND>(g.grid, stream, y, c, e, l, u, m, n, st, lo, lmap, umap, qs, g.nx, g.ny);
         }
       }
       // work of a tile sweep: its entries (the in-tile feedback is latency-, not throughput-bound)
