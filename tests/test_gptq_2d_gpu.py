@@ -247,27 +247,30 @@ def test_fused_fp32_trajectory(m, n, outer):
 
 @pytest.mark.parametrize("last_zp", [0., float("nan"), float("inf"), float("-inf")])
 @pytest.mark.parametrize("qmin,qmax", [(-8., 7.), (0., 15.)])
-def test_fused_fp32_quantizer_special_values(qmin, qmax, last_zp):
-    """The fp32 fused sweep's affine quantizer on entries that leave its fast path (scales outside
-    [2^-60, 2^60] or negative, |y| outside the range where the reciprocal gives the IEEE quotient,
-    a NaN or infinite zero point; qmin > qmax is rejected by the API, as in the reference): with identity factors there is no feedback, so every
-    entry is quantized once, and the result must equal (clamp(round(y / s + z), qmin, qmax) - z) * s in
-    fp32 bit for bit.  A NaN or infinite zero point makes its entry's error NaN, which 0 x NaN would
-    carry to every later entry (as the reference's products would), so it sits on the last entry."""
-    print(f"fp32 quantizer special values qmin={qmin} qmax={qmax} last zp={last_zp}", flush=True)
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+def test_fused_quantizer_special_values(qmin, qmax, last_zp, dtype):
+    """The fused sweep's affine quantizer on entries that leave its fast path (scales outside
+    [2^-60, 2^60] in fp32, [2^-500, 2^500] in fp64, or negative; |y| outside the range where the reciprocal
+    gives the IEEE quotient; a NaN or infinite zero point; qmin > qmax is rejected by the API, as in the
+    reference): with identity factors there is no feedback, so every entry is quantized once, and the result
+    must equal (clamp(round(y / s + z), qmin, qmax) - z) * s in the sweep's dtype bit for bit.  A NaN or
+    infinite zero point makes its entry's error NaN, which 0 x NaN would carry to every later entry (as the
+    reference's products would), so it sits on the last entry."""
+    print(f"{dtype} quantizer special values qmin={qmin} qmax={qmax} last zp={last_zp}", flush=True)
     m, n = 40, 70
     g = torch.Generator().manual_seed(5)
-    x = (3. * torch.randn(m, n, generator=g)).float()
-    s = (0.1 + torch.rand(m, n, generator=g)).float()
-    z = torch.randint(-2, 3, (m, n), generator=g).float()
-    s[0, :10] = 1e-30
-    s[1, :10] = 1e30
+    x = (3. * torch.randn(m, n, generator=g)).to(dtype)
+    s = (0.1 + torch.rand(m, n, generator=g)).to(dtype)
+    z = torch.randint(-2, 3, (m, n), generator=g).to(dtype)
+    big, tiny = (1e30, 1e-30) if dtype == torch.float32 else (1e200, 1e-200)
+    s[0, :10] = tiny
+    s[1, :10] = big
     s[2, :10] = -0.5
-    x[5, :10] = 1e25
-    x[6, :10] = 1e-25
+    x[5, :10] = 1e25 if dtype == torch.float32 else 1e180
+    x[6, :10] = 1e-25 if dtype == torch.float32 else 1e-180
     x[7, :10] = 0.
     z[m - 1, n - 1] = last_zp
-    eye_m, eye_n = torch.eye(m), torch.eye(n)
+    eye_m, eye_n = torch.eye(m, dtype=dtype), torch.eye(n, dtype=dtype)
     quant = functools.partial(QI.affine_quantizer_hip, qmin=qmin, qmax=qmax)
     got = G.gptq_2d(x.to(DEV), eye_m.to(DEV), eye_n.to(DEV), quantizer=quant,
                     quantizer_inputs=(s.to(DEV), z.to(DEV))).cpu()
