@@ -42,7 +42,7 @@ extern "C" {
    * rounded.  c, e: [B,m,n] scratch.  Stages of tiles [stage_begin, stage_end) (-1: to the end),     \
    * outer_tiles tile stages per outer block; both ends on outer-block boundaries (or stage_end at   \
    * the end of the sweep), else GPTQ2D_EINVAL; a later call resumes from the same y, c, e.  y is    \
-   * updated in place. */                                                                              \
+   * updated in place.  m or n of 2^26 or more: GPTQ2D_EUNSUPPORTED (32-bit offsets inside a tile). */ \
   int gptq2d_sweep_fused_##SUF(T* y, T* c, T* e, const T* l, const T* u, int64_t m, int64_t n, int32_t bnd,         \
                                const int64_t* bshape, const int64_t* l_stride, const int64_t* u_stride,             \
                                int32_t qkind, const T* qa, const int64_t* qa_stride, const T* qb,                   \
