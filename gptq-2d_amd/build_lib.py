@@ -37,13 +37,17 @@ COMMON_FLAGS = [
 LINK_LIBS: list[str] = []
 
 # Per-file extra flags.  The trellis search must not contract a*b+c into fma: its costs are
-# compared for exact ties and must equal the reference's unfused sums.  The strided GEMMs keep their
-# MFMA accumulators in VGPRs: by default the compiler put those of the register-staged kernels (fp64,
-# fp32 without 128-bit staging) in AGPRs and copied all of them out and back around every k-block
-# (64 and 192 v_accvgpr moves per k-block, the read-out waiting for the MFMA chain).
+# compared for exact ties and must equal the reference's unfused sums.  The register-staged MFMA kernels
+# (the strided GEMMs, the cell-masked block flush, the fp32 strip Cholesky panel) keep their accumulators
+# in VGPRs: by default the compiler put them in AGPRs and copied all of them out and back around every
+# k-block (64 to 192 v_accvgpr moves, the read-out waiting for the MFMA chain).  In these files the flag
+# changes no other kernel's code.
+VGPR_MFMA = ["-mllvm", "-amdgpu-mfma-vgpr-form"]
 EXTRA_FLAGS = {
     "viterbi.hip": ["-ffp-contract=off"],
-    "gemm.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+    "gemm.hip": VGPR_MFMA,
+    "flush.hip": VGPR_MFMA,
+    "ldl.hip": VGPR_MFMA,
 }
 
 
