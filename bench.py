@@ -278,8 +278,8 @@ def _config_lines(torch, dev, h_layer, names, steps=2):
 
 
 def _h64_line(torch, x, a, b, steps, lines, line):
-    """The headline layer in fp64 end to end: fp64 LDLs (VALU GEMMs) and the fused fp64 sweep (tile sweep on
-    VALU, flushes on fp64 MFMA)."""
+    """The headline layer in fp64 end to end: the fp64 factors (strip Cholesky and inverse products on the fp64
+    MFMA GEMM) and the fused fp64 sweep (push-form in-tile sweeps on VALU, flushes on fp64 MFMA)."""
     import gptq_2d as G
     import gptq_2d_ldl as LDL
     import instances

@@ -24,12 +24,11 @@
 //   3. ldl_of_inverse only: C^{-1} in place by recursive doubling.  Diagonal NB blocks are inverted
 //      by one wave each; then for s = NB, 2 NB, ... every pair of inverted s-blocks A^{-1}, D^{-1}
 //      with off-diagonal block B becomes one inverted 2s-block through -D^{-1} (B A^{-1}) -- two
-//      triangular GEMMs per level, all pairs of a level in one batched launch.  For fp32 and
-//      k >= 512 these are rocBLAS's strided-batched sgemm (a plain library GEMM: dense, on
-//      triangles padded with the zeros of W's cleared upper triangle; at k = 8192 that is twice the
-//      triangular flops at ~130 TFLOP/s, against ~40 TFLOP/s for the triangular MFMA kernel of
-//      gemm.hip), with the unused part of the output buffer as the GEMM's workspace; the rocBLAS
-//      handle of a device and host thread is created on first use.
+//      triangular GEMMs per level, all pairs of a level in one batched launch.  For fp32 with
+//      16-byte aligned rows they run on the triangular MFMA GEMM of trmm_mfma.hip (each block's
+//      k loop restricted to the k-tiles that meet the triangular operand's non-zero part), otherwise
+//      on the strided GEMM of gemm.hip; the unused part of the output buffer holds the products.
+//      No vendor library is called.
 //   4. Normalisation into L (LDS-tiled transposed read for ldl_of_inverse).
 //
 // A non-positive (or NaN) pivot records its 1-based column in `info` (device int, 0 when the
@@ -922,9 +921,13 @@ __global__ __launch_bounds__(256, 2) void panel_step_kernel(PanelGroup grp, int6
 
 // Launch sequence of the blocked Cholesky of W (k x k) in place over the panels [col_begin, col_end)
 // (multiples of PB; col_end < 0: to the end), one panel per step() so that one host thread can
-// interleave two factorisations on two streams.  Between runs (and after finish()), every earlier
-// panel's update has been applied to the whole trailing matrix and every factored diagonal block
-// is in W.  stage: PB x PB elements of scratch (a panel's factored diagonal block between its
+// interleave two factorisations on two streams.  Between runs (and after finish()) every factored
+// diagonal block is in W.  Two-level fp32 path: every earlier panel's update has been applied to the
+// whole trailing matrix (finish() issues a pending one).  Plain path (fp64, fp32 with k % 4 != 0): the
+// panels of the strip [j0 / NS * NS, j0) have updated nothing to their right yet -- a later panel of the
+// strip takes them by its left-looking update and the strip's end by its rank-NS update, both reading
+// W[:, strip start : j0] -- so ranges must be run in column order, as the single call runs them, and
+// then issue the single call's launches in its order.  stage: PB x PB elements of scratch (a panel's factored diagonal block between its
 // launch and the next).  twin() (two-level path only): up to GROUP_MAX - 1 more k x k matrices factored
 // by the same launches, as blockIdx.y = 1, 2, ... of each -- one chain of latency-bound panel launches for
 // all, and the work of all in each throughput-bound update; each matrix sees the launches it would see

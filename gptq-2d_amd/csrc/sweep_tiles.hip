@@ -61,6 +61,24 @@ __device__ __forceinline__ void static_for(F& f, std::integer_sequence<int, I...
   (f(std::integral_constant<int, I>{}), ...);
 }
 
+// The affine quantizer (clamp(round(y / s + z), qmin, qmax) - z) s by IEEE division, the dequantized value
+// rounded on its own (as the reference's plug-in writes it), so that a caller's error z - y is exactly that
+// difference: no contraction of the product into the caller's subtraction.
+template <typename T>
+__device__ __forceinline__ T quantize_entry_div(T yv, T sv, T zv, T qmin, T qmax) {
+#pragma clang fp contract(off)
+  const T code = clamp_val(round_even(yv / sv + zv), qmin, qmax);
+  return (code - zv) * sv;
+}
+
+// The abs-max quantizer clamp(round(y / s), qmin, qmax) s of quantizer_int.py:134 (the product is exact for
+// a 16-bit scale and a small code, and rounded on its own in any case).
+template <typename T>
+__device__ __forceinline__ T quantize_absmax_entry(T yv, T sv, T qmin, T qmax) {
+#pragma clang fp contract(off)
+  return clamp_val(round_even(yv / sv), qmin, qmax) * sv;
+}
+
 // ------------------------------------------------------------------------------------------------ 1 x TR super-entries
 //
 // With super-entries of one row and TR columns (gptq_2d_super_entry with super_entry_shape (1, TR), e.g. the
@@ -140,9 +158,10 @@ __device__ __forceinline__ void sweep_rows(const T* ys, int ysp, const T* cs, in
       const T amax = halfwave_max(a);
       sc = round_scale16(amax / half, qs.dtype16);
       sc = sc == T(0) ? T(1) : sc;
-      z = clamp_val(round_even(yv / sc), qmin, qmax) * sc;
+      z = quantize_absmax_entry(yv, sc, qmin, qmax);
     } else if constexpr (KIND == Q_AFFINE) {
-      z = (clamp_val(round_even(yv / in.s[slot] + in.z[slot]), qmin, qmax) - in.z[slot]) * in.s[slot];
+      // the dequantized value rounded on its own, before the error z - y (no contraction into it)
+      z = quantize_entry_div(yv, in.s[slot], in.z[slot], qmin, qmax);
     } else if constexpr (KIND == Q_FORCED) {
       z = in.s[slot];
     } else {
@@ -355,12 +374,6 @@ __device__ __forceinline__ T quantize_entry_rcp(T yv, T sv, T zv, T rv, bool s_o
   }
 }
 
-template <typename T>
-__device__ __forceinline__ T quantize_entry_div(T yv, T sv, T zv, T qmin, T qmax) {
-#pragma clang fp contract(off)
-  const T code = clamp_val(round_even(yv / sv + zv), qmin, qmax);
-  return (code - zv) * sv;
-}
 
 // Thread ownership of the in-tile sweep.  Thread (r, part) = (tid / 8, tid % 8) owns the four entries
 // (r, c) of its row with (c + r) % 8 == part; slot j holds the one whose antidiagonal t_e = r + c has

@@ -7,9 +7,13 @@ dtype.
 
 Pinned by: tests/test_oracle_quantize.py -- the reference's known answers
 (quantizer_int.py:476-488, 532-533), the closed form checked entry by entry in
-Python ``fractions`` arithmetic, round-half-to-even ties, a zero row (scale 1)
-and a denormal scale, and the bf16/fp16 scale rounding checked against an
-independent bit-level round-to-nearest-even restatement.
+Python float arithmetic, round-half-to-even ties, a zero row (scale 1) and a
+denormal scale, the bf16/fp16 scale rounding checked against an independent
+bit-level round-to-nearest-even restatement, and the abs-max quantizer against
+vectors the reference's ``int_abs_max_quantizer_torch`` wrote on the cases of
+its own test (quantizer_int.py:535-553, ``tests/golden/absmax.npz``) with rows
+of exact ties; planted floor, trunc and half-away-from-zero rounding fail
+those checks.
 """
 
 from __future__ import annotations
@@ -21,9 +25,14 @@ def _pick(flat, selection):
     return selection(flat) if callable(selection) else flat[..., selection]
 
 
+def _round_half_even(t):
+    """In place, to the nearest integer, ties to even (torch.round, as every reference quantizer rounds)."""
+    return t.round_()
+
+
 def round_quantizer(y_flat, selection, *, out):
     """Round half to even into ``out`` (quantizer_int.py:18-35, both variants)."""
-    torch.round(_pick(y_flat, selection), out=out)
+    _round_half_even(out.copy_(_pick(y_flat, selection)))
 
 
 def affine_quantizer(y_flat, selection, scale, zero_point, *, out, qmin=-float("inf"), qmax=float("inf")):
@@ -37,7 +46,7 @@ def affine_quantizer(y_flat, selection, scale, zero_point, *, out, qmin=-float("
     s = _pick(scale.flatten(-2), selection)
     zp = _pick(zero_point.flatten(-2), selection)
     torch.div(y, s, out=out)
-    out.add_(zp).round_().clamp_(qmin, qmax)
+    _round_half_even(out.add_(zp)).clamp_(qmin, qmax)
     out.sub_(zp).mul_(s)
 
 
@@ -52,4 +61,4 @@ def int_abs_max_quantizer(y_flat, select, *, out, qmin, qmax, dtype):
     """Per-row abs-max INT quantizer of super-entries from current values (quantizer_int.py:120-134)."""
     x = select(y_flat)
     s = int_abs_max_scale(x, qmin=qmin, qmax=qmax, dtype=dtype)
-    torch.div(x, s, out=out).round_().clamp_(qmin, qmax).mul_(s)
+    _round_half_even(torch.div(x, s, out=out)).clamp_(qmin, qmax).mul_(s)

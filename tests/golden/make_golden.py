@@ -12,6 +12,13 @@ force pins:
                    tables, and Viterbi states/values of ``_trellis_quantize_torch`` on seeded sequences,
                    including HYB L=16 K=2 V=2 T=256 with and without tail-biting.
 * scales.npz    -- ``int_abs_max_scale_torch`` on rows with zeros and denormal scales, bf16 and fp16.
+* absmax.npz    -- ``int_abs_max_quantizer_torch`` on the cases of the reference's own test
+                   (quantizer_int.py:535-553): the 1 x 32 and 2 x 24 selectors, (qmin, qmax) in
+                   {(-2, 1), (-4, 3), (-8, 7), (-128, 127)}, fp16 and bf16 scales, a zero row and a
+                   1e-38 row (denormal or vanishing scale), in fp32 and fp64, with a CPU generator;
+                   plus rows built so that every entry is an exact tie k + 1/2 of its scale for each
+                   (qmin, qmax), and a 48 x 96 matrix quantized as 1 x 32 super-entries (the input of
+                   the fused row sweep's check).
 
 Run from the repository root: ``python tests/golden/make_golden.py``.  The reference never
 travels to the GPU box; only these data files do.
@@ -128,8 +135,80 @@ def scales():
     print(f"scales: {len(data)} arrays")
 
 
+ABSMAX_PAIRS = ((-2, 1), (-4, 3), (-8, 7), (-128, 127))
+# the two selectors of quantizer_int.py:545-548 on a [*, 64 * 96] flat matrix: the 1 x 32 super-entries
+# (i, j), i + j = 2, and the 2 x 24 super-entries (i, j), i + j = 2
+ABSMAX_SELECTORS = {
+    "r1x32": lambda t: t[..., 64:224].unfold(-1, 32, 64).unflatten(-1, (1, 32)),
+    "r2x24": lambda t: t[..., 48:552].unfold(-1, 120, 168).unfold(-1, 24, 96),
+}
+
+
+def _name(dtype):
+    return str(dtype).split(".")[-1]
+
+
+def _tie_rows(g, count, width, dtype):
+    """Rows of exact ties for each (qmin, qmax): entries (k + 1/2) / 4 with k in [qmin, qmax - 1], one
+    entry per row set to +-(qmax - qmin) / 8, so that the abs-max scale is exactly 1/4 (in fp16 and bf16)
+    and every quotient y / scale is k + 1/2."""
+    rows = []
+    for qmin, qmax in ABSMAX_PAIRS:
+        k = torch.randint(qmin, qmax, (count, width), generator=g).to(dtype)
+        r = (k + .5) / 4
+        r[:, 0] = (qmax - qmin) / 8 * torch.where(torch.rand(count, generator=g) < .5, -1., 1.).to(dtype)
+        rows.append(r)
+    return rows
+
+
+def absmax():
+    """int_abs_max_quantizer_torch on the reference test's cases (quantizer_int.py:535-553)."""
+    g = torch.Generator().manual_seed(5)
+    data = {}
+    for xd in (torch.float32, torch.float64):
+        y = 4. * torch.randn(2 + len(ABSMAX_PAIRS), 64 * 96, generator=g, dtype=xd)
+        y[1, 128:168] = 0.
+        y[0, 192:224] *= 1e-38  # a scale so small that it is denormal (bf16) or vanishes (fp16)
+        # batch rows 2.. : exact ties in every super-entry row either selector reads
+        ties = _tie_rows(g, 1, 64 * 96, xd)
+        for i, r in enumerate(ties):
+            for lo in (64, 128, 192, 48, 144, 216, 312, 384, 480):
+                r[0, lo] = r[0, 0]  # the abs-max entry at the head of each selected row
+            y[2 + i] = r[0]
+        data[f"{_name(xd)}_y"] = y.numpy()
+        for name, select in ABSMAX_SELECTORS.items():
+            x = select(y)
+            for qmin, qmax in ABSMAX_PAIRS:
+                for sd in (torch.float16, torch.bfloat16):
+                    out = torch.empty_like(x)
+                    ref_qi.int_abs_max_quantizer_torch(y, select, out=out, qmin=qmin, qmax=qmax, dtype=sd)
+                    data[f"{_name(xd)}_{name}_{_name(sd)}_{qmin}_{qmax}"] = out.numpy()
+        # a 48 x 96 matrix as 1 x 32 super-entries: random rows, a zero row, a 1e-38 row, tie rows
+        mat = 4. * torch.randn(48, 96, generator=g, dtype=xd)
+        mat[3] = 0.
+        mat[5] *= 1e-38
+        for i, r in enumerate(_tie_rows(g, 6, 96, xd)):
+            r[:, 32] = r[:, 0]
+            r[:, 64] = r[:, 0]
+            mat[8 + 6 * i: 14 + 6 * i] = r
+        data[f"{_name(xd)}_mat"] = mat.numpy()
+        select = lambda t: t.unflatten(-1, (48 * 3, 1, 32))
+        for qmin, qmax in ABSMAX_PAIRS:
+            for sd in (torch.float16, torch.bfloat16):
+                out = torch.empty(48 * 3, 1, 32, dtype=xd)
+                ref_qi.int_abs_max_quantizer_torch(mat.flatten(), select, out=out, qmin=qmin, qmax=qmax, dtype=sd)
+                data[f"{_name(xd)}_mat_{_name(sd)}_{qmin}_{qmax}"] = out.reshape(48, 96).numpy()
+    np.savez_compressed(OUT / "absmax.npz", **data)
+    print(f"absmax: {len(data)} arrays")
+
+
 if __name__ == "__main__":
     torch.set_num_threads(8)
+    if sys.argv[1:]:  # only the named sets
+        for name in sys.argv[1:]:
+            globals()[name]()
+        sys.exit(0)
+    absmax()
     scales()
     trellis()
     c1()

@@ -5,10 +5,11 @@ outer blocks) and are checked against the CPU oracle run over the whole sweep.  
 given the oracle's codes), the engine's own Y before rounding gives the oracle's code in >= 99.99% of the
 entries and every mismatch is a near-tie |frac - 0.5| < 1e-5 (code units) or an entry where the engine
 rounds as the fp64 trajectory of the same forced codes does (the reference path's fp32 sums, not the
-engine's, crossed the rounding boundary); free running, the objective
-tr(R^T A R B) is within 1e-4 relative and the codes agree at least as well as the reference's own path
-agrees with itself under a change of summation order (see test_full_size_layer).  The reduced-size tests
-run the reference's whole algorithm in fp64, where the codes must be equal.
+engine's, crossed the rounding boundary; at most 1e-6 of the entries); free running, the objective
+tr(R^T A R B) is within 1e-4 relative of the oracle's and of its fp64 run's, and the engine's codes agree
+with the oracle's fp64 trajectory at least as well as the oracle's fp32 codes do (see
+test_full_size_layer).  The reduced-size tests run the reference's whole algorithm in fp64, where the
+codes must be equal.
 
 Factors here are Wishart-like as in the benchmark definition, F = G diag(i^-alpha) G^T / (4k) +
 1e-2 I, but G is drawn with torch's GPU generator (the numpy PCG64 draws of the benchmark's
@@ -128,11 +129,14 @@ def test_full_size_layer(name):
           f"|frac - 0.5| >= 1e-5), max |dY| {dev.max():.2e} code units (median {dev.median():.2e}), largest "
           f"mismatch |frac - 0.5| {float(frac[mism].max()) if mism.any() else 0.:.2e}", flush=True)
     assert tf_agree >= 0.9999
+    # far mismatches are rare: at most 1e-6 of the entries
+    assert int(far.sum()) <= 1e-6 * m * n
     if far.any():
         # a mismatch farther from the rounding boundary than 1e-5 code units: the two fp32 trajectories (the
         # engine's and the reference path's) lie on either side of it.  The engine's fp64 run on the same forced
         # codes gives the trajectory both approximate; at every such entry the engine's code must be the fp64
-        # trajectory's (the reference path's fp32 sums crossed the boundary, not the engine's)
+        # trajectory's (the reference path's fp32 sums crossed the boundary, not the engine's), and the entry
+        # must lie within the reference path's own largest deviation from that trajectory of the boundary
         pre64 = torch.full(x.shape, float("nan"), dtype=torch.float64, device=DEV)
         G.gptq_2d(x.double(), lo.double(), up.double(), quantizer=QI.teacher_forced_quantizer,
                   quantizer_inputs=(st.y.to(DEV, torch.float64), pre64), outer_block_size=BENCH_OUTER)
@@ -142,31 +146,42 @@ def test_full_size_layer(name):
         print(f"  fp64 trajectory: max |Y_engine - Y_fp64| {err_e.max():.2e}, max |Y_oracle - Y_fp64| "
               f"{err_o.max():.2e} code units; at the {int(far.sum())} far mismatches the engine's code is the fp64 "
               f"code at {int((own[far] == code64[far]).sum())}, the oracle's at "
-              f"{int((ref_codes[far] == code64[far]).sum())}", flush=True)
+              f"{int((ref_codes[far] == code64[far]).sum())}; their largest |frac - 0.5| {frac[far].max():.2e}",
+              flush=True)
         assert (own[far] == code64[far]).all()
+        assert (frac[far].double() <= err_o.max()).all()
+        del pre64, y64, code64, err_e, err_o
     del pre_e, pre_o, ye, yo, own, frac, dev
 
     # free running.  A rounding sweep is chaotic in floating point: one near-tie decided the other way changes
     # that entry's error by a whole step, which moves every later entry, so two summation orders of the same
-    # algorithm part ways over a large layer.  The yardstick is the reference's own path run on the transposed
-    # layer (X^T with L' = U^T, U' = L^T: the same rounding in exact arithmetic, other fp32 sums): the engine
-    # must agree with the oracle at least as well as that, less 2 points, and its objective must be within
-    # 1e-4 relative of the oracle's.
-    stt = S.TorchSweepState(xc.t().contiguous(), up.cpu().t().contiguous(), lo.cpu().t().contiguous(),
-                            quantizer=functools.partial(OQ.affine_quantizer, qmin=cfg.qmin, qmax=cfg.qmax),
-                            quantizer_inputs=(sc.t().contiguous(), zc.t().contiguous()))
-    for s in range(stt.stages):
-        stt.run_stage(s)
-    zt = stt.y.t()
-    agree = float((codes.cpu() == ref_codes).double().mean())
-    agree_t = float((torch.round(zt / sc + zc) == ref_codes).double().mean())
+    # algorithm part ways over a large layer (the reference's own path run on the transposed layer -- the same
+    # rounding in exact arithmetic, other fp32 sums -- agrees with itself in 95.3% / 98.6% / 99.998% of the
+    # codes at C2 / H / C3).  The yardstick is the trajectory both fp32 runs approximate: the CPU oracle in
+    # fp64 on the same inputs.  The engine's free-running codes must agree with it at least as well as the
+    # reference path's fp32 codes (the oracle) do, and its objective must be within 1e-4 relative of the
+    # oracle's and of the fp64 trajectory's.
+    st64 = S.TorchSweepState(xc.double(), lo.cpu().double(), up.cpu().double(),
+                             quantizer=functools.partial(OQ.affine_quantizer, qmin=cfg.qmin, qmax=cfg.qmax),
+                             quantizer_inputs=(sc.double(), zc.double()))
+    t0 = time.perf_counter()
+    for s in range(st64.stages):
+        st64.run_stage(s)
+        if s % 4096 == 4095:
+            print(f"  fp64 oracle: {s + 1} / {st64.stages} stages, {time.perf_counter() - t0:.0f} s", flush=True)
+    codes64 = torch.round(st64.y / sc.double() + zc.double()).float()
+    ce = codes.cpu()
+    agree = float((ce == ref_codes).double().mean())
+    agree_e64 = float((ce == codes64).double().mean())
+    agree_o64 = float((ref_codes == codes64).double().mean())
     obj_o = _objective(st.y.to(DEV), x, a, b)
-    obj_t = _objective(zt.to(DEV), x, a, b)
-    rel, rel_t = abs(obj - obj_o) / obj_o, abs(obj_t - obj_o) / obj_o
-    print(f"  free running: engine vs oracle code agreement {agree:.6%}, objective rel {rel:.2e}; oracle on the "
-          f"transposed layer vs oracle {agree_t:.6%}, objective rel {rel_t:.2e}", flush=True)
-    assert agree >= min(0.9999, agree_t - 0.02)
-    assert rel <= 1e-4
+    obj_64 = _objective(st64.y.to(DEV), x, a, b)
+    rel, rel_64, rel_o64 = abs(obj - obj_o) / obj_o, abs(obj - obj_64) / obj_64, abs(obj_o - obj_64) / obj_64
+    print(f"  free running: codes agreeing with the fp64 trajectory: engine {agree_e64:.6%}, oracle {agree_o64:.6%}; "
+          f"engine vs oracle {agree:.6%}; objective rel engine-oracle {rel:.2e}, engine-fp64 {rel_64:.2e}, "
+          f"oracle-fp64 {rel_o64:.2e}", flush=True)
+    assert agree_e64 >= agree_o64
+    assert rel <= 1e-4 and rel_64 <= 1e-4
 
 
 @pytest.mark.timeout(900)
@@ -259,9 +274,12 @@ def test_c4_full_size():
     """C4: 8192^2 weights (the headline layer's distribution) in 16 x 16 super-entries under the HYB trellis code,
     L = 16, K = 2, V = 2, tail-biting, scale RMS(W) / (0.9 RMS(table)) (demo.ipynb:541-545), fp32 plug-in engine
     with the one-launch HIP search per stage.  Checks: bitwise determinism; every output pair is a row of the
-    code table times the scale; the objective is below quantizing each super-entry of W on its own; and on the
+    code table times the scale; the objective is below quantizing each super-entry of W on its own; on the
     first 4 coarse antidiagonals the values agree with the CPU oracle (super-entry Algorithm 3 with the PyTorch
-    search on the cropped layer, which holds every entry they depend on) in >= 99% of the entries."""
+    search on the cropped layer, which holds every entry they depend on) in >= 99% of the entries; and at 8
+    coarse antidiagonals sampled over the whole sweep (the longest, 512 super-entries, among them) the oracle's
+    trellis quantizer applied to the super-entries the engine's quantizer received writes the engine's values
+    bit for bit."""
     m = n = 8192
     print(f"C4: {m}x{n}, 16x16 super-entries, HYB L=16 K=2 V=2", flush=True)
     x = instances.weights(m, n, 0, True, False).float().to(DEV)
@@ -280,7 +298,22 @@ def test_c4_full_size():
     z = run()
     torch.cuda.synchronize()
     print(f"  layer sweep {time.perf_counter() - t0:.2f} s", flush=True)
-    assert run().equal(z), "not deterministic"
+    # a second run records, at sampled coarse antidiagonals, the super-entries the quantizer receives (the
+    # engine's own pre-rounding values) and what it writes
+    sampled = {0: None, 1: None, 100: None, 255: None, 511: None, 700: None, 1000: None, 1022: None}
+    calls = [0]
+
+    def spy(y_flat, select, sc_, *, out):
+        s = calls[0]
+        calls[0] += 1
+        y_in = select(y_flat).clone() if s in sampled else None
+        q(y_flat, select, sc_, out=out)
+        if s in sampled:
+            sampled[s] = (y_in, out.clone())
+
+    z_spy = G.gptq_2d_super_entry(x, lo, up, super_entry_shape=(16, 16), quantizer=spy, quantizer_inputs=(scale,))
+    assert calls[0] == 1023
+    assert z_spy.equal(z), "not deterministic"
 
     def keys(pairs):
         bits = pairs.contiguous().view(torch.int32).to(torch.int64) & 0xFFFFFFFF
@@ -314,6 +347,21 @@ def test_c4_full_size():
     print(f"  first {K} coarse antidiagonals ({int(win.sum())} entries): agreement with the oracle {agree:.4%}",
           flush=True)
     assert agree >= 0.99
+
+    # at the sampled antidiagonals across the whole layer, the CPU oracle's quantizer on the engine's own
+    # pre-rounding super-entries (up to 24 of each, spread over the antidiagonal) writes what the engine wrote
+    checked = 0
+    for s_, (y_in, y_out) in sampled.items():
+        d = y_in.size(0)
+        pick = torch.unique(torch.linspace(0, d - 1, min(d, 24)).round().long())
+        yc = y_in[pick].cpu()
+        ref = torch.empty_like(yc)
+        OT.trellis_quantizer_super_entry(yc.flatten(), lambda t: t.unflatten(-1, yc.shape), sc, out=ref,
+                                         table=table_cpu, K=2)
+        assert ref.equal(y_out[pick].cpu()), s_
+        checked += pick.numel()
+    print(f"  {checked} super-entries at {len(sampled)} sampled antidiagonals: the oracle's quantizer on the engine's "
+          f"inputs equals the engine's output", flush=True)
 
 
 def test_c5b_batch_capture():

@@ -200,6 +200,27 @@ def test_feedback_factors_of_grams_ragged(ka, kb, dtype):
     _check_factor(lo, a, 1, True, 1e-9 if dtype == torch.float64 else 2e-4)
 
 
+@pytest.mark.parametrize("k,cuts,dtype", [(601, (64, 320), torch.float32), (600, (64, 320), torch.float64),
+                                          (1536, (192, 640), torch.float64)])
+def test_cholesky_in_parts_plain(k, cuts, dtype):
+    """The one-panel-per-launch Cholesky (fp64, and fp32 with k % 4 != 0) split over calls that end inside a
+    256-column strip: a part leaves its strip's trailing update pending, and the next part's left-looking
+    panel updates and the strip-end update read the strip's factored columns from W, so the parts issue
+    the one call's launches in the same order and give its factor bit for bit."""
+    print(f"cholesky in parts (plain path) k={k} cuts={cuts} {dtype}", flush=True)
+    m = instances.wishart_factor(k, .5, 70 + k).to(dtype).to(DEV)
+    out, work = torch.empty_like(m), torch.empty_like(m)
+    info = torch.zeros(1, dtype=torch.int32, device=DEV)
+    bounds = (0,) + cuts + (-1,)
+    for c0, c1 in zip(bounds[:-1], bounds[1:]):
+        LDL._part(m, out, work, info, k, 1, c0, c1, 0)
+    LDL._part(m, out, work, info, k, 1, k, -1, 1)
+    torch.cuda.synchronize()
+    assert info.item() == 0
+    assert out.equal(LDL.ldl_of_inverse(m))
+    _check_factor(out, m, 1, True, 1e-9 if dtype == torch.float64 else 2e-4)
+
+
 @pytest.mark.parametrize("k,cuts", [(1536, (192, 640)), (600, (64, 320, 512)), (8192, (4160,))])
 def test_cholesky_in_parts(k, cuts):
     """The Cholesky split over calls at panel boundaries that cut the 256-column strips of the fp32 path:

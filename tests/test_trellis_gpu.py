@@ -92,6 +92,30 @@ def test_many_rows(dtype, rows):
         _valid_path(st, table, K, tb)
 
 
+@pytest.mark.parametrize("tb", [True, False])
+def test_bench_call(tb):
+    """The benchmark's call (bench.py's Viterbi line: C4's longest antidiagonal, 512 sequences of 256, HYB L = 16,
+    K = 2, V = 2, the same seeded input, values scaled per row, two sequences per workgroup with four groups per
+    thread): states and values equal the PyTorch formulation (pinned by the reference's L = 16 golden states) on
+    every row, and the CPU oracle on a sample of rows, bit for bit (quantizer_trellis.py:450-479)."""
+    rows, T, K = 512, 256, 2
+    table = QT.hyb(L=16, device=DEV)
+    x = torch.randn(rows, T, generator=torch.Generator().manual_seed(0)).to(DEV)
+    out = torch.empty_like(x)
+    scale = torch.ones(rows, device=DEV)
+    states = torch.empty(rows, T // 2, dtype=torch.int64, device=DEV)
+    QT.trellis_quantize_hip(x, table, K, tb, out=out, scale=scale, states=states)
+    tv, ts = QT.trellis_quantize_torch(x, table, K, tb)
+    assert states.equal(ts) and out.equal(tv)
+    _valid_path(states, table, K, tb)
+    sample = torch.tensor([0, 1, 2, 255, 256, 257, 301, 510, 511])
+    ov, os_ = OT.trellis_quantize(x[sample].cpu(), OT.hyb(L=16), K, tb)
+    assert states[sample].cpu().equal(os_) and out[sample].cpu().equal(ov)
+    scale2 = torch.linspace(.5, 2., rows, device=DEV)
+    QT.trellis_quantize_hip(x, table, K, tb, out=out, scale=scale2, states=states)
+    assert states.equal(ts) and out.equal(tv * scale2[:, None])
+
+
 def test_codes_and_k():
     """The real codes at L = 16 with several K, against the oracle (quantizer_trellis.py:474-479)."""
     g = torch.Generator().manual_seed(12)
