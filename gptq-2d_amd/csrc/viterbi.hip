@@ -110,6 +110,56 @@ struct Sequence {
   }
 };
 
+// Final step of a forward pass: the first argmin over all states of cost_{last} (under the tail-biting masks),
+// per sequence, into best_state[k]; the previous step's minima from LDS (prev_lds) or the history.
+template <typename T, int V, int NS>
+__device__ void final_argmin(const Sequence<T, V> (&seq)[NS], const T* __restrict__ table, T* const (&hist)[NS],
+                             T* prev_lds, const SearchGeom& g, int roll, bool masked, const int64_t (&overlap)[NS],
+                             int64_t* best_state, T* red_v, int64_t* red_i) {
+  const int tid = threadIdx.x;
+  const int64_t G = g.G;
+  const T inf = inf_value<T>();
+  const int last = g.steps - 1;
+  const int64_t S = G << g.KV;
+  const int wave = tid >> 6, lane = tid & 63;
+#pragma unroll
+  for (int k = 0; k < NS; ++k) {
+    T x0, x1;
+    seq[k].at(last, roll, x0, x1);
+    T* pl = prev_lds ? prev_lds + k * 2 * G : nullptr;
+    const T* prev = last == 0 ? nullptr : (pl ? pl + ((last - 1) & 1) * G : hist[k] + (int64_t)(last - 1) * G);
+    T bv = inf;
+    int64_t bi = INT64_MAX;
+    for (int64_t s = tid; s < S; s += VT_THREADS) {
+      T c = local_cost<T, V>(table, s, x0, x1);
+      if (last == 0) {
+        if (masked && (s >> g.KV) != overlap[k]) c = inf;
+      } else {
+        c = prev[s >> g.KV] + c;
+      }
+      if (masked && (s & (G - 1)) != overlap[k]) c = inf;
+      if (c < bv || bi == INT64_MAX) {  // increasing s per thread: the first, then strictly smaller ones
+        bv = c;
+        bi = s;
+      }
+    }
+    wave_argmin(bv, bi);
+    if (lane == 0) {
+      red_v[k * (VT_THREADS / 64) + wave] = bv;
+      red_i[k * (VT_THREADS / 64) + wave] = bi;
+    }
+  }
+  __syncthreads();
+  if (tid < NS) {
+    const int k = tid;
+    T v = red_v[k * (VT_THREADS / 64)];
+    int64_t i = red_i[k * (VT_THREADS / 64)];
+    for (int w = 1; w < VT_THREADS / 64; ++w) arg_better(v, i, red_v[k * (VT_THREADS / 64) + w], red_i[k * (VT_THREADS / 64) + w]);
+    best_state[k] = i & (S - 1);  // every state is a candidate, so i < S; the mask only keeps reads in bounds
+  }
+  __syncthreads();
+}
+
 // Forward pass of NS sequences in lockstep (the workgroup's): history_k[t][j] = best_t(j) of sequence
 // k for t < steps - 1, and best_state[k] the first argmin of its cost_{last} under the masks.  Each
 // table entry is loaded once per step for all NS sequences.  prev_lds: NS x 2 G values of LDS, or
@@ -270,46 +320,145 @@ __device__ void forward_pass(const Sequence<T, V> (&seq)[NS], const bool (&live)
     }
     __syncthreads();
   }
-  // final step: first argmin over all states, per sequence
-  const int last = g.steps - 1;
-  const int64_t S = G << g.KV;
-  const int wave = tid >> 6, lane = tid & 63;
+  final_argmin<T, V, NS>(seq, table, hist, prev_lds, g, roll, masked, overlap, best_state, red_v, red_i);
+}
+
+// ------------------------------------------------------------------------------------------------ few distinct rows
+//
+// Codes whose 2^L table rows take few distinct values -- HYB: 2^9 look-up rows times the sign of the first
+// value; 1MAD: 908 values at L = 16 -- search from a per-step cost table instead of the table itself.  The table is
+// given as E entries of W rows each, urows[E][W][V], and ridx[s] for s < 2^L / W: the entry whose row w is
+// the row of state s + w 2^L / W (table[s + w 2^L / W] == urows[ridx[s]][w] bit for bit).  W = 2 pairs the
+// states h G + j and (h + H / 2) G + j of a group (HYB: the same look-up row with both signs, 1024 ordered pairs);
+// W = 1 is the plain distinct rows.  Each step first evaluates d(row, x_t) of every entry's rows (thread e,
+// the same operations as every state evaluation of forward_pass), double-buffered in LDS; a state's
+// evaluation is then that cost, read from LDS (one 8-byte read for the W = 2 states of an entry), plus the
+// predecessor minimum and the running minimum.  The costs are the same values, so the search is the same.
+// One sequence per workgroup; thread tid owns the four groups j = 4 tid .. 4 tid + 3 (G <= 4 VT_THREADS) and
+// keeps the byte offsets of its (H / W) x 4 entries in the cost table in registers, two 16-bit offsets a
+// register.
+constexpr int ROWS_MAX = 1024;
+
+template <int V, int H, int W>
+__device__ void forward_rows(const Sequence<float, V>& sq, bool live, const float* __restrict__ table,
+                             const float (&urow)[W][V], int E, const int* __restrict__ ridx, float* ctab,
+                             float* hist, float* prev_lds, const SearchGeom& g, int roll, bool masked,
+                             int64_t overlap, int64_t* best_state, float* red_v, int64_t* red_i) {
+  constexpr int HE = H / W;  // entries per group
+  using lds_f = __attribute__((address_space(3))) float*;
+  using lds_cf = const __attribute__((address_space(3))) float*;
+  using lds_cb = const __attribute__((address_space(3))) char*;
+  typedef float f2v __attribute__((ext_vector_type(2)));
+  typedef float f4v __attribute__((ext_vector_type(4)));
+  using lds_cf2 = const __attribute__((address_space(3))) f2v*;
+  using lds_f4 = __attribute__((address_space(3))) f4v*;
+  const int tid = threadIdx.x;
+  const int G32 = (int)g.G, kv = g.KV;
+  const float inf = __builtin_huge_valf();
+  const int j = 4 * tid;
+  const bool owner = j < G32;
+  // the byte offsets of this thread's entries' costs, loaded here (not held across the walks back)
+  uint32_t offp[HE][2];
 #pragma unroll
-  for (int k = 0; k < NS; ++k) {
-    T x0, x1;
-    seq[k].at(last, roll, x0, x1);
-    T* pl = prev_lds ? prev_lds + k * 2 * G : nullptr;
-    const T* prev = last == 0 ? nullptr : (pl ? pl + ((last - 1) & 1) * G : hist[k] + (int64_t)(last - 1) * G);
-    T bv = inf;
-    int64_t bi = INT64_MAX;
-    for (int64_t s = tid; s < S; s += VT_THREADS) {
-      T c = local_cost<T, V>(table, s, x0, x1);
-      if (last == 0) {
-        if (masked && (s >> g.KV) != overlap[k]) c = inf;
-      } else {
-        c = prev[s >> g.KV] + c;
-      }
-      if (masked && (s & (G - 1)) != overlap[k]) c = inf;
-      if (c < bv || bi == INT64_MAX) {  // increasing s per thread: the first, then strictly smaller ones
-        bv = c;
-        bi = s;
+  for (int h = 0; h < HE; ++h)
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const uint32_t o0 = owner ? (uint32_t)ridx[h * G32 + j + 2 * q] * W * 4 : 0u;
+      const uint32_t o1 = owner ? (uint32_t)ridx[h * G32 + j + 2 * q + 1] * W * 4 : 0u;
+      offp[h][q] = o0 | o1 << 16;
+    }
+  // cost table of step t into buffer t & 1: row w of entry e at [(t & 1) E W + e W + w]
+  auto fill = [&](int t) {
+    if (tid < E) {
+      float x0, x1;
+      sq.at(t, roll, x0, x1);
+#pragma unroll
+      for (int w = 0; w < W; ++w) {
+        const float d0 = urow[w][0] - x0;
+        float c = d0 * d0;
+        if constexpr (V == 2) {
+          const float d1 = urow[w][V - 1] - x1;
+          c = c + d1 * d1;
+        }
+        ((lds_f)ctab)[(t & 1) * E * W + tid * W + w] = c;
       }
     }
-    wave_argmin(bv, bi);
-    if (lane == 0) {
-      red_v[k * (VT_THREADS / 64) + wave] = bv;
-      red_i[k * (VT_THREADS / 64) + wave] = bi;
+  };
+  fill(0);
+  __syncthreads();
+  for (int t = 0; t + 1 < g.steps; ++t) {
+    lds_cf prev = (lds_cf)(t == 0 ? prev_lds : prev_lds + ((t - 1) & 1) * g.G);
+    lds_f cur = (lds_f)(prev_lds + (t & 1) * g.G);
+    // the cost tables sit at the start of the workgroup's LDS: byte address = buffer base + offset
+    const uint32_t cbase = (uint32_t)((t & 1) * E * W * 4);
+    auto groups = [&](auto first_c) {
+      constexpr bool first = decltype(first_c)::value;
+      // the step's history row, addressed before the loop (the store after it is the only branch)
+      float4* hrow = reinterpret_cast<float4*>(hist + (int64_t)t * g.G + j);
+      float best[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) best[e] = inf;
+      // the predecessor group of state h G + j is h (G >> kv) + (j >> kv) (G is a multiple of 2^kv)
+      const int pstride = G32 >> kv, pj = j >> kv;
+      // costs of entry h's four groups, read one h ahead: the reads of h + 1 are in flight while h is evaluated
+      auto read_costs = [&](int h, float (&c)[4][W]) __attribute__((always_inline)) {
+        // opaque here, so that the halves are extracted at their use instead of unpacked into 4 HE registers
+        // ahead of the loop
+        asm volatile("" : "+v"(offp[h][0]), "+v"(offp[h][1]));
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t ob = cbase + ((e & 1) ? offp[h][e >> 1] >> 16 : offp[h][e >> 1] & 0xffffu);
+          if constexpr (W == 2) {
+            const f2v c2 = *(lds_cf2)((lds_cb)ctab + ob);
+            c[e][0] = c2.x;
+            c[e][1] = c2.y;
+          } else {
+            c[e][0] = *(lds_cf)((lds_cb)ctab + ob);
+          }
+        }
+      };
+      float cc[2][4][W];
+      read_costs(0, cc[0]);
+#pragma unroll
+      for (int h = 0; h < HE; ++h) {
+        if (h + 1 < HE) read_costs(h + 1, cc[(h + 1) & 1]);
+#pragma unroll
+        for (int w = 0; w < W; ++w) {
+          const int ps = (h + w * HE) * pstride + pj;  // state (h + w HE) G + j
+          const float pv = first ? 0.f : prev[ps];
+          const bool masked_out = first && masked && ps != overlap;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            float v = cc[h & 1][e][w];
+            if constexpr (first)
+              v = masked_out ? inf : v;
+            else
+              v = pv + v;
+            best[e] = fmin(v, best[e]);
+          }
+        }
+        // one h at a time: left alone, the scheduler issues the reads of all HE entries at once and runs out
+        // of registers (spills)
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      const float4 b4 = make_float4(best[0], best[1], best[2], best[3]);
+      *(lds_f4)(cur + j) = f4v{b4.x, b4.y, b4.z, b4.w};
+      if (live) *hrow = b4;
+    };
+    if (owner) {
+      if (t == 0)
+        groups(std::true_type{});
+      else
+        groups(std::false_type{});
     }
+    // the next step's cost table (the last step's costs come from the table itself, in final_argmin)
+    if (t + 2 < g.steps) fill(t + 1);
+    __syncthreads();
   }
-  __syncthreads();
-  if (tid < NS) {
-    const int k = tid;
-    T v = red_v[k * (VT_THREADS / 64)];
-    int64_t i = red_i[k * (VT_THREADS / 64)];
-    for (int w = 1; w < VT_THREADS / 64; ++w) arg_better(v, i, red_v[k * (VT_THREADS / 64) + w], red_i[k * (VT_THREADS / 64) + w]);
-    best_state[k] = i & (S - 1);  // every state is a candidate, so i < S; the mask only keeps reads in bounds
-  }
-  __syncthreads();
+  const Sequence<float, V> seqs[1] = {sq};
+  float* const hists[1] = {hist};
+  const int64_t ovs[1] = {overlap};
+  final_argmin<float, V, 1>(seqs, table, hists, prev_lds, g, roll, masked, ovs, best_state, red_v, red_i);
 }
 
 // Walk back from the last state to step `stop` with wave 0: returns the state at `stop`, and writes
@@ -410,6 +559,82 @@ __global__ __launch_bounds__(VT_THREADS) void viterbi_kernel(const T* __restrict
     }
 }
 
+// viterbi_kernel with the forward passes of forward_rows (fp32, one sequence per workgroup; G <= 4 VT_THREADS,
+// G % 4 == 0, 2^KV == H, E <= ROWS_MAX; the previous minima always in LDS).  Dynamic LDS: the cost tables
+// (2 x E x W floats, at LDS address 0 so that a 16-bit byte offset addresses them), then the minima (2 G floats).
+template <int V, int H, int W>
+__global__ __launch_bounds__(VT_THREADS) void viterbi_rows_kernel(const float* __restrict__ x,
+                                                                  const float* __restrict__ table,
+                                                                  const float* __restrict__ urows,
+                                                                  const int* __restrict__ ridx, int E,
+                                                                  float* __restrict__ hist_all,
+                                                                  const float* __restrict__ scale,
+                                                                  float* __restrict__ out,
+                                                                  int64_t* __restrict__ states, int64_t rows, int L,
+                                                                  int KV, int steps, int tail_biting) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  __shared__ float red_v[VT_THREADS / 64];
+  __shared__ int64_t red_i[VT_THREADS / 64];
+  __shared__ int64_t sh_state[1], sh_overlap;
+  SearchGeom g{L, KV, steps, (int64_t)1 << (L - KV), true};
+  const int64_t row = blockIdx.x;
+  const Sequence<float, V> sq{x + row * (int64_t)steps * V, steps};
+  float* hist = hist_all + row * (int64_t)(steps > 1 ? steps - 1 : 1) * g.G;
+  float* ctab = reinterpret_cast<float*>(smem);
+  float* prev_lds = ctab + ((2 * E * W + 3) & ~3);
+  // this thread's entry (the cost table entry it evaluates each step)
+  float urow[W][V];
+#pragma unroll
+  for (int w = 0; w < W; ++w)
+#pragma unroll
+    for (int v = 0; v < V; ++v) urow[w][v] = (int)threadIdx.x < E ? urows[(threadIdx.x * W + w) * V + v] : 0.f;
+  const bool wave0 = threadIdx.x < 64;
+  int64_t overlap = 0;
+  if (tail_biting) {
+    const int half = steps / 2;
+    forward_rows<V, H, W>(sq, true, table, urow, E, ridx, ctab, hist, prev_lds, g, steps - half, false, 0, sh_state,
+                          red_v, red_i);
+    if (wave0) {
+      const int64_t st = backtrack<float, V>(sq, table, hist, g, steps - half, false, 0, sh_state[0], half, 1.f,
+                                             nullptr, nullptr);
+      if (threadIdx.x == 0) sh_overlap = st >> KV;
+    }
+    __syncthreads();
+    overlap = sh_overlap;
+  }
+  forward_rows<V, H, W>(sq, true, table, urow, E, ridx, ctab, hist, prev_lds, g, 0, tail_biting != 0, overlap,
+                        sh_state, red_v, red_i);
+  if (wave0) {
+    const float sc = scale ? scale[row] : 1.f;
+    float* orow = out ? out + row * (int64_t)steps * V : nullptr;
+    int64_t* srow = states ? states + row * (int64_t)steps : nullptr;
+    backtrack<float, V>(sq, table, hist, g, 0, tail_biting != 0, overlap, sh_state[0], 0, sc, orow, srow);
+  }
+}
+
+template <int V, int H, int W>
+void launch_viterbi_rows(size_t lds, hipStream_t stream, const float* x, const float* table, const float* urows,
+                         const int* ridx, int E, float* hist, const float* scale, float* out, int64_t* states,
+                         int64_t rows, int L, int KV, int steps, int tail_biting) {
+  hipLaunchKernelGGL((viterbi_rows_kernel<V, H, W>), dim3((unsigned)rows), dim3(VT_THREADS), lds, stream, x, table,
+                     urows, ridx, E, hist, scale, out, states, rows, L, KV, steps, tail_biting);
+}
+
+template <int V, int W>
+void launch_viterbi_rows_h(int H, size_t lds, hipStream_t stream, const float* x, const float* table,
+                           const float* urows, const int* ridx, int E, float* hist, const float* scale, float* out,
+                           int64_t* states, int64_t rows, int L, int KV, int steps, int tail_biting) {
+  if (H == 4)
+    launch_viterbi_rows<V, 4, W>(lds, stream, x, table, urows, ridx, E, hist, scale, out, states, rows, L, KV, steps,
+                                 tail_biting);
+  else if (H == 8)
+    launch_viterbi_rows<V, 8, W>(lds, stream, x, table, urows, ridx, E, hist, scale, out, states, rows, L, KV, steps,
+                                 tail_biting);
+  else
+    launch_viterbi_rows<V, 16, W>(lds, stream, x, table, urows, ridx, E, hist, scale, out, states, rows, L, KV,
+                                  steps, tail_biting);
+}
+
 template <typename T, int V, int NS>
 void launch_viterbi(size_t lds, bool in_lds, hipStream_t stream, const T* x, const T* table, T* hist, const T* scale,
                     T* out, int64_t* states, int64_t rows, int L, int KV, int steps, int tail_biting) {
@@ -454,6 +679,46 @@ int viterbi(const T* x, const T* table, T* hist, const T* scale, T* out, int64_t
   return (int)hipGetLastError();
 }
 
+// The search with the cost tables of the distinct rows (W = 1) or row pairs (W = 2) where it applies (fp32,
+// 2 <= KV <= 4, G % 4 == 0 and G % 2^KV == 0, G <= 4 VT_THREADS, 1 <= E <= ROWS_MAX, 16-byte aligned table and
+// history, LDS for the minima and the cost tables), else the plain search.  Same results either way.
+int viterbi_rows(const float* x, const float* table, const float* urows, const int* ridx, int64_t E, int W,
+                 float* hist, const float* scale, float* out, int64_t* states, int64_t rows, int64_t steps, int L,
+                 int K, int V, int tail_biting, hipStream_t stream) {
+  const int KV = K * V;
+  if (rows < 0 || steps < 1 || L < 1 || L > 24 || K < 1 || (V != 1 && V != 2) || KV > L || KV > 8) return GPTQ2D_EINVAL;
+  if (rows == 0) return 0;
+  if (rows > 0x7fffffff || steps > 0x7fffffff) return GPTQ2D_EUNSUPPORTED;
+  const int64_t G = (int64_t)1 << (L - KV);
+  const bool shape_ok = urows && ridx && (W == 1 || W == 2) && E >= 1 && E <= ROWS_MAX && KV >= 2 && KV <= 4 &&
+                        G % 4 == 0 && G % (1 << KV) == 0 && G <= 4 * VT_THREADS && ((uintptr_t)table & 15) == 0 &&
+                        ((uintptr_t)hist & 15) == 0;
+  // one sequence per workgroup: with two, the compiler spills the evaluation loop (two sequences' costs and
+  // minima beside the offsets exceed the 128 registers of a 1024-thread workgroup); more rows than compute
+  // units queue as further rounds
+  const size_t lds = (size_t)2 * G * 4 + (size_t)((2 * E * W + 3) & ~3) * 4;
+  if (!shape_ok || lds > 96 * 1024)
+    return viterbi<float>(x, table, hist, scale, out, states, rows, steps, L, K, V, tail_biting, stream);
+  const int H = 1 << KV;
+  const int Ei = (int)E;
+  if (W == 2) {
+    if (V == 1)
+      launch_viterbi_rows_h<1, 2>(H, lds, stream, x, table, urows, ridx, Ei, hist, scale, out, states, rows, L, KV,
+                                  (int)steps, tail_biting);
+    else
+      launch_viterbi_rows_h<2, 2>(H, lds, stream, x, table, urows, ridx, Ei, hist, scale, out, states, rows, L, KV,
+                                  (int)steps, tail_biting);
+  } else {
+    if (V == 1)
+      launch_viterbi_rows_h<1, 1>(H, lds, stream, x, table, urows, ridx, Ei, hist, scale, out, states, rows, L, KV,
+                                  (int)steps, tail_biting);
+    else
+      launch_viterbi_rows_h<2, 1>(H, lds, stream, x, table, urows, ridx, Ei, hist, scale, out, states, rows, L, KV,
+                                  (int)steps, tail_biting);
+  }
+  return (int)hipGetLastError();
+}
+
 }  // namespace
 
 extern "C" {
@@ -473,5 +738,13 @@ int64_t gptq2d_viterbi_workspace(int64_t rows, int64_t steps, int32_t L, int32_t
 
 GPTQ2D_VITERBI_ABI(f32, float)
 GPTQ2D_VITERBI_ABI(f64, double)
+
+// The fp32 search over a table given as entries of its distinct rows or row pairs (see viterbi_rows).
+int gptq2d_viterbi_rows_f32(const float* x, const float* table, const float* urows, const int32_t* ridx, int64_t E,
+                            int32_t W, float* hist, const float* scale, float* out, int64_t* states, int64_t rows,
+                            int64_t steps, int32_t L, int32_t K, int32_t V, int32_t tail_biting, hipStream_t stream) {
+  return viterbi_rows(x, table, urows, ridx, E, W, hist, scale, out, states, rows, steps, L, K, V, tail_biting,
+                      stream);
+}
 
 }  // extern "C"

@@ -9,7 +9,10 @@ The codes ``one_mad``, ``three_inst`` and ``hyb`` map states to roughly Gaussian
 ``trellis_quantizer_super_entry_hip`` quantizes each super-entry of an antidiagonal, read row by
 row, as one sequence and writes ``scale`` times its values; the whole two-pass search of all the
 stage's sequences is one HIP launch (``csrc/viterbi.hip``), never synchronises with the host, and
-is graph-capturable.  ``trellis_quantizer_super_entry_torch`` is the PyTorch formulation on any
+is graph-capturable.  Tables with at most 1024 distinct rows or row pairs (HYB: 512 look-up rows, each
+with both signs; 1MAD: 908 values at L = 16) are searched from a per-step cost table of those entries; the entries
+and each state's entry are found once per table (one host synchronisation, outside graph capture) and
+cached.  ``trellis_quantizer_super_entry_torch`` is the PyTorch formulation on any
 device; the reference's ``*_triton`` name is an alias of the HIP plug-in.
 
 Reference: IST-DASLab/GPTQ-2D quantizer_trellis.py (codes :28-79, Viterbi :82-143, plug-ins
@@ -18,11 +21,16 @@ Reference: IST-DASLab/GPTQ-2D quantizer_trellis.py (codes :28-79, Viterbi :82-14
 
 from __future__ import annotations
 
+import weakref
 from typing import Callable
 
 import torch
 
 import _hip
+
+# Distinct rows of a code table (bitwise): at most this many make the search use per-step cost tables.
+ROWS_MAX = 1024
+_rows_cache: dict = {}
 
 
 # ------------------------------------------------------------------------------------------------ codes
@@ -85,6 +93,34 @@ def _check(table: torch.Tensor, K: int, T: int):
     return L, V
 
 
+def distinct_rows(table: torch.Tensor):
+    """The table as at most ROWS_MAX entries of its distinct rows, or None: (urows [E, W, V], index [2^L / W]
+    int32, W) with ``table[s + w 2^L / W] == urows[index[s], w]`` bit for bit.  W = 2 (pairs of the states s and
+    s + 2^(L-1): for HYB the same look-up row with both signs, 1024 ordered pairs) where at most ROWS_MAX distinct pairs
+    occur, else W = 1 (the distinct rows).  Only for an fp32 GPU table; computed once per table object and
+    version (one host synchronisation, never inside graph capture) and cached while the table lives."""
+    if table.dtype != torch.float32 or not table.is_cuda or not table.is_contiguous() or table.dim() != 2:
+        return None
+    key = id(table)
+    hit = _rows_cache.get(key)
+    if hit is not None and hit[0]() is table and hit[1] == table._version:
+        return hit[2]
+    if torch.cuda.is_current_stream_capturing():
+        return None
+    bits, index = torch.unique(table.view(torch.int32), dim=0, return_inverse=True)
+    R, S = bits.size(0), table.size(0)
+    found = None
+    if S >= 2:
+        pairs, pindex = torch.unique(index[:S // 2] * R + index[S // 2:], return_inverse=True)
+        if pairs.size(0) <= ROWS_MAX:
+            urows = torch.stack((bits[pairs // R], bits[pairs % R]), dim=1)
+            found = (urows.view(torch.float32).contiguous(), pindex.to(torch.int32).contiguous(), 2)
+    if found is None and R <= ROWS_MAX:
+        found = (bits.view(torch.float32)[:, None, :].contiguous(), index.to(torch.int32).contiguous(), 1)
+    _rows_cache[key] = (weakref.ref(table, lambda _, k=key: _rows_cache.pop(k, None)), table._version, found)
+    return found
+
+
 def trellis_quantize_hip(x: torch.Tensor, table: torch.Tensor, K: int, tail_biting: bool = True, *,
                          out: torch.Tensor | None = None, scale: torch.Tensor | None = None,
                          states: torch.Tensor | None = None):
@@ -116,9 +152,15 @@ def trellis_quantize_hip(x: torch.Tensor, table: torch.Tensor, K: int, tail_biti
     size = int(_hip.lib().gptq2d_viterbi_workspace(cap, steps, L, K, V))
     hist = x.new_empty(size)
     with torch.cuda.device(x.device):
-        _hip.call("viterbi", x.dtype, _hip.ptr(seq), _hip.ptr(tab), _hip.ptr(hist), _hip.ptr(sc),
-                  _hip.ptr(out), _hip.ptr(states), rows, steps, L, K, V, int(bool(tail_biting)),
-                  _hip.stream(x.device))
+        urows = distinct_rows(tab) if tab is table else None
+        if urows is not None:
+            _hip.call_untyped("viterbi_rows_f32", _hip.ptr(seq), _hip.ptr(tab), _hip.ptr(urows[0]), _hip.ptr(urows[1]),
+                              urows[0].size(0), urows[2], _hip.ptr(hist), _hip.ptr(sc), _hip.ptr(out),
+                              _hip.ptr(states), rows, steps, L, K, V, int(bool(tail_biting)), _hip.stream(x.device))
+        else:
+            _hip.call("viterbi", x.dtype, _hip.ptr(seq), _hip.ptr(tab), _hip.ptr(hist), _hip.ptr(sc),
+                      _hip.ptr(out), _hip.ptr(states), rows, steps, L, K, V, int(bool(tail_biting)),
+                      _hip.stream(x.device))
     if ret:
         return out.view(x.shape), states.view(*x.shape[:-1], steps)
     return None

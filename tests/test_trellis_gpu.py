@@ -116,6 +116,56 @@ def test_bench_call(tb):
     assert states.equal(ts) and out.equal(tv * scale2[:, None])
 
 
+def _generic(monkeypatch):
+    monkeypatch.setattr(QT, "distinct_rows", lambda table: None)
+
+
+@pytest.mark.parametrize("rows", [1, 7, 256, 300, 512])
+def test_distinct_rows_search_equals_plain(monkeypatch, rows):
+    """Tables with few distinct rows (HYB L = 16, 1MAD L = 16, and L = 12 tables drawn from 5-300 distinct rows
+    with K V = 2, 3, 4) are searched from per-step cost tables; the states and values equal the plain search's
+    bit for bit, with and without tail-biting, for a row count below, at and above the compute units."""
+    g = torch.Generator().manual_seed(17 + rows)
+    cases = [(QT.hyb(device=DEV), 2), (QT.one_mad(device=DEV), 4), (QT.one_mad(device=DEV), 2)]
+    for (L, V, K), distinct in zip(((12, 2, 1), (12, 1, 3), (12, 2, 2), (12, 1, 4)), (5, 300, 64, 1024)):
+        pool = torch.randn(distinct, V, generator=g)
+        cases.append((pool[torch.randint(0, distinct, (1 << L,), generator=g)].to(DEV), K))
+    for table, K in cases:
+        assert QT.distinct_rows(table) is not None
+        V = table.size(1)
+        T = 256 if V == 2 else 128
+        x = torch.randn(rows, T, generator=g).to(DEV)
+        for tb in (False, True):
+            v_rows, s_rows = QT.trellis_quantize_hip(x, table, K, tb)
+            with pytest.MonkeyPatch.context() as mp:
+                _generic(mp)
+                v_plain, s_plain = QT.trellis_quantize_hip(x, table, K, tb)
+            assert s_rows.equal(s_plain) and v_rows.equal(v_plain), (table.size(0), V, K, tb)
+
+
+def test_distinct_rows_cache():
+    """The distinct rows are found once per table and redone after an in-place change; tables with more than
+    1024 distinct rows, fp64 tables and CPU tables take the plain search."""
+    def expand(r):  # the table the entries stand for
+        urows, index, W = r
+        return urows[index.long()].transpose(0, 1).reshape(-1, urows.size(-1))
+
+    table = QT.hyb(device=DEV)
+    r1 = QT.distinct_rows(table)
+    assert r1 is not None and r1[2] == 2 and r1[0].size(0) == 1024  # HYB: each look-up row, signs in either order
+    assert QT.distinct_rows(table) is r1
+    assert torch.equal(expand(r1).view(torch.int32), table.view(torch.int32))
+    table[0] = table[5]  # another row's values: still at most 1024 distinct row pairs
+    r2 = QT.distinct_rows(table)
+    assert r2 is not r1 and torch.equal(expand(r2).view(torch.int32), table.view(torch.int32))
+    one = QT.one_mad(device=DEV)  # 908 values, pairs of states beyond 1024: the distinct rows
+    r3 = QT.distinct_rows(one)
+    assert r3 is not None and r3[2] == 1 and torch.equal(expand(r3).view(torch.int32), one.view(torch.int32))
+    assert QT.distinct_rows(torch.randn(1 << 12, 2, device=DEV)) is None
+    assert QT.distinct_rows(QT.hyb(device=DEV, dtype=torch.float64)) is None
+    assert QT.distinct_rows(QT.hyb()) is None
+
+
 def test_codes_and_k():
     """The real codes at L = 16 with several K, against the oracle (quantizer_trellis.py:474-479)."""
     g = torch.Generator().manual_seed(12)
