@@ -67,9 +67,15 @@ FLUSH_ALGORITHMIC_BYTES = 0.489e9
 # profiles/flush_traffic_H_int4.md and profiles/counters_H_int4.md.
 TILE_STAGE_TRAFFIC_BYTES = 30.60e6
 VITERBI_TRAFFIC_BYTES = 2.343e9
-# fp32 VALU operations per trellis state evaluation: 2 sub, 2 mul, 1 add (the squared distance),
-# 1 add (the predecessor group's minimum), 1 min.
+# fp32 VALU operations per trellis state evaluation of the plain search: 2 sub, 2 mul, 1 add (the squared
+# distance), 1 add (the predecessor group's minimum), 1 min.
 OPS_PER_STATE_EVAL = 7
+# The benchmark's HYB table has 1024 distinct row pairs, so the search runs from per-step cost tables: each state
+# evaluation gathers its 4-byte cost from LDS (8-byte reads for two states), adds the predecessor minimum and
+# takes the running minimum.  Bound: the LDS gathers, against 64 banks x 4 B per clock per CU = 256 CUs x 256 B x
+# 2.4 GHz; their random addresses make most LDS cycles bank-conflict stalls (profiles/viterbi_hyb_counters.md).
+LDS_BYTES_PER_STATE_EVAL = 4
+LDS_PEAK_TBS = 157.3
 
 
 def _parse():
@@ -189,14 +195,18 @@ def _viterbi_bench(torch, dev, steps_timed=10, warmup=3):
     evals = rows * 2 * (T // V) * (1 << L)  # two passes, every state at every step
     hbm = {"traffic": VITERBI_TRAFFIC_BYTES, "traffic_unit": "B per call (rocprofv3, copy-calibrated)",
            "achieved_gbs": VITERBI_TRAFFIC_BYTES / sec / 1e9, "peak_gbs": HBM_PEAK_GBS}
-    ops = evals * OPS_PER_STATE_EVAL
+    lds = evals * LDS_BYTES_PER_STATE_EVAL / sec / 1e12
     return {
         "workload": "C4 longest antidiagonal: 512 sequences of 256 (16x16 super-entries), HYB L=16 K=2 V=2, "
                     "tail-biting",
         "weights_per_s": rows * T / sec,
         "ms_per_call": sec * 1e3,
-        "roofline": {"bound": "valu", "achieved": ops / sec / 1e12, "peak": VALU_FP32_OPS_PEAK / 1e12,
-                     "unit": "Tops/s (fp32, 7 per state evaluation)", "frac": ops / sec / VALU_FP32_OPS_PEAK},
+        "state_evals_per_s": evals / sec,
+        "roofline": {"bound": "lds", "achieved": lds, "peak": LDS_PEAK_TBS,
+                     "unit": "TB/s of 4-byte cost gathers (bank-conflicted random reads)", "frac": lds / LDS_PEAK_TBS},
+        # the plain search's ceiling for comparison: 7 fp32 VALU operations per state evaluation
+        "plain_search_valu_equivalent": {"achieved": evals * OPS_PER_STATE_EVAL / sec / 1e12,
+                                         "peak": VALU_FP32_OPS_PEAK / 1e12, "unit": "Tops/s"},
         "hbm": hbm,
     }
 

@@ -340,7 +340,7 @@ __device__ void forward_pass(const Sequence<T, V> (&seq)[NS], const bool (&live)
 constexpr int ROWS_MAX = 1024;
 
 template <int V, int H, int W>
-__device__ void forward_rows(const Sequence<float, V>& sq, bool live, const float* __restrict__ table,
+__device__ void forward_rows(const Sequence<float, V>& sq, const float* xs, bool live, const float* __restrict__ table,
                              const float (&urow)[W][V], int E, const int* __restrict__ ridx, float* ctab,
                              float* hist, float* prev_lds, const SearchGeom& g, int roll, bool masked,
                              int64_t overlap, int64_t* best_state, float* red_v, int64_t* red_i) {
@@ -368,10 +368,13 @@ __device__ void forward_rows(const Sequence<float, V>& sq, bool live, const floa
       offp[h][q] = o0 | o1 << 16;
     }
   // cost table of step t into buffer t & 1: row w of entry e at [(t & 1) E W + e W + w]
+  // x_t from the workgroup's LDS copy of the sequence (a global load here would put its latency on every
+  // step's critical path, between the evaluations and the barrier)
   auto fill = [&](int t) {
     if (tid < E) {
-      float x0, x1;
-      sq.at(t, roll, x0, x1);
+      const int tt = (t + roll) % g.steps;
+      const float x0 = ((lds_cf)xs)[tt * V];
+      const float x1 = V == 2 ? ((lds_cf)xs)[tt * V + 1] : 0.f;
 #pragma unroll
       for (int w = 0; w < W; ++w) {
         const float d0 = urow[w][0] - x0;
@@ -417,11 +420,14 @@ __device__ void forward_rows(const Sequence<float, V>& sq, bool live, const floa
           }
         }
       };
-      float cc[2][4][W];
-      read_costs(0, cc[0]);
+      // entries read ahead (2, 3 or 7 ahead, or no schedule barrier below: the same time within 3%)
+      constexpr int PD = 1;
+      float cc[PD + 1][4][W];
+#pragma unroll
+      for (int h = 0; h < PD && h < HE; ++h) read_costs(h, cc[h]);
 #pragma unroll
       for (int h = 0; h < HE; ++h) {
-        if (h + 1 < HE) read_costs(h + 1, cc[(h + 1) & 1]);
+        if (h + PD < HE) read_costs(h + PD, cc[(h + PD) % (PD + 1)]);
 #pragma unroll
         for (int w = 0; w < W; ++w) {
           const int ps = (h + w * HE) * pstride + pj;  // state (h + w HE) G + j
@@ -429,7 +435,7 @@ __device__ void forward_rows(const Sequence<float, V>& sq, bool live, const floa
           const bool masked_out = first && masked && ps != overlap;
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            float v = cc[h & 1][e][w];
+            float v = cc[h % (PD + 1)][e][w];
             if constexpr (first)
               v = masked_out ? inf : v;
             else
@@ -561,7 +567,8 @@ __global__ __launch_bounds__(VT_THREADS) void viterbi_kernel(const T* __restrict
 
 // viterbi_kernel with the forward passes of forward_rows (fp32, one sequence per workgroup; G <= 4 VT_THREADS,
 // G % 4 == 0, 2^KV == H, E <= ROWS_MAX; the previous minima always in LDS).  Dynamic LDS: the cost tables
-// (2 x E x W floats, at LDS address 0 so that a 16-bit byte offset addresses them), then the minima (2 G floats).
+// (2 x E x W floats, at LDS address 0 so that a 16-bit byte offset addresses them), the minima (2 G floats), then
+// the sequence (steps V floats).
 template <int V, int H, int W>
 __global__ __launch_bounds__(VT_THREADS) void viterbi_rows_kernel(const float* __restrict__ x,
                                                                   const float* __restrict__ table,
@@ -582,6 +589,9 @@ __global__ __launch_bounds__(VT_THREADS) void viterbi_rows_kernel(const float* _
   float* hist = hist_all + row * (int64_t)(steps > 1 ? steps - 1 : 1) * g.G;
   float* ctab = reinterpret_cast<float*>(smem);
   float* prev_lds = ctab + ((2 * E * W + 3) & ~3);
+  float* xs = prev_lds + 2 * g.G;  // the sequence, steps V floats
+  for (int i = threadIdx.x; i < steps * V; i += VT_THREADS) xs[i] = sq.x[i];
+  __syncthreads();  // the copy before any thread's first cost-table fill
   // this thread's entry (the cost table entry it evaluates each step)
   float urow[W][V];
 #pragma unroll
@@ -592,8 +602,8 @@ __global__ __launch_bounds__(VT_THREADS) void viterbi_rows_kernel(const float* _
   int64_t overlap = 0;
   if (tail_biting) {
     const int half = steps / 2;
-    forward_rows<V, H, W>(sq, true, table, urow, E, ridx, ctab, hist, prev_lds, g, steps - half, false, 0, sh_state,
-                          red_v, red_i);
+    forward_rows<V, H, W>(sq, xs, true, table, urow, E, ridx, ctab, hist, prev_lds, g, steps - half, false, 0,
+                          sh_state, red_v, red_i);
     if (wave0) {
       const int64_t st = backtrack<float, V>(sq, table, hist, g, steps - half, false, 0, sh_state[0], half, 1.f,
                                              nullptr, nullptr);
@@ -602,7 +612,7 @@ __global__ __launch_bounds__(VT_THREADS) void viterbi_rows_kernel(const float* _
     __syncthreads();
     overlap = sh_overlap;
   }
-  forward_rows<V, H, W>(sq, true, table, urow, E, ridx, ctab, hist, prev_lds, g, 0, tail_biting != 0, overlap,
+  forward_rows<V, H, W>(sq, xs, true, table, urow, E, ridx, ctab, hist, prev_lds, g, 0, tail_biting != 0, overlap,
                         sh_state, red_v, red_i);
   if (wave0) {
     const float sc = scale ? scale[row] : 1.f;
@@ -696,7 +706,7 @@ int viterbi_rows(const float* x, const float* table, const float* urows, const i
   // one sequence per workgroup: with two, the compiler spills the evaluation loop (two sequences' costs and
   // minima beside the offsets exceed the 128 registers of a 1024-thread workgroup); more rows than compute
   // units queue as further rounds
-  const size_t lds = (size_t)2 * G * 4 + (size_t)((2 * E * W + 3) & ~3) * 4;
+  const size_t lds = (size_t)2 * G * 4 + (size_t)((2 * E * W + 3) & ~3) * 4 + (size_t)steps * V * 4;
   if (!shape_ok || lds > 96 * 1024)
     return viterbi<float>(x, table, hist, scale, out, states, rows, steps, L, K, V, tail_biting, stream);
   const int H = 1 << KV;
