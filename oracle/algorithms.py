@@ -10,6 +10,9 @@ explicit Kronecker Gram), the super-entry and D-sided exactness checks, the
 YAQA rotation identity, Algorithm 1 against a brute-force least-squares
 statement on tiny inputs, and the LDL invariants (unit block triangular,
 L^T M L block diagonal, agreement with a numpy LDL of M^{-1}).
+``alg3_pre_rounding``: equal to the values super-entry Algorithm 3 rounds,
+recorded by its quantizer, on plain and super-entry shapes (fp64, within
+summation order), and a transposed or sign-flipped term fails it.
 """
 
 from __future__ import annotations
@@ -225,6 +228,26 @@ def alg3_super_entry(X, L, U, Q=nearest, super_entry_shape=(1, 1)):
 # ----------------------------------------------------------------------------------------------- D-sided
 
 @torch.no_grad()
+def alg3_pre_rounding(X, L, U, Z, Ypre, super_entry_shape=(1, 1), rows=None, slab=4096):
+    """The values super-entry Algorithm 3 rounds, from the errors E = Z - Ypre of the whole matrix (no
+    counterpart in the reference; the closed form of gptq_2d_reference.py:360-382 and gptq_2d.py:1239-1292):
+    Ypre = X + L' E + C U' with C = E + L' E, where L' is L below its p x p block diagonal and U' is U above its
+    q x q block diagonal.  Evaluated in fp64 for the given rows (all by default), in column slabs of U'.
+    Identity of the sweep, not a sweep: it checks a trajectory against its own errors."""
+    p, q = super_entry_shape
+    m, n = X.shape[-2:]
+    dev = X.device
+    rows = torch.arange(m, device=dev) if rows is None else rows
+    e = Z.double() - Ypre.double()
+    ib, jb = torch.arange(m, device=dev) // p, torch.arange(n, device=dev) // q
+    down = (L[rows].double() * (ib[None, :] < ib[rows][:, None])) @ e
+    c = e[rows] + down
+    right = torch.zeros_like(down)
+    for c0 in range(0, n, slab):
+        right[:, c0:c0 + slab] = c @ (U[:, c0:c0 + slab].double() * (jb[:, None] < jb[None, c0:c0 + slab]))
+    return X[rows].double() + down + right
+
+
 def alg2_d_sided(X, Ls, Q=nearest):
     """Algorithm 2 on an n_1 x ... x n_D tensor (gptq_2d_reference.py:248-267)."""
     D = X.dim()

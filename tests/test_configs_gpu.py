@@ -54,6 +54,12 @@ def _objective(z, x, a, b):
     return float(((a.double() @ r) * (r @ b.double())).sum())
 
 
+def _pre_rounding_rows(x, lo, up, z, pre, p, q, rows):
+    """The rows' pre-rounding values as Algorithm 3 fixes them from the engine's own errors (fp64 torch GEMMs on
+    the GPU, independent of the engine's kernels; the identity is pinned on the CPU)."""
+    return A.alg3_pre_rounding(x, lo, up, z, pre, (p, q), rows)
+
+
 # ------------------------------------------------------------------------------------------------ full size
 
 # outer blocks of the benchmark: bench.py OUTER_BLOCK (24 tile stages) and, for the 8192 x 28672 C5a layers,
@@ -191,9 +197,11 @@ def test_c5a_full_size():
     is formed as U_B1 (x) U_B2^(32) (28672^2 entries: the MFMA flush's staging is based per panel).  Checks:
     bitwise determinism; teacher-forced with its own codes, the abs-max quantizer applied to the captured
     pre-rounding values reproduces every output bit for bit; the objective tr(R^T A R (B1 (x) B2)) is below
-    rounding each super-entry row of W on its own; and on the first 96 coarse antidiagonals the codes agree
+    rounding each super-entry row of W on its own; on the first 96 coarse antidiagonals the codes agree
     with the CPU oracle (super-entry Algorithm 3 in fp32 on the cropped layer, which holds every entry those
-    antidiagonals depend on) in >= 99.9% of the entries."""
+    antidiagonals depend on) in >= 99.9% of the entries; and on 24 whole rows spread over the layer the
+    pre-rounding values equal super-entry Algorithm 3's, recomputed in fp64 by torch from the engine's own
+    errors, and the codes of those values agree with the engine's in >= 99.99% of the entries."""
     cfg = instances.THREE_FACTOR["C5a"]
     m, n1, n2 = cfg.m, cfg.n1, cfg.n2
     n = n1 * n2
@@ -217,17 +225,30 @@ def test_c5a_full_size():
 
     half = torch.full((), (cfg.qmax - cfg.qmin) / 2, device=DEV)
 
-    def absmax_rows(v):
-        rows = v.view(m, n // cfg.group, cfg.group)
+    def absmax_rows_of(v, r):
+        rows = v.view(r, n // cfg.group, cfg.group)
         sc = (rows.abs().amax(-1, keepdim=True) / half).to(torch.bfloat16).float()
         sc = torch.where(sc == 0, torch.ones_like(sc), sc)
-        return (torch.clamp(torch.round(rows / sc), cfg.qmin, cfg.qmax) * sc).view(m, n)
+        return (torch.clamp(torch.round(rows / sc), cfg.qmin, cfg.qmax) * sc).view(r, n)
+
+    absmax_rows = functools.partial(absmax_rows_of, r=m)
 
     pre = torch.full_like(x, float("nan"))
     assert run(quantizer=QI.teacher_forced_quantizer, quantizer_inputs=(z, pre)).equal(z)
     assert not pre.isnan().any()
     assert torch.equal(absmax_rows(pre), z), "outputs are not the abs-max quantizer of their own pre-rounding values"
-    del pre
+    # every entry of 24 rows spread over the layer: the pre-rounding values equal Algorithm 3's, recomputed in fp64
+    # from the engine's own errors, within fp32 summation error, and their quantizer gives the engine's codes
+    rows = torch.linspace(0, m - 1, 24, device=DEV).round().long()
+    y64 = _pre_rounding_rows(x, lo, up, z, pre, 1, cfg.group, rows)
+    dy = (y64 - pre[rows].double()).abs()
+    rel = float(dy.max() / y64.abs().max())
+    zr = absmax_rows_of(y64.float(), rows.numel())
+    agree = float((zr == z[rows]).double().mean())
+    print(f"  {rows.numel()} rows ({rows.numel() * n} entries): max |Y_pre - Y_alg3(fp64)| {dy.max():.2e} "
+          f"({rel:.2e} of max |Y|), codes of the fp64 values agree in {agree:.6%}", flush=True)
+    assert rel < 5e-6 and agree >= 0.9999
+    del pre, y64, dy
 
     def objective(zz):
         r = (zz - x).double()
@@ -279,7 +300,8 @@ def test_c4_full_size():
     search on the cropped layer, which holds every entry they depend on) in >= 99% of the entries; and at 8
     coarse antidiagonals sampled over the whole sweep (the longest, 512 super-entries, among them) the oracle's
     trellis quantizer applied to the super-entries the engine's quantizer received writes the engine's values
-    bit for bit."""
+    bit for bit; and on 24 whole rows spread over the layer the pre-rounding values equal super-entry Algorithm
+    3's, recomputed in fp64 by torch from the engine's own errors."""
     m = n = 8192
     print(f"C4: {m}x{n}, 16x16 super-entries, HYB L=16 K=2 V=2", flush=True)
     x = instances.weights(m, n, 0, True, False).float().to(DEV)
@@ -362,6 +384,20 @@ def test_c4_full_size():
         checked += pick.numel()
     print(f"  {checked} super-entries at {len(sampled)} sampled antidiagonals: the oracle's quantizer on the engine's "
           f"inputs equals the engine's output", flush=True)
+
+    # every entry of 24 rows spread over the layer: the pre-rounding values (teacher-forced with the engine's own
+    # values) equal Algorithm 3's, recomputed in fp64 from the engine's own errors, within fp32 summation error
+    pre = torch.full_like(x, float("nan"))
+    zf = G.gptq_2d_super_entry(x, lo, up, super_entry_shape=(16, 16), quantizer=QI.teacher_forced_quantizer,
+                               quantizer_inputs=(z, pre))
+    assert zf.equal(z) and not pre.isnan().any()
+    rows = torch.linspace(0, m - 1, 24, device=DEV).round().long()
+    y64 = _pre_rounding_rows(x, lo, up, z, pre, 16, 16, rows)
+    dy = (y64 - pre[rows].double()).abs()
+    rel = float(dy.max() / y64.abs().max())
+    print(f"  {rows.numel()} rows ({rows.numel() * n} entries): max |Y_pre - Y_alg3(fp64)| {dy.max():.2e} "
+          f"({rel:.2e} of max |Y|)", flush=True)
+    assert rel < 5e-6
 
 
 def test_c5b_batch_capture():

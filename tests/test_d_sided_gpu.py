@@ -9,8 +9,9 @@ depend on every coordinate) and on the per-stage plug-in engine.
 fp32 at full size: C5a's three-factor layer as the 8192 x 112 x 256 tensor X[i, b1, b2] under
 ldl_of_inverse of A, B1, B2 with static INT4 abs-max scales per 32 consecutive b2 (bf16): deterministic, codes
 on the grid, each output the affine quantizer of its own pre-rounding value, objective below rounding
-without feedback, and the first hyper-antidiagonals (a crop holding every entry they depend on) in
-agreement with the oracle's alg4.
+without feedback, the first hyper-antidiagonals (a crop holding every entry they depend on) in
+agreement with the oracle's alg4, and 24 whole rows of the two-sided view whose pre-rounding values equal
+Algorithm 3's recomputed in fp64 from the engine's own errors.
 """
 
 import functools
@@ -128,7 +129,20 @@ def test_c5a_three_sided_full_size():
     assert run(quantizer=QI.teacher_forced_quantizer, quantizer_inputs=(z, pre)).equal(z)
     assert not pre.isnan().any()
     assert torch.equal(affine(pre), z), "outputs are not the quantizer of their own pre-rounding values"
-    del pre, codes
+    # every entry of 24 rows spread over the layer, on the two-sided view the sweep runs (columns b1 + n1 b2, U =
+    # (L_B2 (x) L_B1)^T): the pre-rounding values equal Algorithm 3's, recomputed in fp64 by torch from the
+    # engine's own errors, and their rounding gives the engine's codes
+    flat = lambda t: t.permute(0, 2, 1).reshape(m, -1)
+    rows = torch.linspace(0, m - 1, 24, device=DEV).round().long()
+    y64 = A.alg3_pre_rounding(flat(x), ls[0], DS.column_factor(ls), flat(z), flat(pre), (1, 1), rows)
+    dy = (y64 - flat(pre)[rows].double()).abs()
+    rel = float(dy.max() / y64.abs().max())
+    sr = flat(scale)[rows]
+    agree = float((torch.clamp(torch.round(y64.float() / sr), cfg.qmin, cfg.qmax) * sr == flat(z)[rows]).double().mean())
+    print(f"  {rows.numel()} rows ({rows.numel() * n1 * n2} entries): max |Y_pre - Y_alg3(fp64)| {dy.max():.2e} "
+          f"({rel:.2e} of max |Y|), codes of the fp64 values agree in {agree:.6%}", flush=True)
+    assert rel < 5e-6 and agree >= 0.9999
+    del pre, codes, y64, dy
 
     def objective(zz):
         r = (zz - x).double()

@@ -193,3 +193,29 @@ def test_d_sided_is_a_2d_sweep(shape):
         got = A.alg3(W, Ls[0], U, Q=Q2)
         got = got.reshape(n1, *reversed(rest)).permute(*[perm.index(d) for d in range(D)])
         assert got.equal(expected), seed
+
+
+@pytest.mark.parametrize("m,n,p,q", [(12, 10, 1, 1), (16, 24, 4, 8), (8, 64, 1, 32), (32, 32, 16, 16)])
+def test_alg3_pre_rounding_identity(m, n, p, q):
+    """The closed form of the values Algorithm 3 rounds, from its own errors, equals the values its quantizer
+    receives (fp64, within summation order); a dropped transpose or sign fails it."""
+    g = torch.Generator().manual_seed(m * n + p)
+    x = 3 * torch.randn(m, n, generator=g, dtype=torch.float64)
+    lo = A.unit_diagonal_blocks(torch.randn(m, m, generator=g, dtype=torch.float64).tril(), p) if p > 1 else \
+        torch.randn(m, m, generator=g, dtype=torch.float64).tril(-1) * .3 + torch.eye(m, dtype=torch.float64)
+    up = (A.unit_diagonal_blocks(torch.randn(n, n, generator=g, dtype=torch.float64).tril(), q) if q > 1 else
+          torch.randn(n, n, generator=g, dtype=torch.float64).tril(-1) * .3 + torch.eye(n, dtype=torch.float64)).t()
+    pre = torch.full_like(x, float("nan"))
+
+    def spy(y, i, j):  # y [d, p, q] of the super-entries (i, j) of one antidiagonal
+        pre.view(m // p, p, n // q, q)[i.flatten(), :, j.flatten(), :] = y
+        return y.round()
+
+    z = A.alg3_super_entry(x, lo, up, Q=spy, super_entry_shape=(p, q))
+    assert not pre.isnan().any()
+    got = A.alg3_pre_rounding(x, lo, up, z, pre, (p, q))
+    assert torch.allclose(got, pre, rtol=0, atol=1e-9 * float(pre.abs().max()))
+    bad = A.alg3_pre_rounding(x, lo, up.t().contiguous(), z, pre, (p, q))  # transposed U
+    assert not torch.allclose(bad, pre, rtol=0, atol=1e-6 * float(pre.abs().max()))
+    bad = A.alg3_pre_rounding(x, lo, up, 2 * pre - z, pre, (p, q))  # errors with the wrong sign
+    assert not torch.allclose(bad, pre, rtol=0, atol=1e-6 * float(pre.abs().max()))
