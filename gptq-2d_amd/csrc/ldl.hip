@@ -727,8 +727,13 @@ __device__ __forceinline__ void syrk_wide_block(WideLds& sm, float* __restrict__
   const int I0 = bi * WB, J0 = bj * WB;
   const int ild = (int)ld;
   const int CR = C < R ? C : R;
-  // offsets below ld * R * 4 < 2^31 (checked by the host)
-  const __amdgpu_buffer_rsrc_t rp = matrix_rsrc(w + r0 * ld + pc, (int64_t)(R - 1) * ld + K);
+  // the panels' buffer resources are based at the block's own first rows (A: rows r0 + I0 .., B: rows
+  // r0 + J0 ..), so that every byte offset stays below 128 rows of ld floats at any matrix size
+  const int arows = R - I0 < WB ? R - I0 : WB, brows = CR - J0 < WB ? CR - J0 : WB;
+  const __amdgpu_buffer_rsrc_t rpa =
+      matrix_rsrc(w + (r0 + I0) * ld + pc, arows > 0 ? (int64_t)(arows - 1) * ld + K : 0);
+  const __amdgpu_buffer_rsrc_t rpb =
+      matrix_rsrc(w + (r0 + J0) * ld + pc, brows > 0 ? (int64_t)(brows - 1) * ld + K : 0);
 
   // per-lane staging offsets of the wave's four 128-bit loads per panel and k-tile
   int aoff[4], boff[4];
@@ -736,9 +741,8 @@ __device__ __forceinline__ void syrk_wide_block(WideLds& sm, float* __restrict__
   for (int x = 0; x < 4; ++x) {
     const int f = (wave + 4 * x) * 256 + 4 * lane;
     const int row = f >> 5, kq = ((f >> 2) & 7) ^ quad_swizzle(row);
-    const int ia = I0 + row, ib = J0 + row;
-    aoff[x] = ia < R ? (ia * ild + 4 * kq) * 4 : OOB;
-    boff[x] = ib < CR ? (ib * ild + 4 * kq) * 4 : OOB;
+    aoff[x] = row < arows ? (row * ild + 4 * kq) * 4 : OOB;
+    boff[x] = row < brows ? (row * ild + 4 * kq) * 4 : OOB;
   }
   // a block whose rows and columns all lie inside the update takes the k offset in the loads' scalar field:
   // no vector instruction beside the MFMA bursts
@@ -748,16 +752,16 @@ __device__ __forceinline__ void syrk_wide_block(WideLds& sm, float* __restrict__
 #pragma unroll
       for (int x = 0; x < 4; ++x) {
         const int f0 = (wave + 4 * x) * 256;
-        dma_load_so<4>(rp, &sm.a[buf][f0], aoff[x], t * WK * 4);
-        dma_load_so<4>(rp, &sm.b[buf][f0], boff[x], t * WK * 4);
+        dma_load_so<4>(rpa, &sm.a[buf][f0], aoff[x], t * WK * 4);
+        dma_load_so<4>(rpb, &sm.b[buf][f0], boff[x], t * WK * 4);
       }
       return;
     }
 #pragma unroll
     for (int x = 0; x < 4; ++x) {
       const int f0 = (wave + 4 * x) * 256;
-      dma_load<4>(rp, &sm.a[buf][f0], aoff[x] == OOB ? OOB : aoff[x] + t * WK * 4);
-      dma_load<4>(rp, &sm.b[buf][f0], boff[x] == OOB ? OOB : boff[x] + t * WK * 4);
+      dma_load<4>(rpa, &sm.a[buf][f0], aoff[x] == OOB ? OOB : aoff[x] + t * WK * 4);
+      dma_load<4>(rpb, &sm.b[buf][f0], boff[x] == OOB ? OOB : boff[x] + t * WK * 4);
     }
   };
 
@@ -811,7 +815,8 @@ __device__ __forceinline__ void syrk_wide_block(WideLds& sm, float* __restrict__
     if (t + 1 < K / WK) step(t + 1, std::integral_constant<int, 1>{});
   }
   if (!act) return;
-  const __amdgpu_buffer_rsrc_t rd = matrix_rsrc(w + r0 * ld + r0, (int64_t)(R - 1) * ld + R);
+  // the block of D at rows r0 + I0 .., columns r0 + J0 .. (a resource based there: offsets below 128 rows)
+  const __amdgpu_buffer_rsrc_t rd = matrix_rsrc(w + (r0 + I0) * ld + r0 + J0, (int64_t)(arows - 1) * ld + WB);
 #pragma unroll
   for (int a = 0; a < 2; ++a)
 #pragma unroll
@@ -821,7 +826,7 @@ __device__ __forceinline__ void syrk_wide_block(WideLds& sm, float* __restrict__
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int i = I0 + 64 * wy + 32 * a + 8 * (r >> 2) + 4 * hh + (r & 3), j = J0 + 64 * wx + 32 * d + li;
-        off[r] = (i < R && j < C && j <= i) ? (i * ild + j) * 4 : OOB;
+        off[r] = (i < R && j < C && j <= i) ? ((i - I0) * ild + (j - J0)) * 4 : OOB;
         cur[r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rd, off[r], 0, 0));
       }
 #pragma unroll
@@ -953,7 +958,8 @@ struct CholeskyRun {
   CholeskyRun(T* w_, int64_t k_, int* info_, T* stage_, hipStream_t s, int64_t cb = 0, int64_t ce = -1)
       : w(w_), k(k_), info(info_), stage(stage_), stream(s), col_begin(cb), col_end(ce < 0 || ce > k_ ? k_ : ce),
         j0(cb) {
-    two_level = sizeof(T) == 4 && k % 4 == 0 && k * k < (int64_t)1 << 29;
+    // (the update kernels' offsets are relative to their blocks' rows: 128 ld floats, any k below 2^22)
+    two_level = sizeof(T) == 4 && k % 4 == 0 && k < ((int64_t)1 << 22);
     fuse = two_level && k * k >= 2 * (int64_t)PB * PB;
     done = j0 >= col_end;
     wg[0] = w_;
@@ -1170,8 +1176,9 @@ __global__ __launch_bounds__(256) void zero_upper_kernel(T* __restrict__ w, int6
 
 // A level product of the triangular inverse, D = alpha A B (tri = 1: B lower, 2: A lower): the MFMA
 // kernel that skips the zero triangle of the inverted block, or, where that kernel's layout
-// conditions do not hold (rows not on 16-byte boundaries, operands of 2^29 elements or more), the
-// library's general strided GEMM with the same triangular structure.
+// conditions do not hold (rows not on 16-byte boundaries), the
+// library's general strided GEMM with the same triangular structure.  (Sizes are not a condition: the MFMA
+// kernel's buffer offsets are relative to its block's rows and to each k-tile's rows.)
 int level_gemm(int64_t M, int64_t N, int64_t K, int64_t batch, const float* A, int64_t lda, int64_t sa,
                const float* B, int64_t ldb, int64_t sb, float* D, int64_t ldd, int64_t sd, float alpha, int tri,
                hipStream_t stream, int64_t ng = 1, int64_t mst = 0) {

@@ -66,8 +66,14 @@ __global__ __launch_bounds__(256, 2) void tri_gemm_kernel(TriGemm g, int64_t nbn
 
   const int tid = threadIdx.x, lane = tid & 63, li = lane & 31, hh = lane >> 5;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const __amdgpu_buffer_rsrc_t ra = matrix_rsrc(A, (int64_t)(M - 1) * lda + K);
-  const __amdgpu_buffer_rsrc_t rb = matrix_rsrc(B, (int64_t)(K - 1) * ldb + N);
+  // buffer resources based at the block's rows of A and, per k-tile, at the k-tile's rows of B, so that every
+  // byte offset stays below 128 rows of lda (A) or 32 rows of ldb (B) floats at any operand size
+  const int arows = M - I0 < TB ? M - I0 : TB;
+  const __amdgpu_buffer_rsrc_t ra = matrix_rsrc(A + (int64_t)I0 * lda, (int64_t)(arows - 1) * lda + K);
+  auto b_rsrc = [&](int k0) {
+    const int krows = K - k0 < KT ? K - k0 : KT;
+    return matrix_rsrc(B + (int64_t)k0 * ldb + J0, (int64_t)(krows - 1) * ldb + (N - J0));
+  };
 
   // per-lane staging of the wave's four 128-bit loads per panel and k-tile: A row `arow`, k-quad
   // akq (swizzled); B k-row bk, columns bcol .. bcol + 3
@@ -77,22 +83,23 @@ __global__ __launch_bounds__(256, 2) void tri_gemm_kernel(TriGemm g, int64_t nbn
     const int f = (wave + 4 * x) * 256 + 4 * lane;
     const int row = f >> 5, kq = ((f >> 2) & 7) ^ quad_swizzle(row);
     akk[x] = 4 * kq;
-    aoff[x] = I0 + row < M ? ((I0 + row) * lda + akk[x]) * 4 : OOB;
+    aoff[x] = row < arows ? (row * lda + akk[x]) * 4 : OOB;
     bk[x] = f >> 7;
-    const int col = J0 + (f & (TB - 1));
-    boff[x] = col < N ? (bk[x] * ldb + col) * 4 : OOB;
+    const int col = f & (TB - 1);
+    boff[x] = J0 + col < N ? (bk[x] * ldb + col) * 4 : OOB;
   }
   // a block whose rows and columns all lie inside D takes its interior k-tiles (every lane in range) with
   // the k offset in the loads' scalar field: no vector instruction beside the MFMA bursts
   const bool full = I0 + TB <= M && J0 + TB <= N;
   auto issue = [&](int t, int buf) {
     const int k0 = t * KT;
+    const __amdgpu_buffer_rsrc_t rb = b_rsrc(k0);
     if (full && k0 + KT <= K) {
 #pragma unroll
       for (int x = 0; x < 4; ++x) {
         const int f0 = (wave + 4 * x) * 256;
         dma_load_so<4>(ra, &sm.a[buf][f0], aoff[x], k0 * 4);
-        dma_load_so<4>(rb, &sm.b[buf][f0 + f0 / 256 * BPAD], boff[x], k0 * ldb * 4);
+        dma_load_so<4>(rb, &sm.b[buf][f0 + f0 / 256 * BPAD], boff[x], 0);
       }
       return;
     }
@@ -102,7 +109,7 @@ __global__ __launch_bounds__(256, 2) void tri_gemm_kernel(TriGemm g, int64_t nbn
       const bool aok = aoff[x] != OOB && k0 + akk[x] < K;
       dma_load<4>(ra, &sm.a[buf][f0], aok ? aoff[x] + k0 * 4 : OOB);
       const bool bok = boff[x] != OOB && k0 + bk[x] < K;
-      dma_load<4>(rb, &sm.b[buf][f0 + f0 / 256 * BPAD], bok ? boff[x] + k0 * ldb * 4 : OOB);
+      dma_load<4>(rb, &sm.b[buf][f0 + f0 / 256 * BPAD], bok ? boff[x] : OOB);
     }
   };
 
@@ -190,9 +197,9 @@ int gptq2d_tri_gemm_f32(const TriGemm& g, hipStream_t stream) {
   // 128-bit staging: rows and the block offsets of every operand on 16-byte boundaries
   if (g.K % 4 || g.N % 4 || g.lda % 4 || g.ldb % 4 || g.sa % 4 || g.sb % 4 || !aligned16(g.A) || !aligned16(g.B))
     return GPTQ2D_EUNSUPPORTED;
-  // 32-bit byte offsets inside each operand
+  // 32-bit byte offsets inside a block's 128 rows of A (plus K) and a k-tile's 32 rows of B (plus N)
   const int64_t lim = (int64_t)1 << 29;
-  if ((g.M - 1) * g.lda + g.K >= lim || (g.K - 1) * g.ldb + g.N >= lim || g.M * g.ldd >= lim || g.K == 0)
+  if (TB * g.lda + g.K >= lim || KT * g.ldb + g.N >= lim || g.M >= lim || g.N >= lim || g.K >= lim || g.K == 0)
     return GPTQ2D_EUNSUPPORTED;
   const int64_t nbm = (g.M + TB - 1) / TB, nbn = (g.N + TB - 1) / TB;
   if (nbm * nbn > 0x7fffffff) return GPTQ2D_EUNSUPPORTED;

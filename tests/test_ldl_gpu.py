@@ -8,8 +8,10 @@ factors, condition number < 1e3).
 """
 
 import ctypes
+import time
 
 import numpy as np
+
 import pytest
 import torch
 
@@ -257,6 +259,42 @@ def test_headline_size_fp32():
     err = ((got.double() - ref).abs().max() / ref.abs().max()).item()
     print(f"8192 fp32 vs fp64: max rel err {err:.2e}", flush=True)
     assert err < 1e-3
+
+
+@pytest.mark.timeout(600)
+def test_beyond_2_29_elements_fp32():
+    """A 24576 x 24576 fp32 factor (6.0e8 elements, past 2^29: the 28672-column Grams of a 70B MLP are larger
+    still) on the two-level Cholesky and the MFMA inverse levels, whose buffer offsets are relative to their
+    blocks' rows: structure, agreement with the fp64 path, and faster than the one-panel-per-launch sequence
+    (forced by a size that is not a multiple of 4)."""
+    k = 24576
+    gen = torch.Generator(device=DEV).manual_seed(5)
+    g = torch.randn(k, k // 2, generator=gen, device=DEV, dtype=torch.float64)
+    m64 = g @ g.t() / (k // 2)
+    m64.diagonal().add_(.1)
+    del g
+    m32 = m64.float()
+    LDL.ldl_of_inverse(m32[:512, :512])  # load and warm up
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    got = LDL.ldl_of_inverse(m32)
+    torch.cuda.synchronize()
+    t_two = time.perf_counter() - t0
+    assert torch.isfinite(got).all()
+    assert (got.diagonal() == 1).all() and (got.triu(1) == 0).all()
+    ref = LDL.ldl_of_inverse(m64)
+    err = ((got.double() - ref).abs().max() / ref.abs().max()).item()
+    del ref
+    m_odd = m32[:k - 2, :k - 2].contiguous()  # k % 4 != 0: the one-panel-per-launch sequence
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    LDL.ldl_of_inverse(m_odd)
+    torch.cuda.synchronize()
+    t_plain = time.perf_counter() - t0
+    print(f"{k} fp32 vs fp64: max rel err {err:.2e}; {1e3 * t_two:.0f} ms (two-level) against {1e3 * t_plain:.0f} ms "
+          f"(plain sequence, k = {k - 2})", flush=True)
+    assert err < 1e-3
+    assert t_two < t_plain
 
 
 @pytest.mark.parametrize("k", [3584, 7168])
