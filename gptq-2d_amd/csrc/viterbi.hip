@@ -337,12 +337,26 @@ __device__ void forward_pass(const Sequence<T, V> (&seq)[NS], const bool (&live)
 // One sequence per workgroup; thread tid owns the four groups j = 4 tid .. 4 tid + 3 (G <= 4 VT_THREADS) and
 // keeps the byte offsets of its (H / W) x 4 entries in the cost table in registers, two 16-bit offsets a
 // register.
+//
+// The states' reads are random gathers: 32 lanes of 8 bytes (W = 2) or 64 lanes of 4 bytes (W = 1) meet the
+// 64 four-byte banks, and the busiest bank sets the cycles of the read (3.4 deep on average for HYB's pairs
+// against 1).  With copies == 2 each step's table is written twice, the second copy with its entries rotated
+// in every row of banks (entry e of row r = e / NB at bank (e + r) mod NB, NB = 64 / W entries a row), and
+// bit 16 of ridx[s] sends state s's reads to the second copy: a host-side choice per state that spreads each
+// read's lanes over the banks (2.0 deep).  Either copy holds the same values.
 constexpr int ROWS_MAX = 1024;
+
+// the slot of entry e in the second copy: rotated by its row within its row of NB entries
+template <int W>
+__device__ __forceinline__ int second_slot(int e) {
+  constexpr int NB = 64 / W;
+  return (e & ~(NB - 1)) | ((e + e / NB) & (NB - 1));
+}
 
 template <int V, int H, int W>
 __device__ void forward_rows(const Sequence<float, V>& sq, const float* xs, bool live, const float* __restrict__ table,
-                             const float (&urow)[W][V], int E, const int* __restrict__ ridx, float* ctab,
-                             float* hist, float* prev_lds, const SearchGeom& g, int roll, bool masked,
+                             const float (&urow)[W][V], int E, int Ep, int copies, const int* __restrict__ ridx,
+                             float* ctab, float* hist, float* prev_lds, const SearchGeom& g, int roll, bool masked,
                              int64_t overlap, int64_t* best_state, float* red_v, int64_t* red_i) {
   constexpr int HE = H / W;  // entries per group
   using lds_f = __attribute__((address_space(3))) float*;
@@ -357,17 +371,28 @@ __device__ void forward_rows(const Sequence<float, V>& sq, const float* xs, bool
   const float inf = __builtin_huge_valf();
   const int j = 4 * tid;
   const bool owner = j < G32;
-  // the byte offsets of this thread's entries' costs, loaded here (not held across the walks back)
+  // the byte offsets of this thread's entries' costs in a buffer, loaded here (not held across the walks back):
+  // entry ridx & 0xffff (clamped to the table), in the second copy where bit 16 is set and two are written
+  const int cmask = copies - 1;
+  auto slot_bytes = [&](int r) -> uint32_t {  // branch-free: a branch per entry costs scalar registers
+    const int e = min(r & 0xffff, E - 1);
+    const int c = (r >> 16) & cmask;
+    return (uint32_t)(e + c * (Ep + second_slot<W>(e) - e)) * W * 4;
+  };
   uint32_t offp[HE][2];
 #pragma unroll
   for (int h = 0; h < HE; ++h)
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
-      const uint32_t o0 = owner ? (uint32_t)ridx[h * G32 + j + 2 * q] * W * 4 : 0u;
-      const uint32_t o1 = owner ? (uint32_t)ridx[h * G32 + j + 2 * q + 1] * W * 4 : 0u;
+      const uint32_t o0 = owner ? slot_bytes(ridx[h * G32 + j + 2 * q]) : 0u;
+      const uint32_t o1 = owner ? slot_bytes(ridx[h * G32 + j + 2 * q + 1]) : 0u;
       offp[h][q] = o0 | o1 << 16;
     }
-  // cost table of step t into buffer t & 1: row w of entry e at [(t & 1) E W + e W + w]
+  // cost table of step t into buffer t & 1 (copies Ep W floats each): row w of entry e at [(t & 1) B + e W + w],
+  // and with two copies also at [(t & 1) B + (Ep + second_slot(e)) W + w]
+  // (with one copy the second store repeats the first: a branch there costs the loop 20 registers)
+  const int B = copies * Ep * W;
+  const int second = copies == 2 ? (Ep + second_slot<W>(tid)) * W : tid * W;
   // x_t from the workgroup's LDS copy of the sequence (a global load here would put its latency on every
   // step's critical path, between the evaluations and the barrier)
   auto fill = [&](int t) {
@@ -383,26 +408,34 @@ __device__ void forward_rows(const Sequence<float, V>& sq, const float* xs, bool
           const float d1 = urow[w][V - 1] - x1;
           c = c + d1 * d1;
         }
-        ((lds_f)ctab)[(t & 1) * E * W + tid * W + w] = c;
+        ((lds_f)ctab)[(t & 1) * B + tid * W + w] = c;
+        ((lds_f)ctab)[(t & 1) * B + second + w] = c;
       }
     }
   };
-  fill(0);
-  __syncthreads();
-  for (int t = 0; t + 1 < g.steps; ++t) {
-    lds_cf prev = (lds_cf)(t == 0 ? prev_lds : prev_lds + ((t - 1) & 1) * g.G);
-    lds_f cur = (lds_f)(prev_lds + (t & 1) * g.G);
+  // one step; the first (no predecessor minima, the overlap mask) written apart from the loop of the others, so
+  // that the loop holds one version of the evaluations whatever the compiler makes of the rest
+  auto step = [&](int t, auto first_c) __attribute__((always_inline)) {
+    constexpr bool first = decltype(first_c)::value;
+    // 32-bit LDS indices: 64-bit ones take scalar register pairs, and at more than 80 scalar registers (with
+    // the trap handler's) two 1024-thread workgroups no longer fit a CU
+    lds_cf prev = (lds_cf)(first ? prev_lds : prev_lds + ((t - 1) & 1) * G32);
+    lds_f cur = (lds_f)(prev_lds + (t & 1) * G32);
     // the cost tables sit at the start of the workgroup's LDS: byte address = buffer base + offset
-    const uint32_t cbase = (uint32_t)((t & 1) * E * W * 4);
-    auto groups = [&](auto first_c) {
-      constexpr bool first = decltype(first_c)::value;
+    const uint32_t cbase = (uint32_t)((t & 1) * B * 4);
+    auto groups = [&]() {
       // the step's history row, addressed before the loop (the store after it is the only branch)
       float4* hrow = reinterpret_cast<float4*>(hist + (int64_t)t * g.G + j);
       float best[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) best[e] = inf;
-      // the predecessor group of state h G + j is h (G >> kv) + (j >> kv) (G is a multiple of 2^kv)
+      // the predecessor group of state h G + j is h (G >> kv) + (j >> kv) (G is a multiple of 2^kv), read
+      // through a pointer per w advanced by G >> kv at every h (opaque, so that the compiler does not turn the
+      // advances into one scalar register per (h, w): 15 of them would put the kernel past 80)
       const int pstride = G32 >> kv, pj = j >> kv;
+      lds_cf pp[W];
+#pragma unroll
+      for (int w = 0; w < W; ++w) pp[w] = prev + w * HE * pstride + pj;
       // costs of entry h's four groups, read one h ahead: the reads of h + 1 are in flight while h is evaluated
       auto read_costs = [&](int h, float (&c)[4][W]) __attribute__((always_inline)) {
         // opaque here, so that the halves are extracted at their use instead of unpacked into 4 HE registers
@@ -431,7 +464,12 @@ __device__ void forward_rows(const Sequence<float, V>& sq, const float* xs, bool
 #pragma unroll
         for (int w = 0; w < W; ++w) {
           const int ps = (h + w * HE) * pstride + pj;  // state (h + w HE) G + j
-          const float pv = first ? 0.f : prev[ps];
+          float pv = 0.f;
+          if constexpr (!first) {
+            pv = *pp[w];
+            pp[w] += pstride;
+            asm volatile("" : "+v"(pp[w]));
+          }
           const bool masked_out = first && masked && ps != overlap;
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
@@ -451,16 +489,15 @@ __device__ void forward_rows(const Sequence<float, V>& sq, const float* xs, bool
       *(lds_f4)(cur + j) = f4v{b4.x, b4.y, b4.z, b4.w};
       if (live) *hrow = b4;
     };
-    if (owner) {
-      if (t == 0)
-        groups(std::true_type{});
-      else
-        groups(std::false_type{});
-    }
+    if (owner) groups();
     // the next step's cost table (the last step's costs come from the table itself, in final_argmin)
     if (t + 2 < g.steps) fill(t + 1);
     __syncthreads();
-  }
+  };
+  fill(0);
+  __syncthreads();
+  if (g.steps > 1) step(0, std::true_type{});
+  for (int t = 1; t + 1 < g.steps; ++t) step(t, std::false_type{});
   const Sequence<float, V> seqs[1] = {sq};
   float* const hists[1] = {hist};
   const int64_t ovs[1] = {overlap};
@@ -567,14 +604,15 @@ __global__ __launch_bounds__(VT_THREADS) void viterbi_kernel(const T* __restrict
 
 // viterbi_kernel with the forward passes of forward_rows (fp32, one sequence per workgroup; G <= 4 VT_THREADS,
 // G % 4 == 0, 2^KV == H, E <= ROWS_MAX; the previous minima always in LDS).  Dynamic LDS: the cost tables
-// (2 x E x W floats, at LDS address 0 so that a 16-bit byte offset addresses them), the minima (2 G floats), then
-// the sequence (steps V floats).
+// (2 x copies x Ep x W floats, Ep = E for one copy, E rounded up to a row of 64 / W entries for two; at LDS
+// address 0 so that a 16-bit byte offset addresses them), the minima (2 G floats), then the sequence (steps V
+// floats).
 template <int V, int H, int W>
 __global__ __launch_bounds__(VT_THREADS) void viterbi_rows_kernel(const float* __restrict__ x,
                                                                   const float* __restrict__ table,
                                                                   const float* __restrict__ urows,
-                                                                  const int* __restrict__ ridx, int E,
-                                                                  float* __restrict__ hist_all,
+                                                                  const int* __restrict__ ridx, int E, int Ep,
+                                                                  int copies, float* __restrict__ hist_all,
                                                                   const float* __restrict__ scale,
                                                                   float* __restrict__ out,
                                                                   int64_t* __restrict__ states, int64_t rows, int L,
@@ -588,7 +626,7 @@ __global__ __launch_bounds__(VT_THREADS) void viterbi_rows_kernel(const float* _
   const Sequence<float, V> sq{x + row * (int64_t)steps * V, steps};
   float* hist = hist_all + row * (int64_t)(steps > 1 ? steps - 1 : 1) * g.G;
   float* ctab = reinterpret_cast<float*>(smem);
-  float* prev_lds = ctab + ((2 * E * W + 3) & ~3);
+  float* prev_lds = ctab + ((2 * copies * Ep * W + 3) & ~3);
   float* xs = prev_lds + 2 * g.G;  // the sequence, steps V floats
   for (int i = threadIdx.x; i < steps * V; i += VT_THREADS) xs[i] = sq.x[i];
   __syncthreads();  // the copy before any thread's first cost-table fill
@@ -602,8 +640,8 @@ __global__ __launch_bounds__(VT_THREADS) void viterbi_rows_kernel(const float* _
   int64_t overlap = 0;
   if (tail_biting) {
     const int half = steps / 2;
-    forward_rows<V, H, W>(sq, xs, true, table, urow, E, ridx, ctab, hist, prev_lds, g, steps - half, false, 0,
-                          sh_state, red_v, red_i);
+    forward_rows<V, H, W>(sq, xs, true, table, urow, E, Ep, copies, ridx, ctab, hist, prev_lds, g, steps - half,
+                          false, 0, sh_state, red_v, red_i);
     if (wave0) {
       const int64_t st = backtrack<float, V>(sq, table, hist, g, steps - half, false, 0, sh_state[0], half, 1.f,
                                              nullptr, nullptr);
@@ -612,8 +650,8 @@ __global__ __launch_bounds__(VT_THREADS) void viterbi_rows_kernel(const float* _
     __syncthreads();
     overlap = sh_overlap;
   }
-  forward_rows<V, H, W>(sq, xs, true, table, urow, E, ridx, ctab, hist, prev_lds, g, 0, tail_biting != 0, overlap,
-                        sh_state, red_v, red_i);
+  forward_rows<V, H, W>(sq, xs, true, table, urow, E, Ep, copies, ridx, ctab, hist, prev_lds, g, 0, tail_biting != 0,
+                        overlap, sh_state, red_v, red_i);
   if (wave0) {
     const float sc = scale ? scale[row] : 1.f;
     float* orow = out ? out + row * (int64_t)steps * V : nullptr;
@@ -624,25 +662,28 @@ __global__ __launch_bounds__(VT_THREADS) void viterbi_rows_kernel(const float* _
 
 template <int V, int H, int W>
 void launch_viterbi_rows(size_t lds, hipStream_t stream, const float* x, const float* table, const float* urows,
-                         const int* ridx, int E, float* hist, const float* scale, float* out, int64_t* states,
-                         int64_t rows, int L, int KV, int steps, int tail_biting) {
+                         const int* ridx, int E, int Ep, int copies, float* hist, const float* scale, float* out,
+                         int64_t* states, int64_t rows, int L, int KV, int steps, int tail_biting) {
   hipLaunchKernelGGL((viterbi_rows_kernel<V, H, W>), dim3((unsigned)rows), dim3(VT_THREADS), lds, stream, x, table,
-                     urows, ridx, E, hist, scale, out, states, rows, L, KV, steps, tail_biting);
+                     urows, ridx, E, Ep, copies, hist, scale, out, states, rows, L, KV, steps, tail_biting);
 }
 
 template <int V, int W>
 void launch_viterbi_rows_h(int H, size_t lds, hipStream_t stream, const float* x, const float* table,
-                           const float* urows, const int* ridx, int E, float* hist, const float* scale, float* out,
-                           int64_t* states, int64_t rows, int L, int KV, int steps, int tail_biting) {
+                           const float* urows, const int* ridx, int E, int Ep, int copies, float* hist,
+                           const float* scale, float* out, int64_t* states, int64_t rows, int L, int KV, int steps,
+                           int tail_biting) {
+  auto go = [&](auto kernel_h) {
+    constexpr int HH = decltype(kernel_h)::value;
+    launch_viterbi_rows<V, HH, W>(lds, stream, x, table, urows, ridx, E, Ep, copies, hist, scale, out, states, rows, L,
+                                  KV, steps, tail_biting);
+  };
   if (H == 4)
-    launch_viterbi_rows<V, 4, W>(lds, stream, x, table, urows, ridx, E, hist, scale, out, states, rows, L, KV, steps,
-                                 tail_biting);
+    go(std::integral_constant<int, 4>{});
   else if (H == 8)
-    launch_viterbi_rows<V, 8, W>(lds, stream, x, table, urows, ridx, E, hist, scale, out, states, rows, L, KV, steps,
-                                 tail_biting);
+    go(std::integral_constant<int, 8>{});
   else
-    launch_viterbi_rows<V, 16, W>(lds, stream, x, table, urows, ridx, E, hist, scale, out, states, rows, L, KV,
-                                  steps, tail_biting);
+    go(std::integral_constant<int, 16>{});
 }
 
 template <typename T, int V, int NS>
@@ -705,26 +746,36 @@ int viterbi_rows(const float* x, const float* table, const float* urows, const i
                         ((uintptr_t)hist & 15) == 0;
   // one sequence per workgroup: with two, the compiler spills the evaluation loop (two sequences' costs and
   // minima beside the offsets exceed the 128 registers of a 1024-thread workgroup); more rows than compute
-  // units queue as further rounds
-  const size_t lds = (size_t)2 * G * 4 + (size_t)((2 * E * W + 3) & ~3) * 4 + (size_t)steps * V * 4;
-  if (!shape_ok || lds > 96 * 1024)
+  // units queue as further rounds.  Two copies of the cost table where they fit beside a second workgroup on
+  // the CU (160 KB of LDS), or where one copy does not leave room for it either.
+  const int NB = 64 / W;
+  const int64_t Ep2 = (E + NB - 1) / NB * NB;
+  auto lds_of = [&](int64_t copies, int64_t ep) {
+    return (size_t)2 * G * 4 + (size_t)((2 * copies * ep * W + 3) & ~3) * 4 + (size_t)steps * V * 4;
+  };
+  constexpr size_t two_per_cu = 78 * 1024, most = 96 * 1024;
+  const bool two = lds_of(2, Ep2) <= most && (lds_of(2, Ep2) <= two_per_cu || lds_of(1, E) > two_per_cu);
+  const int copies = two ? 2 : 1;
+  const int Ep = (int)(two ? Ep2 : E);
+  const size_t lds = lds_of(copies, Ep);
+  if (!shape_ok || lds > most)
     return viterbi<float>(x, table, hist, scale, out, states, rows, steps, L, K, V, tail_biting, stream);
   const int H = 1 << KV;
   const int Ei = (int)E;
   if (W == 2) {
     if (V == 1)
-      launch_viterbi_rows_h<1, 2>(H, lds, stream, x, table, urows, ridx, Ei, hist, scale, out, states, rows, L, KV,
-                                  (int)steps, tail_biting);
+      launch_viterbi_rows_h<1, 2>(H, lds, stream, x, table, urows, ridx, Ei, Ep, copies, hist, scale, out, states,
+                                  rows, L, KV, (int)steps, tail_biting);
     else
-      launch_viterbi_rows_h<2, 2>(H, lds, stream, x, table, urows, ridx, Ei, hist, scale, out, states, rows, L, KV,
-                                  (int)steps, tail_biting);
+      launch_viterbi_rows_h<2, 2>(H, lds, stream, x, table, urows, ridx, Ei, Ep, copies, hist, scale, out, states,
+                                  rows, L, KV, (int)steps, tail_biting);
   } else {
     if (V == 1)
-      launch_viterbi_rows_h<1, 1>(H, lds, stream, x, table, urows, ridx, Ei, hist, scale, out, states, rows, L, KV,
-                                  (int)steps, tail_biting);
+      launch_viterbi_rows_h<1, 1>(H, lds, stream, x, table, urows, ridx, Ei, Ep, copies, hist, scale, out, states,
+                                  rows, L, KV, (int)steps, tail_biting);
     else
-      launch_viterbi_rows_h<2, 1>(H, lds, stream, x, table, urows, ridx, Ei, hist, scale, out, states, rows, L, KV,
-                                  (int)steps, tail_biting);
+      launch_viterbi_rows_h<2, 1>(H, lds, stream, x, table, urows, ridx, Ei, Ep, copies, hist, scale, out, states,
+                                  rows, L, KV, (int)steps, tail_biting);
   }
   return (int)hipGetLastError();
 }

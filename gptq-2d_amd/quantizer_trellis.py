@@ -24,6 +24,7 @@ from __future__ import annotations
 import weakref
 from typing import Callable
 
+import numpy as np
 import torch
 
 import _hip
@@ -117,8 +118,71 @@ def distinct_rows(table: torch.Tensor):
             found = (urows.view(torch.float32).contiguous(), pindex.to(torch.int32).contiguous(), 2)
     if found is None and R <= ROWS_MAX:
         found = (bits.view(torch.float32)[:, None, :].contiguous(), index.to(torch.int32).contiguous(), 1)
-    _rows_cache[key] = (weakref.ref(table, lambda _, k=key: _rows_cache.pop(k, None)), table._version, found)
+    _rows_cache[key] = (weakref.ref(table, lambda _, k=key: _rows_cache.pop(k, None)), table._version, found, {})
     return found
+
+
+def bank_copies(index: torch.Tensor, W: int, kv: int, sweeps: int = 2) -> torch.Tensor:
+    """``index`` with bit 16 set for the states whose cost the distinct-row search reads from the second copy
+    of its per-step cost table (``csrc/viterbi.hip``, ``second_slot``).
+
+    The search's thread t reads, at (h, e), the entry of state h G + 4 t + e (G = 2^(L - kv), h < 2^kv / W,
+    e < 4); 64 / W neighbouring threads read together (32 lanes of 8 bytes, or 64 of 4) and wait for the busiest
+    of the 64 four-byte banks.  Entry x lies at bank x mod NB of the first copy and (x + x div NB) mod NB of the
+    second (NB = 64 / W entries a bank row).  Per read, each distinct entry in turn takes the copy whose bank is
+    less loaded, then ``sweeps`` passes move each to the other copy where that is less loaded: the busiest bank
+    of HYB's pair reads drops from 3.4 to 2.0 on average.  Lanes that read one entry read one copy (a broadcast).
+    Either copy holds the same values, so any choice gives the same search."""
+    idx = index.cpu().numpy().astype(np.int64)
+    he = (1 << kv) // W
+    G = idx.size // he
+    nl = nb = 64 // W
+    T = min(G // 4, 1024)  # threads that own groups
+    tp = -(-T // nl) * nl
+    tid = np.arange(tp)
+    st = np.stack([h * G + 4 * tid + e for h in range(he) for e in range(4)])  # [he 4, tp] states
+    st = np.where(tid[None, :] < T, st, -1).reshape(-1, nl)  # [reads, lanes]
+    ent = np.where(st >= 0, idx[np.maximum(st, 0)], -1)
+    valid = ent >= 0
+    e0 = np.maximum(ent, 0)
+    banks = np.stack((e0 % nb, (e0 + e0 // nb) % nb))  # [2, reads, lanes]
+    n = ent.shape[0]
+    first = np.argmax((ent[:, :, None] == ent[:, None, :]) & valid[:, :, None], axis=2)
+    lead = (first == np.arange(nl)[None, :]) & valid
+    rows = np.arange(n)
+    load = np.zeros((n, nb), np.int64)
+    pick = np.zeros((n, nl), np.int64)
+    for sweep in range(sweeps + 1):
+        for i in range(nl):
+            m = lead[:, i]
+            if sweep:  # take the lane's entry off its bank, then place it again
+                np.add.at(load, (rows[m], banks[pick[m, i], rows[m], i]), -1)
+            l0, l1 = load[rows, banks[0, :, i]], load[rows, banks[1, :, i]]
+            pick[:, i] = np.where(l1 == l0, pick[:, i], l1 < l0)
+            np.add.at(load, (rows[m], banks[pick[m, i], rows[m], i]), 1)
+    pick = np.take_along_axis(pick, first, 1)
+    out = idx.copy()
+    ok = st >= 0
+    out[st[ok]] |= pick[ok] << 16
+    return torch.from_numpy(out.astype(np.int32)).to(index.device)
+
+
+def rows_index(table: torch.Tensor, kv: int):
+    """``distinct_rows(table)`` with its index as the search reads it for K V = kv: (urows, index | copy << 16,
+    W) with the copies of ``bank_copies``, or None.  Cached beside the rows; None under graph capture when not
+    yet computed."""
+    found = distinct_rows(table)
+    if found is None:
+        return None
+    per_kv = _rows_cache[id(table)][3]
+    ridx = per_kv.get(kv)
+    if ridx is None:
+        urows, index, W = found
+        he = (1 << kv) // W
+        if torch.cuda.is_current_stream_capturing() or he < 1 or index.numel() % he:
+            return None
+        ridx = per_kv[kv] = bank_copies(index, W, kv)
+    return found[0], ridx, found[2]
 
 
 def trellis_quantize_hip(x: torch.Tensor, table: torch.Tensor, K: int, tail_biting: bool = True, *,
@@ -152,7 +216,7 @@ def trellis_quantize_hip(x: torch.Tensor, table: torch.Tensor, K: int, tail_biti
     size = int(_hip.lib().gptq2d_viterbi_workspace(cap, steps, L, K, V))
     hist = x.new_empty(size)
     with torch.cuda.device(x.device):
-        urows = distinct_rows(tab) if tab is table else None
+        urows = rows_index(tab, K * V) if tab is table else None
         if urows is not None:
             _hip.call_untyped("viterbi_rows_f32", _hip.ptr(seq), _hip.ptr(tab), _hip.ptr(urows[0]), _hip.ptr(urows[1]),
                               urows[0].size(0), urows[2], _hip.ptr(hist), _hip.ptr(sc), _hip.ptr(out),

@@ -224,8 +224,10 @@ int64_t gptq2d_sweep_fused_noalloc_capacity(int32_t elem_bytes);
  * pairs of the rows of states s and s + 2^(L-1) (HYB: 512 look-up rows with both signs, in either order: 1024).  Where 1 <= E <= 1024,
  * 2 <= K*V <= 4, max(4, 2^(K*V)) <= 2^(L-K*V) <= 4096 and table and hist are 16-byte aligned (e.g. HYB L = 16,
  * K*V = 4), each step first evaluates the entries' costs and the states read theirs from LDS (the same values,
- * so the same search); other shapes run gptq2d_viterbi_f32.  Other arguments and the result as
- * gptq2d_viterbi_f32 (quantizer_trellis.py:146-341, 82-143). */
+ * so the same search); other shapes run gptq2d_viterbi_f32.  Bit 16 of ridx[s] (the entry in bits 0-15) sends
+ * state s's reads to a second copy of the step's costs, placed in other LDS banks, where the two copies fit
+ * beside a second workgroup per CU; it is ignored otherwise, and never changes the result.  Other arguments
+ * and the result as gptq2d_viterbi_f32 (quantizer_trellis.py:146-341, 82-143). */
 int gptq2d_viterbi_rows_f32(const float* x, const float* table, const float* urows, const int32_t* ridx, int64_t E,
                             int32_t W, float* hist, const float* scale, float* out, int64_t* states, int64_t rows,
                             int64_t steps, int32_t L, int32_t K, int32_t V, int32_t tail_biting, void* stream);

@@ -123,8 +123,9 @@ def _generic(monkeypatch):
 @pytest.mark.parametrize("rows", [1, 7, 256, 300, 512])
 def test_distinct_rows_search_equals_plain(monkeypatch, rows):
     """Tables with few distinct rows (HYB L = 16, 1MAD L = 16, and L = 12 tables drawn from 5-300 distinct rows
-    with K V = 2, 3, 4) are searched from per-step cost tables; the states and values equal the plain search's
-    bit for bit, with and without tail-biting, for a row count below, at and above the compute units."""
+    with K V = 2, 3, 4) are searched from per-step cost tables, written twice with each state's copy chosen by
+    ``bank_copies``; the states and values equal the plain search's bit for bit, with and without tail-biting,
+    for a row count below, at and above the compute units."""
     g = torch.Generator().manual_seed(17 + rows)
     cases = [(QT.hyb(device=DEV), 2), (QT.one_mad(device=DEV), 4), (QT.one_mad(device=DEV), 2)]
     for (L, V, K), distinct in zip(((12, 2, 1), (12, 1, 3), (12, 2, 2), (12, 1, 4)), (5, 300, 64, 1024)):
@@ -141,6 +142,22 @@ def test_distinct_rows_search_equals_plain(monkeypatch, rows):
                 _generic(mp)
                 v_plain, s_plain = QT.trellis_quantize_hip(x, table, K, tb)
             assert s_rows.equal(s_plain) and v_rows.equal(v_plain), (table.size(0), V, K, tb)
+
+
+def test_distinct_rows_one_copy(monkeypatch):
+    """Sequences so long that two copies of the cost table leave no room for a second workgroup per CU (HYB,
+    T = 4096) take one copy and ignore the copy bits; sequences whose minima and costs exceed the LDS take the
+    plain search.  Both equal the plain search bit for bit."""
+    g = torch.Generator().manual_seed(5)
+    table = QT.hyb(device=DEV)
+    for T in (4096, 16384):
+        x = torch.randn(3, T, generator=g).to(DEV)
+        v_rows, s_rows = QT.trellis_quantize_hip(x, table, 2, True)
+        assert (QT.rows_index(table, 4)[1] >> 16).any()  # copy bits were passed
+        with pytest.MonkeyPatch.context() as mp:
+            _generic(mp)
+            v_plain, s_plain = QT.trellis_quantize_hip(x, table, 2, True)
+        assert s_rows.equal(s_plain) and v_rows.equal(v_plain), T
 
 
 def test_distinct_rows_cache():
