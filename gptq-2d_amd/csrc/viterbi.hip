@@ -353,7 +353,7 @@ __device__ __forceinline__ int second_slot(int e) {
   return (e & ~(NB - 1)) | ((e + e / NB) & (NB - 1));
 }
 
-template <int V, int H, int W>
+template <int V, int H, int W, int PS>
 __device__ void forward_rows(const Sequence<float, V>& sq, const float* xs, bool live, const float* __restrict__ table,
                              const float (&urow)[W][V], int E, int Ep, int copies, const int* __restrict__ ridx,
                              float* ctab, float* hist, float* prev_lds, const SearchGeom& g, int roll, bool masked,
@@ -397,7 +397,7 @@ __device__ void forward_rows(const Sequence<float, V>& sq, const float* xs, bool
   // step's critical path, between the evaluations and the barrier)
   auto fill = [&](int t) {
     if (tid < E) {
-      const int tt = (t + roll) % g.steps;
+      const int tt = t + roll < g.steps ? t + roll : t + roll - g.steps;  // roll < steps
       const float x0 = ((lds_cf)xs)[tt * V];
       const float x1 = V == 2 ? ((lds_cf)xs)[tt * V + 1] : 0.f;
 #pragma unroll
@@ -429,10 +429,11 @@ __device__ void forward_rows(const Sequence<float, V>& sq, const float* xs, bool
       float best[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) best[e] = inf;
-      // the predecessor group of state h G + j is h (G >> kv) + (j >> kv) (G is a multiple of 2^kv), read
-      // through a pointer per w advanced by G >> kv at every h (opaque, so that the compiler does not turn the
-      // advances into one scalar register per (h, w): 15 of them would put the kernel past 80)
-      const int pstride = G32 >> kv, pj = j >> kv;
+      // the predecessor group of state h G + j is h (G >> kv) + (j >> kv) (G is a multiple of 2^kv).  With
+      // G >> kv known at compile time (PS) the reads take immediate offsets; otherwise they go through a
+      // pointer per w advanced by G >> kv at every h (opaque, so that the compiler does not turn the advances
+      // into one scalar register per (h, w): 15 of them would put the kernel past 80)
+      const int pstride = PS ? PS : G32 >> kv, pj = j >> kv;
       lds_cf pp[W];
 #pragma unroll
       for (int w = 0; w < W; ++w) pp[w] = prev + w * HE * pstride + pj;
@@ -466,9 +467,13 @@ __device__ void forward_rows(const Sequence<float, V>& sq, const float* xs, bool
           const int ps = (h + w * HE) * pstride + pj;  // state (h + w HE) G + j
           float pv = 0.f;
           if constexpr (!first) {
-            pv = *pp[w];
-            pp[w] += pstride;
-            asm volatile("" : "+v"(pp[w]));
+            if constexpr (PS != 0) {
+              pv = pp[0][(h + w * HE) * PS];
+            } else {
+              pv = *pp[w];
+              pp[w] += pstride;
+              asm volatile("" : "+v"(pp[w]));
+            }
           }
           const bool masked_out = first && masked && ps != overlap;
 #pragma unroll
@@ -607,7 +612,7 @@ __global__ __launch_bounds__(VT_THREADS) void viterbi_kernel(const T* __restrict
 // (2 x copies x Ep x W floats, Ep = E for one copy, E rounded up to a row of 64 / W entries for two; at LDS
 // address 0 so that a 16-bit byte offset addresses them), the minima (2 G floats), then the sequence (steps V
 // floats).
-template <int V, int H, int W>
+template <int V, int H, int W, int PS>
 __global__ __launch_bounds__(VT_THREADS) void viterbi_rows_kernel(const float* __restrict__ x,
                                                                   const float* __restrict__ table,
                                                                   const float* __restrict__ urows,
@@ -640,7 +645,7 @@ __global__ __launch_bounds__(VT_THREADS) void viterbi_rows_kernel(const float* _
   int64_t overlap = 0;
   if (tail_biting) {
     const int half = steps / 2;
-    forward_rows<V, H, W>(sq, xs, true, table, urow, E, Ep, copies, ridx, ctab, hist, prev_lds, g, steps - half,
+    forward_rows<V, H, W, PS>(sq, xs, true, table, urow, E, Ep, copies, ridx, ctab, hist, prev_lds, g, steps - half,
                           false, 0, sh_state, red_v, red_i);
     if (wave0) {
       const int64_t st = backtrack<float, V>(sq, table, hist, g, steps - half, false, 0, sh_state[0], half, 1.f,
@@ -650,7 +655,7 @@ __global__ __launch_bounds__(VT_THREADS) void viterbi_rows_kernel(const float* _
     __syncthreads();
     overlap = sh_overlap;
   }
-  forward_rows<V, H, W>(sq, xs, true, table, urow, E, Ep, copies, ridx, ctab, hist, prev_lds, g, 0, tail_biting != 0,
+  forward_rows<V, H, W, PS>(sq, xs, true, table, urow, E, Ep, copies, ridx, ctab, hist, prev_lds, g, 0, tail_biting != 0,
                         overlap, sh_state, red_v, red_i);
   if (wave0) {
     const float sc = scale ? scale[row] : 1.f;
@@ -660,11 +665,11 @@ __global__ __launch_bounds__(VT_THREADS) void viterbi_rows_kernel(const float* _
   }
 }
 
-template <int V, int H, int W>
+template <int V, int H, int W, int PS>
 void launch_viterbi_rows(size_t lds, hipStream_t stream, const float* x, const float* table, const float* urows,
                          const int* ridx, int E, int Ep, int copies, float* hist, const float* scale, float* out,
                          int64_t* states, int64_t rows, int L, int KV, int steps, int tail_biting) {
-  hipLaunchKernelGGL((viterbi_rows_kernel<V, H, W>), dim3((unsigned)rows), dim3(VT_THREADS), lds, stream, x, table,
+  hipLaunchKernelGGL((viterbi_rows_kernel<V, H, W, PS>), dim3((unsigned)rows), dim3(VT_THREADS), lds, stream, x, table,
                      urows, ridx, E, Ep, copies, hist, scale, out, states, rows, L, KV, steps, tail_biting);
 }
 
@@ -673,17 +678,20 @@ void launch_viterbi_rows_h(int H, size_t lds, hipStream_t stream, const float* x
                            const float* urows, const int* ridx, int E, int Ep, int copies, float* hist,
                            const float* scale, float* out, int64_t* states, int64_t rows, int L, int KV, int steps,
                            int tail_biting) {
-  auto go = [&](auto kernel_h) {
-    constexpr int HH = decltype(kernel_h)::value;
-    launch_viterbi_rows<V, HH, W>(lds, stream, x, table, urows, ridx, E, Ep, copies, hist, scale, out, states, rows, L,
-                                  KV, steps, tail_biting);
+  auto go = [&](auto kernel_h, auto kernel_ps) {
+    constexpr int HH = decltype(kernel_h)::value, PS = decltype(kernel_ps)::value;
+    launch_viterbi_rows<V, HH, W, PS>(lds, stream, x, table, urows, ridx, E, Ep, copies, hist, scale, out, states,
+                                      rows, L, KV, steps, tail_biting);
   };
+  using rt = std::integral_constant<int, 0>;
   if (H == 4)
-    go(std::integral_constant<int, 4>{});
+    go(std::integral_constant<int, 4>{}, rt{});
   else if (H == 8)
-    go(std::integral_constant<int, 8>{});
+    go(std::integral_constant<int, 8>{}, rt{});
+  else if (L == 16)  // HYB and 1MAD at L = 16, K V = 4: the predecessor stride 2^(L - 2 K V) = 256 at compile time
+    go(std::integral_constant<int, 16>{}, std::integral_constant<int, 256>{});
   else
-    go(std::integral_constant<int, 16>{});
+    go(std::integral_constant<int, 16>{}, rt{});
 }
 
 template <typename T, int V, int NS>
