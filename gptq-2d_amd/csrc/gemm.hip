@@ -366,18 +366,57 @@ __global__ __launch_bounds__(256, 2) void gemm_mfma_vec_kernel(GemmProblem<float
 
 constexpr int DT = 64, DK = 32;
 
+// Tiles of a problem in the order the kernel takes them, heaviest k range first, so that the shortest tiles
+// fill in behind the longest instead of the longest starting last (issued row by row, a triangular operand's
+// product took 77% of the dense product's time, not half).  A lower triangular square D takes only its lower
+// triangle of tiles (the others would be empty).
+enum TileOrder : int32_t {
+  ORDER_ROWS = 0,
+  ORDER_COLS_UP = 1,
+  ORDER_COLS_DOWN = 2,
+  ORDER_ROWS_DOWN = 3,
+  ORDER_LOWER = 4,
+};
+
+__host__ __device__ inline TileOrder tile_order(const GemmProblem<double>& p, int64_t tm, int64_t tn) {
+  if (p.a_tri == TRI_NONE && p.b_tri == TRI_NONE && p.d_tri == TRI_LOWER && tm == tn) return ORDER_LOWER;
+  if (p.a_tri == TRI_LOWER) return ORDER_ROWS_DOWN;  // work grows with the row
+  if (p.a_tri == TRI_NONE && p.b_tri == TRI_LOWER) return ORDER_COLS_UP;  // work falls with the column
+  if (p.a_tri == TRI_NONE && p.b_tri == TRI_UPPER) return ORDER_COLS_DOWN;  // work grows with the column
+  return ORDER_ROWS;  // equal work, or work falling with the row (A upper)
+}
+
+__device__ __forceinline__ void tile_of(TileOrder o, int64_t id, int64_t tm, int64_t tn, int64_t& ti, int64_t& tj) {
+  switch (o) {
+    case ORDER_LOWER: {  // id = ti (ti + 1) / 2 + tj, tj <= ti
+      int64_t r = (int64_t)((__builtin_sqrt(8.0 * (double)id + 1.0) - 1.0) * 0.5);
+      while (r * (r + 1) / 2 > id) --r;
+      while ((r + 1) * (r + 2) / 2 <= id) ++r;
+      ti = r;
+      tj = id - r * (r + 1) / 2;
+      return;
+    }
+    case ORDER_COLS_UP: tj = id / tm; ti = id % tm; return;
+    case ORDER_COLS_DOWN: tj = tn - 1 - id / tm; ti = id % tm; return;
+    case ORDER_ROWS_DOWN: ti = tm - 1 - id / tn; tj = id % tn; return;
+    default: ti = id / tn; tj = id % tn; return;
+  }
+}
+
 // 256 threads = 4 waves; wave w owns the 32 x 32 quadrant (w / 2, w % 2) of the 64 x 64 tile as 2 x 2 blocks
 // of v_mfma_f64_16x16x4_f64, whose lane l supplies A(l % 16, l / 16) and B(l / 16, l % 16) and whose
 // accumulator element r of lane l holds D(l / 16 + 4 r, l % 16).  K is staged through LDS 32 deep, with the
 // next k-block loaded into registers while the current one's MFMAs run; the loads apply the operands'
 // triangle masks.
-__global__ __launch_bounds__(256) void gemm_mfma64_kernel(GemmProblem<double> p) {
+__global__ __launch_bounds__(256) void gemm_mfma64_kernel(GemmProblem<double> p, TileOrder order) {
   typedef double double4_t __attribute__((ext_vector_type(4)));
   constexpr int AL = DT * DK / 256;  // staged entries per thread and operand
   __shared__ double As[DK][DT + 1];
   __shared__ double Bs[DK][DT + 1];
   const int64_t bi = blockIdx.z;
-  const int64_t i0 = (int64_t)blockIdx.y * DT, j0 = (int64_t)blockIdx.x * DT;
+  int64_t ti, tj;
+  tile_of(order, blockIdx.x, cdiv(p.M, DT), cdiv(p.N, DT), ti, tj);
+  const int64_t i0 = ti * DT, j0 = tj * DT;
   const int64_t i1 = i0 + DT < p.M ? i0 + DT : p.M, j1 = j0 + DT < p.N ? j0 + DT : p.N;
   const TileRange kr = tile_k_range(p, i0, i1, j0, j1);
   if (kr.empty) return;
@@ -460,8 +499,12 @@ int gptq2d_gemm(const GemmProblem<T>& p, hipStream_t stream) {
   if (p.M == 0 || p.N == 0 || p.batch == 0) return 0;
   if (p.batch > 65535) return GPTQ2D_EUNSUPPORTED;
   if constexpr (sizeof(T) == 8) {
-    const dim3 grid((unsigned)cdiv(p.N, DT), (unsigned)cdiv(p.M, DT), (unsigned)p.batch);
-    hipLaunchKernelGGL(gemm_mfma64_kernel, grid, dim3(256), 0, stream, p);
+    const int64_t tm = cdiv(p.M, DT), tn = cdiv(p.N, DT);
+    const TileOrder order = tile_order(p, tm, tn);
+    const int64_t tiles = order == ORDER_LOWER ? tm * (tm + 1) / 2 : tm * tn;
+    if (tiles > 0x7fffffff) return GPTQ2D_EUNSUPPORTED;
+    const dim3 grid((unsigned)tiles, 1u, (unsigned)p.batch);
+    hipLaunchKernelGGL(gemm_mfma64_kernel, grid, dim3(256), 0, stream, p, order);
     return (int)hipGetLastError();
   } else {
     bool bk = false;

@@ -36,12 +36,15 @@ def _gemm(M, N, K, batch, a, b, d, alpha, beta, a_tri=0, b_tri=0, d_tri=0, a_t=F
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
 @pytest.mark.parametrize("M,N,K", [(200, 300, 77), (128, 128, 16), (257, 129, 33), (64, 64, 1000), (5, 700, 9),
                                    (1000, 6, 64), (320, 256, 96), (130, 260, 36)])
-@pytest.mark.parametrize("tri", [(0, 0, 0), (1, 0, 0), (0, 1, 0), (0, 0, 1), (2, 2, 0), (1, 1, 1)])
+@pytest.mark.parametrize("tri", [(0, 0, 0), (1, 0, 0), (0, 1, 0), (0, 0, 1), (2, 0, 0), (0, 2, 0), (2, 2, 0),
+                                 (1, 1, 1)])
 @pytest.mark.parametrize("b_layout", ["nk", "kn"])
 def test_gemm(dtype, M, N, K, tri, b_layout):
     """Strided GEMM with triangular operand structure against a host fp64 product; the structurally zero
     parts hold NaN, which must not reach the result.  B is either a transposed view (contiguous along k)
-    or contiguous along j, which selects the two layouts of the vectorised MFMA path."""
+    or contiguous along j, which selects the two layouts of the vectorised MFMA path.  The structures cover
+    every fp64 tile order (rows, rows from the last, columns from the first or the last, a square lower D's
+    triangle of tiles)."""
     print(f"gemm {M}x{N}x{K} {dtype} tri={tri} B {b_layout}", flush=True)
     g = torch.Generator().manual_seed(M * 7 + N * 3 + K)
     batch = 2
