@@ -8,6 +8,7 @@
 // rows or columns on the VALU path (64 x 64 tile, 4 x 4 outputs per thread); fp64 on MFMA
 // (v_mfma_f64_16x16x4_f64, 64 x 64 tile).
 #include "linalg.h"
+#include "lds_dma.h"
 
 namespace {
 
@@ -479,7 +480,220 @@ __global__ __launch_bounds__(256) void gemm_mfma64_kernel(GemmProblem<double> p,
         store_d(p, d, i0 + wi + 16 * r + kq + 4 * e, j0 + wj + 16 * c + li, acc[r][c][e]);
 }
 
+// ------------------------------------------------------------------------------------------------ MFMA path (fp64, LDS-direct)
+
+// D = beta D + alpha A B with A's rows and B's rows (BKN: B(k, j) = b[k b_rs + j]) or columns (!BKN: B(k, j) =
+// b[j b_cs + k]) contiguous -- the LDL's products.  The tile order, output tile and MFMA blocks of
+// gemm_mfma64_kernel; k-tiles of 32 loaded one ahead straight into LDS (128-bit buffer loads with the LDS
+// destination bit), double-buffered, one barrier per k-tile.  LDS layouts (as the fp64 outer flush's): a row
+// panel (A, and B for !BKN) holds row r's 16 k-pairs at pair positions q ^ (r % 16), so that the 16 rows that
+// one cycle of a 128-bit read takes cover the 64 banks; a k-row panel (B for BKN) holds 64 columns per k-row
+// plus 16 doubles per 8 k-rows, so that the k-rows k and k + 8 that a half-wave reads together fall 32 banks
+// apart.  A k-tile that crosses a triangle's edge or the end of the k range is zeroed where the product may
+// not read it, in LDS after it has landed (one more barrier); the others are multiplied as loaded.
+constexpr int GT = 64, GK = 32;         // tile edge, k-tile depth (doubles)
+constexpr int GBGRP = 512, GBPAD = 16;  // k-row panel: 16 doubles of padding per 8 k-rows of 64
+
+template <bool BKN>
+struct Gemm64Lds {
+  static constexpr int BSZ = BKN ? GT * GK + GT * GK / GBGRP * GBPAD : GT * GK;
+  double a[2][GT * GK];
+  double b[2][BSZ];
+};
+
+template <bool BKN>
+__global__ __launch_bounds__(256, 2) void gemm_mfma64_dma_kernel(GemmProblem<double> p, TileOrder order) {
+  typedef double double4_t __attribute__((ext_vector_type(4)));
+  __shared__ __align__(16) Gemm64Lds<BKN> sm;
+  int64_t ti, tj;
+  tile_of(order, blockIdx.x, cdiv(p.M, GT), cdiv(p.N, GT), ti, tj);
+  const int64_t i0 = ti * GT, j0 = tj * GT;
+  const int64_t i1 = i0 + GT < p.M ? i0 + GT : p.M, j1 = j0 + GT < p.N ? j0 + GT : p.N;
+  const TileRange kr = tile_k_range(p, i0, i1, j0, j1);
+  if (kr.empty) return;
+  const int64_t bi = blockIdx.z;
+  const double* a = p.A + bi * p.a_bs;
+  const double* b = p.B + bi * p.b_bs;
+  double* d = p.D + bi * p.d_bs;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int K = (int)p.K, arows = (int)(i1 - i0), bcols = (int)(j1 - j0);
+  const int64_t k_lo = kr.k_lo, k_hi = kr.k_hi;
+  const int nt = k_lo < k_hi ? (int)((k_hi - k_lo + GK - 1) / GK) : 0;
+
+  // resources: A from the tile's first row; B (BKN) from each k-tile's first row and the tile's first
+  // column, B (!BKN) from the tile's first column
+  const __amdgpu_buffer_rsrc_t ra =
+      matrix_rsrc(reinterpret_cast<const float*>(a + i0 * p.a_rs), 2 * ((int64_t)(arows - 1) * p.a_rs + K));
+  auto b_rsrc = [&](int64_t k0) {
+    if constexpr (BKN) {
+      const int64_t krows = p.K - k0 < GK ? p.K - k0 : GK;
+      return matrix_rsrc(reinterpret_cast<const float*>(b + k0 * p.b_rs + j0), 2 * ((krows - 1) * p.b_rs + bcols));
+    } else {
+      return matrix_rsrc(reinterpret_cast<const float*>(b + j0 * p.b_cs), 2 * ((int64_t)(bcols - 1) * p.b_cs + K));
+    }
+  };
+  // each wave's four 128-bit loads per panel and k-tile: chunk c = wave + 4 x of 128 doubles (1 KB)
+  int aoff[4], boff[4];
+#pragma unroll
+  for (int x = 0; x < 4; ++x) {
+    const int c = wave + 4 * x;
+    const int row = 4 * c + (lane >> 4), kk = 2 * ((lane & 15) ^ (row & 15));  // row panel: row, first k
+    aoff[x] = row < arows ? (int)((row * p.a_rs + kk) * 8) : OOB;
+    if constexpr (BKN) {
+      const int kr2 = 2 * c + (lane >> 5), jj = 2 * (lane & 31);  // k-row panel: k-row, first column
+      boff[x] = jj < bcols ? (int)((kr2 * p.b_rs + jj) * 8) : OOB;
+    } else {
+      boff[x] = row < bcols ? (int)((row * p.b_cs + kk) * 8) : OOB;
+    }
+  }
+  const bool full = arows == GT && bcols == GT;
+  // whether k-tile t needs the triangle / k-range pass (uniform)
+  auto ragged = [&](int64_t k0) {
+    return k0 + GK > k_hi || (p.a_tri == TRI_LOWER && k0 + GK - 1 > i0) || (p.a_tri == TRI_UPPER && k0 < i1 - 1) ||
+           (p.b_tri == TRI_LOWER && k0 < j1 - 1) || (p.b_tri == TRI_UPPER && k0 + GK - 1 > j0);
+  };
+  auto issue = [&](int t, int buf) {
+    const int64_t k0 = k_lo + (int64_t)t * GK;
+    const __amdgpu_buffer_rsrc_t rb = b_rsrc(k0);
+    const int ak = (int)(k0 * 8);
+#pragma unroll
+    for (int x = 0; x < 4; ++x) {
+      const int f0 = (wave + 4 * x) * 128;
+      const int bf0 = BKN ? f0 + f0 / GBGRP * GBPAD : f0;
+      if (full && k0 + GK <= p.K) {  // every lane in range: the k offset in the scalar field (which the range
+                                     // check does not cover, so never for a k-tile that reaches past K)
+        dma_load_so<4>(ra, reinterpret_cast<float*>(&sm.a[buf][f0]), aoff[x], ak);
+        if constexpr (BKN)
+          dma_load<4>(rb, reinterpret_cast<float*>(&sm.b[buf][bf0]), boff[x]);
+        else
+          dma_load_so<4>(rb, reinterpret_cast<float*>(&sm.b[buf][bf0]), boff[x], ak);
+      } else {
+        dma_load<4>(ra, reinterpret_cast<float*>(&sm.a[buf][f0]), aoff[x] == OOB ? OOB : aoff[x] + ak);
+        if constexpr (BKN)
+          dma_load<4>(rb, reinterpret_cast<float*>(&sm.b[buf][bf0]), boff[x]);
+        else
+          dma_load<4>(rb, reinterpret_cast<float*>(&sm.b[buf][bf0]), boff[x] == OOB ? OOB : boff[x] + ak);
+      }
+    }
+  };
+  // zero what the product may not read in a landed k-tile: k at or past k_hi, and the operands' zero triangles
+  auto clear = [&](int t, int buf) {
+    const int64_t k0 = k_lo + (int64_t)t * GK;
+    for (int f = tid; f < GT * GK; f += 256) {
+      const int row = f / GK, q = (f % GK) / 2, e = f % 2;
+      const int64_t k = k0 + 2 * (q ^ (row & 15)) + e;  // the element at f of a row panel
+      const int64_t i = i0 + row;
+      if (k >= k_hi || (p.a_tri == TRI_LOWER && k > i) || (p.a_tri == TRI_UPPER && k < i)) sm.a[buf][f] = 0.;
+      if constexpr (BKN) {
+        const int kk = f / GT, jj = f % GT;
+        const int64_t kb = k0 + kk, j = j0 + jj;
+        if (kb >= k_hi || (p.b_tri == TRI_LOWER && kb < j) || (p.b_tri == TRI_UPPER && kb > j))
+          sm.b[buf][kk * GT + jj + kk / (GBGRP / GT) * GBPAD] = 0.;
+      } else {
+        const int64_t j = j0 + row;
+        if (k >= k_hi || (p.b_tri == TRI_LOWER && k < j) || (p.b_tri == TRI_UPPER && k > j)) sm.b[buf][f] = 0.;
+      }
+    }
+  };
+
+  double4_t acc[2][2];
+#pragma unroll
+  for (int r = 0; r < 2; ++r)
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[r][c][e] = 0.;
+  // fragments: lane (li, hh) supplies A(row 32 wi + 16 a2 + li, k) and B(k, column 32 wj + 16 d2 + li) with
+  // k = 8 hh + 2 v + s2 in MFMA (v, s2)
+  const int li = lane & 15, hh = lane >> 4;
+  const int wi = wave >> 1, wj = wave & 1;
+  const int a_base = (32 * wi + li) * GK;
+  const int b_base = BKN ? 8 * hh * GT + 32 * wj + li + hh * GBPAD : (32 * wj + li) * GK;
+  auto step = [&](int t, auto cur_c) {
+    constexpr int cur = decltype(cur_c)::value;
+    __syncthreads();  // buffer cur has landed; buffer 1 - cur is no longer read
+    if (ragged(k_lo + (int64_t)t * GK)) {
+      clear(t, cur);
+      __syncthreads();
+    }
+    if (t + 1 < nt) issue(t + 1, 1 - cur);
+    const double* as = &sm.a[cur][a_base];
+    const double* bs = &sm.b[cur][b_base];
+    double2 fa[2][2], fbv[2][2];  // [slot][block]
+    double fb[2][2][2];           // [slot][block][s2] (BKN)
+    auto frag = [&](int v, int slot) {
+#pragma unroll
+      for (int a2 = 0; a2 < 2; ++a2)
+        fa[slot][a2] = *reinterpret_cast<const double2*>(as + a2 * 16 * GK + 2 * ((4 * hh + v) ^ li));
+#pragma unroll
+      for (int d2 = 0; d2 < 2; ++d2) {
+        if constexpr (BKN) {
+#pragma unroll
+          for (int s2 = 0; s2 < 2; ++s2) fb[slot][d2][s2] = bs[16 * d2 + (2 * v + s2) * GT];
+        } else {
+          fbv[slot][d2] = *reinterpret_cast<const double2*>(bs + d2 * 16 * GK + 2 * ((4 * hh + v) ^ li));
+        }
+      }
+    };
+    frag(0, 0);
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      if (v < 3) frag(v + 1, (v + 1) & 1);
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+        for (int a2 = 0; a2 < 2; ++a2)
+#pragma unroll
+          for (int d2 = 0; d2 < 2; ++d2) {
+            const double av = s2 ? fa[v & 1][a2].y : fa[v & 1][a2].x;
+            double bv;
+            if constexpr (BKN)
+              bv = fb[v & 1][d2][s2];
+            else
+              bv = s2 ? fbv[v & 1][d2].y : fbv[v & 1][d2].x;
+            acc[a2][d2] = __builtin_amdgcn_mfma_f64_16x16x4f64(av, bv, acc[a2][d2], 0, 0, 0);
+          }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    wait_dma();  // this wave's loads of k-tile t + 1 have landed before the next barrier
+  };
+  if (nt > 0) {
+    issue(0, 0);
+    wait_dma();
+    for (int t = 0; t < nt; t += 2) {
+      step(t, std::integral_constant<int, 0>{});
+      if (t + 1 < nt) step(t + 1, std::integral_constant<int, 1>{});
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < 2; ++r)
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        store_d(p, d, i0 + 32 * wi + 16 * r + hh + 4 * e, j0 + 32 * wj + 16 * c + li, acc[r][c][e]);
+}
+
 bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15) == 0; }
+
+// The LDS-direct fp64 path applies: A's rows and B's rows (bkn) or columns contiguous, every row stride, batch
+// stride and K in whole 16-byte pairs, both operands on 16-byte boundaries, and every byte offset inside a
+// 64-row (or 32 k-row) panel below 2^30.
+bool dma64_ok(const GemmProblem<double>& p, bool& bkn) {
+  constexpr int64_t lim = (int64_t)1 << 27;  // doubles
+  if (p.a_cs != 1 || p.a_rs <= 0 || p.a_rs % 2 || p.a_bs % 2 || !aligned16(p.A)) return false;
+  if (p.K <= 0 || p.K % 2 || GT * p.a_rs + p.K >= lim || !aligned16(p.B) || p.b_bs % 2) return false;
+  if (p.b_cs == 1 && p.b_rs > 0 && p.b_rs % 2 == 0 && p.N % 2 == 0 && GK * p.b_rs + p.N < lim) {
+    bkn = true;
+    return true;
+  }
+  if (p.b_rs == 1 && p.b_cs > 0 && p.b_cs % 2 == 0 && GT * p.b_cs + p.K < lim) {
+    bkn = false;
+    return true;
+  }
+  return false;
+}
 
 // The vectorised path applies: strides, offsets and the K extent in float4 granules.
 bool vec_ok(const GemmProblem<float>& p, bool& bk) {
@@ -504,7 +718,15 @@ int gptq2d_gemm(const GemmProblem<T>& p, hipStream_t stream) {
     const int64_t tiles = order == ORDER_LOWER ? tm * (tm + 1) / 2 : tm * tn;
     if (tiles > 0x7fffffff) return GPTQ2D_EUNSUPPORTED;
     const dim3 grid((unsigned)tiles, 1u, (unsigned)p.batch);
-    hipLaunchKernelGGL(gemm_mfma64_kernel, grid, dim3(256), 0, stream, p, order);
+    bool bkn = false;
+    if (dma64_ok(p, bkn)) {
+      if (bkn)
+        hipLaunchKernelGGL(gemm_mfma64_dma_kernel<true>, grid, dim3(256), 0, stream, p, order);
+      else
+        hipLaunchKernelGGL(gemm_mfma64_dma_kernel<false>, grid, dim3(256), 0, stream, p, order);
+    } else {
+      hipLaunchKernelGGL(gemm_mfma64_kernel, grid, dim3(256), 0, stream, p, order);
+    }
     return (int)hipGetLastError();
   } else {
     bool bk = false;
