@@ -2,11 +2,12 @@
 //
 // D = beta D + alpha A B over arbitrary element strides, so the callers express transposes,
 // reversals (negative strides) and sub-blocks without copies.  Structurally zero parts of
-// triangular operands are skipped in the K loop and masked at load time, so they are never
-// read.  fp32 runs on the MFMA path (v_mfma_f32_32x32x2_f32: 128 x 128 output tile per
-// workgroup, four waves of 64 x 64, K staged through LDS 16 deep), fp32 products of fewer than 64
-// rows or columns on the VALU path (64 x 64 tile, 4 x 4 outputs per thread); fp64 on MFMA
-// (v_mfma_f64_16x16x4_f64, 64 x 64 tile).
+// triangular operands are skipped in the K loop and masked (at load time, or in LDS after an
+// LDS-direct load), so they never reach the result.  fp32 runs on the MFMA path
+// (v_mfma_f32_32x32x2_f32: 128 x 128 output tile per workgroup, four waves of 64 x 64, K staged
+// through LDS 16 deep), fp32 products of fewer than 64 rows or columns on the VALU path (64 x 64 tile,
+// 4 x 4 outputs per thread); fp64 on MFMA (v_mfma_f64_16x16x4_f64, 64 x 64 tile), with LDS-direct
+// double-buffered panels where the operands' rows (A) and rows or columns (B) are contiguous.
 #include "linalg.h"
 #include "lds_dma.h"
 
