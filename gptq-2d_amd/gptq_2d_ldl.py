@@ -8,7 +8,9 @@ M are supported.  Everything runs on the current stream of M's device in blocked
 (reverse-order Cholesky, recursive-doubling triangular inverse, normalisation; the GEMM-shaped
 parts on fp32 MFMA).  A matrix that is not positive definite raises
 ``torch.linalg.LinAlgError`` as ``torch.linalg.cholesky`` does; ``check=False`` skips that test
-(it is the only host synchronisation) so that the call can be captured in a graph.
+(it is the only host synchronisation) so that ``ldl_of_inverse`` and ``ldl`` can be captured in a graph.
+``feedback_factors_of_grams``, which spreads the two factors over three side streams, refuses to run
+under stream capture: capture the two ``ldl_of_inverse`` calls instead.
 """
 
 from __future__ import annotations
@@ -87,6 +89,9 @@ def feedback_factors_of_grams(G: torch.Tensor, H: torch.Tensor, super_entry_shap
     its own stream, its matrices sharing the Cholesky launches in groups of up to 16.  Bitwise equal to the
     two ldl_of_inverse calls.  No counterpart in the reference, whose callers compute the two factors one
     after the other (demo.ipynb cell 5)."""
+    if torch.cuda.is_available() and torch.cuda.is_current_stream_capturing():
+        raise RuntimeError("feedback_factors_of_grams runs on three side streams and cannot be captured in a graph; "
+                           "capture ldl_of_inverse(G, p) and ldl_of_inverse(H, q).T instead")
     p, q = super_entry_shape
     main = torch.cuda.current_stream(G.device)
     streams = _side_streams(G.device)
