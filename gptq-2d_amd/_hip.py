@@ -46,7 +46,7 @@ _SIGNATURES = {
     "ldl_of_inverse": [_P, _P, _P, _P, _I64, _I64, _I64, _P],
     "ldl": [_P, _P, _P, _P, _I64, _I64, _I64, _P],
     "ldl_of_inverse_part": [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I32, _P],
-    "ldl_of_inverse_pair": [_P, _P, _P, _P, _I64, _I64, _P, _P, _P, _P, _I64, _I64, _P, _P, _P],
+    "ldl_of_inverse_pair": [_P, _P, _P, _P, _I64, _I64, _P, _P, _P, _P, _I64, _I64, _I32, _P, _P, _P],
     "gemm": [_I64, _I64, _I64, _I64, _P, _I64, _I64, _I64, _P, _I64, _I64, _I64, _P, _I64, _I64, _I64, _F64, _F64,
              _I32, _I32, _I32, _P],
     "viterbi": [_P, _P, _P, _P, _P, _P, _I64, _I64, _I32, _I32, _I32, _I32, _P],

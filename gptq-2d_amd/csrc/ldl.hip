@@ -586,6 +586,34 @@ __global__ __launch_bounds__(256) void normalize_unit_kernel(T* __restrict__ out
   }
 }
 
+// U = L^T for unit (size 1) normalisation: U(i, j) = L_raw(j, i) / L_raw(i, i) above the diagonal, 1 on it, 0
+// below -- the same quotients as L(j, i), so U is L's transpose bit for bit.  L_raw(j, i) = w[base + j rs + i cs]
+// runs along j with stride rs (the reversed copy of ldl_of_inverse: rs = -1), so threads along j read and write
+// contiguously without an LDS transpose.
+template <typename T>
+__global__ __launch_bounds__(256) void normalize_unit_upper_kernel(T* __restrict__ out, const T* __restrict__ w,
+                                                                   int64_t k, int64_t base, int64_t rs, int64_t cs,
+                                                                   int64_t mstride) {
+  out += (int64_t)blockIdx.z * mstride;
+  w += (int64_t)blockIdx.z * mstride;
+  __shared__ T diag[32];
+  const int64_t i0 = (int64_t)blockIdx.y * 32, j0 = (int64_t)blockIdx.x * 32;
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
+  if (threadIdx.x < 32) {
+    const int64_t i = i0 + threadIdx.x;
+    diag[threadIdx.x] = i < k ? w[base + i * rs + i * cs] : T(1);
+  }
+  __syncthreads();
+  for (int yy = ty; yy < 32; yy += 8) {
+    const int64_t i = i0 + yy, j = j0 + tx;
+    if (i >= k || j >= k) continue;
+    T v = T(0);
+    if (j == i) v = T(1);
+    else if (j > i) v = w[base + j * rs + i * cs] / diag[yy];
+    out[i * k + j] = v;
+  }
+}
+
 // Block normalisation for p x p blocks (p <= NB): a workgroup owns column block b and 64 rows.
 // Rows below the block get L_raw(i, block) D_b^{-1}; the block itself becomes I; rows above, 0.
 template <typename T, int NB>
@@ -1361,19 +1389,20 @@ int trtri_inplace(T* w, int64_t k, T* tmp, hipStream_t stream, int64_t ng = 1, i
 
 template <typename T>
 int normalize(T* out, const T* w, int64_t k, int64_t size, int64_t base, int64_t rs, int64_t cs, hipStream_t stream,
-              int64_t ng = 1, int64_t mst = 0);
+              int64_t ng = 1, int64_t mst = 0, bool upper = false);
 
 // Part `phase` (1, 2, 3 as at trtri_split) of the inverse of the Cholesky factor in work and the
 // normalisation into out (L_raw(i, j) = C^{-1}(k-1-j, k-1-i) = work[(k-1-j) k + (k-1-i)]).  Without
 // a split, part 1 does nothing, part 2 is the whole inverse and part 3 the normalisation.  ng > 1: the
 // same part of a group of ng matrices k^2 elements apart (out and w alike), in one launch per step.
 template <typename T>
-int trtri_part(T* out, T* w, int64_t k, int64_t size, int phase, hipStream_t stream, int64_t ng = 1) {
+int trtri_part(T* out, T* w, int64_t k, int64_t size, int phase, hipStream_t stream, int64_t ng = 1,
+               bool upper = false) {
   const int64_t s = trtri_split<T>(k), mst = k * k;
   int rc = 0;
   if (s == 0) {
     if (phase == 2) return trtri_inplace<T>(w, k, out, stream, ng, mst);
-    if (phase == 3) return normalize<T>(out, w, k, size, (k - 1) * k + (k - 1), -1, -k, stream, ng, mst);
+    if (phase == 3) return normalize<T>(out, w, k, size, (k - 1) * k + (k - 1), -1, -k, stream, ng, mst, upper);
     return 0;
   }
   if constexpr (sizeof(T) == 4) {
@@ -1389,7 +1418,7 @@ int trtri_part(T* out, T* w, int64_t k, int64_t size, int phase, hipStream_t str
       if ((rc = level_gemm(L.n2, s, L.n2, 1, w + s * k + s, k, 0, out + L.t_off, s, 0, w + s * k, k, 0, -1.f, 2,
                            stream, ng, mst)))
         return rc;
-      return normalize<T>(out, w, k, size, (k - 1) * k + (k - 1), -1, -k, stream, ng, mst);
+      return normalize<T>(out, w, k, size, (k - 1) * k + (k - 1), -1, -k, stream, ng, mst, upper);
     }
   }
   return rc;
@@ -1397,10 +1426,14 @@ int trtri_part(T* out, T* w, int64_t k, int64_t size, int phase, hipStream_t str
 
 template <typename T>
 int normalize(T* out, const T* w, int64_t k, int64_t size, int64_t base, int64_t rs, int64_t cs, hipStream_t stream,
-              int64_t ng, int64_t mst) {
+              int64_t ng, int64_t mst, bool upper) {
   constexpr int NB = LdlBlock<T>::NB;
   // ng matrices mst elements apart (out and w alike) as blockIdx.z
-  if (size == 1) {
+  if (upper) {  // U = L^T (unit diagonal only)
+    if (size != 1) return GPTQ2D_EUNSUPPORTED;
+    const dim3 grid((unsigned)cdiv(k, 32), (unsigned)cdiv(k, 32), (unsigned)ng);
+    hipLaunchKernelGGL(normalize_unit_upper_kernel<T>, grid, dim3(256), 0, stream, out, w, k, base, rs, cs, mst);
+  } else if (size == 1) {
     const dim3 grid((unsigned)cdiv(k, 32), (unsigned)cdiv(k, 32), (unsigned)ng);
     hipLaunchKernelGGL(normalize_unit_kernel<T>, grid, dim3(256), 0, stream, out, w, k, base, rs, cs, mst);
   } else {
@@ -1479,11 +1512,12 @@ int pair_events(hipEvent_t (&ev)[4]) {
 // workgroups' arithmetic, in another order of launches).
 template <typename T>
 int ldl_of_inverse_pair(const T* const* m, T* const* out, T* const* work, int* const* info, const int64_t* k,
-                        const int64_t* size, hipStream_t const* stream) {
+                        const int64_t* size, bool upper1, hipStream_t const* stream) {
   for (int f = 0; f < 2; ++f) {
     if (k[f] < 0 || size[f] <= 0 || (k[f] > 0 && k[f] % size[f])) return GPTQ2D_EINVAL;
     if (size[f] > 1 && size[f] > LdlBlock<T>::NB) return GPTQ2D_EUNSUPPORTED;
   }
+  if (upper1 && size[1] != 1) return GPTQ2D_EUNSUPPORTED;  // U = L^T: unit diagonal only
   if (stream[0] == stream[1] || stream[0] == stream[2] || stream[1] == stream[2]) return GPTQ2D_EINVAL;
   hipEvent_t ev[4];  // per factor: Cholesky past the split (on stream[f]), part 1 done (on stream[2])
   int rc;
@@ -1527,7 +1561,7 @@ int ldl_of_inverse_pair(const T* const* m, T* const* out, T* const* work, int* c
     for (int f = 0; f < 2; ++f) {
       if ((rc = trtri_part<T>(out[f], work[f], k[f], size[f], 2, stream[f]))) return rc;
       if (f == 0 && split[0] && hipStreamWaitEvent(stream[0], ev[2], 0) != hipSuccess) return GPTQ2D_EUNSUPPORTED;
-      if ((rc = trtri_part<T>(out[f], work[f], k[f], size[f], 3, stream[f]))) return rc;
+      if ((rc = trtri_part<T>(out[f], work[f], k[f], size[f], 3, stream[f], 1, f == 1 && upper1))) return rc;
     }
     return 0;
   }
@@ -1553,7 +1587,7 @@ int ldl_of_inverse_pair(const T* const* m, T* const* out, T* const* work, int* c
     if (k[f] == 0) continue;
     if ((rc = trtri_part<T>(out[f], work[f], k[f], size[f], 2, stream[f]))) return rc;
     if (split[f] && hipStreamWaitEvent(stream[f], ev[2 + f], 0) != hipSuccess) return GPTQ2D_EUNSUPPORTED;
-    if ((rc = trtri_part<T>(out[f], work[f], k[f], size[f], 3, stream[f]))) return rc;
+    if ((rc = trtri_part<T>(out[f], work[f], k[f], size[f], 3, stream[f], 1, f == 1 && upper1))) return rc;
   }
   return 0;
 }
@@ -1625,14 +1659,15 @@ GPTQ2D_LDL_ABI(f64, double)
   }                                                                                                                 \
   int gptq2d_ldl_of_inverse_pair_##SUF(const T* m0, T* out0, T* work0, int* info0, int64_t k0, int64_t size0,      \
                                        const T* m1, T* out1, T* work1, int* info1, int64_t k1, int64_t size1,      \
-                                       hipStream_t stream0, hipStream_t stream1, hipStream_t stream2) {            \
+                                       int32_t upper1, hipStream_t stream0, hipStream_t stream1,                   \
+                                       hipStream_t stream2) {                                                      \
     const T* m[2] = {m0, m1};                                                                                       \
     T* out[2] = {out0, out1};                                                                                       \
     T* work[2] = {work0, work1};                                                                                    \
     int* info[2] = {info0, info1};                                                                                  \
     const int64_t k[2] = {k0, k1}, size[2] = {size0, size1};                                                        \
     const hipStream_t st[3] = {stream0, stream1, stream2};                                                          \
-    return ldl_of_inverse_pair<T>(m, out, work, info, k, size, st);                                                  \
+    return ldl_of_inverse_pair<T>(m, out, work, info, k, size, upper1 != 0, st);                                     \
   }
 
 GPTQ2D_LDL_PART_ABI(f32, float)

@@ -107,6 +107,7 @@ def feedback_factors_of_grams(G: torch.Tensor, H: torch.Tensor, super_entry_shap
         assert size <= MAX_BLOCK[m.dtype], f"diagonal blocks up to {MAX_BLOCK[m.dtype]} are supported for {m.dtype}"
         jobs.append((m, size, k))
     out = []
+    upper = False  # whether out[1] holds U itself (else the second factor, U its transpose)
     with torch.cuda.device(G.device):
         # each factor's buffers on its stream's pool
         bufs = []
@@ -125,11 +126,13 @@ def feedback_factors_of_grams(G: torch.Tensor, H: torch.Tensor, super_entry_shap
                     _hip.call("ldl_of_inverse", src.dtype, _hip.ptr(src), _hip.ptr(o), _hip.ptr(w), _hip.ptr(info),
                               src.size(0), k, size, _hip.stream(m.device))
         elif sa.dtype == sb.dtype and sa.size(0) == sb.size(0):
+            # U = ldl_of_inverse(H)^T written by the library (unit diagonal): no transposed copy in the sweep
+            upper = pb == 1
             sp = [ctypes.c_void_p(s.cuda_stream) for s in streams]
             for b in range(sa.size(0)):
                 _hip.call("ldl_of_inverse_pair", sa.dtype, _hip.ptr(sa[b]), _hip.ptr(oa[b]), _hip.ptr(wa[b]),
                           _hip.ptr(ia[b:b + 1]), ka, pa, _hip.ptr(sb[b]), _hip.ptr(ob[b]), _hip.ptr(wb[b]),
-                          _hip.ptr(ib[b:b + 1]), kb, pb, *sp)
+                          _hip.ptr(ib[b:b + 1]), kb, pb, int(upper), *sp)
         else:  # one matrix each, of different dtypes: each factor on its own stream
             for s, (m, size, k), (src, o, w, info) in zip(streams, jobs, bufs):
                 with torch.cuda.stream(s):
@@ -144,7 +147,7 @@ def feedback_factors_of_grams(G: torch.Tensor, H: torch.Tensor, super_entry_shap
         for t, m in zip(out, (G, H)):
             if not bool(torch.isfinite(t).all()):
                 ldl_of_inverse(m, size=1)  # raises the LinAlgError with the failing minor
-    return out[0], out[1].transpose(-1, -2)
+    return out[0], out[1] if upper else out[1].transpose(-1, -2)
 
 
 def feedback_factors(A: torch.Tensor, B: torch.Tensor, super_entry_shape=(1, 1)):

@@ -159,10 +159,11 @@ extern "C" {
    * one device).  Two fp32 matrices of one size share every Cholesky launch; other pairs are         \
    * enqueued panel by panel, alternating.  The inverse of a factor's leading block starts as soon as \
    * its factorisation has passed it, and the normalisations wait for it.  Results equal two          \
-   * gptq2d_ldl_of_inverse calls bit for bit. */                                                     \
+   * gptq2d_ldl_of_inverse calls bit for bit; with upper1 != 0 (size1 == 1 only) out1 receives the     \
+   * transpose of the second factor (U = L^T, the sweep's upper factor) written directly. */         \
   int gptq2d_ldl_of_inverse_pair_##SUF(const T* m0, T* out0, T* work0, int* info0, int64_t k0, int64_t size0,      \
                                        const T* m1, T* out1, T* work1, int* info1, int64_t k1, int64_t size1,      \
-                                       void* stream0, void* stream1, void* stream2);                               \
+                                       int32_t upper1, void* stream0, void* stream1, void* stream2);               \
   /* Unit lower (block) triangular L with M = L Lambda L^T (ldl, gptq_2d_reference.py:52-55). */       \
   int gptq2d_ldl_##SUF(const T* m, T* out, T* work, int* info, int64_t batch, int64_t k, int64_t size,              \
                        void* stream);                                                                               \

@@ -320,6 +320,7 @@ def test_split_inverse_fp32(k):
     b = instances.wishart_factor(k, .5, 80 + k, device=DEV).float()
     lo, up = LDL.feedback_factors_of_grams(m, b, check=False)
     assert lo.equal(got) and up.equal(LDL.ldl_of_inverse(b, check=False).t())
+    assert up.is_contiguous()  # U written by the library, not a transposed view
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
@@ -348,7 +349,12 @@ def test_info_zeroed_by_library(dtype, k):
     for s in streams:
         s.wait_stream(torch.cuda.current_stream())
     _hip.call("ldl_of_inverse_pair", dtype, _hip.ptr(m), _hip.ptr(out), _hip.ptr(work), _hip.ptr(infos[0:1]), k, 1,
-              _hip.ptr(m1), _hip.ptr(out1), _hip.ptr(work1), _hip.ptr(infos[1:2]), k, 1,
+              _hip.ptr(m1), _hip.ptr(out1), _hip.ptr(work1), _hip.ptr(infos[1:2]), k, 1, 0,
               *(ctypes.c_void_p(s.cuda_stream) for s in streams))
     torch.cuda.synchronize()
     assert infos.tolist() == [0, 0]
+    if k:  # U = L^T only for unit diagonal blocks: a block size with upper1 is refused before any launch
+        with pytest.raises(_hip.GPTQ2DError):
+            _hip.call("ldl_of_inverse_pair", dtype, _hip.ptr(m), _hip.ptr(out), _hip.ptr(work), _hip.ptr(infos[0:1]),
+                      k, 1, _hip.ptr(m1), _hip.ptr(out1), _hip.ptr(work1), _hip.ptr(infos[1:2]), k, 2, 1,
+                      *(ctypes.c_void_p(s.cuda_stream) for s in streams))
