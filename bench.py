@@ -63,10 +63,10 @@ FLUSH_ALGORITHMIC_BYTES = 0.489e9
 # The same two counter passes give the other kernels' HBM bytes, from which the line reports their achieved
 # HBM rates against the live timings: a tile-stage launch at OUTER_BLOCK on the headline layer (FETCH_SIZE
 # 13703.9 KiB x 1.9997 + WRITE_SIZE 2479.6 KiB, mean over a step's 511 launches) and one Viterbi call of the
-# benchmark's search (FETCH_SIZE 130677.4 KiB x 2.0 + WRITE_SIZE 2081299.5 KiB: its step-minimum history);
+# benchmark's search (FETCH_SIZE 132672.3 KiB x 2.0 + WRITE_SIZE 2081294.9 KiB: its step-minimum history);
 # profiles/flush_traffic_H_int4.md, profiles/counters_H_int4.md and profiles/viterbi_hyb_counters.md.
 TILE_STAGE_TRAFFIC_BYTES = 30.60e6
-VITERBI_TRAFFIC_BYTES = 2.399e9
+VITERBI_TRAFFIC_BYTES = 2.403e9
 # fp32 VALU operations per trellis state evaluation of the plain search: 2 sub, 2 mul, 1 add (the squared
 # distance), 1 add (the predecessor group's minimum), 1 min.
 OPS_PER_STATE_EVAL = 7
