@@ -226,25 +226,51 @@ __global__ __launch_bounds__(256) void flush_mfma_kernel(T* __restrict__ y, T* _
     product(accr, arow, alo, ahi, ub + (j < j1 ? j : 0), n, 0, bhi, k_lo, k_hi);
   }
 
-  // ---------------- epilogue: only the targets receive the feedback
+  // ---------------- epilogue: only the targets receive the feedback.  Every load of C and Y first, then the
+  // new values, then the stores: entry by entry, each load would wait behind the previous entry's stores
+  // (the compiler cannot prove the entries distinct), one memory round trip per entry and matrix.
+  T cv[2][2][4], yv[2][2][4];
+  uint32_t ok = 0;
 #pragma unroll
   for (int d = 0; d < 2; ++d) {
     const int64_t j = j0 + wj + 16 * d + li;
-    if (j >= j1) continue;
     const int64_t jc = j / g.Q;
 #pragma unroll
     for (int a = 0; a < 2; ++a)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int64_t i = i0 + wi + 16 * a + M::row(kq, r);
-        if (i >= i1) continue;
         const int64_t st = i / g.P + jc;
-        if (st < g.s1 || st >= g.s_end) continue;
-        const int64_t off = mat + i * n + j;
-        c[off] = c[off] + accd[a][d][r];
-        y[off] = (y[off] + accd[a][d][r]) + accr[a][d][r];
+        cv[a][d][r] = yv[a][d][r] = T(0);
+        if (j < j1 && i < i1 && st >= g.s1 && st < g.s_end) {
+          ok |= 1u << (8 * d + 4 * a + r);
+          const int64_t off = mat + i * n + j;
+          cv[a][d][r] = c[off];
+          yv[a][d][r] = y[off];
+        }
       }
   }
+#pragma unroll
+  for (int d = 0; d < 2; ++d)
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        cv[a][d][r] = cv[a][d][r] + accd[a][d][r];
+        yv[a][d][r] = (yv[a][d][r] + accd[a][d][r]) + accr[a][d][r];
+        asm volatile("" : "+v"(cv[a][d][r]), "+v"(yv[a][d][r]));  // here, not inside the stores' branches
+      }
+#pragma unroll
+  for (int d = 0; d < 2; ++d)
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        if ((ok >> (8 * d + 4 * a + r)) & 1) {
+          const int64_t off = mat + (i0 + wi + 16 * a + M::row(kq, r)) * n + (j0 + wj + 16 * d + li);
+          c[off] = cv[a][d][r];
+          y[off] = yv[a][d][r];
+        }
 }
 
 }  // namespace

@@ -49,14 +49,42 @@ __device__ __forceinline__ T load_b(const GemmProblem<T>& p, const T* b, int64_t
   return b[k * p.b_rs + j * p.b_cs];
 }
 
-template <typename T>
-__device__ __forceinline__ void store_d(const GemmProblem<T>& p, T* d, int64_t i, int64_t j, T acc) {
-  if (i >= p.M || j >= p.N) return;
-  if (p.d_tri == TRI_LOWER && j > i) return;
-  if (p.d_tri == TRI_UPPER && j < i) return;
-  T* dst = d + i * p.d_rs + j * p.d_cs;
-  const T v = p.alpha * acc;
-  *dst = p.beta == T(0) ? v : p.beta * *dst + v;
+// D = beta D + alpha acc for NV outputs of one lane, output x at (i, j) = at(x): every load of D first, then
+// every new value (outside the stores' branches, so that one wait covers all loads), then the stores.
+// Output by output (load, wait, store), the compiler must keep each load behind the previous store --
+// through one pointer with run-time strides it cannot prove two outputs distinct -- and a tile's epilogue
+// waited on one memory round trip per output (16 to 64 in a row).  Same arithmetic as one output at a
+// time; D is not read where beta = 0.
+template <int NV, typename T, typename At>
+__device__ __forceinline__ void store_d_group(const GemmProblem<T>& p, T* d, const T (&acc)[NV], At at) {
+  static_assert(NV <= 64, "one mask bit per output");
+  T old[NV];
+  uint64_t ok = 0;
+#pragma unroll
+  for (int x = 0; x < NV; ++x) {
+    int64_t i, j;
+    at(x, i, j);
+    const bool in = i < p.M && j < p.N && !(p.d_tri == TRI_LOWER && j > i) && !(p.d_tri == TRI_UPPER && j < i);
+    old[x] = T(0);
+    if (in) {
+      ok |= 1ull << x;
+      if (p.beta != T(0)) old[x] = d[i * p.d_rs + j * p.d_cs];
+    }
+  }
+#pragma unroll
+  for (int x = 0; x < NV; ++x) {
+    const T v = p.alpha * acc[x];
+    old[x] = p.beta == T(0) ? v : p.beta * old[x] + v;
+    asm volatile("" : "+v"(old[x]));  // computed here: not sunk into the store's branch, behind a wait of its own
+  }
+#pragma unroll
+  for (int x = 0; x < NV; ++x) {
+    if ((ok >> x) & 1) {
+      int64_t i, j;
+      at(x, i, j);
+      d[i * p.d_rs + j * p.d_cs] = old[x];
+    }
+  }
 }
 
 // ------------------------------------------------------------------------------------------------ VALU path
@@ -104,10 +132,13 @@ __global__ __launch_bounds__(256) void gemm_valu_kernel(GemmProblem<T> p) {
     }
     __syncthreads();
   }
+  T out[16];
 #pragma unroll
-  for (int r = 0; r < 4; ++r)
-#pragma unroll
-    for (int c = 0; c < 4; ++c) store_d(p, d, i0 + ty + 16 * r, j0 + tx + 16 * c, acc[r][c]);
+  for (int x = 0; x < 16; ++x) out[x] = acc[x / 4][x % 4];
+  store_d_group(p, d, out, [&](int x, int64_t& i, int64_t& j) {
+    i = i0 + ty + 16 * (x / 4);
+    j = j0 + tx + 16 * (x % 4);
+  });
 }
 
 // ------------------------------------------------------------------------------------------------ MFMA path (fp32)
@@ -181,15 +212,16 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmProblem<float> p) {
     __syncthreads();
   }
 #pragma unroll
-  for (int r = 0; r < 2; ++r)
+  for (int r = 0; r < 2; ++r) {  // two groups of 32 outputs (registers for all 64 at once would spill)
+    float out[32];
 #pragma unroll
-    for (int c = 0; c < 2; ++c)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int64_t i = i0 + wr + 32 * r + 8 * (e >> 2) + 4 * half + (e & 3);
-        const int64_t j = j0 + wc + 32 * c + li;
-        store_d(p, d, i, j, acc[r][c][e]);
-      }
+    for (int x = 0; x < 32; ++x) out[x] = acc[r][x / 16][x % 16];
+    store_d_group(p, d, out, [&](int x, int64_t& i, int64_t& j) {
+      const int c = x / 16, e = x % 16;
+      i = i0 + wr + 32 * r + 8 * (e >> 2) + 4 * half + (e & 3);
+      j = j0 + wc + 32 * c + li;
+    });
+  }
 }
 
 // ------------------------------------------------------------------------------------------------ MFMA, vectorised
@@ -353,15 +385,16 @@ __global__ __launch_bounds__(256, 2) void gemm_mfma_vec_kernel(GemmProblem<float
     }
   }
 #pragma unroll
-  for (int r = 0; r < 2; ++r)
+  for (int r = 0; r < 2; ++r) {  // two groups of 32 outputs
+    float out[32];
 #pragma unroll
-    for (int c = 0; c < 2; ++c)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int64_t i = i0 + wr + 32 * r + 8 * (e >> 2) + 4 * hh + (e & 3);
-        const int64_t j = j0 + wc + 32 * c + li;
-        store_d(p, d, i, j, acc[r][c][e]);
-      }
+    for (int x = 0; x < 32; ++x) out[x] = acc[r][x / 16][x % 16];
+    store_d_group(p, d, out, [&](int x, int64_t& i, int64_t& j) {
+      const int c = x / 16, e = x % 16;
+      i = i0 + wr + 32 * r + 8 * (e >> 2) + 4 * hh + (e & 3);
+      j = j0 + wc + 32 * c + li;
+    });
+  }
 }
 
 // ------------------------------------------------------------------------------------------------ MFMA path (fp64)
@@ -472,13 +505,13 @@ __global__ __launch_bounds__(256) void gemm_mfma64_kernel(GemmProblem<double> p,
     }
     __syncthreads();
   }
+  double out[16];
 #pragma unroll
-  for (int r = 0; r < 2; ++r)
-#pragma unroll
-    for (int c = 0; c < 2; ++c)
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        store_d(p, d, i0 + wi + 16 * r + kq + 4 * e, j0 + wj + 16 * c + li, acc[r][c][e]);
+  for (int x = 0; x < 16; ++x) out[x] = acc[x / 8][(x / 4) % 2][x % 4];
+  store_d_group(p, d, out, [&](int x, int64_t& i, int64_t& j) {
+    i = i0 + wi + 16 * (x / 8) + kq + 4 * (x % 4);
+    j = j0 + wj + 16 * ((x / 4) % 2) + li;
+  });
 }
 
 // ------------------------------------------------------------------------------------------------ MFMA path (fp64, LDS-direct)
@@ -667,13 +700,13 @@ __global__ __launch_bounds__(256, 2) void gemm_mfma64_dma_kernel(GemmProblem<dou
       if (t + 1 < nt) step(t + 1, std::integral_constant<int, 1>{});
     }
   }
+  double out[16];
 #pragma unroll
-  for (int r = 0; r < 2; ++r)
-#pragma unroll
-    for (int c = 0; c < 2; ++c)
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        store_d(p, d, i0 + 32 * wi + 16 * r + hh + 4 * e, j0 + 32 * wj + 16 * c + li, acc[r][c][e]);
+  for (int x = 0; x < 16; ++x) out[x] = acc[x / 8][(x / 4) % 2][x % 4];
+  store_d_group(p, d, out, [&](int x, int64_t& i, int64_t& j) {
+    i = i0 + 32 * wi + 16 * (x / 8) + hh + 4 * (x % 4);
+    j = j0 + 32 * wj + 16 * ((x / 4) % 2) + li;
+  });
 }
 
 bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15) == 0; }
