@@ -35,6 +35,7 @@ int gptq2d_fill(T* x, T v, int64_t count, hipStream_t stream);
 namespace {
 
 constexpr int TR = 32;       // tile edge
+constexpr int64_t BAND64 = 4;  // fp64 fused sweep: tile stages per band flush inside an outer block
 constexpr int PARTS = 8;     // threads cooperating on one entry of an antidiagonal
 constexpr int NTHREADS = TR * PARTS;
 
@@ -628,10 +629,11 @@ struct TileRegs {
   }
 
   // LDS image of the tile with the pulled feedback D (down) and R (right) added: C + D, Y + (D + R),
-  // the zero padding of the diagonal blocks and of the C image, and the zeroed E image.  red holds
-  // the waves' partial sums when `pulled` (pulled_sums: the first wd waves' are D's; fp32 only).
-  __device__ __forceinline__ void store(TileLdsT<T>& tl, const float (*red)[2][TR][TR + 1], bool pulled,
-                                        int wd) const {
+  // the zero padding of the diagonal blocks and of the C image, and the zeroed E image.  fp32: red holds
+  // the waves' partial sums when `pulled` (pulled_sums: the first wd waves' are D's).  fp64: red64, when
+  // given, holds D (red64[0]) and R (red64[1]) whole.
+  __device__ __forceinline__ void store(TileLdsT<T>& tl, const float (*red)[2][TR][TR + 1], bool pulled, int wd,
+                                        const double (*red64)[TR][TR + 1] = nullptr) const {
 #pragma unroll
     for (int q = 0; q < NQ; ++q) {
       const int t = threadIdx.x + NTHREADS * q;
@@ -639,6 +641,8 @@ struct TileRegs {
       T dd = T(0), rr = T(0);
       if constexpr (sizeof(T) == 4) {
         if (pulled) pulled_sums(red, wd, r, cc, dd, rr);
+      } else {
+        if (red64) dd = red64[0][r][cc], rr = red64[1][r][cc];
       }
       tl.Ys[r][cc] = y[q] + (dd + rr);
       tl.Cs[r][TR + cc] = c[q] + dd;
@@ -793,43 +797,126 @@ __global__ __launch_bounds__(NTHREADS, 2) void tile_stage_kernel(float* __restri
     sweep_tile<KIND, YPRE>(tl, qin, y, c, e, qs, m, n, i0, j0, mat);
 }
 
-// One launch per coarse stage of the fused fp64 sweep: each workgroup takes one tile of the stage, whose
-// feedback from all earlier tiles has been flushed into its Y and C (outer flushes, then the per-stage band
-// flushes inside an outer block), builds the fp32 sweep's LDS image of it in fp64 and runs the same push-form
-// sweep of its 63 antidiagonals (sweep_tile).  The image takes 122 KB of LDS: one workgroup per CU, at most
-// one per tile of the stage.
+// fp64 feedback of tile (I, J) from the k-tiles t in [d0, d1) (down: D = sum L[I,t] E[t,J]) and [r0, r1) (right:
+// R = sum C[I,t] U[t,J]), on MFMA (v_mfma_f64_16x16x4_f64), into red[0] (D) and red[1] (R).  Wave w owns the
+// 16 x 16 quadrant (w / 2, w % 2) of both products; lane l (q = l % 16, h = l / 16) supplies A(q, 8 h + s) and
+// B(8 h + s, q) to MFMA s = 0..7 of a k-tile (which k a slot carries is free as long as A and B agree), and
+// accumulator element r of lane l holds (h + 4 r, q) of the quadrant.  The k-tiles of both products form one
+// list of jobs (D's first), loaded PJ jobs at a time, one chunk ahead of the chunk whose MFMAs run.
+__device__ __forceinline__ void pull64(double (*red)[TR][TR + 1], const double* __restrict__ lb,
+                                       const double* __restrict__ eb, const double* __restrict__ cb,
+                                       const double* __restrict__ ub, int64_t m, int64_t n, int64_t i0, int64_t j0,
+                                       int d0, int d1, int r0, int r1) {
+  typedef double doublex4 __attribute__((ext_vector_type(4)));
+  constexpr int PJ = 4;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int q = lane & 15, h = lane >> 4;
+  const int64_t i = i0 + 16 * (wave >> 1) + q, j = j0 + 16 * (wave & 1) + q;
+  const bool iin = i < m, jin = j < n;
+  // this lane's rows of L and C, columns of E and U (64-bit arithmetic once)
+  const double* la = lb + (iin ? i : 0) * m;
+  const double* ca = cb + (iin ? i : 0) * n;
+  const double* ej = eb + (jin ? j : 0);
+  const double* uj = ub + (jin ? j : 0);
+  const int nd = d1 - d0, nj = nd + (r1 - r0);
+  double a[2][PJ][8], bv[2][PJ][8];
+  // job x's operands: k = 32 t + 8 h + s, inside k < m (L's columns, E's rows) or k < n (C's columns, U's rows)
+  auto load = [&](int x, double (&av)[8], double (&bb)[8]) {
+    const bool dn = x < nd;
+    const int64_t k0 = (int64_t)(dn ? d0 + x : r0 + (x - nd)) * TR + 8 * h;
+    const int64_t kmax = dn ? m : n;
+    const double* ap = dn ? la : ca;
+    const double* bp = dn ? ej : uj;
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      const bool ok = x < nj && k0 + s < kmax;
+      av[s] = ok && iin ? ap[k0 + s] : 0.;
+      bb[s] = ok && jin ? bp[(k0 + s) * n] : 0.;
+    }
+  };
+  doublex4 accd = {0., 0., 0., 0.}, accr = {0., 0., 0., 0.};
+  auto chunk = [&](int c0, auto cur_c) {
+    constexpr int cur = decltype(cur_c)::value;
+    if (c0 + PJ < nj) {
+#pragma unroll
+      for (int x = 0; x < PJ; ++x) load(c0 + PJ + x, a[1 - cur][x], bv[1 - cur][x]);
+    }
+#pragma unroll
+    for (int x = 0; x < PJ; ++x) {
+      const int job = c0 + x;  // uniform
+      if (job >= nj) break;
+      if (job < nd) {
+#pragma unroll
+        for (int s = 0; s < 8; ++s) accd = __builtin_amdgcn_mfma_f64_16x16x4f64(a[cur][x][s], bv[cur][x][s], accd, 0, 0, 0);
+      } else {
+#pragma unroll
+        for (int s = 0; s < 8; ++s) accr = __builtin_amdgcn_mfma_f64_16x16x4f64(a[cur][x][s], bv[cur][x][s], accr, 0, 0, 0);
+      }
+    }
+  };
+#pragma unroll
+  for (int x = 0; x < PJ; ++x) load(x, a[0][x], bv[0][x]);
+  for (int c0 = 0; c0 < nj; c0 += 2 * PJ) {
+    chunk(c0, std::integral_constant<int, 0>{});
+    if (c0 + PJ < nj) chunk(c0 + PJ, std::integral_constant<int, 1>{});
+  }
+  const int rq = 16 * (wave >> 1) + h, cq = 16 * (wave & 1) + q;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    red[0][rq + 4 * r][cq] = accd[r];
+    red[1][rq + 4 * r][cq] = accr[r];
+  }
+}
+
+// One launch per coarse stage of the fused fp64 sweep: each workgroup takes one tile of the stage.  Its
+// feedback from the outer blocks before its own and from its own block's stages before `band_lo` has been
+// flushed into its Y and C (outer flushes, then band flushes of `band` stages inside an outer block); the rest,
+// from the tiles of stages [band_lo, stage), it pulls itself on MFMA (pull64).  Then it builds the fp32 sweep's
+// LDS image in fp64 and runs the same push-form sweep of its 63 antidiagonals (sweep_tile).  The image and the
+// pulled sums take 139 KB of LDS: one workgroup per CU, at most one per tile of the stage.
 template <int KIND, bool YPRE>
 __global__ __launch_bounds__(NTHREADS) void sweep_tile64_kernel(double* __restrict__ y, double* __restrict__ c,
                                                                 double* __restrict__ e, const double* __restrict__ l,
                                                                 const double* __restrict__ u, int64_t m, int64_t n,
-                                                                int64_t stage, int64_t tile_lo, BatchMap lmap,
-                                                                BatchMap umap, QSpec<double> qs, int64_t nx,
-                                                                int64_t ny) {
+                                                                int64_t stage, int64_t tile_lo, int64_t band_lo,
+                                                                BatchMap lmap, BatchMap umap, QSpec<double> qs,
+                                                                int64_t nx, int64_t ny) {
   __shared__ TileLdsT<double> tl;
+  __shared__ double red[2][TR][TR + 1];
   const GridIds id = grid_ids(nx, ny);
   const int64_t b = id.b;
   const int64_t I = tile_lo + id.x, J = stage - I;
   const int64_t i0 = I * TR, j0 = J * TR;
   const int64_t mat = b * m * n;
+  const double* lb = l + lmap.offset(b);
+  const double* ub = u + umap.offset(b);
+  // k-tiles of the pull: the tiles (t, J) and (I, t) of stages [band_lo, stage)
+  const int64_t dlo = band_lo - J > 0 ? band_lo - J : 0, rlo = band_lo - I > 0 ? band_lo - I : 0;
+  const int d0 = (int)dlo, d1 = (int)(I > dlo ? I : dlo), r0 = (int)rlo, r1 = (int)(J > rlo ? J : rlo);
+  const bool pulled = d0 < d1 || r0 < r1;
   SweepInputs<KIND, double> in;
   in.load(qs, b, m, n, i0, j0);
   TileRegs<false, double> regs;
-  regs.load(y, c, l + lmap.offset(b), u + umap.offset(b), m, n, i0, j0, mat);
-  regs.store(tl, nullptr, false, 0);
+  regs.load(y, c, lb, ub, m, n, i0, j0, mat);  // own data first: its loads overlap the pull's
+  if (pulled) {
+    pull64(red, lb, e + mat, c + mat, ub, m, n, i0, j0, d0, d1, r0, r1);
+    __syncthreads();
+  }
+  regs.store(tl, nullptr, false, 0, pulled ? red : nullptr);
   __syncthreads();
   sweep_tile<KIND, YPRE>(tl, in, y, c, e, qs, m, n, i0, j0, mat);
 }
 
 template <int KIND>
 void launch_tile64_k(dim3 grid, hipStream_t stream, double* y, double* c, double* e, const double* l, const double* u,
-                     int64_t m, int64_t n, int64_t st, int64_t lo, const BatchMap& lmap, const BatchMap& umap,
-                     const QSpec<double>& qs, int64_t nx, int64_t ny) {
+                     int64_t m, int64_t n, int64_t st, int64_t lo, int64_t band_lo, const BatchMap& lmap,
+                     const BatchMap& umap, const QSpec<double>& qs, int64_t nx, int64_t ny) {
   if (qs.ypre)
     hipLaunchKernelGGL((sweep_tile64_kernel<KIND, true>), grid, dim3(NTHREADS), 0, stream, y, c, e, l, u, m, n, st, lo,
-                       lmap, umap, qs, nx, ny);
+                       band_lo, lmap, umap, qs, nx, ny);
   else
     hipLaunchKernelGGL((sweep_tile64_kernel<KIND, false>), grid, dim3(NTHREADS), 0, stream, y, c, e, l, u, m, n, st,
-                       lo, lmap, umap, qs, nx, ny);
+                       lo, band_lo, lmap, umap, qs, nx, ny);
 }
 
 template <bool VEC, int KIND, bool ROWS>
@@ -923,6 +1010,9 @@ int sweep_fused(T* y, T* c, T* e, const T* l, const T* u, int64_t m, int64_t n, 
   // 128-bit operand loads of the MFMA pull: rows, matrices and pointers 16-byte aligned
   const bool vec = m % 4 == 0 && n % 4 == 0 && aligned16(y) && aligned16(c) && aligned16(e) && aligned16(l) &&
                    aligned16(u) && strides_mult4(lmap) && strides_mult4(umap);
+  // fp64: stages per band flush inside an outer block (the tile sweeps pull the band's earlier stages); the row
+  // sweep pulls nothing, so its every stage is flushed
+  const int64_t band = rows ? 1 : BAND64;
   for (int64_t S0 = stage_begin; S0 < stage_end; S0 += outer_tiles) {
     const int64_t S1 = S0 + outer_tiles < stages ? S0 + outer_tiles : stages;
     for (int64_t st = S0; st < S1; ++st) {
@@ -960,20 +1050,23 @@ int sweep_fused(T* y, T* c, T* e, const T* l, const T* u, int64_t m, int64_t n, 
           else
             launch_rows_stage<T, Q_ROUND>(g.grid, stream, y, c, e, l, m, n, st, lo, lmap, qs, g.nx, g.ny);
         } else {
-          // the push-form sweep of the fp32 engine, in fp64
+          // the push-form sweep of the fp32 engine, in fp64, pulling its band's earlier stages
+          const int64_t blo = st - (st - S0) % band;
           if (qkind == Q_AFFINE)
-            launch_tile64_k<Q_AFFINE>(g.grid, stream, y, c, e, l, u, m, n, st, lo, lmap, umap, qs, g.nx, g.ny);
+            launch_tile64_k<Q_AFFINE>(g.grid, stream, y, c, e, l, u, m, n, st, lo, blo, lmap, umap, qs, g.nx, g.ny);
           else if (qkind == Q_FORCED)
-            launch_tile64_k<Q_FORCED>(g.grid, stream, y, c, e, l, u, m, n, st, lo, lmap, umap, qs, g.nx, g.ny);
+            launch_tile64_k<Q_FORCED>(g.grid, stream, y, c, e, l, u, m, n, st, lo, blo, lmap, umap, qs, g.nx, g.ny);
           else
-            launch_tile64_k<Q_ROUND>(g.grid, stream, y, c, e, l, u, m, n, st, lo, lmap, umap, qs, g.nx, g.ny);
+            launch_tile64_k<Q_ROUND>(g.grid, stream, y, c, e, l, u, m, n, st, lo, blo, lmap, umap, qs, g.nx, g.ny);
         }
       }
       // work of a tile sweep: its entries (the in-tile feedback is latency-, not throughput-bound)
       if (prof) gptq2d_prof_end(PROF_TILE_SWEEP, (double)B * (hi - lo + 1) * TR * TR, stream);
       if ((rc = (int)hipGetLastError())) return rc;
       if constexpr (sizeof(T) == 8) {
-        if (st + 1 < S1 && (rc = gptq2d_flush<T>(y, c, e, l, u, m, n, TR, TR, st, st + 1, S1, lmap, umap, B, stream)))
+        // a band's stages into the rest of the outer block, after the band's last stage
+        if (st + 1 < S1 && (st + 1 - S0) % band == 0 &&
+            (rc = gptq2d_flush<T>(y, c, e, l, u, m, n, TR, TR, st + 1 - band, st + 1, S1, lmap, umap, B, stream)))
           return rc;
       }
     }

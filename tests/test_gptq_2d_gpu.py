@@ -83,6 +83,18 @@ def test_fused_multi_tile(m, n):
         assert G.gptq_2d(x, l, u, outer_block_size=outer).equal(expected), outer
 
 
+@pytest.mark.parametrize("outer", [256, 384, 10_000])
+def test_fused_fp64_bands(outer):
+    """The fp64 fused sweep's bands inside an outer block: each tile pulls the tiles of its band's earlier stages
+    itself, and a band flush delivers a finished band to the rest of the block.  300 x 420 has 23 tile stages:
+    blocks of 8, 12 and all 23 stages, so several bands per block, with a partial band where the block's length
+    is not a multiple of the band's (4 stages: the last block of 384 and the single block of 23)."""
+    print(f"fp64 fused bands 300x420 outer={outer}", flush=True)
+    x, l, u = _instance(300, 420, 11)
+    expected = _expected(x, l, u, (1, 1))
+    assert G.gptq_2d(x, l, u, outer_block_size=outer).equal(expected)
+
+
 def test_quantizer_sees_quantized_values():
     """Live Y holds the quantized values of all earlier antidiagonals (test_gptq_2d.py:113-127)."""
     x, l, u = _instance(12, 8, 7, (2, 2))
