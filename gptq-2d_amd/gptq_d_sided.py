@@ -36,11 +36,13 @@ def mode_permutation(D: int) -> tuple:
 
 
 def column_factor(ls: Sequence[torch.Tensor]) -> torch.Tensor:
-    """U = (L_D (x) ... (x) L_2)^T, unit upper triangular of size n_2 ... n_D."""
-    f = _unit_lower(ls[-1])
+    """U = (L_D (x) ... (x) L_2)^T = L_D^T (x) ... (x) L_2^T, unit upper triangular of size n_2 ... n_D, formed
+    from the transposed mode factors: every entry is the same product of the same factor entries as in the
+    transposed product (equal bits), without a transposed copy of the n_2 ... n_D squared result."""
+    f = _unit_lower(ls[-1]).t()
     for fd in reversed(ls[1:-1]):
-        f = torch.kron(f, _unit_lower(fd))
-    return f.t().contiguous()
+        f = torch.kron(f, _unit_lower(fd).t())
+    return f.contiguous()
 
 
 @torch.no_grad()
