@@ -72,9 +72,11 @@ def gptq_d_sided(x: torch.Tensor, ls: Sequence[torch.Tensor], *, quantizer: Call
     w = x.permute(*perm).reshape(n1, -1)
     # x already in the flattened order: the sweep runs on its memory when it may write there
     in_place_2d = inplace and w.is_contiguous() and w.data_ptr() == x.data_ptr()
+    # otherwise the flattening copied x, and the sweep may run on that copy instead of a clone of it
+    fresh = w.untyped_storage().data_ptr() != x.untyped_storage().data_ptr()
     z = _g2.gptq_2d(w, ls[0].contiguous(), column_factor(ls), quantizer=quantizer,
                     quantizer_inputs=tuple(t.permute(*perm).reshape(n1, -1).contiguous() for t in quantizer_inputs),
-                    outer_block_size=outer_block_size, inplace=in_place_2d, fused=fused)
+                    outer_block_size=outer_block_size, inplace=in_place_2d or fresh, fused=fused)
     out = z.reshape(n1, *(x.size(d) for d in perm[1:])).permute(*[perm.index(d) for d in range(D)])
     if inplace:
         if not in_place_2d:
