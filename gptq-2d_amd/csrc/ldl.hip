@@ -13,8 +13,8 @@
 //   2. Right-looking blocked Cholesky of W in place, panels of PB columns: a panel's diagonal
 //      block is factored (redundantly in every workgroup) and the panel below solved against it;
 //      the trailing lower triangle takes the rank-PB update.  fp32 (k % 4 == 0) blocks it on two
-//      levels: strips of four panels, where each panel updates only its strip's later columns and
-//      a strip's end brings one rank-256 update of the whole trailing triangle (MFMA-bound, where
+//      levels: strips of eight panels, where each panel updates only its strip's later columns and
+//      a strip's end brings one rank-512 update of the whole trailing triangle (MFMA-bound, where
 //      rank-64 updates are bound by moving the triangle through HBM), with a look-ahead of one
 //      panel on the one stream: after a panel, a strip launch updates only the next panel's
 //      columns, and the next panel's factorisation shares one launch (panel_step_kernel) with the
@@ -737,8 +737,8 @@ __global__ __launch_bounds__(256) void normalize_block_solve_kernel(T* __restric
 // 16 entries of a block, then write), masked to the lower triangle, to i < R and to j < C.
 //
 // The same kernel serves the three updates of the two-level Cholesky below: a panel's update of the
-// next panel's columns (C = 64), its update of the rest of its 256-column strip (rank 64), and a
-// strip's rank-256 update of the whole trailing triangle.
+// next panel's columns (C = 64), its update of the rest of its 512-column strip (rank 64), and a
+// strip's rank-512 update of the whole trailing triangle.
 constexpr int WB = 128;  // block edge
 constexpr int WK = 32;   // k-tile depth
 
@@ -968,7 +968,12 @@ __global__ __launch_bounds__(256, 2) void panel_step_kernel(PanelGroup grp, int6
 template <typename T>
 struct CholeskyRun {
   static constexpr int PB = LdlBlock<T>::PB;
-  static constexpr int64_t SW = 4 * PB;  // strip width of the two-level fp32 path
+  // strip width of the two-level fp32 path.  512 columns: both 8192 factors 10.53 -> 10.32 ms against 256 (1024:
+  // 10.26 ms, but 4096 factors 3.15 -> 3.22 ms).  The inverse's split points (multiples of 1024, trtri_split)
+  // must be strip boundaries: the strip launch of the panel before one copies that panel's diagonal block into
+  // W, which the inverse's first part reads from beside the rest of the chain.
+  static constexpr int64_t SW = 8 * PB;
+  static_assert(1024 % SW == 0, "every split point of the inverse is a strip boundary");
   T* w;
   int64_t k;
   int* info;
