@@ -95,6 +95,18 @@ def test_fused_fp64_bands(outer):
     assert G.gptq_2d(x, l, u, outer_block_size=outer).equal(expected)
 
 
+def test_fused_fp64_bands_batched():
+    """A batch of layers with a factor pair each through the fp64 fused sweep (bands with pulls and band flushes
+    inside one outer block) equals the layers swept one by one, bit for bit: the pulls read each layer's own
+    E, C, L and U."""
+    print("fp64 fused bands, batch of 2, 300x420", flush=True)
+    xs, ls, us = zip(*(_instance(300, 420, 20 + b) for b in range(2)))
+    x, l, u = torch.stack(xs), torch.stack(ls), torch.stack(us)
+    got = G.gptq_2d(x, l, u, outer_block_size=10_000)
+    for b in range(2):
+        assert got[b].equal(G.gptq_2d(xs[b], ls[b], us[b], outer_block_size=10_000)), b
+
+
 def test_quantizer_sees_quantized_values():
     """Live Y holds the quantized values of all earlier antidiagonals (test_gptq_2d.py:113-127)."""
     x, l, u = _instance(12, 8, 7, (2, 2))
@@ -292,14 +304,16 @@ def test_fused_quantizer_special_values(qmin, qmax, last_zp, dtype):
     assert torch.equal(got[ok], expected[ok])
 
 
+@pytest.mark.parametrize("outer_tiles", [2, 6])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
-def test_fused_resume_at_block_boundary(dtype):
+def test_fused_resume_at_block_boundary(dtype, outer_tiles):
     """gptq2d_sweep_fused over [0, S) then [S, end) with S on an outer-block boundary equals one call over the
-    whole sweep bit for bit (the C scratch carries the state); an end inside an outer block is rejected."""
+    whole sweep bit for bit (the C scratch carries the state); an end inside an outer block is rejected.  Blocks
+    of 6 tile stages hold a band flush of the fp64 sweep (bands of 4) as well as its pulls."""
     import _hip
 
-    print(f"fused resume {dtype}", flush=True)
-    m, n, outer_tiles = 200, 330, 2
+    print(f"fused resume {dtype} outer_tiles={outer_tiles}", flush=True)
+    m, n = 200, 330
     g = torch.Generator().manual_seed(9)
     x = (4. * torch.randn(m, n, generator=g, dtype=torch.float64)).to(DEV, dtype)
     lo = S.unit_triangular(.3 / m ** .5 * torch.randn(m, m, generator=g, dtype=torch.float64), upper=False)
@@ -318,8 +332,8 @@ def test_fused_resume_at_block_boundary(dtype):
     run(whole, c, e, 0, -1)
     split = x.clone()
     c, e = torch.empty_like(x), torch.empty_like(x)
-    run(split, c, e, 0, 4)
-    run(split, c, e, 4, stages)
+    run(split, c, e, 0, 2 * outer_tiles)
+    run(split, c, e, 2 * outer_tiles, stages)
     torch.cuda.synchronize()
     assert split.equal(whole)
     with pytest.raises(_hip.GPTQ2DError):
