@@ -500,13 +500,6 @@ __device__ __forceinline__ void potrf_panel(PotrfLds<T, PB>& sm, T* __restrict__
   }
 }
 
-template <typename T, int PB>
-__global__ __launch_bounds__(256) void potrf_panel_kernel(T* __restrict__ w, int64_t ld, int64_t j0, int n,
-                                                          int64_t k, int* __restrict__ info, T* __restrict__ stage) {
-  __shared__ PotrfLds<T, PB> sm;
-  potrf_panel<T, PB>(sm, w, ld, j0, n, k, info, stage, blockIdx.x, gridDim.x);
-}
-
 // The staged factored diagonal block of panel j0 (n rows) into W, by one workgroup.
 template <typename T, int PB>
 __device__ __forceinline__ void stage_to_w(T* __restrict__ w, int64_t ld, int64_t j0, int n,
@@ -525,6 +518,22 @@ __device__ __forceinline__ void stage_to_w(T* __restrict__ w, int64_t ld, int64_
     const int t = threadIdx.x + 256 * u, r = t / PB, c = t % PB;
     if (r < n && c <= r) w[(j0 + r) * ld + j0 + c] = v[u];
   }
+}
+
+// Panel j0 of the one-panel-per-launch Cholesky.  copy != nullptr: the last workgroup moves the staged block of
+// an earlier panel (at column copy_j0, copy_n rows; another staging slot) into W instead -- the block no
+// launch between the two panels reads, so that it needs no launch of its own.
+template <typename T, int PB>
+__global__ __launch_bounds__(256) void potrf_panel_kernel(T* __restrict__ w, int64_t ld, int64_t j0, int n,
+                                                          int64_t k, int* __restrict__ info, T* __restrict__ stage,
+                                                          const T* __restrict__ copy, int64_t copy_j0, int copy_n) {
+  __shared__ PotrfLds<T, PB> sm;
+  const bool copier = copy != nullptr && blockIdx.x == gridDim.x - 1;
+  if (copier) {
+    stage_to_w<T, PB>(w, ld, copy_j0, copy_n, copy);
+    return;
+  }
+  potrf_panel<T, PB>(sm, w, ld, j0, n, k, info, stage, blockIdx.x, gridDim.x - (copy != nullptr ? 1 : 0));
 }
 
 template <typename T, int PB>
@@ -955,7 +964,8 @@ __global__ __launch_bounds__(256, 2) void panel_step_kernel(PanelGroup grp, int6
 // Launch sequence of the blocked Cholesky of W (k x k) in place over the panels [col_begin, col_end)
 // (multiples of PB; col_end < 0: to the end), one panel per step() so that one host thread can
 // interleave two factorisations on two streams.  Between runs (and after finish()) every factored
-// diagonal block is in W.  Two-level fp32 path: every earlier panel's update has been applied to the
+// diagonal block is in W; between two steps of a run the fp64 path may still hold the last panel's block in
+// its staging slot (the next panel's launch moves it).  Two-level fp32 path: every earlier panel's update has been applied to the
 // whole trailing matrix (finish() issues a pending one).  Plain path (fp64, fp32 with k % 4 != 0): the
 // panels of the strip [j0 / NS * NS, j0) have updated nothing to their right yet -- a later panel of the
 // strip takes them by its left-looking update and the strip's end by its rank-NS update, both reading
@@ -980,8 +990,10 @@ struct CholeskyRun {
   T* stage;
   hipStream_t stream;
   int64_t col_begin, col_end, j0;
-  bool two_level, fuse, done = false;
+  bool two_level, fuse, fold, done = false;
   int64_t pr0 = 0, pC = 0, ppc = 0;  // pending trapezoid update (columns < pC of W[pr0.., pr0..])
+  int64_t pend_j0 = -1;              // plain path: a panel whose staged block is not in W yet (or -1)
+  int pend_n = 0;
   int pK = 0;
   int ng = 1;  // matrices of the group; entry 0 is (w, info, stage)
   T* wg[GROUP_MAX] = {};
@@ -994,6 +1006,10 @@ struct CholeskyRun {
     // (the update kernels' offsets are relative to their blocks' rows: 128 ld floats, any k below 2^22)
     two_level = sizeof(T) == 4 && k % 4 == 0 && k < ((int64_t)1 << 22);
     fuse = two_level && k * k >= 2 * (int64_t)PB * PB;
+    // fp64 with two staging slots: a panel's block moves into W in the next panel's launch.  Not in fp32: there
+    // the factor pair's inverse reads the leading columns from W beside the rest of the chain, as soon as the
+    // chain has passed them (trtri_split); the fp64 inverse starts after the factorisation.
+    fold = sizeof(T) == 8 && !two_level && k * k >= 2 * (int64_t)PB * PB;
     done = j0 >= col_end;
     wg[0] = w_;
     infog[0] = info_;
@@ -1011,11 +1027,11 @@ struct CholeskyRun {
     return true;
   }
 
-  // Staging block of panel j of matrix f (two alternating ones when fused: a panel's launch copies
+  // Staging block of panel j of matrix f (two alternating ones when fused or folded: a panel's launch copies
   // the previous panel's block into W while its own workgroups stage the new one).
   T* slot(int64_t j, int f = 0) const {
     T* st = stageg[f];
-    return fuse && ((j / PB) & 1) ? st + (int64_t)PB * PB : st;
+    return (fuse || fold) && ((j / PB) & 1) ? st + (int64_t)PB * PB : st;
   }
 
   // The launches of panel j0, then j0 += PB.
@@ -1131,13 +1147,24 @@ struct CholeskyRun {
       if ((rc = gptq2d_gemm<T>(g, stream))) return rc;
     }
     const unsigned blocks = rest > 0 ? (unsigned)(cdiv(rest, 64) < 256 ? cdiv(rest, 64) : 256) : 1u;
-    hipLaunchKernelGGL((potrf_panel_kernel<T, PB>), dim3(blocks), dim3(256), 0, stream, w, k, j0, n, k, info, stage);
+    // the previous panel's staged block moves into W in this launch: no launch between the two panels reads
+    // it (the updates read rows from the next panel's first on)
+    const bool copy = pend_j0 >= 0;
+    T* st = slot(j0);
+    hipLaunchKernelGGL((potrf_panel_kernel<T, PB>), dim3(blocks + (copy ? 1u : 0u)), dim3(256), 0, stream, w, k, j0,
+                       n, k, info, st, copy ? (const T*)slot(pend_j0) : nullptr, pend_j0, pend_n);
     if ((rc = (int)hipGetLastError())) return rc;
-    hipLaunchKernelGGL((stage_to_w_kernel<T, PB>), dim3(1), dim3(256), 0, stream, w, k, j0, n, (const T*)stage);
-    if ((rc = (int)hipGetLastError())) return rc;
-    if (rest <= 0) {
-      done = true;
-      return 0;
+    pend_j0 = -1;
+    if (rest <= 0 || !fold) {  // the last panel, or one staging slot: the block into W on its own
+      hipLaunchKernelGGL((stage_to_w_kernel<T, PB>), dim3(1), dim3(256), 0, stream, w, k, j0, n, (const T*)st);
+      if ((rc = (int)hipGetLastError())) return rc;
+      if (rest <= 0) {
+        done = true;
+        return 0;
+      }
+    } else {
+      pend_j0 = j0;
+      pend_n = n;
     }
     const int64_t s1 = j0 + PB;
     if (s1 % NS) return 0;  // the strip goes on
@@ -1161,8 +1188,14 @@ struct CholeskyRun {
     return gptq2d_gemm<T>(g, stream);
   }
 
-  // A range that stops early: the pending update on its own.
+  // A range that stops early: the pending update (or the pending staged block) on its own.
   int finish() {
+    if (pend_j0 >= 0) {
+      hipLaunchKernelGGL((stage_to_w_kernel<T, PB>), dim3(1), dim3(256), 0, stream, w, k, pend_j0, pend_n,
+                         (const T*)slot(pend_j0));
+      pend_j0 = -1;
+      if (const int rc = (int)hipGetLastError()) return rc;
+    }
     if constexpr (sizeof(T) == 4) {
       if (pC <= 0) return 0;
       const int64_t pR = k - pr0;
