@@ -542,6 +542,61 @@ __global__ __launch_bounds__(256) void stage_to_w_kernel(T* __restrict__ w, int6
   stage_to_w<T, PB>(w, ld, j0, n, stage);
 }
 
+// fp64 left-looking update of a panel's columns from its strip's earlier panels (the one-panel-per-launch
+// Cholesky's narrow product): D = W[j0:, j0:j0+n] -= W[j0:, s0:j0] W[j0:j0+n, s0:j0]^T, on D's lower triangle,
+// with K = j0 - s0 = 32 NT.  One workgroup per 32 rows of D (M rows in all), wave w the 16 x 16 block
+// (w / 2, w % 2) over the whole k range: every operand load issued at once, 128 bits at a time (rows contiguous
+// along k, 16-byte aligned), then the MFMA chain (v_mfma_f64_16x16x4_f64) in the order of the LDS-direct
+// strided GEMM's tiles -- lane (q, h) = (l % 16, l / 16) supplies A(q, k) and B(k, q) with k = 32 t + 8 h + 2 v + s2
+// to MFMA (v, s2) of k-tile t -- then D - acc, so the result is that GEMM's bit for bit.  The GEMM takes a k-tile
+// at a time through LDS behind a barrier each; this kernel waits out one memory latency for the whole product.
+template <int NT>
+__global__ __launch_bounds__(256) void narrow_update64_kernel(double* __restrict__ w, int64_t ld, int64_t j0,
+                                                              int64_t s0, int64_t M, int n) {
+  typedef double doublex4 __attribute__((ext_vector_type(4)));
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int q = lane & 15, h = lane >> 4;
+  const int64_t ib = (int64_t)blockIdx.x * 32 + 16 * (wave >> 1);  // the block's first row of D
+  const int cb = 16 * (wave & 1);                                   // and first column
+  const bool a_in = ib + q < M, b_in = cb + q < n;
+  const double* ap = w + (j0 + (a_in ? ib + q : 0)) * ld + s0 + 8 * h;
+  const double* bp = w + (j0 + (b_in ? cb + q : 0)) * ld + s0 + 8 * h;
+  double2 av[NT][4], bv[NT][4];
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      av[t][v] = a_in ? *reinterpret_cast<const double2*>(ap + 32 * t + 2 * v) : double2{0., 0.};
+      bv[t][v] = b_in ? *reinterpret_cast<const double2*>(bp + 32 * t + 2 * v) : double2{0., 0.};
+    }
+  doublex4 acc = {0., 0., 0., 0.};
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      acc = __builtin_amdgcn_mfma_f64_16x16x4f64(av[t][v].x, bv[t][v].x, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f64_16x16x4f64(av[t][v].y, bv[t][v].y, acc, 0, 0, 0);
+    }
+  // accumulator element r: D(ib + h + 4 r, cb + q); the loads of D first, then the stores
+  const int c = cb + q;
+  double old[4];
+  bool ok[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int64_t i = ib + h + 4 * r;
+    ok[r] = i < M && c < n && c <= i;
+    old[r] = ok[r] ? w[(j0 + i) * ld + j0 + c] : 0.;
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    old[r] = old[r] - acc[r];
+    asm volatile("" : "+v"(old[r]));  // computed before the stores' branches
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+    if (ok[r]) w[(j0 + ib + h + 4 * r) * ld + j0 + c] = old[r];
+}
+
 // One wave per diagonal NB block of the lower triangular W: replace it by its inverse.
 template <typename T, int NB>
 __global__ __launch_bounds__(64) void trtri_leaf_kernel(T* __restrict__ w, int64_t ld, int64_t k, int64_t mstride) {
@@ -1120,13 +1175,32 @@ struct CholeskyRun {
   // strip instead of once per panel (the update is bound by that traffic, not by its flops).
   static constexpr int64_t NS = 256;
   static_assert(NS % PB == 0, "strips hold whole panels");
+  static_assert(sizeof(T) != 8 || (NS - PB) / 32 <= 7, "the fp64 narrow product's k-tiles: narrow_update64_kernel<1..7>");
 
   int step_plain() {
     int rc;
     const int n = k - j0 < PB ? (int)(k - j0) : PB;
     const int64_t rest = k - j0 - PB;
     const int64_t s0 = j0 / NS * NS;  // this panel's strip
-    if (j0 > s0) {
+    // fp64 with 16-byte aligned rows: the narrow product on its own kernel (the GEMM's bits, one memory
+    // latency instead of one per k-tile)
+    const bool narrow = sizeof(T) == 8 && k % 2 == 0 && ((uintptr_t)w & 15) == 0;
+    if (j0 > s0 && narrow) {
+      const int nt = (int)((j0 - s0) / 32);
+      const dim3 grid((unsigned)cdiv(k - j0, 32));
+      double* wd = reinterpret_cast<double*>(w);
+      switch (nt) {
+        case 1: hipLaunchKernelGGL(narrow_update64_kernel<1>, grid, dim3(256), 0, stream, wd, k, j0, s0, k - j0, n); break;
+        case 2: hipLaunchKernelGGL(narrow_update64_kernel<2>, grid, dim3(256), 0, stream, wd, k, j0, s0, k - j0, n); break;
+        case 3: hipLaunchKernelGGL(narrow_update64_kernel<3>, grid, dim3(256), 0, stream, wd, k, j0, s0, k - j0, n); break;
+        case 4: hipLaunchKernelGGL(narrow_update64_kernel<4>, grid, dim3(256), 0, stream, wd, k, j0, s0, k - j0, n); break;
+        case 5: hipLaunchKernelGGL(narrow_update64_kernel<5>, grid, dim3(256), 0, stream, wd, k, j0, s0, k - j0, n); break;
+        case 6: hipLaunchKernelGGL(narrow_update64_kernel<6>, grid, dim3(256), 0, stream, wd, k, j0, s0, k - j0, n); break;
+        case 7: hipLaunchKernelGGL(narrow_update64_kernel<7>, grid, dim3(256), 0, stream, wd, k, j0, s0, k - j0, n); break;
+        default: return GPTQ2D_EINVAL;
+      }
+      if ((rc = (int)hipGetLastError())) return rc;
+    } else if (j0 > s0) {
       GemmProblem<T> g{};
       g.M = k - j0;
       g.N = n;
