@@ -1061,9 +1061,10 @@ struct CholeskyRun {
     // (the update kernels' offsets are relative to their blocks' rows: 128 ld floats, any k below 2^22)
     two_level = sizeof(T) == 4 && k % 4 == 0 && k < ((int64_t)1 << 22);
     fuse = two_level && k * k >= 2 * (int64_t)PB * PB;
-    // fp64 with two staging slots: a panel's block moves into W in the next panel's launch.  Not in fp32: there
-    // the factor pair's inverse reads the leading columns from W beside the rest of the chain, as soon as the
-    // chain has passed them (trtri_split); the fp64 inverse starts after the factorisation.
+    // fp64 with two staging slots: a panel's block moves into W in the next panel's launch.  The factor pair's
+    // inverse reads the leading columns from W beside the rest of the chain as soon as the chain has passed them
+    // (trtri_split): it moves the last of those blocks first (flush_staged).  Not in fp32, whose two-level path
+    // copies each strip's last block in its strip launch.
     fold = sizeof(T) == 8 && !two_level && k * k >= 2 * (int64_t)PB * PB;
     done = j0 >= col_end;
     wg[0] = w_;
@@ -1104,6 +1105,15 @@ struct CholeskyRun {
       return finish();
     }
     return 0;
+  }
+
+  // The pending staged block (fold) into W now, with no launch of its own left to wait for it.
+  int flush_staged() {
+    if (pend_j0 < 0) return 0;
+    hipLaunchKernelGGL((stage_to_w_kernel<T, PB>), dim3(1), dim3(256), 0, stream, w, k, pend_j0, pend_n,
+                       (const T*)slot(pend_j0));
+    pend_j0 = -1;
+    return (int)hipGetLastError();
   }
 
  private:
@@ -1264,12 +1274,7 @@ struct CholeskyRun {
 
   // A range that stops early: the pending update (or the pending staged block) on its own.
   int finish() {
-    if (pend_j0 >= 0) {
-      hipLaunchKernelGGL((stage_to_w_kernel<T, PB>), dim3(1), dim3(256), 0, stream, w, k, pend_j0, pend_n,
-                         (const T*)slot(pend_j0));
-      pend_j0 = -1;
-      if (const int rc = (int)hipGetLastError()) return rc;
-    }
+    if (const int rc = flush_staged()) return rc;
     if constexpr (sizeof(T) == 4) {
       if (pC <= 0) return 0;
       const int64_t pR = k - pr0;
@@ -1452,8 +1457,8 @@ int trtri_block(T* w, int64_t ld, int64_t n, T* tmp, bool tri, hipStream_t strea
   return 0;
 }
 
-// Split point of the triangular inverse of a k x k factor: s = NB 2^j, the largest below k, for
-// fp32 from k = 2048 (levels on level_gemm); 0: no split.  With a split, the inverse of C = [A 0; B D]
+// Split point of the triangular inverse of a k x k factor: s = NB 2^j, the largest below k, from k = 2048
+// (fp32: levels on level_gemm; fp64: on the strided GEMM); 0: no split.  With a split, the inverse of C = [A 0; B D]
 // (A: s x s) runs in three parts:
 //   1. A^{-1} in place and T = B A^{-1} -- these read only the Cholesky's columns < s, so they can
 //      run while the factorisation of the columns >= s goes on;
@@ -1463,14 +1468,10 @@ int trtri_block(T* w, int64_t ld, int64_t n, T* tmp, bool tri, hipStream_t strea
 // blocks aligned to multiples of their size, and s is a multiple of every lower level's pair size).
 template <typename T>
 int64_t trtri_split(int64_t k) {
-  if constexpr (sizeof(T) != 4) {
-    return 0;
-  } else {
-    if (k < 2048) return 0;
-    int64_t s = LdlBlock<T>::NB;
-    while (2 * s < k) s *= 2;
-    return s;
-  }
+  if (k < 2048) return 0;
+  int64_t s = LdlBlock<T>::NB;
+  while (2 * s < k) s *= 2;
+  return s;
 }
 
 // Where the three parts keep their data in `out` (k x k elements, free until the normalisation; its
@@ -1517,8 +1518,8 @@ int trtri_part(T* out, T* w, int64_t k, int64_t size, int phase, hipStream_t str
     if (phase == 3) return normalize<T>(out, w, k, size, (k - 1) * k + (k - 1), -1, -k, stream, ng, mst, upper);
     return 0;
   }
+  const TrtriLayout L = trtri_layout<T>(out, k, s);
   if constexpr (sizeof(T) == 4) {
-    const TrtriLayout L = trtri_layout<T>(out, k, s);
     if (phase == 1) {
       if ((rc = trtri_block<T>(w, k, s, out + L.t_off, true, stream, ng, mst))) return rc;
       // T = B A^{-1}: (n2 x s) = (n2 x s) (s x s)
@@ -1532,6 +1533,56 @@ int trtri_part(T* out, T* w, int64_t k, int64_t size, int phase, hipStream_t str
         return rc;
       return normalize<T>(out, w, k, size, (k - 1) * k + (k - 1), -1, -k, stream, ng, mst, upper);
     }
+  } else {
+    // fp64: the same parts on the strided GEMM -- the calls that trtri_inplace's levels make for these blocks
+    // (its top level is this split's T and -D^{-1} T), so the same bits; a group one matrix after the other
+    for (int64_t z = 0; z < ng; ++z) {
+      T* wz = w + z * mst;
+      T* tz = out + z * mst + L.t_off;
+      if (phase == 1) {
+        if ((rc = trtri_block<T>(wz, k, s, tz, false, stream))) return rc;
+        GemmProblem<T> g{};  // T = B A^{-1}: (n2 x s) = (n2 x s) (s x s, lower)
+        g.M = L.n2;
+        g.N = s;
+        g.K = s;
+        g.batch = 1;
+        g.A = wz + s * k;
+        g.a_rs = k;
+        g.a_cs = 1;
+        g.B = wz;
+        g.b_rs = k;
+        g.b_cs = 1;
+        g.b_tri = TRI_LOWER;
+        g.D = tz;
+        g.d_rs = s;
+        g.d_cs = 1;
+        g.alpha = T(1);
+        g.beta = T(0);
+        if ((rc = gptq2d_gemm<T>(g, stream))) return rc;
+      } else if (phase == 2) {
+        if ((rc = trtri_block<T>(wz + s * k + s, k, L.n2, out + z * mst + L.tmp2_off, false, stream))) return rc;
+      } else if (phase == 3) {
+        GemmProblem<T> h{};  // B <- -D^{-1} T: (n2 x s) = (n2 x n2, lower) (n2 x s)
+        h.M = L.n2;
+        h.N = s;
+        h.K = L.n2;
+        h.batch = 1;
+        h.A = wz + s * k + s;
+        h.a_rs = k;
+        h.a_cs = 1;
+        h.a_tri = TRI_LOWER;
+        h.B = tz;
+        h.b_rs = s;
+        h.b_cs = 1;
+        h.D = wz + s * k;
+        h.d_rs = k;
+        h.d_cs = 1;
+        h.alpha = T(-1);
+        h.beta = T(0);
+        if ((rc = gptq2d_gemm<T>(h, stream))) return rc;
+      }
+    }
+    if (phase == 3) return normalize<T>(out, w, k, size, (k - 1) * k + (k - 1), -1, -k, stream, ng, mst, upper);
   }
   return rc;
 }
@@ -1659,6 +1710,7 @@ int ldl_of_inverse_pair(const T* const* m, T* const* out, T* const* work, int* c
     while (!twin.done || !lead) {
       if ((rc = twin.step())) return rc;
       if (!lead && (twin.done || twin.j0 >= split[0])) {
+        if ((rc = twin.flush_staged())) return rc;
         if (hipEventRecord(ev[0], stream[0]) != hipSuccess || hipStreamWaitEvent(stream[2], ev[0], 0) != hipSuccess ||
             hipStreamWaitEvent(stream[1], ev[0], 0) != hipSuccess)
           return GPTQ2D_EUNSUPPORTED;
@@ -1685,8 +1737,9 @@ int ldl_of_inverse_pair(const T* const* m, T* const* out, T* const* work, int* c
     for (int f = 0; f < 2; ++f) {
       if ((rc = run[f].step())) return rc;
       // columns < split final: every panel before the split factored and its block copied into W
-      // (the strip launch of the panel before the split does the copy)
+      // (fp32: the strip launch of the panel before the split does the copy; fp64: flush_staged)
       if (!lead[f] && (run[f].done || run[f].j0 >= split[f])) {
+        if ((rc = run[f].flush_staged())) return rc;
         if (hipEventRecord(ev[f], stream[f]) != hipSuccess || hipStreamWaitEvent(stream[2], ev[f], 0) != hipSuccess)
           return GPTQ2D_EUNSUPPORTED;
         if ((rc = trtri_part<T>(out[f], work[f], k[f], size[f], 1, stream[2]))) return rc;
