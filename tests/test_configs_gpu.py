@@ -60,6 +60,13 @@ def _pre_rounding_rows(x, lo, up, z, pre, p, q, rows):
     return A.alg3_pre_rounding(x, lo, up, z, pre, (p, q), rows)
 
 
+def _say(capsys, *parts, **kw):
+    """A progress line straight to the terminal, past pytest's output capture: the full-size tests run CPU
+    oracles for minutes between their results, and the lines show that they are running."""
+    with capsys.disabled():
+        print(*parts, flush=True)
+
+
 # ------------------------------------------------------------------------------------------------ full size
 
 # outer blocks of the benchmark: bench.py OUTER_BLOCK (24 tile stages) and, for the 8192 x 28672 C5a layers,
@@ -70,14 +77,14 @@ BENCH_OUTER_WIDE = 1024
 
 @pytest.mark.timeout(900)
 @pytest.mark.parametrize("name", ["C2", "H", "C3"])
-def test_full_size_layer(name):
+def test_full_size_layer(name, capsys):
     """C2 (4096^2 INT4 asymmetric g128), H (8192^2 INT4 per-row), C3 (14336 x 4096 INT3 per-row), fp32 fused
     engine with the benchmark's outer blocks, against the CPU oracle over every stage (see the module
     docstring for the tolerances).  Also: codes in range and on the grid, bitwise identical on a second run,
     objective below round-to-nearest's."""
     cfg = instances.CONFIGS[name]
     m, n = cfg.m, cfg.n
-    print(f"{name}: {m}x{n} qmin={cfg.qmin} qmax={cfg.qmax} outer={BENCH_OUTER}", flush=True)
+    _say(capsys, f"{name}: {m}x{n} qmin={cfg.qmin} qmax={cfg.qmax} outer={BENCH_OUTER}", flush=True)
     x = instances.weights(m, n, cfg.seeds[0], cfg.outliers, cfg.bf16).float().to(DEV)
     a = _gpu_factor(m, cfg.alpha, 11)
     b = _gpu_factor(n, cfg.alpha, 12)
@@ -95,7 +102,7 @@ def test_full_size_layer(name):
     rtn = (torch.clamp(torch.round(x / scale + zp), cfg.qmin, cfg.qmax) - zp) * scale
     obj = _objective(z, x, a, b)
     ratio = obj / _objective(rtn, x, a, b)
-    print(f"  objective / RTN = {ratio:.4f}", flush=True)
+    _say(capsys, f"  objective / RTN = {ratio:.4f}", flush=True)
     assert ratio < 1.
 
     # the CPU oracle over the whole sweep (fp32, the reference's own operation sequence), recording every
@@ -111,8 +118,8 @@ def test_full_size_layer(name):
     t0 = time.perf_counter()
     for s in range(st.stages):
         st.run_stage(s)
-        if s % 4096 == 4095:
-            print(f"  oracle: {s + 1} / {st.stages} stages, {time.perf_counter() - t0:.0f} s", flush=True)
+        if s % 1024 == 1023:
+            _say(capsys, f"  oracle: {s + 1} / {st.stages} stages, {time.perf_counter() - t0:.0f} s", flush=True)
     assert not pre_o.isnan().any()
     ref_codes = torch.round(st.y / sc + zc)
 
@@ -131,7 +138,7 @@ def test_full_size_layer(name):
     dev = (ye - yo).abs()
     tf_agree = 1. - float(mism.double().mean())
     far = mism & (frac >= 1e-5)
-    print(f"  teacher forced: code agreement {tf_agree:.6%} ({int(mism.sum())} mismatches, {int(far.sum())} with "
+    _say(capsys, f"  teacher forced: code agreement {tf_agree:.6%} ({int(mism.sum())} mismatches, {int(far.sum())} with "
           f"|frac - 0.5| >= 1e-5), max |dY| {dev.max():.2e} code units (median {dev.median():.2e}), largest "
           f"mismatch |frac - 0.5| {float(frac[mism].max()) if mism.any() else 0.:.2e}", flush=True)
     assert tf_agree >= 0.9999
@@ -149,7 +156,7 @@ def test_full_size_layer(name):
         y64 = (pre64 / scale.double() + zp.double()).cpu()
         code64 = y64.round().clamp(cfg.qmin, cfg.qmax)
         err_e, err_o = (ye.double() - y64).abs(), (yo.double() - y64).abs()
-        print(f"  fp64 trajectory: max |Y_engine - Y_fp64| {err_e.max():.2e}, max |Y_oracle - Y_fp64| "
+        _say(capsys, f"  fp64 trajectory: max |Y_engine - Y_fp64| {err_e.max():.2e}, max |Y_oracle - Y_fp64| "
               f"{err_o.max():.2e} code units; at the {int(far.sum())} far mismatches the engine's code is the fp64 "
               f"code at {int((own[far] == code64[far]).sum())}, the oracle's at "
               f"{int((ref_codes[far] == code64[far]).sum())}; their largest |frac - 0.5| {frac[far].max():.2e}",
@@ -173,8 +180,8 @@ def test_full_size_layer(name):
     t0 = time.perf_counter()
     for s in range(st64.stages):
         st64.run_stage(s)
-        if s % 4096 == 4095:
-            print(f"  fp64 oracle: {s + 1} / {st64.stages} stages, {time.perf_counter() - t0:.0f} s", flush=True)
+        if s % 1024 == 1023:
+            _say(capsys, f"  fp64 oracle: {s + 1} / {st64.stages} stages, {time.perf_counter() - t0:.0f} s", flush=True)
     codes64 = torch.round(st64.y / sc.double() + zc.double()).float()
     ce = codes.cpu()
     agree = float((ce == ref_codes).double().mean())
@@ -183,7 +190,7 @@ def test_full_size_layer(name):
     obj_o = _objective(st.y.to(DEV), x, a, b)
     obj_64 = _objective(st64.y.to(DEV), x, a, b)
     rel, rel_64, rel_o64 = abs(obj - obj_o) / obj_o, abs(obj - obj_64) / obj_64, abs(obj_o - obj_64) / obj_64
-    print(f"  free running: codes agreeing with the fp64 trajectory: engine {agree_e64:.6%}, oracle {agree_o64:.6%}; "
+    _say(capsys, f"  free running: codes agreeing with the fp64 trajectory: engine {agree_e64:.6%}, oracle {agree_o64:.6%}; "
           f"engine vs oracle {agree:.6%}; objective rel engine-oracle {rel:.2e}, engine-fp64 {rel_64:.2e}, "
           f"oracle-fp64 {rel_o64:.2e}", flush=True)
     assert agree_e64 >= agree_o64
@@ -191,7 +198,7 @@ def test_full_size_layer(name):
 
 
 @pytest.mark.timeout(900)
-def test_c5a_full_size():
+def test_c5a_full_size(capsys):
     """C5a: W 8192 x 28672 = 8192 x (112 x 256) under A (x) B1 (x) B2, INT4 abs-max per 1 x 32 super-entry row
     with bf16 scales, fp32 fused engine with the benchmark's outer blocks.  U = ldl_of_inverse(B1 (x) B2, 32)^T
     is formed as U_B1 (x) U_B2^(32) (28672^2 entries: the MFMA flush's staging is based per panel).  Checks:
@@ -205,7 +212,7 @@ def test_c5a_full_size():
     cfg = instances.THREE_FACTOR["C5a"]
     m, n1, n2 = cfg.m, cfg.n1, cfg.n2
     n = n1 * n2
-    print(f"C5a: {m}x{n} = {m}x({n1}x{n2}), 1x{cfg.group} abs-max INT4 bf16", flush=True)
+    _say(capsys, f"C5a: {m}x{n} = {m}x({n1}x{n2}), 1x{cfg.group} abs-max INT4 bf16", flush=True)
     x = instances.weights(m, n, cfg.seeds[0], True, False).float().to(DEV)
     a = _gpu_factor(m, cfg.alpha, 21)
     b1 = _gpu_factor(n1, cfg.alpha, 23)
@@ -220,7 +227,7 @@ def test_c5a_full_size():
     t0 = time.perf_counter()
     z = run(quantizer=q)
     torch.cuda.synchronize()
-    print(f"  sweep {1e3 * (time.perf_counter() - t0):.1f} ms (first call)", flush=True)
+    _say(capsys, f"  sweep {1e3 * (time.perf_counter() - t0):.1f} ms (first call)", flush=True)
     assert run(quantizer=q).equal(z), "not deterministic"
 
     half = torch.full((), (cfg.qmax - cfg.qmin) / 2, device=DEV)
@@ -245,7 +252,7 @@ def test_c5a_full_size():
     rel = float(dy.max() / y64.abs().max())
     zr = absmax_rows_of(y64.float(), rows.numel())
     agree = float((zr == z[rows]).double().mean())
-    print(f"  {rows.numel()} rows ({rows.numel() * n} entries): max |Y_pre - Y_alg3(fp64)| {dy.max():.2e} "
+    _say(capsys, f"  {rows.numel()} rows ({rows.numel() * n} entries): max |Y_pre - Y_alg3(fp64)| {dy.max():.2e} "
           f"({rel:.2e} of max |Y|), codes of the fp64 values agree in {agree:.6%}", flush=True)
     assert rel < 5e-6 and agree >= 0.9999
     del pre, y64, dy
@@ -256,7 +263,7 @@ def test_c5a_full_size():
         return float(((a @ r) * rb).sum())
 
     ratio = objective(z) / objective(absmax_rows(x))
-    print(f"  objective / no-feedback rounding = {ratio:.4f}", flush=True)
+    _say(capsys, f"  objective / no-feedback rounding = {ratio:.4f}", flush=True)
     assert ratio < 1.
 
     K = 96
@@ -272,7 +279,7 @@ def test_c5a_full_size():
     stage = torch.arange(K)[:, None] + (torch.arange(K * cfg.group) // cfg.group)[None, :]
     win = stage < K
     agree = float((z[:K, :K * cfg.group].cpu()[win] == zo[win]).double().mean())
-    print(f"  first {K} coarse antidiagonals ({int(win.sum())} entries): agreement with the oracle {agree:.6%}",
+    _say(capsys, f"  first {K} coarse antidiagonals ({int(win.sum())} entries): agreement with the oracle {agree:.6%}",
           flush=True)
     assert agree >= 0.999
 
@@ -291,7 +298,7 @@ def _trellis_rows(v, table, scale, K, rows_per_call=512):
 
 
 @pytest.mark.timeout(900)
-def test_c4_full_size():
+def test_c4_full_size(capsys):
     """C4: 8192^2 weights (the headline layer's distribution) in 16 x 16 super-entries under the HYB trellis code,
     L = 16, K = 2, V = 2, tail-biting, scale RMS(W) / (0.9 RMS(table)) (demo.ipynb:541-545), fp32 plug-in engine
     with the one-launch HIP search per stage.  Checks: bitwise determinism; every output pair is a row of the
@@ -303,7 +310,7 @@ def test_c4_full_size():
     bit for bit; and on 24 whole rows spread over the layer the pre-rounding values equal super-entry Algorithm
     3's, recomputed in fp64 by torch from the engine's own errors."""
     m = n = 8192
-    print(f"C4: {m}x{n}, 16x16 super-entries, HYB L=16 K=2 V=2", flush=True)
+    _say(capsys, f"C4: {m}x{n}, 16x16 super-entries, HYB L=16 K=2 V=2", flush=True)
     x = instances.weights(m, n, 0, True, False).float().to(DEV)
     a = _gpu_factor(m, .5, 31)
     b = _gpu_factor(n, .5, 32)
@@ -319,7 +326,7 @@ def test_c4_full_size():
     t0 = time.perf_counter()
     z = run()
     torch.cuda.synchronize()
-    print(f"  layer sweep {time.perf_counter() - t0:.2f} s", flush=True)
+    _say(capsys, f"  layer sweep {time.perf_counter() - t0:.2f} s", flush=True)
     # a second run records, at sampled coarse antidiagonals, the super-entries the quantizer receives (the
     # engine's own pre-rounding values) and what it writes
     sampled = {0: None, 1: None, 100: None, 255: None, 511: None, 700: None, 1000: None, 1022: None}
@@ -349,7 +356,7 @@ def test_c4_full_size():
         return float(((a @ r) * (r @ b)).sum())
 
     ratio = objective(z) / objective(_trellis_rows(x, table, scale, 2))
-    print(f"  objective / no-feedback trellis = {ratio:.4f}", flush=True)
+    _say(capsys, f"  objective / no-feedback trellis = {ratio:.4f}", flush=True)
     assert ratio < 1.
 
     K = 4
@@ -366,7 +373,7 @@ def test_c4_full_size():
                             super_entry_shape=(16, 16))
     win = (torch.arange(W)[:, None] // 16 + torch.arange(W)[None, :] // 16) < K
     agree = float((z[:W, :W].cpu()[win] == zo[win]).double().mean())
-    print(f"  first {K} coarse antidiagonals ({int(win.sum())} entries): agreement with the oracle {agree:.4%}",
+    _say(capsys, f"  first {K} coarse antidiagonals ({int(win.sum())} entries): agreement with the oracle {agree:.4%}",
           flush=True)
     assert agree >= 0.99
 
@@ -382,7 +389,7 @@ def test_c4_full_size():
                                          table=table_cpu, K=2)
         assert ref.equal(y_out[pick].cpu()), s_
         checked += pick.numel()
-    print(f"  {checked} super-entries at {len(sampled)} sampled antidiagonals: the oracle's quantizer on the engine's "
+    _say(capsys, f"  {checked} super-entries at {len(sampled)} sampled antidiagonals: the oracle's quantizer on the engine's "
           f"inputs equals the engine's output", flush=True)
 
     # every entry of 24 rows spread over the layer: the pre-rounding values (teacher-forced with the engine's own
@@ -395,7 +402,7 @@ def test_c4_full_size():
     y64 = _pre_rounding_rows(x, lo, up, z, pre, 16, 16, rows)
     dy = (y64 - pre[rows].double()).abs()
     rel = float(dy.max() / y64.abs().max())
-    print(f"  {rows.numel()} rows ({rows.numel() * n} entries): max |Y_pre - Y_alg3(fp64)| {dy.max():.2e} "
+    _say(capsys, f"  {rows.numel()} rows ({rows.numel() * n} entries): max |Y_pre - Y_alg3(fp64)| {dy.max():.2e} "
           f"({rel:.2e} of max |Y|)", flush=True)
     assert rel < 5e-6
 
