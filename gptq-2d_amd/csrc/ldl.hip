@@ -13,8 +13,9 @@
 //   2. Right-looking blocked Cholesky of W in place, panels of PB columns: a panel's diagonal
 //      block is factored (redundantly in every workgroup) and the panel below solved against it;
 //      the trailing lower triangle takes the rank-PB update.  fp32 (k % 4 == 0) blocks it on two
-//      levels: strips of eight panels, where each panel updates only its strip's later columns and
-//      a strip's end brings one rank-512 update of the whole trailing triangle (MFMA-bound, where
+//      levels: strips of 8 panels (16 from k = 8192), where each panel updates only its strip's later
+//      columns and a strip's end brings one update of the whole trailing triangle of the strip's rank
+//      (512 or 1024; MFMA-bound, where
 //      rank-64 updates are bound by moving the triangle through HBM), with a look-ahead of one
 //      panel on the one stream: after a panel, a strip launch updates only the next panel's
 //      columns, and the next panel's factorisation shares one launch (panel_step_kernel) with the
@@ -801,8 +802,8 @@ __global__ __launch_bounds__(256) void normalize_block_solve_kernel(T* __restric
 // 16 entries of a block, then write), masked to the lower triangle, to i < R and to j < C.
 //
 // The same kernel serves the three updates of the two-level Cholesky below: a panel's update of the
-// next panel's columns (C = 64), its update of the rest of its 512-column strip (rank 64), and a
-// strip's rank-512 update of the whole trailing triangle.
+// next panel's columns (C = 64), its update of the rest of its strip (rank 64), and a strip's update of the
+// whole trailing triangle (rank 512 or 1024).
 constexpr int WB = 128;  // block edge
 constexpr int WK = 32;   // k-tile depth
 
@@ -1033,18 +1034,20 @@ __global__ __launch_bounds__(256, 2) void panel_step_kernel(PanelGroup grp, int6
 template <typename T>
 struct CholeskyRun {
   static constexpr int PB = LdlBlock<T>::PB;
-  // strip width of the two-level fp32 path.  512 columns: both 8192 factors 10.53 -> 10.32 ms against 256 (1024:
-  // 10.26 ms, but 4096 factors 3.15 -> 3.22 ms).  The inverse's split points (multiples of 1024, trtri_split)
-  // must be strip boundaries: the strip launch of the panel before one copies that panel's diagonal block into
-  // W, which the inverse's first part reads from beside the rest of the chain.
-  static constexpr int64_t SW = 8 * PB;
-  static_assert(1024 % SW == 0, "every split point of the inverse is a strip boundary");
+  // strip width of the two-level fp32 path: 1024 columns from k = 8192, 512 below (both 8192 factors 10.53 ms
+  // with 256, 10.32 with 512, 10.16-10.25 with 1024; 14336 + 4096: 23.14 with 512, 22.72-22.90 with 1024; 4096:
+  // 3.15 with 256, 3.12 with 512, 3.22 with 1024).  The inverse's split points (multiples of 1024,
+  // trtri_split) must be strip boundaries: the strip launch of the panel before one copies that panel's
+  // diagonal block into W, which the inverse's first part reads from beside the rest of the chain.
+  static constexpr int64_t SW_SMALL = 8 * PB, SW_LARGE = 16 * PB;
+  static_assert(1024 % SW_SMALL == 0 && 1024 % SW_LARGE == 0, "every split point of the inverse is a strip boundary");
   T* w;
   int64_t k;
   int* info;
   T* stage;
   hipStream_t stream;
   int64_t col_begin, col_end, j0;
+  int64_t sw;  // strip width (two-level path)
   bool two_level, fuse, fold, done = false;
   int64_t pr0 = 0, pC = 0, ppc = 0;  // pending trapezoid update (columns < pC of W[pr0.., pr0..])
   int64_t pend_j0 = -1;              // plain path: a panel whose staged block is not in W yet (or -1)
@@ -1060,6 +1063,7 @@ struct CholeskyRun {
         j0(cb) {
     // (the update kernels' offsets are relative to their blocks' rows: 128 ld floats, any k below 2^22)
     two_level = sizeof(T) == 4 && k % 4 == 0 && k < ((int64_t)1 << 22);
+    sw = k >= 8192 ? SW_LARGE : SW_SMALL;
     fuse = two_level && k * k >= 2 * (int64_t)PB * PB;
     // fp64 with two staging slots: a panel's block moves into W in the next panel's launch.  The factor pair's
     // inverse reads the leading columns from W beside the rest of the chain as soon as the chain has passed them
@@ -1117,7 +1121,7 @@ struct CholeskyRun {
   }
 
  private:
-  // fp32, two levels: strips of SW columns (aligned to multiples of SW, cut at the range ends).
+  // fp32, two levels: strips of sw columns (aligned to multiples of sw, cut at the range ends).
   // Inside a strip, each panel updates only the strip's later columns (rank PB); after a strip's
   // last panel, one rank-(strip width) update covers everything to its right -- four times the
   // arithmetic per byte of the trailing triangle that a rank-PB update moves.  Look-ahead: the
@@ -1131,9 +1135,9 @@ struct CholeskyRun {
     const int64_t pR = pC > 0 ? k - pr0 : 0;
     const int64_t upd = pC > 0 ? trapezoid_blocks(pR, pC) : 0;
     // the strip of panel j0: [s_lo, s_hi)
-    const int64_t s_al = j0 / SW * SW;
+    const int64_t s_al = j0 / sw * sw;
     const int64_t s_lo = s_al > col_begin ? s_al : col_begin;
-    const int64_t s_hi = s_al + SW < col_end ? s_al + SW : col_end;
+    const int64_t s_hi = s_al + sw < col_end ? s_al + sw : col_end;
     // fused: a panel after the first of its strip takes the previous panel's rank-PB update itself
     // (no launch of its own for it), and its launch moves the previous panel's staged block into W
     const bool in_strip = fuse && j0 > s_lo;

@@ -228,9 +228,9 @@ def test_cholesky_in_parts_plain(k, cuts, dtype):
 
 @pytest.mark.parametrize("k,cuts", [(1536, (192, 640)), (600, (64, 320, 512)), (8192, (4160,))])
 def test_cholesky_in_parts(k, cuts):
-    """The Cholesky split over calls at panel boundaries that cut the 512-column strips of the fp32 path:
-    each call ends with the update of everything right of its range, so the parts make the same factor
-    (up to rounding: the strips' rank-512 updates are grouped differently)."""
+    """The Cholesky split over calls at panel boundaries that cut the strips of the fp32 path (512 columns,
+    1024 from k = 8192): each call ends with the update of everything right of its range, so the parts make
+    the same factor (up to rounding: the strips' updates are grouped differently)."""
     print(f"cholesky in parts k={k} cuts={cuts}", flush=True)
     m = instances.wishart_factor(k, .5, 60 + k).float().to(DEV)
     out, work = torch.empty_like(m), torch.empty_like(m)
