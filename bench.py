@@ -342,8 +342,8 @@ def _c5a_line(torch, dev, a, m, steps, lines, line):
 
     def factors5():
         lo5 = LDL.ldl_of_inverse(a5, check=False)
-        up5 = torch.kron(LDL.ldl_of_inverse(b1, check=False).t().contiguous(),
-                         LDL.ldl_of_inverse(b2, size=cfg.group, check=False).t().contiguous())
+        up5 = G.KroneckerU(LDL.ldl_of_inverse(b1, check=False).t().contiguous(),
+                           LDL.ldl_of_inverse(b2, size=cfg.group, check=False).t().contiguous())
         return lo5, up5
 
     lo, up = factors5()
@@ -351,7 +351,8 @@ def _c5a_line(torch, dev, a, m, steps, lines, line):
     t_sw = _timed(torch, lambda: G.gptq_2d_super_entry(w, lo, up, super_entry_shape=(1, cfg.group), quantizer=q,
                                                        outer_block_size=OUTER_BLOCK_WIDE), steps)
     lines["C5a"] = line(f"{cfg.m}x{n} = {cfg.m}x({cfg.n1}x{cfg.n2}), A (x) B1 (x) B2, INT4 abs-max per 1x{cfg.group} "
-                        "super-entry (bf16 scales), fused sweep; U = U_B1 (x) U_B2", t_ldl, t_sw)
+                        "super-entry (bf16 scales), fused sweep; U = U_B1 (x) U_B2 read from its two factors", t_ldl,
+                        t_sw)
 
 
 def _c5a3_line(torch, dev, steps, lines, line):

@@ -79,6 +79,9 @@ def lib() -> ctypes.CDLL:
         handle.gptq2d_viterbi_rows_f32.argtypes = [_P, _P, _P, _P, _I64, _I32, _P, _P, _P, _P, _I64, _I64, _I32, _I32,
                                                    _I32, _I32, _P]
         handle.gptq2d_viterbi_rows_f32.restype = ctypes.c_int
+        handle.gptq2d_sweep_fused_kron_f32.argtypes = [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I32,
+                                                       _P, _P, _F64, _F64, _I32, _P, _P, _I64, _I64, _I64, _P]
+        handle.gptq2d_sweep_fused_kron_f32.restype = ctypes.c_int
         handle.gptq2d_viterbi_workspace.argtypes = [_I64, _I64, _I32, _I32, _I32]
         handle.gptq2d_viterbi_workspace.restype = ctypes.c_int64
         handle.gptq2d_int_code_bits.argtypes = [_F64, _F64]

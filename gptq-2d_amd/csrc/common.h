@@ -49,6 +49,45 @@ static inline bool make_batch_map(BatchMap& bm, int32_t nd, const int64_t* shape
   return true;
 }
 
+// U = P (x) Q given by its two factors, P [np, np] and Q [nq, nq] (row-major fp32, nq a multiple of 32), instead
+// of its n^2 = (np nq)^2 entries.  With dq = nq / 32, tile (t, J) of U (32 x 32) is one entry of P times one
+// 32 x 32 block of Q:
+//   U[32 t + r, 32 J + c] = P[t / dq, J / dq] * Q[32 (t % dq) + r, 32 (J % dq) + c],
+// each entry formed by one fp32 multiplication, as torch.kron forms the explicit product (the same bits).
+// Tile indices are divided by dq with a multiply-high (Granlund and Montgomery, "Division by invariant integers
+// using multiplication", 1994): exact for every 32-bit dividend, and on the scalar unit for uniform ones.
+struct KronU {
+  const float* p;
+  const float* q;
+  int np, nq, dq;
+  unsigned mag;  // floor(2^32 (2^l - dq) / dq) + 1, l = ceil(log2 dq)
+  int sh1, sh2;  // min(l, 1), max(l - 1, 0)
+};
+
+static inline bool make_kron_u(KronU& k, const float* p, const float* q, int64_t np, int64_t nq) {
+  if (!p || !q || np <= 0 || nq <= 0 || nq % 32 || np >= ((int64_t)1 << 26) || nq >= ((int64_t)1 << 26) ||
+      np * nq >= ((int64_t)1 << 26))
+    return false;
+  k.p = p;
+  k.q = q;
+  k.np = (int)np;
+  k.nq = (int)nq;
+  k.dq = (int)(nq / 32);
+  int l = 0;
+  while (((int64_t)1 << l) < k.dq) ++l;
+  k.mag = (unsigned)((((uint64_t)1 << 32) * (((uint64_t)1 << l) - (uint64_t)k.dq)) / (uint64_t)k.dq + 1);
+  k.sh1 = l < 1 ? l : 1;
+  k.sh2 = l - 1 > 0 ? l - 1 : 0;
+  return true;
+}
+
+// Tile index t split as t = dq i + r, 0 <= r < dq.
+__device__ __forceinline__ void kron_split(const KronU& k, unsigned t, int& i, int& r) {
+  const unsigned t1 = __umulhi(k.mag, t);
+  i = (int)((t1 + ((t - t1) >> k.sh1)) >> k.sh2);
+  r = (int)t - i * k.dq;
+}
+
 static inline int64_t batch_count(int32_t nd, const int64_t* shape) {
   int64_t b = 1;
   for (int d = 0; d < nd; ++d) b *= shape[d];

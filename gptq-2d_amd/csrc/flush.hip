@@ -344,6 +344,21 @@ int gptq2d_flush(T* y, T* c, const T* e, const T* l, const T* u, int64_t m, int6
   return (int)hipGetLastError();
 }
 
+int gptq2d_flush_tiles_mfma_kron(float* y, float* c, const float* e, const float* l, const KronU& kr, int64_t m,
+                                 int64_t n, int64_t S0, int64_t S1, int64_t S_end, hipStream_t stream);
+
+// The fused sweep's flush with U = P (x) Q read from its factors (32 x 32 tiles, fp32, one matrix).
+int gptq2d_flush_kron(float* y, float* c, const float* e, const float* l, const KronU& kr, int64_t m, int64_t n,
+                      int64_t s0, int64_t s1, int64_t s_end, hipStream_t stream) {
+  if (m <= 0 || n <= 0 || s0 < 0 || s1 <= s0 || s_end < s1) return GPTQ2D_EINVAL;
+  if (s_end == s1) return 0;
+  const bool prof = gptq2d_prof_on(PROF_FLUSH);
+  if (prof) gptq2d_prof_begin(PROF_FLUSH, stream);
+  const int rc = gptq2d_flush_tiles_mfma_kron(y, c, e, l, kr, m, n, s0, s1, s_end, stream);
+  if (prof) gptq2d_prof_end(PROF_FLUSH, gptq2d_flush_flops(m, n, 32, 32, s0, s1, s_end), stream);
+  return rc;
+}
+
 template int gptq2d_flush<float>(float*, float*, const float*, const float*, const float*, int64_t, int64_t, int64_t,
                                  int64_t, int64_t, int64_t, int64_t, const BatchMap&, const BatchMap&, int64_t,
                                  hipStream_t);

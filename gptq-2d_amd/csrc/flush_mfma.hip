@@ -252,14 +252,19 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rebased_rsrc(const T* base, in
 // operand matrices (a_elems / b_elems elements): A is staged through a buffer resource based at the
 // workgroup's first row, B through one based at each k-tile's first row and the workgroup's first
 // column, so that every offset stays below 2^31 bytes for any matrix a tile row or a k-tile of which does.
-template <typename T, int WT, bool VEC, int PHASE>
+// KR (the right product with U = P (x) Q given by its factors, fp32): B is staged from Q, through a resource
+// based at the k-tile's first row of Q, and every B value is multiplied by the P entry of its wave's U tile
+// when the fragments are read -- the U entries of the explicit product, bit for bit.
+template <typename T, int WT, bool VEC, int PHASE, bool KR = false>
 __device__ __forceinline__ void flush_phase(typename AccOf<T, WT / 2>::type& acc, FlushLds<T, WT>& sm,
                                             const T* a_mat, int64_t a_elems, const T* b_mat, int64_t b_elems,
                                             const TileFlush& g, int64_t I0, int64_t J0, int wi, int wj,
                                             int t_lo, int t_hi, const int (&tlo)[WT / 2][WT / 2],
-                                            const int (&thi)[WT / 2][WT / 2]) {
+                                            const int (&thi)[WT / 2][WT / 2], const KronU& kr = KronU{}) {
   using L = FlushLds<T, WT>;
   static_assert(sizeof(T) == 4 || VEC, "fp64 panels are staged 128 bits at a time");
+  static_assert(!KR || (sizeof(T) == 4 && VEC && WT == 2 && PHASE == 1), "U from its Kronecker factors: fp32 "
+                "right products of 2 x 2-tile workgroups staged 128 bits at a time");
   constexpr int H = WT / 2;
   constexpr int ROWS = L::ROWS;
   constexpr int QE = L::QE;
@@ -295,7 +300,13 @@ __device__ __forceinline__ void flush_phase(typename AccOf<T, WT / 2>::type& acc
     const int j = (int)J0 * TS + f % ROWS;
     o.b_in = j < gn;
     o.b_t = j >> 5;
-    o.b_off = (o.b_kb * gn + (o.b_in ? f % ROWS : 0)) * ES;  // from the k-tile's first row, the first column
+    if constexpr (KR) {  // column j of U is column 32 (J % dq) + j % 32 of Q, from the k-tile's first row of Q
+      int ji, jr;
+      kron_split(kr, (unsigned)o.b_t, ji, jr);
+      o.b_off = (o.b_kb * kr.nq + (o.b_in ? jr * TS + (j & (TS - 1)) : 0)) * ES;
+    } else {
+      o.b_off = (o.b_kb * gn + (o.b_in ? f % ROWS : 0)) * ES;  // from the k-tile's first row, the first column
+    }
     return o;
   };
   Geo pre[VEC ? NI : 1];
@@ -308,11 +319,34 @@ __device__ __forceinline__ void flush_phase(typename AccOf<T, WT / 2>::type& acc
   const int i0t = (int)I0, j0t = (int)J0;
   const bool full = (i0t + WT) * TS <= gm && (j0t + WT) * TS <= gn;
 
+  // KR: (t / dq, t % dq) of the next k-tile to stage (issue takes the k-tiles in order, each once), the P column of
+  // the wave's U tiles (clamped: a tile column past the matrix has its B values masked to zero), and the P entry
+  // of the U tile staged in each buffer (uniform values)
+  int kti = 0, ktr = 0, pcol = 0;
+  float pk0 = 0.f, pk1 = 0.f;
+  if constexpr (KR) {
+    kron_split(kr, (unsigned)t_lo, kti, ktr);
+    int jr;
+    kron_split(kr, (unsigned)(j0t + wj), pcol, jr);
+    pcol = pcol < kr.np - 1 ? pcol : kr.np - 1;
+  }
+
   // loads of k-tile t into buffer buf, each masked to what a product may read (L strictly below its
   // diagonal tiles, C and E on the band, U strictly above its diagonal tiles, nothing outside)
   auto issue = [&](int t, int buf) {
     const int ts = (int)t, k0 = ts * TS;
-    const __amdgpu_buffer_rsrc_t rb_src = rebased_rsrc(b_mat, (int64_t)k0 * gn + J0 * TS, b_elems);
+    __amdgpu_buffer_rsrc_t rb_src;
+    if constexpr (KR) {
+      rb_src = rebased_rsrc(kr.q, (int64_t)ktr * TS * kr.nq, (int64_t)kr.nq * kr.nq);
+      const float pv = kr.p[kti * kr.np + pcol];
+      if (buf)
+        pk1 = pv;
+      else
+        pk0 = pv;
+      if (++ktr == kr.dq) ktr = 0, ++kti;
+    } else {
+      rb_src = rebased_rsrc(b_mat, (int64_t)k0 * gn + J0 * TS, b_elems);
+    }
     // an interior k-tile, where no lane of the workgroup is masked (every row and column inside the matrix and
     // every A row / B column tile inside its band or triangle -- all k-tiles of a product but its first and
     // last few): the loads take their loop-invariant lane offsets with the k-tile's offset added in the
@@ -402,6 +436,7 @@ __device__ __forceinline__ void flush_phase(typename AccOf<T, WT / 2>::type& acc
     } else if (any) {
       const float* as = &sm.a[cur][a_base];
       const float* bs = &sm.b[cur][b_base];
+      const float pkc = cur ? pk1 : pk0;  // KR: the P entry of this k-tile's U tile
       float4 fa[2][H];
       float fb[2][H][4];
       auto frag = [&](int v, int slot) {
@@ -414,6 +449,7 @@ __device__ __forceinline__ void flush_phase(typename AccOf<T, WT / 2>::type& acc
           for (int s2 = 0; s2 < 4; ++s2) {
             const int s = 4 * v + s2;
             fb[slot][d][s2] = bs[d * TS + s * ROWS + s * ROWS / L::BGRP * L::BPAD];
+            if constexpr (KR) fb[slot][d][s2] *= pkc;
           }
       };
       frag(0, 0);
@@ -443,11 +479,12 @@ __device__ __forceinline__ void flush_phase(typename AccOf<T, WT / 2>::type& acc
   }
 }
 
-template <typename T, int WT, bool VEC>
+template <typename T, int WT, bool VEC, bool KR = false>
 __global__ __launch_bounds__(256, 2) void flush_tiles_mfma_kernel(T* __restrict__ y, T* __restrict__ c,
                                                                   const T* __restrict__ e, const T* __restrict__ l,
                                                                   const T* __restrict__ u, TileFlush g,
-                                                                  BatchMap lmap, BatchMap umap, int64_t b0) {
+                                                                  BatchMap lmap, BatchMap umap, int64_t b0,
+                                                                  KronU kr) {
   constexpr int H = WT / 2;        // tiles per wave per direction
   __shared__ __align__(16) FlushLds<T, WT> sm;
 
@@ -530,12 +567,13 @@ __global__ __launch_bounds__(256, 2) void flush_tiles_mfma_kernel(T* __restrict_
 
   // phase 0: D = L E, then C += D; phase 1: R = C U on top of D, then Y += D + R
   const T* lm = l + lmap.offset(b);
-  const T* um = u + umap.offset(b);
+  const T* um = KR ? nullptr : u + umap.offset(b);
   flush_phase<T, WT, VEC, 0>(acc, sm, lm, g.m * g.m, e + mat, g.m * g.n, g, I0, J0, wi, wj, lo0, hi0, tlo[0], thi[0]);
 #pragma unroll
   for (int ph = 0; ph < 2; ++ph) {
     if (ph == 1)
-      flush_phase<T, WT, VEC, 1>(acc, sm, c + mat, g.m * g.n, um, g.n * g.n, g, I0, J0, wi, wj, lo1, hi1, tlo[1], thi[1]);
+      flush_phase<T, WT, VEC, 1, KR>(acc, sm, c + mat, g.m * g.n, um, g.n * g.n, g, I0, J0, wi, wj, lo1, hi1, tlo[1],
+                                     thi[1], kr);
     // epilogue of the phase: C += D after the down products, Y += D + R after the right ones
 #pragma unroll
     for (int a = 0; a < H; ++a)
@@ -601,16 +639,16 @@ int64_t count_items(const TileFlush& g) {
   return items;
 }
 
-template <typename T, int WT, bool VEC>
+template <typename T, int WT, bool VEC, bool KR = false>
 int launch(T* y, T* c, const T* e, const T* l, const T* u, const TileFlush& g, const BatchMap& lmap,
-           const BatchMap& umap, int64_t B, hipStream_t stream) {
+           const BatchMap& umap, int64_t B, hipStream_t stream, const KronU& kr = KronU{}) {
   const int64_t items = count_items<WT>(g);
   if (items == 0 || B == 0) return 0;
   if (items > 0x7fffffff) return GPTQ2D_EUNSUPPORTED;
   for (int64_t b0 = 0; b0 < B; b0 += 65535) {
     const dim3 grid((unsigned)items, (unsigned)(B - b0 < 65535 ? B - b0 : 65535));
-    hipLaunchKernelGGL((flush_tiles_mfma_kernel<T, WT, VEC>), grid, dim3(256), 0, stream, y, c, e, l, u, g, lmap,
-                       umap, b0);
+    hipLaunchKernelGGL((flush_tiles_mfma_kernel<T, WT, VEC, KR>), grid, dim3(256), 0, stream, y, c, e, l, u, g, lmap,
+                       umap, b0, kr);
   }
   return (int)hipGetLastError();
 }
@@ -654,6 +692,19 @@ int gptq2d_flush_tiles_mfma(T* y, T* c, const T* e, const T* l, const T* u, int6
     if (!vec) return launch<T, 2, false>(y, c, e, l, u, g, lmap, umap, B, stream);
   }
   return launch<T, 2, true>(y, c, e, l, u, g, lmap, umap, B, stream);
+}
+
+// The same flush with U = P (x) Q read from its factors (fp32, one matrix): rows of y, c, e, l and of Q staged
+// 128 bits at a time (m and n multiples of 4, 16-byte aligned matrices), m, n < 2^20.
+int gptq2d_flush_tiles_mfma_kron(float* y, float* c, const float* e, const float* l, const KronU& kr, int64_t m,
+                                 int64_t n, int64_t S0, int64_t S1, int64_t S_end, hipStream_t stream) {
+  BatchMap none;
+  make_batch_map(none, 0, nullptr, nullptr);
+  if (m >= ((int64_t)1 << 20) || n >= ((int64_t)1 << 20) || n != (int64_t)kr.np * kr.nq ||
+      !quad_aligned<float>(y, c, e, l, kr.q, m, n, none, none))
+    return GPTQ2D_EUNSUPPORTED;
+  TileFlush g{m, n, cdiv(m, TS), cdiv(n, TS), S0, S1, S_end};
+  return launch<float, 2, true, true>(y, c, e, l, nullptr, g, none, none, 1, stream, kr);
 }
 
 #define GPTQ2D_FLUSH_TILES_INST(T)                                                                                  \

@@ -31,6 +31,8 @@ int gptq2d_flush(T* y, T* c, const T* e, const T* l, const T* u, int64_t m, int6
                  hipStream_t stream);
 template <typename T>
 int gptq2d_fill(T* x, T v, int64_t count, hipStream_t stream);
+int gptq2d_flush_kron(float* y, float* c, const float* e, const float* l, const KronU& kr, int64_t m, int64_t n,
+                      int64_t s0, int64_t s1, int64_t s_end, hipStream_t stream);
 
 namespace {
 
@@ -290,6 +292,61 @@ __device__ __forceinline__ void pull_chunks(floatx16& acc, const float* __restri
 #pragma unroll
     for (int q = 0; q < G; ++q) {
       if (base + nparts * q >= chi) break;
+#pragma unroll
+      for (int s2 = 0; s2 < 4; ++s2) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[q][s2], bv[q][s2], acc, 0, 0, 0);
+    }
+  }
+}
+
+// pull_chunks for the right product R = C U with U = P (x) Q given by its factors: B value (k, j) of tile column
+// J = j0 / 32 is Q[32 (t % dq) + k % 32, 32 (J % dq) + j % 32] times P[t / dq, J / dq], t = k / 32 -- one fp32
+// multiplication, the entry of the explicit product bit for bit.  The chunk and tile indices are wave-uniform,
+// so the divisions by dq and the P reads run on the scalar unit.
+template <bool VEC>
+__device__ __forceinline__ void pull_chunks_kron(floatx16& acc, const float* __restrict__ A, int64_t lda,
+                                                 int64_t a_rows, int64_t a_cols, const KronU& kr, int64_t b_rows,
+                                                 int64_t b_cols, int64_t i0, int64_t j0, int64_t c_lo, int64_t c_hi,
+                                                 int part, int nparts, int li, int hh) {
+  const int64_t ia = i0 + li, jb = j0 + li;
+  const bool arow = ia < a_rows, bcol = jb < b_cols;
+  const float* ap = A + (arow ? ia : 0) * lda;
+  int pj, qj;  // P column and Q column block of the tile column
+  kron_split(kr, (unsigned)(j0 / TR), pj, qj);
+  const int nq = kr.nq;
+  const float* qp = kr.q + (bcol ? qj * TR + li : 0) + (int64_t)(4 * hh) * nq;  // the lane's column, its k slot
+  const float* pp = kr.p + pj;
+  const int clo = (int)c_lo, chi = (int)c_hi, acols = (int)a_cols, brows = (int)b_rows;
+  const int upart = __builtin_amdgcn_readfirstlane(part), unparts = __builtin_amdgcn_readfirstlane(nparts);
+  constexpr int G = 4;
+  for (int base = clo + upart; base < chi; base += unparts * G) {
+    float av[G][4], bv[G][4];
+#pragma unroll
+    for (int q = 0; q < G; ++q) {
+      const int ch = base + unparts * q;
+      const int k0 = 8 * ch + 4 * hh;
+      const bool ok = ch < chi;
+      if (VEC) {
+        const float4 f = (ok && arow && k0 < acols) ? *reinterpret_cast<const float4*>(ap + k0)
+                                                    : make_float4(0.f, 0.f, 0.f, 0.f);
+        av[q][0] = f.x, av[q][1] = f.y, av[q][2] = f.z, av[q][3] = f.w;
+      } else {
+#pragma unroll
+        for (int s2 = 0; s2 < 4; ++s2) av[q][s2] = (ok && arow && k0 + s2 < acols) ? ap[k0 + s2] : 0.f;
+      }
+      int ti, tr;
+      kron_split(kr, (unsigned)(ok ? ch >> 2 : 0), ti, tr);
+      const float pv = pp[ti * kr.np];
+      const float* bk = qp + (int64_t)(tr * TR + 8 * (ch & 3)) * nq;
+      // the masked loads first, the products after them: a product inside the mask's branch would make each
+      // load wait for its data before the next one issues
+#pragma unroll
+      for (int s2 = 0; s2 < 4; ++s2) bv[q][s2] = (ok && bcol && k0 + s2 < brows) ? bk[s2 * nq] : 0.f;
+#pragma unroll
+      for (int s2 = 0; s2 < 4; ++s2) bv[q][s2] *= pv;
+    }
+#pragma unroll
+    for (int q = 0; q < G; ++q) {
+      if (base + unparts * q >= chi) break;
 #pragma unroll
       for (int s2 = 0; s2 < 4; ++s2) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[q][s2], bv[q][s2], acc, 0, 0, 0);
     }
@@ -602,9 +659,13 @@ struct TileRegs {
   static constexpr int NQ = TR * TR / NTHREADS;
   T y[NQ], c[NQ], l[NQ], u[NQ];
 
+  // KR (fp32): U given by its Kronecker factors (ub unused); the diagonal tile (J, J) of U is
+  // P[J / dq, J / dq] times the diagonal block 32 (J % dq) of Q.
+  template <bool KR = false>
   __device__ __forceinline__ void load(const T* __restrict__ yg, const T* __restrict__ cg,
                                        const T* __restrict__ lb, const T* __restrict__ ub, int64_t m,
-                                       int64_t n, int64_t i0, int64_t j0, int64_t mat) {
+                                       int64_t n, int64_t i0, int64_t j0, int64_t mat, const KronU& kr = KronU{}) {
+    static_assert(!KR || sizeof(T) == 4, "Kronecker U: fp32");
     // the tile's corner in every operand (64-bit arithmetic once, uniform), then 32-bit offsets in
     // the tile (32 rows of at most 2^26 elements)
     const int rows_in = m - i0 < TR ? (int)(m - i0) : TR, cols_in = n - j0 < TR ? (int)(n - j0) : TR;
@@ -613,7 +674,15 @@ struct TileRegs {
     const T* yt = yg + mat + corner;
     const T* ct = cg + mat + corner;
     const T* lt = lb + i0 * m + i0;  // L[i0 + r, i0 + cc] at r m + cc
-    const T* ut = ub + j0 * n + j0;  // U[j0 + r, j0 + cc] at r n + cc
+    const T* ut = KR ? nullptr : ub + j0 * n + j0;  // U[j0 + r, j0 + cc] at r n + cc
+    const float* qt = nullptr;  // KR: Q[32 (J % dq) + r, 32 (J % dq) + cc] at r nq + cc, times pd
+    float pd = 0.f;
+    if constexpr (KR) {
+      int ji, jr;
+      kron_split(kr, (unsigned)(j0 / TR), ji, jr);
+      qt = kr.q + (int64_t)jr * TR * (kr.nq + 1);
+      pd = kr.p[(int64_t)ji * (kr.np + 1)];
+    }
 #pragma unroll
     for (int q = 0; q < NQ; ++q) {
       const int t = threadIdx.x + NTHREADS * q;
@@ -624,7 +693,14 @@ struct TileRegs {
       c[q] = in ? ct[off] : T(0);
       // L[i0+r, i0+cc] strictly below the diagonal; U[j0+r, j0+cc] strictly above it
       l[q] = (cc < r && r < rows_in) ? lt[r * mi + cc] : T(0);
-      u[q] = (!ROWS && r < cc && cc < cols_in) ? ut[off] : T(0);
+      if constexpr (KR)
+        u[q] = (!ROWS && r < cc && cc < cols_in) ? qt[r * kr.nq + cc] : T(0);
+      else
+        u[q] = (!ROWS && r < cc && cc < cols_in) ? ut[off] : T(0);
+    }
+    if constexpr (KR) {  // the products after all loads (masked entries: 0 times pd)
+#pragma unroll
+      for (int q = 0; q < NQ; ++q) u[q] *= pd;
     }
   }
 
@@ -702,14 +778,15 @@ __device__ __forceinline__ void stash_partial(float (*red)[2][TR][TR + 1], const
 // So only one k-tile of each product is on the stage-to-stage critical path; the rest runs beside
 // the previous stage's sweeps.  Waves 0-1 take the down product, waves 2-3 the right one, each
 // every second 8-deep k-chunk; the two halves meet in LDS.
-template <bool VEC, int KIND, bool YPRE, bool ROWS>
+// KR: U = P (x) Q given by its factors (kr; u unused): the right products pull Q times P entries.
+template <bool VEC, int KIND, bool YPRE, bool ROWS, bool KR = false>
 __global__ __launch_bounds__(NTHREADS, 2) void tile_stage_kernel(float* __restrict__ y, float* __restrict__ c,
                                                                  float* __restrict__ e, const float* __restrict__ l,
                                                                  const float* __restrict__ u, int64_t m, int64_t n,
                                                                  int64_t stage, int64_t S0, int64_t tile_lo,
                                                                  int64_t n_sweep, int64_t prep_lo, BatchMap lmap,
                                                                  BatchMap umap, QSpec<float> qs, int64_t nx,
-                                                                 int64_t ny) {
+                                                                 int64_t ny, KronU kr) {
   __shared__ float red[2][2][TR][TR + 1];
   __shared__ TileLds tl;
 
@@ -721,7 +798,7 @@ __global__ __launch_bounds__(NTHREADS, 2) void tile_stage_kernel(float* __restri
   const int64_t i0 = I * TR, j0 = J * TR;
   const int64_t mat = b * m * n;
   const float* lb = l + lmap.offset(b);
-  const float* ub = u + umap.offset(b);
+  const float* ub = KR ? nullptr : u + umap.offset(b);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int li = lane & 31, hh = lane >> 5;
 
@@ -743,7 +820,7 @@ __global__ __launch_bounds__(NTHREADS, 2) void tile_stage_kernel(float* __restri
   SweepInputs<ROWS ? Q_ROUND : KIND> qin;
   RowInputs<float, ROWS ? KIND : Q_ROUND> rin;
   if (sweep) {
-    own.load(y, c, lb, ub, m, n, i0, j0, mat);
+    own.template load<KR>(y, c, lb, ub, m, n, i0, j0, mat, kr);
     if constexpr (ROWS)
       rin.load(qs, b, m, n, i0, j0);
     else
@@ -762,6 +839,8 @@ __global__ __launch_bounds__(NTHREADS, 2) void tile_stage_kernel(float* __restri
     for (int r = 0; r < 16; ++r) acc[r] = 0.f;
     if (wave < wd)
       pull_chunks<VEC>(acc, lb, m, m, m, e + mat, n, m, n, i0, j0, d0, d1, wave, wd, li, hh);
+    else if constexpr (KR)
+      pull_chunks_kron<VEC>(acc, c + mat, n, m, n, kr, n, n, i0, j0, r0, r1, wave - wd, 4 - wd, li, hh);
     else
       pull_chunks<VEC>(acc, c + mat, n, m, n, ub, n, n, n, i0, j0, r0, r1, wave - wd, 4 - wd, li, hh);
     stash_partial(red, acc, wave >> 1, wave & 1);
@@ -919,35 +998,36 @@ void launch_tile64_k(dim3 grid, hipStream_t stream, double* y, double* c, double
                        lo, band_lo, lmap, umap, qs, nx, ny);
 }
 
-template <bool VEC, int KIND, bool ROWS>
+template <bool VEC, int KIND, bool ROWS, bool KR>
 void launch_tile_stage_k(dim3 grid, hipStream_t stream, float* y, float* c, float* e, const float* l, const float* u,
                          int64_t m, int64_t n, int64_t st, int64_t S0, int64_t lo, int64_t n_sweep, int64_t prep_lo,
-                         const BatchMap& lmap, const BatchMap& umap, const QSpec<float>& qs, int64_t nx, int64_t ny) {
+                         const BatchMap& lmap, const BatchMap& umap, const QSpec<float>& qs, int64_t nx, int64_t ny,
+                         const KronU& kr) {
   if (qs.ypre)
-    hipLaunchKernelGGL((tile_stage_kernel<VEC, KIND, true, ROWS>), grid, dim3(NTHREADS), 0, stream, y, c, e, l, u, m, n,
-                       st, S0, lo, n_sweep, prep_lo, lmap, umap, qs, nx, ny);
+    hipLaunchKernelGGL((tile_stage_kernel<VEC, KIND, true, ROWS, KR>), grid, dim3(NTHREADS), 0, stream, y, c, e, l, u,
+                       m, n, st, S0, lo, n_sweep, prep_lo, lmap, umap, qs, nx, ny, kr);
   else
-    hipLaunchKernelGGL((tile_stage_kernel<VEC, KIND, false, ROWS>), grid, dim3(NTHREADS), 0, stream, y, c, e, l, u, m,
-                       n, st, S0, lo, n_sweep, prep_lo, lmap, umap, qs, nx, ny);
+    hipLaunchKernelGGL((tile_stage_kernel<VEC, KIND, false, ROWS, KR>), grid, dim3(NTHREADS), 0, stream, y, c, e, l, u,
+                       m, n, st, S0, lo, n_sweep, prep_lo, lmap, umap, qs, nx, ny, kr);
 }
 
-template <bool VEC, bool ROWS>
+template <bool VEC, bool ROWS, bool KR = false>
 void launch_tile_stage(int32_t kind, dim3 grid, hipStream_t stream, float* y, float* c, float* e, const float* l,
                        const float* u, int64_t m, int64_t n, int64_t st, int64_t S0, int64_t lo, int64_t n_sweep,
                        int64_t prep_lo, const BatchMap& lmap, const BatchMap& umap, const QSpec<float>& qs, int64_t nx,
-                       int64_t ny) {
+                       int64_t ny, const KronU& kr = KronU{}) {
   if (kind == Q_AFFINE)
-    launch_tile_stage_k<VEC, Q_AFFINE, ROWS>(grid, stream, y, c, e, l, u, m, n, st, S0, lo, n_sweep, prep_lo, lmap,
-                                             umap, qs, nx, ny);
+    launch_tile_stage_k<VEC, Q_AFFINE, ROWS, KR>(grid, stream, y, c, e, l, u, m, n, st, S0, lo, n_sweep, prep_lo, lmap,
+                                                 umap, qs, nx, ny, kr);
   else if (kind == Q_FORCED)
-    launch_tile_stage_k<VEC, Q_FORCED, ROWS>(grid, stream, y, c, e, l, u, m, n, st, S0, lo, n_sweep, prep_lo, lmap,
-                                             umap, qs, nx, ny);
+    launch_tile_stage_k<VEC, Q_FORCED, ROWS, KR>(grid, stream, y, c, e, l, u, m, n, st, S0, lo, n_sweep, prep_lo, lmap,
+                                                 umap, qs, nx, ny, kr);
   else if (ROWS && kind == Q_ABSMAX)
-    launch_tile_stage_k<VEC, Q_ABSMAX, true>(grid, stream, y, c, e, l, u, m, n, st, S0, lo, n_sweep, prep_lo, lmap,
-                                             umap, qs, nx, ny);
+    launch_tile_stage_k<VEC, Q_ABSMAX, true, KR>(grid, stream, y, c, e, l, u, m, n, st, S0, lo, n_sweep, prep_lo, lmap,
+                                                 umap, qs, nx, ny, kr);
   else
-    launch_tile_stage_k<VEC, Q_ROUND, ROWS>(grid, stream, y, c, e, l, u, m, n, st, S0, lo, n_sweep, prep_lo, lmap,
-                                            umap, qs, nx, ny);
+    launch_tile_stage_k<VEC, Q_ROUND, ROWS, KR>(grid, stream, y, c, e, l, u, m, n, st, S0, lo, n_sweep, prep_lo, lmap,
+                                                umap, qs, nx, ny, kr);
 }
 
 template <typename T, int KIND>
@@ -969,16 +1049,18 @@ bool strides_mult4(const BatchMap& bm) {
   return true;
 }
 
-// rows: super-entries of 1 x TR (the row sweep); dtype16: the abs-max scale's 16-bit type.
+// rows: super-entries of 1 x TR (the row sweep); dtype16: the abs-max scale's 16-bit type; kron: U given by its
+// Kronecker factors (u unused; fp32, one matrix, rows staged 128 bits at a time).
 template <typename T>
 int sweep_fused(T* y, T* c, T* e, const T* l, const T* u, int64_t m, int64_t n, int32_t bnd, const int64_t* bshape,
                 const int64_t* lstride, const int64_t* ustride, int32_t qkind, const T* qa, const int64_t* qa_stride,
                 const T* qb, const int64_t* qb_stride, double qmin, double qmax, T* ypre, int64_t outer_tiles,
                 int64_t stage_begin, int64_t stage_end, hipStream_t stream, bool rows = false, int32_t dtype16 = 0,
-                T* scale_out = nullptr) {
+                T* scale_out = nullptr, const KronU* kron = nullptr) {
   BatchMap lmap, umap;
   if (!make_batch_map(lmap, bnd, bshape, lstride) || !make_batch_map(umap, bnd, bshape, ustride)) return GPTQ2D_EINVAL;
   if (m <= 0 || n <= 0 || outer_tiles < 1) return GPTQ2D_EINVAL;
+  if (kron && (sizeof(T) != 4 || bnd != 0 || n != (int64_t)kron->np * kron->nq)) return GPTQ2D_EUNSUPPORTED;
   // the tile kernels index inside a tile with 32-bit offsets (32 rows of a row length < 2^26)
   if (m >= ((int64_t)1 << 26) || n >= ((int64_t)1 << 26)) return GPTQ2D_EUNSUPPORTED;
   if (qkind != Q_ROUND && qkind != Q_AFFINE && qkind != Q_FORCED && !(rows && qkind == Q_ABSMAX)) return GPTQ2D_EINVAL;
@@ -1005,11 +1087,12 @@ int sweep_fused(T* y, T* c, T* e, const T* l, const T* u, int64_t m, int64_t n, 
   if (stage_begin < 0 || stage_begin > stage_end || stage_begin % outer_tiles ||
       (stage_end % outer_tiles && stage_end != stages))
     return GPTQ2D_EINVAL;
-  int rc;
-  if (stage_begin == 0 && (rc = gptq2d_fill<T>(c, T(0), B * m * n, stream))) return rc;
   // 128-bit operand loads of the MFMA pull: rows, matrices and pointers 16-byte aligned
   const bool vec = m % 4 == 0 && n % 4 == 0 && aligned16(y) && aligned16(c) && aligned16(e) && aligned16(l) &&
                    aligned16(u) && strides_mult4(lmap) && strides_mult4(umap);
+  if (kron && !(vec && aligned16(kron->q))) return GPTQ2D_EUNSUPPORTED;
+  int rc;
+  if (stage_begin == 0 && (rc = gptq2d_fill<T>(c, T(0), B * m * n, stream))) return rc;
   // fp64: stages per band flush inside an outer block (the tile sweeps pull the band's earlier stages); the row
   // sweep pulls nothing, so its every stage is flushed
   const int64_t band = rows ? 1 : BAND64;
@@ -1034,7 +1117,14 @@ int sweep_fused(T* y, T* c, T* e, const T* l, const T* u, int64_t m, int64_t n, 
         };
         using True = std::true_type;
         using False = std::false_type;
-        if (vec)
+        if (kron) {
+          if (rows)
+            launch_tile_stage<true, true, true>(qkind, g.grid, stream, y, c, e, l, nullptr, m, n, st, S0, lo,
+                                                hi - lo + 1, plo, lmap, umap, qs, g.nx, g.ny, *kron);
+          else
+            launch_tile_stage<true, false, true>(qkind, g.grid, stream, y, c, e, l, nullptr, m, n, st, S0, lo,
+                                                 hi - lo + 1, plo, lmap, umap, qs, g.nx, g.ny, *kron);
+        } else if (vec)
           rows ? launch(True{}, True{}) : launch(True{}, False{});
         else
           rows ? launch(False{}, True{}) : launch(False{}, False{});
@@ -1070,8 +1160,15 @@ int sweep_fused(T* y, T* c, T* e, const T* l, const T* u, int64_t m, int64_t n, 
           return rc;
       }
     }
-    if (S1 < stages && (rc = gptq2d_flush<T>(y, c, e, l, u, m, n, TR, TR, S0, S1, stages, lmap, umap, B, stream)))
-      return rc;
+    if (S1 < stages) {
+      if constexpr (sizeof(T) == 4) {
+        if (kron) {
+          if ((rc = gptq2d_flush_kron(y, c, e, l, *kron, m, n, S0, S1, stages, stream))) return rc;
+          continue;
+        }
+      }
+      if ((rc = gptq2d_flush<T>(y, c, e, l, u, m, n, TR, TR, S0, S1, stages, lmap, umap, B, stream))) return rc;
+    }
   }
   return 0;
 }
@@ -1168,5 +1265,22 @@ int64_t gptq2d_sweep_fused_noalloc_capacity(int32_t elem_bytes) {
 
 GPTQ2D_FUSED_ABI(f32, float)
 GPTQ2D_FUSED_ABI(f64, double)
+
+int gptq2d_sweep_fused_kron_f32(float* y, float* c, float* e, const float* l, const float* up, const float* uq,
+                                int64_t m, int64_t np, int64_t nq, int64_t p, int64_t q, int32_t qkind,
+                                const float* qa, const float* qb, double qmin, double qmax, int32_t dtype16,
+                                float* ypre, float* scale_out, int64_t outer_tiles, int64_t stage_begin,
+                                int64_t stage_end, hipStream_t stream) {
+  if (!up || !uq || np <= 0 || nq <= 0 || p <= 0 || q <= 0) return GPTQ2D_EINVAL;
+  KronU kr;
+  if (!make_kron_u(kr, up, uq, np, nq)) return GPTQ2D_EUNSUPPORTED;
+  const int64_t n = np * nq;
+  if (m % p || n % q) return GPTQ2D_EINVAL;
+  const bool rows = !(p == 1 && q == 1 && qkind != Q_ABSMAX);
+  if (rows && (p != 1 || q != TR)) return GPTQ2D_EUNSUPPORTED;
+  return sweep_fused<float>(y, c, e, l, nullptr, m, n, 0, nullptr, nullptr, nullptr, qkind, qa, nullptr, qb, nullptr,
+                            qmin, qmax, ypre, outer_tiles, stage_begin, stage_end, stream, rows, dtype16, scale_out,
+                            &kr);
+}
 
 }  // extern "C"

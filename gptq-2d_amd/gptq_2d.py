@@ -42,6 +42,45 @@ TILE = 32
 
 # ------------------------------------------------------------------------------------------------ contract
 
+class KroneckerU:
+    """U = outer (x) inner given by its two factors ([k, k] each, one dtype and device), for the sweeps' ``u``
+    argument in place of the (k_outer k_inner)^2 entries of the explicit product (Algorithm 4's per-mode form,
+    gptq_2d_reference.py:270-294, whose factors the reference never multiplies out).  Entries are read as
+    torch.kron(outer, inner) forms them -- every entry of both factors, the product's zeros and diagonal
+    included -- so results equal those with ``dense()`` bit for bit.  The fused fp32 engine reads the factors
+    directly (one matrix, no batch; inner size a multiple of 32, sizes multiples of 4); every other path forms
+    ``dense()`` first."""
+
+    def __init__(self, outer: torch.Tensor, inner: torch.Tensor):
+        assert outer.dim() == 2 and inner.dim() == 2, "the Kronecker factors must be matrices"
+        assert outer.size(0) == outer.size(1) and inner.size(0) == inner.size(1), "the Kronecker factors must be square"
+        assert outer.dtype == inner.dtype and outer.device == inner.device, (
+            "the Kronecker factors must share dtype and device")
+        self.outer, self.inner = outer, inner
+
+    @property
+    def shape(self) -> torch.Size:
+        k = self.outer.size(0) * self.inner.size(0)
+        return torch.Size((k, k))
+
+    @property
+    def dtype(self) -> torch.dtype:
+        return self.outer.dtype
+
+    @property
+    def device(self) -> torch.device:
+        return self.outer.device
+
+    def dim(self) -> int:
+        return 2
+
+    def contiguous(self) -> "KroneckerU":
+        return KroneckerU(self.outer.contiguous(), self.inner.contiguous())
+
+    def dense(self) -> torch.Tensor:
+        return torch.kron(self.outer, self.inner)
+
+
 def _validate_inputs(x, l, u, inplace, require_cuda=False, super_entry_shape=(1, 1)):
     """The shared input contract (gptq_2d.py:65-84); returns m, n and the broadcast batch shape."""
     assert x.dim() >= 2 and l.dim() >= 2 and u.dim() >= 2, "X, L, and U must have at least two dimensions"
@@ -164,6 +203,30 @@ def _fused_spec(quantizer, quantizer_inputs, y, batch_shape, rows=False):
     return None
 
 
+def _run_fused_kron(y, l, u, m, n, spec, outer_block_size, p=1, q=1):
+    """The fused sweep of one matrix with U given by its Kronecker factors (gptq2d_sweep_fused_kron_f32)."""
+    c = torch.empty_like(y)  # zeroed by the library
+    e = torch.empty_like(y)
+    qa, qb = spec["qa"], spec["qb"]
+    _hip.call_untyped(
+        "sweep_fused_kron_f32", _hip.ptr(y), _hip.ptr(c), _hip.ptr(e), _hip.ptr(l), _hip.ptr(u.outer),
+        _hip.ptr(u.inner), m, u.outer.size(0), u.inner.size(0), p, q, spec["kind"], _hip.ptr(qa), _hip.ptr(qb),
+        spec["qmin"], spec["qmax"], spec.get("dtype16", 0), _hip.ptr(spec["ypre"]), _hip.ptr(spec.get("sout")),
+        _outer_tiles(outer_block_size), 0, -1, _hip.stream(y.device),
+    )
+
+
+def _kron_fusable(y, l, u, batch_shape, spec):
+    """Whether the fused engine reads U = u.outer (x) u.inner from its factors (else the product is formed)."""
+    if spec is None or len(batch_shape) != 0 or y.dtype != torch.float32 or l.dim() != 2:
+        return False
+    m, n = y.shape
+    tensors = [y, l, u.inner] + [t for t in (spec["qa"], spec["qb"]) if t is not None]
+    return (u.inner.size(0) % TILE == 0 and m % 4 == 0 and n % 4 == 0 and n < 1 << 26 and
+            all(t.data_ptr() % 16 == 0 for t in tensors) and
+            all(t.shape == y.shape for t in (spec["qa"], spec["qb"]) if t is not None))
+
+
 def _outer_tiles(outer_block_size):
     return max(1, int(outer_block_size) // TILE) if outer_block_size and outer_block_size > 0 else 1
 
@@ -253,8 +316,13 @@ def _sweep(x, l, u, quantizer, super_entry_shape, inner_block_size, outer_block_
         spec = _fused_spec(quantizer, quantizer_inputs, y, batch_shape, rows=(p, q) == (1, TILE))
     assert not (fused is True and spec is None), (
         "fused=True needs a built-in quantizer and plain entries or 1 x 32 super-entries")
+    kron = isinstance(u, KroneckerU)
+    if kron and not _kron_fusable(y, l, u, batch_shape, spec):
+        u, kron = u.dense(), False
     with torch.cuda.device(x.device):
-        if spec is not None:
+        if kron:
+            _run_fused_kron(y, l, u, m, n, spec, outer_block_size, p, q)
+        elif spec is not None:
             _run_fused(y, l, u, m, n, batch_shape, spec, outer_block_size, p, q)
         else:
             _run_blocked(y, l, u, m, n, batch_shape, p, q, super_entry_shape is not None, quantizer,

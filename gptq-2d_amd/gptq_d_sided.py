@@ -6,9 +6,10 @@ Algorithm 4 equals Algorithm 1 on the column-major vec(X) with the feedback fact
 F = L_D (x) ... (x) L_1 (L_d = ldl_of_inverse(H_d)), and so does the two-sided sweep of the
 n_1 x (n_2 ... n_D) matrix whose column index is i_2 + n_2 (i_3 + n_3 (...)) under L = L_1 and
 U = (L_D (x) ... (x) L_2)^T -- the same vec order and the same factor.  The GPU path therefore runs
-the tensor on the two-sided engine: X permuted to modes (1, D, ..., 2) and flattened, U formed once as
-a Kronecker product (n_2 ... n_D squared entries), the fused tile sweep (built-in quantizers) or the
-per-stage plug-in path, and the result permuted back.  The rounding decisions are those of
+the tensor on the two-sided engine: X permuted to modes (1, D, ..., 2) and flattened, U passed as the
+Kronecker pair (L_D^T (x) ... (x) L_3^T, L_2^T) -- read from its factors by the fused fp32 engine where n_2 is
+a multiple of 32, formed once as the product (n_2 ... n_D squared entries) elsewhere --, the fused tile sweep
+(built-in quantizers) or the per-stage plug-in path, and the result permuted back.  The rounding decisions are those of
 Algorithm 4 in exact arithmetic (bitwise in fp64 on the test instances); the schedule is the two-sided
 engine's tiles rather than Algorithm 4's 1 + sum_d (n_d - 1) hyper-antidiagonals.
 """
@@ -45,6 +46,15 @@ def column_factor(ls: Sequence[torch.Tensor]) -> torch.Tensor:
     return f.contiguous()
 
 
+def column_factor_pair(ls: Sequence[torch.Tensor]):
+    """column_factor(ls) as the Kronecker pair of its last product, (L_D^T (x) ... (x) L_3^T) (x) L_2^T
+    (gptq_2d.KroneckerU; D >= 3): the outer factor is the product column_factor forms before its last step, so
+    the pair's entries are column_factor's bit for bit.  D = 2: the single factor L_2^T."""
+    if len(ls) == 2:
+        return column_factor(ls)
+    return _g2.KroneckerU(column_factor([ls[0], *ls[2:]]), _unit_lower(ls[1]).t().contiguous())
+
+
 @torch.no_grad()
 def gptq_d_sided(x: torch.Tensor, ls: Sequence[torch.Tensor], *, quantizer: Callable = round_quantizer,
                  quantizer_inputs: tuple = (), inplace: bool = False, outer_block_size: int = 1024,
@@ -74,7 +84,7 @@ def gptq_d_sided(x: torch.Tensor, ls: Sequence[torch.Tensor], *, quantizer: Call
     in_place_2d = inplace and w.is_contiguous() and w.data_ptr() == x.data_ptr()
     # otherwise the flattening copied x, and the sweep may run on that copy instead of a clone of it
     fresh = w.untyped_storage().data_ptr() != x.untyped_storage().data_ptr()
-    z = _g2.gptq_2d(w, ls[0].contiguous(), column_factor(ls), quantizer=quantizer,
+    z = _g2.gptq_2d(w, ls[0].contiguous(), column_factor_pair(ls), quantizer=quantizer,
                     quantizer_inputs=tuple(t.permute(*perm).reshape(n1, -1).contiguous() for t in quantizer_inputs),
                     outer_block_size=outer_block_size, inplace=in_place_2d or fresh, fused=fused)
     out = z.reshape(n1, *(x.size(d) for d in perm[1:])).permute(*[perm.index(d) for d in range(D)])

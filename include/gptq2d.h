@@ -215,6 +215,21 @@ extern "C" {
                                   const T* table, const T* scale, int64_t scale_stride, T* values, int64_t* states,  \
                                   void* stream);
 
+/* gptq2d_sweep_fused_se_f32 on one matrix (no batch) with U = P (x) Q given by its Kronecker factors
+ * instead of its n^2 entries: up [np, np] and uq [nq, nq] row-major, n = np nq, every entry of both
+ * read (the product's own zeros and diagonal included), and U[i, j] = up[i / nq, j / nq] * uq[i % nq,
+ * j % nq] formed as one fp32 product per use -- the entries of torch.kron(up, uq), so the result is
+ * bit for bit that of gptq2d_sweep_fused_se_f32 with the explicit product.  qa and qb are [m, n]
+ * (contiguous); other arguments as gptq2d_sweep_fused_se_f32.  Replaces the explicit U that the
+ * reference's Algorithm 4 never forms (gptq_2d_reference.py:270-294 reads only the per-mode factors;
+ * the reference's GPU sweep, gptq_2d.py:1378-1447, takes the n x n U).  GPTQ2D_EUNSUPPORTED unless
+ * nq % 32 == 0, n < 2^26, m % 4 == n % 4 == 0 and y, c, e, l, uq are 16-byte aligned. */
+int gptq2d_sweep_fused_kron_f32(float* y, float* c, float* e, const float* l, const float* up, const float* uq,
+                                int64_t m, int64_t np, int64_t nq, int64_t p, int64_t q, int32_t qkind,
+                                const float* qa, const float* qb, double qmin, double qmax, int32_t dtype16,
+                                float* ypre, float* scale_out, int64_t outer_tiles, int64_t stage_begin,
+                                int64_t stage_end, void* stream);
+
 /* Largest B m n (elements per matrix of the batch) gptq2d_sweep_fused_noalloc_* accepts for elements of
  * elem_bytes bytes (4 or 8; -1 otherwise): 2^24 for float, 2^23 for double.  No counterpart in the
  * reference (see gptq2d_sweep_fused_noalloc). */
