@@ -377,7 +377,8 @@ def _c5a3_line(torch, dev, steps, lines, line):
     t_sw = _timed(torch, lambda: DS.gptq_d_sided(x, ls, quantizer=q, quantizer_inputs=(scale, zero),
                                                  outer_block_size=OUTER_BLOCK_WIDE), steps)
     lines["C5a3"] = line(f"{cfg.m}x{cfg.n1}x{cfg.n2} three-sided (D-sided sweep on the two-sided engine, U = "
-                         f"(L_B2 (x) L_B1)^T formed per call), static INT4 abs-max scale per {cfg.group} b2 (bf16)",
+                         f"(L_B2 (x) L_B1)^T read from its two factors), static INT4 abs-max scale per {cfg.group} b2 "
+                         "(bf16)",
                          t_ldl, t_sw)
 
 

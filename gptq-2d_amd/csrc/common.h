@@ -49,43 +49,58 @@ static inline bool make_batch_map(BatchMap& bm, int32_t nd, const int64_t* shape
   return true;
 }
 
-// U = P (x) Q given by its two factors, P [np, np] and Q [nq, nq] (row-major fp32, nq a multiple of 32), instead
-// of its n^2 = (np nq)^2 entries.  With dq = nq / 32, tile (t, J) of U (32 x 32) is one entry of P times one
-// 32 x 32 block of Q:
-//   U[32 t + r, 32 J + c] = P[t / dq, J / dq] * Q[32 (t % dq) + r, 32 (J % dq) + c],
-// each entry formed by one fp32 multiplication, as torch.kron forms the explicit product (the same bits).
-// Tile indices are divided by dq with a multiply-high (Granlund and Montgomery, "Division by invariant integers
-// using multiplication", 1994): exact for every 32-bit dividend, and on the scalar unit for uniform ones.
+// U = P (x) Q given by its two factors, P [np, np] and Q [nq, nq] (row-major fp32, nq a multiple of 16), instead
+// of its n^2 = (np nq)^2 entries:
+//   U[i, j] = P[i / nq, j / nq] * Q[i % nq, j % nq],
+// each entry formed by one fp32 multiplication, as torch.kron forms the explicit product (the same bits).  Since
+// 16 divides nq, every aligned run of 16 rows or columns lies in one block of P: indices are split in units of
+// 16, u = i / 16 = d16 (i / nq) + (i % nq) / 16 with d16 = nq / 16, by a multiply-high (Granlund and Montgomery,
+// "Division by invariant integers using multiplication", 1994): exact for every 32-bit dividend, and on the
+// scalar unit for uniform ones.
 struct KronU {
   const float* p;
   const float* q;
-  int np, nq, dq;
-  unsigned mag;  // floor(2^32 (2^l - dq) / dq) + 1, l = ceil(log2 dq)
+  int np, nq, d16;
+  unsigned mag;  // floor(2^32 (2^l - d16) / d16) + 1, l = ceil(log2 d16)
   int sh1, sh2;  // min(l, 1), max(l - 1, 0)
 };
 
 static inline bool make_kron_u(KronU& k, const float* p, const float* q, int64_t np, int64_t nq) {
-  if (!p || !q || np <= 0 || nq <= 0 || nq % 32 || np >= ((int64_t)1 << 26) || nq >= ((int64_t)1 << 26) ||
+  if (!p || !q || np <= 0 || nq <= 0 || nq % 16 || np >= ((int64_t)1 << 26) || nq >= ((int64_t)1 << 26) ||
       np * nq >= ((int64_t)1 << 26))
     return false;
   k.p = p;
   k.q = q;
   k.np = (int)np;
   k.nq = (int)nq;
-  k.dq = (int)(nq / 32);
+  k.d16 = (int)(nq / 16);
   int l = 0;
-  while (((int64_t)1 << l) < k.dq) ++l;
-  k.mag = (unsigned)((((uint64_t)1 << 32) * (((uint64_t)1 << l) - (uint64_t)k.dq)) / (uint64_t)k.dq + 1);
+  while (((int64_t)1 << l) < k.d16) ++l;
+  k.mag = (unsigned)((((uint64_t)1 << 32) * (((uint64_t)1 << l) - (uint64_t)k.d16)) / (uint64_t)k.d16 + 1);
   k.sh1 = l < 1 ? l : 1;
   k.sh2 = l - 1 > 0 ? l - 1 : 0;
   return true;
 }
 
-// Tile index t split as t = dq i + r, 0 <= r < dq.
-__device__ __forceinline__ void kron_split(const KronU& k, unsigned t, int& i, int& r) {
-  const unsigned t1 = __umulhi(k.mag, t);
-  i = (int)((t1 + ((t - t1) >> k.sh1)) >> k.sh2);
-  r = (int)t - i * k.dq;
+// A 16-row (or column) unit u split as u = d16 i + r, 0 <= r < d16: index 16 u + w (0 <= w < 16) is row
+// 16 r + w of block i of P.
+__device__ __forceinline__ void kron_split(const KronU& k, unsigned u, int& i, int& r) {
+  const unsigned t1 = __umulhi(k.mag, u);
+  i = (int)((t1 + ((u - t1) >> k.sh1)) >> k.sh2);
+  r = (int)u - i * k.d16;
+}
+
+// P[idx] for a wave-uniform idx, read through the scalar data cache (P is never written while a kernel reads it).
+__device__ __forceinline__ float kron_p_uniform(const KronU& k, int idx) {
+  typedef const __attribute__((address_space(4))) float* cptr;
+  return ((cptr)k.p)[__builtin_amdgcn_readfirstlane(idx)];
+}
+
+// (block of P, index in Q) of index j of U's rows or columns.
+__device__ __forceinline__ void kron_index(const KronU& k, int j, int& blk, int& in_q) {
+  int r;
+  kron_split(k, (unsigned)(j >> 4), blk, r);
+  in_q = 16 * r + (j & 15);
 }
 
 static inline int64_t batch_count(int32_t nd, const int64_t* shape) {

@@ -252,15 +252,17 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rebased_rsrc(const T* base, in
 // operand matrices (a_elems / b_elems elements): A is staged through a buffer resource based at the
 // workgroup's first row, B through one based at each k-tile's first row and the workgroup's first
 // column, so that every offset stays below 2^31 bytes for any matrix a tile row or a k-tile of which does.
-// KR (the right product with U = P (x) Q given by its factors, fp32): B is staged from Q, through a resource
-// based at the k-tile's first row of Q, and every B value is multiplied by the P entry of its wave's U tile
-// when the fragments are read -- the U entries of the explicit product, bit for bit.
+// KR (the right product with U = P (x) Q given by its factors, fp32, nq % 16 == 0): B is staged from Q, each
+// 16-row half of a k-tile through a resource based at its first row of Q, and every B value is multiplied by its
+// P entry when the fragments are read -- the U entries of the explicit product, bit for bit.  A lane's fragment
+// values share one P entry per k-tile: its column is fixed, and its k slot covers 16 aligned rows.
 template <typename T, int WT, bool VEC, int PHASE, bool KR = false>
 __device__ __forceinline__ void flush_phase(typename AccOf<T, WT / 2>::type& acc, FlushLds<T, WT>& sm,
                                             const T* a_mat, int64_t a_elems, const T* b_mat, int64_t b_elems,
                                             const TileFlush& g, int64_t I0, int64_t J0, int wi, int wj,
                                             int t_lo, int t_hi, const int (&tlo)[WT / 2][WT / 2],
-                                            const int (&thi)[WT / 2][WT / 2], const KronU& kr = KronU{}) {
+                                            const int (&thi)[WT / 2][WT / 2], const KronU& kr = KronU{},
+                                            float* pk_lds = nullptr) {
   using L = FlushLds<T, WT>;
   static_assert(sizeof(T) == 4 || VEC, "fp64 panels are staged 128 bits at a time");
   static_assert(!KR || (sizeof(T) == 4 && VEC && WT == 2 && PHASE == 1), "U from its Kronecker factors: fp32 "
@@ -300,10 +302,10 @@ __device__ __forceinline__ void flush_phase(typename AccOf<T, WT / 2>::type& acc
     const int j = (int)J0 * TS + f % ROWS;
     o.b_in = j < gn;
     o.b_t = j >> 5;
-    if constexpr (KR) {  // column j of U is column 32 (J % dq) + j % 32 of Q, from the k-tile's first row of Q
-      int ji, jr;
-      kron_split(kr, (unsigned)o.b_t, ji, jr);
-      o.b_off = (o.b_kb * kr.nq + (o.b_in ? jr * TS + (j & (TS - 1)) : 0)) * ES;
+    if constexpr (KR) {  // row kb % 16 of the half k-tile's rows of Q, column j % nq of Q
+      int jb, jq;
+      kron_index(kr, j, jb, jq);
+      o.b_off = ((o.b_kb & 15) * kr.nq + (o.b_in ? jq : 0)) * ES;
     } else {
       o.b_off = (o.b_kb * gn + (o.b_in ? f % ROWS : 0)) * ES;  // from the k-tile's first row, the first column
     }
@@ -319,34 +321,51 @@ __device__ __forceinline__ void flush_phase(typename AccOf<T, WT / 2>::type& acc
   const int i0t = (int)I0, j0t = (int)J0;
   const bool full = (i0t + WT) * TS <= gm && (j0t + WT) * TS <= gn;
 
-  // KR: (t / dq, t % dq) of the next k-tile to stage (issue takes the k-tiles in order, each once), the P column of
-  // the wave's U tiles (clamped: a tile column past the matrix has its B values masked to zero), and the P entry
-  // of the U tile staged in each buffer (uniform values)
-  int kti = 0, ktr = 0, pcol = 0;
-  float pk0 = 0.f, pk1 = 0.f;
+  // KR: (block of P, 16-row unit of Q) of the first half of the next k-tile to stage (issue takes the k-tiles in
+  // order, each once; uniform), and the byte offset in a row of P of the block of the workgroup's column `lane`
+  // (clamped: a column past the matrix has its B values masked to zero).  The P entries of a k-tile -- its two
+  // halves' blocks times the workgroup's 64 columns -- are staged into pk_lds[buffer][half][column] with the
+  // panels (waves 0 and 1, one LDS-direct load each): P never passes through registers, so the compiler's own
+  // waits for vector loads do not hold up the MFMAs of the k-tile before
+  constexpr int LQ = sizeof(T) == 4 ? 32 : 16;  // lanes of one k slot of the fragments below
+  const int li = lane % LQ, hh = lane / LQ;
+  int kub = 0, kur = 0, pofs = 0;
   if constexpr (KR) {
-    kron_split(kr, (unsigned)t_lo, kti, ktr);
-    int jr;
-    kron_split(kr, (unsigned)(j0t + wj), pcol, jr);
-    pcol = pcol < kr.np - 1 ? pcol : kr.np - 1;
+    kron_split(kr, (unsigned)(2 * t_lo), kub, kur);
+    int pb, jq;
+    kron_index(kr, j0t * TS + lane < gn - 1 ? j0t * TS + lane : gn - 1, pb, jq);
+    pofs = pb * 4;
   }
 
   // loads of k-tile t into buffer buf, each masked to what a product may read (L strictly below its
   // diagonal tiles, C and E on the band, U strictly above its diagonal tiles, nothing outside)
   auto issue = [&](int t, int buf) {
     const int ts = (int)t, k0 = ts * TS;
-    __amdgpu_buffer_rsrc_t rb_src;
+    __amdgpu_buffer_rsrc_t rb_src, rb_hi;  // KR: the k-tile's first and second halves of rows
+    int b1 = 0, r1 = 0;                      // KR: the second half's block of P and unit of Q
     if constexpr (KR) {
-      rb_src = rebased_rsrc(kr.q, (int64_t)ktr * TS * kr.nq, (int64_t)kr.nq * kr.nq);
-      const float pv = kr.p[kti * kr.np + pcol];
-      if (buf)
-        pk1 = pv;
-      else
-        pk0 = pv;
-      if (++ktr == kr.dq) ktr = 0, ++kti;
+      b1 = kub, r1 = kur + 1;
+      if (r1 == kr.d16) r1 = 0, ++b1;
+      rb_src = rebased_rsrc(kr.q, (int64_t)kur * 16 * kr.nq, (int64_t)kr.nq * kr.nq);
+      rb_hi = rebased_rsrc(kr.q, (int64_t)r1 * 16 * kr.nq, (int64_t)kr.nq * kr.nq);
     } else {
-      rb_src = rebased_rsrc(b_mat, (int64_t)k0 * gn + J0 * TS, b_elems);
+      rb_src = rb_hi = rebased_rsrc(b_mat, (int64_t)k0 * gn + J0 * TS, b_elems);
     }
+    // KR, after the panels: the k-tile's P entries into pk_lds (wave h stages half h), then the next k-tile's
+    // position
+    auto stage_p = [&]() {
+      if constexpr (KR) {
+        if (wave < 2) {
+          const int pb = wave ? b1 : kub;
+          dma_load<1>(rebased_rsrc(kr.p, (int64_t)pb * kr.np, (int64_t)kr.np * kr.np),
+                      &pk_lds[(buf * 2 + wave) * ROWS], pofs);
+        }
+        kub = b1, kur = r1 + 1;
+        if (kur == kr.d16) kur = 0, ++kub;
+      }
+    };
+    // the B resource of load x: its four k-rows lie in one half of the k-tile
+    auto rb_of = [&](int x) { return KR && (wave + 4 * x) * PER / ROWS >= 16 ? rb_hi : rb_src; };
     // an interior k-tile, where no lane of the workgroup is masked (every row and column inside the matrix and
     // every A row / B column tile inside its band or triangle -- all k-tiles of a product but its first and
     // last few): the loads take their loop-invariant lane offsets with the k-tile's offset added in the
@@ -361,8 +380,9 @@ __device__ __forceinline__ void flush_phase(typename AccOf<T, WT / 2>::type& acc
         for (int x = 0; x < NI; ++x) {
           const int f0 = (wave + 4 * x) * PER;
           dma_load_so<DW>(ra_src, lds_dst(&sm.a[buf][f0]), pre[x].a_off, k0 * ES);
-          dma_load<DW>(rb_src, lds_dst(&sm.b[buf][f0 + f0 / L::BGRP * L::BPAD]), pre[x].b_off);
+          dma_load<DW>(rb_of(x), lds_dst(&sm.b[buf][f0 + f0 / L::BGRP * L::BPAD]), pre[x].b_off);
         }
+        stage_p();
         return;
       }
     }
@@ -375,16 +395,15 @@ __device__ __forceinline__ void flush_phase(typename AccOf<T, WT / 2>::type& acc
       dma_load<DW>(ra_src, lds_dst(&sm.a[buf][f0]), aok ? o.a_off + k0 * ES : OOB);
       const bool bband = PHASE == 0 ? (ts + o.b_t >= s0 && ts + o.b_t < s1) : ts < o.b_t;
       const bool bok = o.b_in && bband && k0 + o.b_kb < kmax;
-      dma_load<DW>(rb_src, lds_dst(&sm.b[buf][f0 + f0 / L::BGRP * L::BPAD]), bok ? o.b_off : OOB);
+      dma_load<DW>(rb_of(x), lds_dst(&sm.b[buf][f0 + f0 / L::BGRP * L::BPAD]), bok ? o.b_off : OOB);
     }
+    stage_p();
   };
 
   // fragments.  fp32: A tile a, k-quad 4 hh + v of row (wi + a) 32 + li; B tile d, k = 16 hh + s, column
   // (wj + d) 32 + li -- the k of MFMA s is 16 hh + s for both operands.  fp64 (one tile per wave): A block a2,
   // k-quad 4 hh + v of row 32 wi + 16 a2 + li; B block d2, k = 8 hh + s, column 32 wj + 16 d2 + li -- the k of
   // MFMA s is 8 hh + s for both operands
-  constexpr int LQ = sizeof(T) == 4 ? 32 : 16;  // lanes of one k slot
-  const int li = lane % LQ, hh = lane / LQ;
   const int kh = (sizeof(T) == 4 ? 16 : 8) * hh;  // first k of the lane's slot
   const int a_base = (wi * TS + li) * TS;
   const int sw = panel_swizzle<T>(li);
@@ -436,7 +455,7 @@ __device__ __forceinline__ void flush_phase(typename AccOf<T, WT / 2>::type& acc
     } else if (any) {
       const float* as = &sm.a[cur][a_base];
       const float* bs = &sm.b[cur][b_base];
-      const float pkc = cur ? pk1 : pk0;  // KR: the P entry of this k-tile's U tile
+      const float pkc = KR ? pk_lds[(cur * 2 + hh) * ROWS + wj * TS + li] : 0.f;  // KR: the lane's P entry
       float4 fa[2][H];
       float fb[2][H][4];
       auto frag = [&](int v, int slot) {
@@ -487,6 +506,7 @@ __global__ __launch_bounds__(256, 2) void flush_tiles_mfma_kernel(T* __restrict_
                                                                   KronU kr) {
   constexpr int H = WT / 2;        // tiles per wave per direction
   __shared__ __align__(16) FlushLds<T, WT> sm;
+  __shared__ float pk_lds[KR ? 2 * 2 * 2 * TS : 1];  // KR: the P entries of each buffer's k-tile (flush_phase)
 
   // XCD-aware order: the hardware deals workgroup w to XCD w % 8; runs of XG consecutive work items
   // (about SR x SR neighbouring blocks, item_block) go to one XCD and its L2, and the XCDs take turns
@@ -573,7 +593,7 @@ __global__ __launch_bounds__(256, 2) void flush_tiles_mfma_kernel(T* __restrict_
   for (int ph = 0; ph < 2; ++ph) {
     if (ph == 1)
       flush_phase<T, WT, VEC, 1, KR>(acc, sm, c + mat, g.m * g.n, um, g.n * g.n, g, I0, J0, wi, wj, lo1, hi1, tlo[1],
-                                     thi[1], kr);
+                                     thi[1], kr, pk_lds);
     // epilogue of the phase: C += D after the down products, Y += D + R after the right ones
 #pragma unroll
     for (int a = 0; a < H; ++a)

@@ -19,6 +19,7 @@
 //   y = (Y[r,c] + sum_{r'<r} L[r,r'] E[r',c]) + sum_{c'<c} C[r,c'] U[c',c]
 // where C[r,c'] is already complete (all rows above in the tile were rounded earlier).
 #include "common.h"
+#include "lds_dma.h"
 #include "profile.h"
 
 #include <mutex>
@@ -298,10 +299,13 @@ __device__ __forceinline__ void pull_chunks(floatx16& acc, const float* __restri
   }
 }
 
-// pull_chunks for the right product R = C U with U = P (x) Q given by its factors: B value (k, j) of tile column
-// J = j0 / 32 is Q[32 (t % dq) + k % 32, 32 (J % dq) + j % 32] times P[t / dq, J / dq], t = k / 32 -- one fp32
-// multiplication, the entry of the explicit product bit for bit.  The chunk and tile indices are wave-uniform,
-// so the divisions by dq and the P reads run on the scalar unit.
+// pull_chunks for the right product R = C U with U = P (x) Q given by its factors (nq % 16 == 0): B value (k, j)
+// is Q[k % nq, j % nq] times P[k / nq, j / nq] -- one fp32 multiplication, the entry of the explicit product bit
+// for bit.  A lane's column is fixed, and an 8-row chunk lies in one block of P, so each chunk takes one P entry
+// per lane; the chunk's 16-row unit is split on the scalar unit.  Q is read through a buffer resource based at
+// the chunk's first row (the lane's column in the vector offset, the row step in the scalar one, a lane past
+// the matrix masked by an offset beyond the extent): no branches and no 64-bit address arithmetic per load.
+// Every row a chunk reads lies below n (the right product's k-tiles are t < J <= nt - 1).
 template <bool VEC>
 __device__ __forceinline__ void pull_chunks_kron(floatx16& acc, const float* __restrict__ A, int64_t lda,
                                                  int64_t a_rows, int64_t a_cols, const KronU& kr, int64_t b_rows,
@@ -310,47 +314,70 @@ __device__ __forceinline__ void pull_chunks_kron(floatx16& acc, const float* __r
   const int64_t ia = i0 + li, jb = j0 + li;
   const bool arow = ia < a_rows, bcol = jb < b_cols;
   const float* ap = A + (arow ? ia : 0) * lda;
-  int pj, qj;  // P column and Q column block of the tile column
-  kron_split(kr, (unsigned)(j0 / TR), pj, qj);
+  int pj = 0, qj = 0;  // the lane's column: block of P, column of Q
+  if (bcol) kron_index(kr, (int)jb, pj, qj);
+  // the tile's columns in one block of P (all but the tiles that straddle a block edge): the chunks' P entries
+  // are read through the scalar cache
+  int pu0, pu1, qu;
+  kron_index(kr, (int)j0, pu0, qu);
+  kron_index(kr, (int)(j0 + TR - 1 < b_cols - 1 ? j0 + TR - 1 : b_cols - 1), pu1, qu);
   const int nq = kr.nq;
-  const float* qp = kr.q + (bcol ? qj * TR + li : 0) + (int64_t)(4 * hh) * nq;  // the lane's column, its k slot
+  const int qoff = bcol ? (qj + 4 * hh * nq) * 4 : OOB;  // bytes: the lane's column of Q, its k slot
   const float* pp = kr.p + pj;
-  const int clo = (int)c_lo, chi = (int)c_hi, acols = (int)a_cols, brows = (int)b_rows;
+  const int clo = (int)c_lo, chi = (int)c_hi, acols = (int)a_cols;
   const int upart = __builtin_amdgcn_readfirstlane(part), unparts = __builtin_amdgcn_readfirstlane(nparts);
   constexpr int G = 4;
-  for (int base = clo + upart; base < chi; base += unparts * G) {
-    float av[G][4], bv[G][4];
+  auto run = [&](auto uniform_c) {
+    constexpr bool UNI = decltype(uniform_c)::value;
+    for (int base = clo + upart; base < chi; base += unparts * G) {
+      float av[G][4], bv[G][4], pv[G];
 #pragma unroll
-    for (int q = 0; q < G; ++q) {
-      const int ch = base + unparts * q;
-      const int k0 = 8 * ch + 4 * hh;
-      const bool ok = ch < chi;
-      if (VEC) {
-        const float4 f = (ok && arow && k0 < acols) ? *reinterpret_cast<const float4*>(ap + k0)
-                                                    : make_float4(0.f, 0.f, 0.f, 0.f);
-        av[q][0] = f.x, av[q][1] = f.y, av[q][2] = f.z, av[q][3] = f.w;
-      } else {
+      for (int q = 0; q < G; ++q) {
+        const int ch = base + unparts * q;
+        const int k0 = 8 * ch + 4 * hh;
+        const bool ok = ch < chi;
+        if (VEC) {
+          const float4 f = (ok && arow && k0 < acols) ? *reinterpret_cast<const float4*>(ap + k0)
+                                                      : make_float4(0.f, 0.f, 0.f, 0.f);
+          av[q][0] = f.x, av[q][1] = f.y, av[q][2] = f.z, av[q][3] = f.w;
+        } else {
 #pragma unroll
-        for (int s2 = 0; s2 < 4; ++s2) av[q][s2] = (ok && arow && k0 + s2 < acols) ? ap[k0 + s2] : 0.f;
+          for (int s2 = 0; s2 < 4; ++s2) av[q][s2] = (ok && arow && k0 + s2 < acols) ? ap[k0 + s2] : 0.f;
+        }
+        int ub, ur;  // the chunk's rows: 16-row unit ch / 2 = block ub of P, rows 16 ur + 8 (ch % 2) + .. of Q
+        kron_split(kr, (unsigned)(ok ? ch >> 1 : 0), ub, ur);
+        if constexpr (UNI)
+          pv[q] = kron_p_uniform(kr, ub * kr.np + pu0);
+        else
+          pv[q] = pp[ub * kr.np];
+        const int row0 = 16 * ur + 8 * (ch & 1);
+        const int64_t ext = ok ? (int64_t)(nq - row0) * nq : 0;  // elements from the chunk's first row
+        const __amdgpu_buffer_rsrc_t qr =
+            __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(kr.q + (int64_t)row0 * nq), (short)0,
+                                              (int)(ext < OOB / 4 ? ext * 4 : OOB), 0x00020000);
+#pragma unroll
+        for (int s2 = 0; s2 < 4; ++s2)
+          bv[q][s2] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(qr, qoff, s2 * nq * 4, 0));
       }
-      int ti, tr;
-      kron_split(kr, (unsigned)(ok ? ch >> 2 : 0), ti, tr);
-      const float pv = pp[ti * kr.np];
-      const float* bk = qp + (int64_t)(tr * TR + 8 * (ch & 3)) * nq;
-      // the masked loads first, the products after them: a product inside the mask's branch would make each
-      // load wait for its data before the next one issues
+      // the products after all loads: a product inside a mask's branch would make each load wait for its data
+      // before the next one issues
 #pragma unroll
-      for (int s2 = 0; s2 < 4; ++s2) bv[q][s2] = (ok && bcol && k0 + s2 < brows) ? bk[s2 * nq] : 0.f;
+      for (int q = 0; q < G; ++q)
 #pragma unroll
-      for (int s2 = 0; s2 < 4; ++s2) bv[q][s2] *= pv;
+        for (int s2 = 0; s2 < 4; ++s2) bv[q][s2] *= pv[q];
+#pragma unroll
+      for (int q = 0; q < G; ++q) {
+        if (base + unparts * q >= chi) break;
+#pragma unroll
+        for (int s2 = 0; s2 < 4; ++s2)
+          acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[q][s2], bv[q][s2], acc, 0, 0, 0);
+      }
     }
-#pragma unroll
-    for (int q = 0; q < G; ++q) {
-      if (base + unparts * q >= chi) break;
-#pragma unroll
-      for (int s2 = 0; s2 < 4; ++s2) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[q][s2], bv[q][s2], acc, 0, 0, 0);
-    }
-  }
+  };
+  if (pu0 == pu1)
+    run(std::true_type{});
+  else
+    run(std::false_type{});
 }
 
 // LDS row pitch of the tile's Y and E images: 40 = 8 (mod 32) keeps the column walks of the E reads
@@ -659,8 +686,8 @@ struct TileRegs {
   static constexpr int NQ = TR * TR / NTHREADS;
   T y[NQ], c[NQ], l[NQ], u[NQ];
 
-  // KR (fp32): U given by its Kronecker factors (ub unused); the diagonal tile (J, J) of U is
-  // P[J / dq, J / dq] times the diagonal block 32 (J % dq) of Q.
+  // KR (fp32): U given by its Kronecker factors (ub unused), each entry of the diagonal tile (J, J) read as its
+  // P entry times its Q entry.
   template <bool KR = false>
   __device__ __forceinline__ void load(const T* __restrict__ yg, const T* __restrict__ cg,
                                        const T* __restrict__ lb, const T* __restrict__ ub, int64_t m,
@@ -675,14 +702,7 @@ struct TileRegs {
     const T* ct = cg + mat + corner;
     const T* lt = lb + i0 * m + i0;  // L[i0 + r, i0 + cc] at r m + cc
     const T* ut = KR ? nullptr : ub + j0 * n + j0;  // U[j0 + r, j0 + cc] at r n + cc
-    const float* qt = nullptr;  // KR: Q[32 (J % dq) + r, 32 (J % dq) + cc] at r nq + cc, times pd
-    float pd = 0.f;
-    if constexpr (KR) {
-      int ji, jr;
-      kron_split(kr, (unsigned)(j0 / TR), ji, jr);
-      qt = kr.q + (int64_t)jr * TR * (kr.nq + 1);
-      pd = kr.p[(int64_t)ji * (kr.np + 1)];
-    }
+    T pu[NQ];  // KR: the P entries of the u[q]
 #pragma unroll
     for (int q = 0; q < NQ; ++q) {
       const int t = threadIdx.x + NTHREADS * q;
@@ -693,14 +713,22 @@ struct TileRegs {
       c[q] = in ? ct[off] : T(0);
       // L[i0+r, i0+cc] strictly below the diagonal; U[j0+r, j0+cc] strictly above it
       l[q] = (cc < r && r < rows_in) ? lt[r * mi + cc] : T(0);
-      if constexpr (KR)
-        u[q] = (!ROWS && r < cc && cc < cols_in) ? qt[r * kr.nq + cc] : T(0);
-      else
+      if constexpr (KR) {
+        const bool on = !ROWS && r < cc && cc < cols_in;
+        int ib = 0, iq = 0, jb = 0, jq = 0;
+        if (on) {
+          kron_index(kr, (int)j0 + r, ib, iq);
+          kron_index(kr, (int)j0 + cc, jb, jq);
+        }
+        u[q] = on ? kr.q[(int64_t)iq * kr.nq + jq] : T(0);
+        pu[q] = on ? kr.p[(int64_t)ib * kr.np + jb] : T(0);
+      } else {
         u[q] = (!ROWS && r < cc && cc < cols_in) ? ut[off] : T(0);
+      }
     }
-    if constexpr (KR) {  // the products after all loads (masked entries: 0 times pd)
+    if constexpr (KR) {  // the products after all loads (masked entries: 0 times 0)
 #pragma unroll
-      for (int q = 0; q < NQ; ++q) u[q] *= pd;
+      for (int q = 0; q < NQ; ++q) u[q] *= pu[q];
     }
   }
 

@@ -48,7 +48,7 @@ class KroneckerU:
     gptq_2d_reference.py:270-294, whose factors the reference never multiplies out).  Entries are read as
     torch.kron(outer, inner) forms them -- every entry of both factors, the product's zeros and diagonal
     included -- so results equal those with ``dense()`` bit for bit.  The fused fp32 engine reads the factors
-    directly (one matrix, no batch; inner size a multiple of 32, sizes multiples of 4); every other path forms
+    directly (one matrix, no batch; inner size a multiple of 16, sizes multiples of 4); every other path forms
     ``dense()`` first."""
 
     def __init__(self, outer: torch.Tensor, inner: torch.Tensor):
@@ -222,7 +222,7 @@ def _kron_fusable(y, l, u, batch_shape, spec):
         return False
     m, n = y.shape
     tensors = [y, l, u.inner] + [t for t in (spec["qa"], spec["qb"]) if t is not None]
-    return (u.inner.size(0) % TILE == 0 and m % 4 == 0 and n % 4 == 0 and n < 1 << 26 and
+    return (u.inner.size(0) % 16 == 0 and m % 4 == 0 and n % 4 == 0 and n < 1 << 26 and
             all(t.data_ptr() % 16 == 0 for t in tensors) and
             all(t.shape == y.shape for t in (spec["qa"], spec["qb"]) if t is not None))
 

@@ -8,7 +8,7 @@ n_1 x (n_2 ... n_D) matrix whose column index is i_2 + n_2 (i_3 + n_3 (...)) und
 U = (L_D (x) ... (x) L_2)^T -- the same vec order and the same factor.  The GPU path therefore runs
 the tensor on the two-sided engine: X permuted to modes (1, D, ..., 2) and flattened, U passed as the
 Kronecker pair (L_D^T (x) ... (x) L_3^T, L_2^T) -- read from its factors by the fused fp32 engine where n_2 is
-a multiple of 32, formed once as the product (n_2 ... n_D squared entries) elsewhere --, the fused tile sweep
+a multiple of 16, formed once as the product (n_2 ... n_D squared entries) elsewhere --, the fused tile sweep
 (built-in quantizers) or the per-stage plug-in path, and the result permuted back.  The rounding decisions are those of
 Algorithm 4 in exact arithmetic (bitwise in fp64 on the test instances); the schedule is the two-sided
 engine's tiles rather than Algorithm 4's 1 + sum_d (n_d - 1) hyper-antidiagonals.

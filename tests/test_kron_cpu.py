@@ -45,7 +45,7 @@ def test_column_factor_pair_equals_formed_product(shape):
 
 
 def test_fused_reader_selection():
-    """One fp32 matrix, inner size a multiple of 32, sizes multiples of 4, 16-byte aligned operands, a built-in
+    """One fp32 matrix, inner size a multiple of 16, sizes multiples of 4, 16-byte aligned operands, a built-in
     quantizer: read from the factors; anything else forms the product."""
     def fusable(m, np_, nq, dtype=torch.float32, batch=(), spec_kind="round"):
         y = torch.zeros(*batch, m, np_ * nq, dtype=dtype)
@@ -54,8 +54,8 @@ def test_fused_reader_selection():
         spec = G._fused_spec(QI.round_quantizer, (), y, torch.Size(batch)) if spec_kind == "round" else None
         return G._kron_fusable(y, l, u, torch.Size(batch), spec)
 
-    assert fusable(64, 3, 32) and fusable(100, 2, 96)
-    assert not fusable(64, 3, 24)                          # inner size not a multiple of 32
+    assert fusable(64, 3, 32) and fusable(100, 2, 96) and fusable(64, 2, 112) and fusable(32, 5, 48)
+    assert not fusable(64, 3, 24)                          # inner size not a multiple of 16
     assert not fusable(62, 3, 32)                          # m not a multiple of 4
     assert not fusable(64, 3, 32, dtype=torch.float64)     # fp64 engine
     assert not fusable(64, 3, 32, batch=(2,))              # a batch of matrices
@@ -77,7 +77,7 @@ def test_entry_point_rejects_bad_arguments():
 
     assert call(up=None) == EINVAL
     assert call(np_=0) == EINVAL
-    assert call(nq=48) == EUNSUPPORTED                      # inner size not a multiple of 32
+    assert call(nq=40) == EUNSUPPORTED                      # inner size not a multiple of 16
     assert call(np_=1 << 20, nq=64) == EUNSUPPORTED         # n >= 2^26
     assert call(p=3) == EINVAL                              # super-entry rows must divide m
     assert call(q=16) == EUNSUPPORTED                       # only 1 x 1 and 1 x 32 super-entries

@@ -2,11 +2,12 @@
 gptq2d_sweep_fused_kron_f32): U = P (x) Q read as P[i / nq, j / nq] * Q[i % nq, j % nq] by the tile stages and the
 flushes, against the same sweep with the explicit product torch.kron(P, Q) -- the entries Algorithm 4 forms from
 its per-mode factors (gptq_2d_reference.py:270-294) -- bit for bit: outputs, and for the teacher-forced quantizer
-every pre-rounding value.  Cases cross the tile and workgroup edges of both factors (nq = 32, where the two tile
-columns of a flush workgroup lie in different blocks of P; nq = 96, three tiles per block; m and n not multiples
-of 32), plain entries and 1 x 32 super-entry rows, several outer block sizes, a resumed call, the D-sided sweep
-(D = 3, 4) and C5a's full-size layer.  Shapes the fused reader does not take (fp64, a batch, nq % 32 != 0) form
-the product and give the same result.
+every pre-rounding value.  Cases cross the tile and workgroup edges of both factors (nq = 16 and 48, where
+blocks of P change inside a 32-row k-tile and inside a tile's columns; nq = 32, where the two tile columns of a
+flush workgroup lie in different blocks; nq = 96 and 112; m and n not multiples of 32), plain entries and 1 x 32
+super-entry rows, several outer block sizes, a resumed call, the D-sided sweep (D = 3, 4) and the full-size
+three-factor layer in both forms (C5a, C5a three-sided).  Shapes the fused reader does not take (fp64, a batch,
+nq % 16 != 0) form the product and give the same result.
 """
 
 import functools
@@ -56,6 +57,12 @@ def _quantizer(kind, x, seed):
 
 CASES = [  # m, np, nq, quantizer, 1 x 32 rows, outer block (antidiagonals)
     (64, 3, 32, "round", False, 64),
+    (64, 5, 16, "round", False, 64),
+    (68, 3, 48, "affine", False, 96),
+    (96, 3, 112, "affine", False, 128),
+    (40, 2, 80, "round", False, 64),
+    (64, 4, 48, "absmax", True, 96),
+    (32, 2, 112, "affine", True, 64),
     (100, 5, 32, "affine", False, 128),
     (96, 2, 64, "affine", False, 96),
     (128, 3, 96, "round", False, 256),
@@ -83,7 +90,8 @@ def test_kron_equals_explicit(m, np_, nq, kind, rows, outer):
     assert z_kron.isfinite().all()
 
 
-@pytest.mark.parametrize("m,np_,nq,outer", [(96, 3, 32, 64), (100, 4, 64, 128), (64, 2, 96, 96)])
+@pytest.mark.parametrize("m,np_,nq,outer", [(96, 3, 32, 64), (100, 4, 64, 128), (64, 2, 96, 96), (72, 3, 112, 96),
+                                             (64, 7, 16, 64)])
 def test_kron_teacher_forced_values(m, np_, nq, outer):
     """Teacher-forced with the dense run's codes: every pre-rounding value of the Kronecker run equals the
     explicit run's bit for bit (the feedback sums, not only the codes)."""
@@ -124,7 +132,7 @@ def test_kron_resumed_call():
 
 
 def test_kron_other_paths_form_the_product():
-    """fp64, a batch of matrices and an inner factor whose size is not a multiple of 32 take the explicit product:
+    """fp64, a batch of matrices and an inner factor whose size is not a multiple of 16 take the explicit product:
     the same result as passing it."""
     x, lo, p, q = _instance(64, 3, 32, 5, torch.float64)
     assert torch.equal(G.gptq_2d(x, lo, G.KroneckerU(p, q)), G.gptq_2d(x, lo, torch.kron(p, q)))
@@ -137,9 +145,9 @@ def test_kron_other_paths_form_the_product():
                        G.gptq_2d(x, lo, torch.kron(p, q), fused=False))
 
 
-@pytest.mark.parametrize("shape", [(40, 64, 3), (36, 32, 2, 3), (64, 96, 2)])
+@pytest.mark.parametrize("shape", [(40, 64, 3), (36, 32, 2, 3), (64, 96, 2), (40, 112, 3), (32, 16, 3, 2)])
 def test_d_sided_kron(shape):
-    """The D-sided sweep passes U as the pair (L_D^T (x) ... (x) L_3^T, L_2^T); with n_2 a multiple of 32 the
+    """The D-sided sweep passes U as the pair (L_D^T (x) ... (x) L_3^T, L_2^T); with n_2 a multiple of 16 the
     fused engine reads it from the factors: equal to the sweep with U = column_factor(ls) formed."""
     print(f"d-sided kron {shape}", flush=True)
     g = torch.Generator().manual_seed(sum(shape))
@@ -176,3 +184,28 @@ def test_kron_c5a_full_size():
     del up
     assert torch.equal(z_kron, z_dense)
     print(f"  equal ({z_kron.numel()} entries)", flush=True)
+
+
+@pytest.mark.timeout(600)
+def test_kron_c5a_three_sided_full_size():
+    """C5a's layer as the three-sided tensor X[i, b1, b2] (8192 x 112 x 256, D-sided sweep, static abs-max INT4
+    scales per 32 consecutive b2): U = (L_B2 (x) L_B1)^T read from its factors (the inner one 112 x 112) gives the
+    outputs of the sweep with the explicit 28672^2 U bit for bit."""
+    cfg = instances.THREE_FACTOR["C5a"]
+    m, n1, n2 = cfg.m, cfg.n1, cfg.n2
+    print(f"C5a three-sided kron: {m}x{n1}x{n2}", flush=True)
+    x = instances.weights(m, n1 * n2, cfg.seeds[0], True, False).float().view(m, n1, n2).to(DEV)
+    ls = [LDL.ldl_of_inverse(instances.wishart_factor(k, cfg.alpha, s, device=DEV).float())
+          for k, s in zip((m, n1, n2), cfg.seeds[1:])]
+    scale = instances.abs_max_group_scale(x, cfg.group, cfg.qmin, cfg.qmax)
+    q = functools.partial(QI.affine_quantizer_hip, qmin=cfg.qmin, qmax=cfg.qmax)
+    z_kron = DS.gptq_d_sided(x, ls, quantizer=q, quantizer_inputs=(scale, torch.zeros_like(x)), outer_block_size=1024,
+                             fused=True)
+    perm = DS.mode_permutation(3)
+    flat = lambda t: t.permute(*perm).reshape(m, -1).contiguous()
+    up = DS.column_factor(ls)
+    z = G.gptq_2d(flat(x), ls[0], up, quantizer=q, quantizer_inputs=(flat(scale), torch.zeros(m, n1 * n2, device=DEV)),
+                  outer_block_size=1024, fused=True)
+    del up
+    assert torch.equal(flat(z_kron), z)
+    print(f"  equal ({z.numel()} entries)", flush=True)
