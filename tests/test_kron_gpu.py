@@ -26,10 +26,10 @@ pytestmark = pytest.mark.gpu
 DEV = "cuda"
 
 
-def _unit_upper(k, seed, dtype=torch.float32, scale=.3):
+def _unit_upper(k, seed, dtype=torch.float32, scale=.3, diag=1.):
     g = torch.Generator().manual_seed(seed)
     f = scale / k ** .5 * torch.randn(k, k, generator=g, dtype=torch.float64)
-    return (f.triu(1) + torch.eye(k, dtype=torch.float64)).to(dtype).to(DEV)
+    return (f.triu(1) + diag * torch.eye(k, dtype=torch.float64)).to(dtype).to(DEV)
 
 
 def _unit_lower(k, seed, dtype=torch.float32):
@@ -88,6 +88,28 @@ def test_kron_equals_explicit(m, np_, nq, kind, rows, outer):
     z_dense = run(torch.kron(p, q))
     assert torch.equal(z_kron, z_dense)
     assert z_kron.isfinite().all()
+
+
+def test_kron_factor_diagonals_enter():
+    """Factors whose diagonals are not 1 (the engine reads U strictly above its diagonal, which then holds P's
+    diagonal entries times Q's upper entries, and Q's diagonal times P's upper ones) and a 1 x 1 outer factor:
+    equal to the explicit product's sweep, values before rounding included."""
+    for m, np_, nq, rows in ((64, 3, 48, False), (96, 1, 64, False), (64, 2, 32, True), (40, 4, 16, False)):
+        print(f"kron diagonals {m}x({np_}x{nq}) rows={rows}", flush=True)
+        x, lo, _, _ = _instance(m, np_, nq, 3 * m + nq)
+        p = _unit_upper(np_, m + 1, diag=1.25)
+        q = _unit_upper(nq, m + 2, diag=0.75)
+        se = dict(super_entry_shape=(1, 32)) if rows else {}
+        run = functools.partial(G.gptq_2d_super_entry, **se) if rows else G.gptq_2d
+        z = run(x, lo, torch.kron(p, q), outer_block_size=64, fused=True)
+        pre_k, pre_d = torch.full_like(x, float("nan")), torch.full_like(x, float("nan"))
+        zk = run(x, lo, G.KroneckerU(p, q), quantizer=QI.teacher_forced_quantizer, quantizer_inputs=(z, pre_k),
+                 outer_block_size=64, fused=True)
+        zd = run(x, lo, torch.kron(p, q), quantizer=QI.teacher_forced_quantizer, quantizer_inputs=(z, pre_d),
+                 outer_block_size=64, fused=True)
+        assert torch.equal(zk, z) and torch.equal(zd, z)
+        assert torch.equal(run(x, lo, G.KroneckerU(p, q), outer_block_size=64, fused=True), z)
+        assert not pre_k.isnan().any() and torch.equal(pre_k, pre_d)
 
 
 @pytest.mark.parametrize("m,np_,nq,outer", [(96, 3, 32, 64), (100, 4, 64, 128), (64, 2, 96, 96), (72, 3, 112, 96),
