@@ -74,6 +74,9 @@ class KroneckerU:
     def dim(self) -> int:
         return 2
 
+    def numel(self) -> int:
+        return self.shape.numel()
+
     def contiguous(self) -> "KroneckerU":
         return KroneckerU(self.outer.contiguous(), self.inner.contiguous())
 
@@ -385,14 +388,17 @@ def capture_gptq_2d(x, l, u, *, quantizer: Callable | None = None, super_entry_s
                             **{k: v for k, v in options.items() if v is not None})
     names = ("X", "L", "U", *(f"quantizer input {i}" for i in range(len(quantizer_inputs))))
     inputs = (x, l, u, *quantizer_inputs)
-    expected = tuple((t.shape, t.dtype, t.device) for t in inputs)
+    # a KroneckerU is captured as its two factors (static copies of both; replays take a pair of the same sizes)
+    factors = lambda t: (t.outer.shape, t.inner.shape) if isinstance(t, KroneckerU) else None
+    expected = tuple((t.shape, t.dtype, t.device, factors(t)) for t in inputs)
 
     def validate_replay(*replay_inputs):
         assert len(replay_inputs) == len(expected), f"expected {len(expected) - 3} quantizer inputs"
-        for name, t, (shape, dtype, device) in zip(names, replay_inputs, expected):
+        for name, t, (shape, dtype, device, fs) in zip(names, replay_inputs, expected):
             assert t.shape == shape, f"{name} shape must match its capture example"
             assert t.dtype == dtype, f"{name} dtype must match its capture example"
             assert t.device == device, f"{name} device must match its capture example"
+            assert factors(t) == fs, f"{name} must be given as its capture example was (tensor or Kronecker pair)"
         if inplace:
             assert replay_inputs[0].is_contiguous(), "inplace=True requires contiguous X"
 
@@ -406,7 +412,19 @@ def capture_gptq_2d(x, l, u, *, quantizer: Callable | None = None, super_entry_s
 
         return replay_empty
 
-    statics = tuple(t.detach().clone(memory_format=torch.contiguous_format) for t in inputs)
+    def static(t):
+        if isinstance(t, KroneckerU):
+            return KroneckerU(static(t.outer), static(t.inner))
+        return t.detach().clone(memory_format=torch.contiguous_format)
+
+    def refill(dst, src):
+        if isinstance(dst, KroneckerU):
+            dst.outer.copy_(src.outer)
+            dst.inner.copy_(src.inner)
+        else:
+            dst.copy_(src)
+
+    statics = tuple(static(t) for t in inputs)
     sx, sl, su = statics[:3]
     sq = statics[3:]
     with torch.cuda.device(x.device):
@@ -426,7 +444,7 @@ def capture_gptq_2d(x, l, u, *, quantizer: Callable | None = None, super_entry_s
         validate_replay(x, l, u, *qi)
         sx.copy_(x)
         sl.copy_(l)
-        su.copy_(u)
+        refill(su, u)
         for s, t in zip(sq, qi):
             s.copy_(t)
         graph.replay()

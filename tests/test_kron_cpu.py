@@ -26,7 +26,8 @@ def _unit_lower(k, seed, dtype=torch.float32):
 def test_kronecker_u_contract():
     p, q = _unit_lower(3, 1).t(), _unit_lower(32, 2).t()
     u = G.KroneckerU(p, q)
-    assert u.shape == (96, 96) and u.dim() == 2 and u.dtype == torch.float32 and u.device == p.device
+    assert u.shape == (96, 96) and u.dim() == 2 and u.numel() == 96 * 96 and u.dtype == torch.float32
+    assert u.device == p.device
     assert torch.equal(u.dense(), torch.kron(p, q))
     assert u.contiguous().outer.is_contiguous() and torch.equal(u.contiguous().dense(), u.dense())
     with pytest.raises(AssertionError):

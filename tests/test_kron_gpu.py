@@ -231,3 +231,23 @@ def test_kron_c5a_three_sided_full_size():
     del up
     assert torch.equal(flat(z_kron), z)
     print(f"  equal ({z.numel()} entries)", flush=True)
+
+
+def test_kron_graph_replay():
+    """capture_gptq_2d with U given as a Kronecker pair: every replay -- new inputs each time, with eager work and
+    synchronisations between replays -- equals the eager sweep with the explicit product."""
+    m, np_, nq = 64, 3, 48
+    x, lo, p, q = _instance(m, np_, nq, 77)
+    eye = torch.eye(np_, device=DEV)
+    replay = G.capture_gptq_2d(x, lo, G.KroneckerU(p, q), outer_block_size=64)
+    for r in range(3):
+        print(f"kron graph replay {r}", flush=True)
+        xr = x * (1. + .25 * r)
+        pr = (p - eye) * (1. + .1 * r) + eye
+        got = replay(xr, lo, G.KroneckerU(pr, q))
+        torch.cuda.synchronize()
+        want = G.gptq_2d(xr, lo, torch.kron(pr, q), outer_block_size=64, fused=True)
+        torch.cuda.synchronize()
+        assert torch.equal(got, want)
+    with pytest.raises(AssertionError):
+        replay(x, lo, torch.kron(p, q))  # captured as a pair: replays take a pair
