@@ -103,6 +103,11 @@ def _validate_inputs(x, l, u, inplace, require_cuda=False, super_entry_shape=(1,
     return m, n, batch_shape
 
 
+def _dense_u(u):
+    """U as a tensor: a KroneckerU's product (the PyTorch variants multiply U's entries directly)."""
+    return u.dense() if isinstance(u, KroneckerU) else u
+
+
 def _prepare_output(x, l, u, inplace, require_cuda=False, super_entry_shape=(1, 1)):
     """Validate and create the work matrix Y (a clone, or x itself in place) (gptq_2d.py:87-100)."""
     m, n, batch_shape = _validate_inputs(x, l, u, inplace, require_cuda, super_entry_shape)
@@ -462,6 +467,7 @@ def capture_gptq_2d(x, l, u, *, quantizer: Callable | None = None, super_entry_s
 def gptq_2d_torch(x, l, u, *, quantizer: Callable = round_quantizer, inplace: bool = False,
                   quantizer_inputs: tuple = ()) -> torch.Tensor:
     """Algorithm 3 in PyTorch on any device: three ``addcmul_`` per stage (gptq_2d.py:1196-1236)."""
+    u = _dense_u(u)
     y, m, n, batch_shape = _prepare_output(x, l, u, inplace)
     if y.numel() == 0:
         return y
@@ -488,6 +494,7 @@ def gptq_2d_torch(x, l, u, *, quantizer: Callable = round_quantizer, inplace: bo
 def gptq_2d_super_entry_torch(x, l, u, *, quantizer: Callable = round_quantizer_super_entry, super_entry_shape=(1, 1),
                               inplace: bool = False, quantizer_inputs: tuple = ()) -> torch.Tensor:
     """Super-entry Algorithm 3 in PyTorch on any device (gptq_2d.py:1239-1292)."""
+    u = _dense_u(u)
     p, q = super_entry_shape
     y, m, n, batch_shape = _prepare_output(x, l, u, inplace, super_entry_shape=(p, q))
     if y.numel() == 0:
@@ -518,6 +525,7 @@ def gptq_2d_super_entry_torch(x, l, u, *, quantizer: Callable = round_quantizer_
 def direct_2d(x, l, u, *, quantizer: Callable = round_quantizer, inplace: bool = False,
               quantizer_inputs: tuple = ()) -> torch.Tensor:
     """Direct quartic Algorithm 2 in PyTorch (gptq_2d.py:1122-1151)."""
+    u = _dense_u(u)
     y, m, n, batch_shape = _prepare_output(x, l, u, inplace)
     if y.numel() == 0:
         return y
@@ -539,6 +547,7 @@ def direct_2d(x, l, u, *, quantizer: Callable = round_quantizer, inplace: bool =
 def direct_2d_super_entry(x, l, u, *, quantizer: Callable = round_quantizer_super_entry, super_entry_shape=(1, 1),
                           inplace: bool = False, quantizer_inputs: tuple = ()) -> torch.Tensor:
     """Direct quartic Algorithm 2 over super-entries in PyTorch (gptq_2d.py:1154-1193)."""
+    u = _dense_u(u)
     p, q = super_entry_shape
     y, m, n, batch_shape = _prepare_output(x, l, u, inplace, super_entry_shape=(p, q))
     if y.numel() == 0:

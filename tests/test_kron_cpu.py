@@ -87,3 +87,16 @@ def test_entry_point_rejects_bad_arguments():
     assert call(qkind=7) == EINVAL
     assert call(m=62) == EUNSUPPORTED                       # rows of 62 entries: no 128-bit staging
     assert call(ptr=dummy + 4) == EUNSUPPORTED              # operands not 16-byte aligned
+
+
+def test_torch_variants_take_the_pair():
+    """The PyTorch variants (CPU here) run a KroneckerU as its product: the same outputs as with torch.kron."""
+    g = torch.Generator().manual_seed(5)
+    x = 3. * torch.randn(6, 8, generator=g, dtype=torch.float64)
+    lo = _unit_lower(6, 21, torch.float64)
+    p, q = _unit_lower(2, 22, torch.float64).t(), _unit_lower(4, 23, torch.float64).t()
+    for fn in (G.gptq_2d_torch, G.direct_2d):
+        assert torch.equal(fn(x, lo, G.KroneckerU(p, q)), fn(x, lo, torch.kron(p, q)))
+    for fn in (G.gptq_2d_super_entry_torch, G.direct_2d_super_entry):
+        assert torch.equal(fn(x, lo, G.KroneckerU(p, q), super_entry_shape=(2, 2)),
+                           fn(x, lo, torch.kron(p, q), super_entry_shape=(2, 2)))
