@@ -1088,7 +1088,11 @@ int sweep_fused(T* y, T* c, T* e, const T* l, const T* u, int64_t m, int64_t n, 
   BatchMap lmap, umap;
   if (!make_batch_map(lmap, bnd, bshape, lstride) || !make_batch_map(umap, bnd, bshape, ustride)) return GPTQ2D_EINVAL;
   if (m <= 0 || n <= 0 || outer_tiles < 1) return GPTQ2D_EINVAL;
-  if (kron && (sizeof(T) != 4 || bnd != 0 || n != (int64_t)kron->np * kron->nq)) return GPTQ2D_EUNSUPPORTED;
+  // U from its factors: the outer flush that reads them is the tuned tile flush alone (m, n < 2^20), so sizes it
+  // rejects are refused here, before any stage has written y
+  if (kron && (sizeof(T) != 4 || bnd != 0 || n != (int64_t)kron->np * kron->nq || m >= ((int64_t)1 << 20) ||
+               n >= ((int64_t)1 << 20)))
+    return GPTQ2D_EUNSUPPORTED;
   // the tile kernels index inside a tile with 32-bit offsets (32 rows of a row length < 2^26)
   if (m >= ((int64_t)1 << 26) || n >= ((int64_t)1 << 26)) return GPTQ2D_EUNSUPPORTED;
   if (qkind != Q_ROUND && qkind != Q_AFFINE && qkind != Q_FORCED && !(rows && qkind == Q_ABSMAX)) return GPTQ2D_EINVAL;

@@ -230,7 +230,7 @@ def _kron_fusable(y, l, u, batch_shape, spec):
         return False
     m, n = y.shape
     tensors = [y, l, u.inner] + [t for t in (spec["qa"], spec["qb"]) if t is not None]
-    return (u.inner.size(0) % 16 == 0 and m % 4 == 0 and n % 4 == 0 and n < 1 << 26 and
+    return (u.inner.size(0) % 16 == 0 and m % 4 == 0 and n % 4 == 0 and m < 1 << 20 and n < 1 << 20 and
             all(t.data_ptr() % 16 == 0 for t in tensors) and
             all(t.shape == y.shape for t in (spec["qa"], spec["qb"]) if t is not None))
 

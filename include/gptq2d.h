@@ -223,7 +223,8 @@ extern "C" {
  * (contiguous); other arguments as gptq2d_sweep_fused_se_f32.  Replaces the explicit U that the
  * reference's Algorithm 4 never forms (gptq_2d_reference.py:270-294 reads only the per-mode factors;
  * the reference's GPU sweep, gptq_2d.py:1378-1447, takes the n x n U).  GPTQ2D_EUNSUPPORTED unless
- * nq % 16 == 0, n < 2^26, m % 4 == n % 4 == 0 and y, c, e, l, uq are 16-byte aligned. */
+ * nq % 16 == 0, m < 2^20, n < 2^20, m % 4 == n % 4 == 0 and y, c, e, l, uq are 16-byte aligned, all
+ * checked before any device work. */
 int gptq2d_sweep_fused_kron_f32(float* y, float* c, float* e, const float* l, const float* up, const float* uq,
                                 int64_t m, int64_t np, int64_t nq, int64_t p, int64_t q, int32_t qkind,
                                 const float* qa, const float* qb, double qmin, double qmax, int32_t dtype16,

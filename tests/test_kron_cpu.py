@@ -61,6 +61,13 @@ def test_fused_reader_selection():
     assert not fusable(64, 3, 32, dtype=torch.float64)     # fp64 engine
     assert not fusable(64, 3, 32, batch=(2,))              # a batch of matrices
     assert not fusable(64, 3, 32, spec_kind=None)          # a plug-in quantizer
+    # m = 2^20 rows: beyond the factor-reading flush (the check reads only L's rank and alignment, so a small
+    # stand-in L keeps this test's memory at the 64 MiB of y)
+    y = torch.zeros(1 << 20, 16)
+    u = G.KroneckerU(torch.eye(1), torch.eye(16))
+    spec = G._fused_spec(QI.round_quantizer, (), y, torch.Size(()))
+    assert not G._kron_fusable(y, torch.eye(4), u, torch.Size(()), spec)
+    assert G._kron_fusable(y[: (1 << 20) - 4], torch.eye(4), u, torch.Size(()), spec)
 
 
 def test_entry_point_rejects_bad_arguments():
@@ -80,6 +87,8 @@ def test_entry_point_rejects_bad_arguments():
     assert call(np_=0) == EINVAL
     assert call(nq=40) == EUNSUPPORTED                      # inner size not a multiple of 16
     assert call(np_=1 << 20, nq=64) == EUNSUPPORTED         # n >= 2^26
+    assert call(np_=1 << 15, nq=32) == EUNSUPPORTED         # n = 2^20: beyond the factor-reading flush
+    assert call(m=1 << 20) == EUNSUPPORTED                  # m = 2^20: the same
     assert call(p=3) == EINVAL                              # super-entry rows must divide m
     assert call(q=16) == EUNSUPPORTED                       # only 1 x 1 and 1 x 32 super-entries
     assert call(m=0) == EINVAL
